@@ -1,0 +1,381 @@
+// The C ABI (include/hat.h): the boundary a Rust (or any FFI) caller binds.
+#include "../../include/hat.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gpu.h"
+#include "hip_rt.h"
+#include "weights.h"
+
+struct hat_weights {
+    std::unique_ptr<hat::Weights> w;
+};
+struct hat_backend {
+    std::unique_ptr<hat::GpuBackend> b;
+};
+
+namespace {
+thread_local std::string g_err;
+
+template <class F>
+int guard(F&& f)
+{
+    try {
+        g_err.clear();
+        return f();
+    } catch (const hat::Error& e) {
+        g_err = e.msg;
+    } catch (const std::bad_alloc&) {
+        g_err = "out of host memory";
+    } catch (const std::exception& e) {
+        g_err = e.what();
+    }
+    return -1;
+}
+}  // namespace
+
+extern "C" {
+
+const char* hat_version(void) { return "hat-mi355x 0.1.0"; }
+const char* hat_last_error(void) { return g_err.c_str(); }
+
+hat_weights* hat_weights_open(const char* path)
+{
+    hat_weights* out = nullptr;
+    guard([&] {
+        if (!path) throw hat::Error("null path");
+        out = new hat_weights{std::unique_ptr<hat::Weights>(hat::Weights::load(path))};
+        return 0;
+    });
+    return out;
+}
+
+void hat_weights_close(hat_weights* w) { delete w; }
+
+int hat_weights_info(const hat_weights* w, hat_model_info* o)
+{
+    return guard([&] {
+        if (!w || !o) throw hat::Error("null argument");
+        const hat::Weights& x = *w->w;
+        memset(o, 0, sizeof *o);
+        o->scale = x.scale;
+        o->window = x.window;
+        o->owin = x.owin;
+        o->embed = x.embed;
+        o->heads = x.heads;
+        o->head_dim = x.head_dim;
+        o->mlp_ratio = x.mlp_ratio;
+        if (x.depths.size() > 32) throw hat::Error("more than 32 stages");
+        o->n_stages = (int)x.depths.size();
+        for (size_t i = 0; i < x.depths.size(); ++i) o->depths[i] = x.depths[i];
+        o->compressed = x.compressed;
+        o->squeezed = x.squeezed;
+        o->head_feat = x.head_feat;
+        o->conv_scale = x.conv_scale;
+        o->img_range = x.img_range;
+        for (int i = 0; i < 3; ++i) o->mean[i] = x.mean[i];
+        return 0;
+    });
+}
+
+int hat_weights_count(const hat_weights* w) { return w ? (int)w->w->names.size() : -1; }
+
+const char* hat_weights_name(const hat_weights* w, int i)
+{
+    if (!w || i < 0 || i >= (int)w->w->names.size()) return nullptr;
+    return w->w->names[i].c_str();
+}
+
+const float* hat_weights_tensor(const hat_weights* w, const char* name, size_t* numel)
+{
+    const float* p = nullptr;
+    guard([&] {
+        if (!w || !name) throw hat::Error("null argument");
+        p = w->w->t(name);
+        if (numel) *numel = w->w->info(name).numel();
+        return 0;
+    });
+    return p;
+}
+
+long hat_weights_index_i64(const hat_weights* w, const char* name, long long* out, size_t n)
+{
+    long r = -1;
+    guard([&] {
+        if (!w || !name) throw hat::Error("null argument");
+        std::vector<int64_t> v = w->w->i64(name);
+        for (size_t i = 0; i < v.size() && i < n && out; ++i) out[i] = v[i];
+        r = (long)v.size();
+        return 0;
+    });
+    return r;
+}
+
+int hat_weights_generate(const char* path, const char* variant, int scale, unsigned long long seed,
+                         const int* depths, int n_depths)
+{
+    return guard([&] {
+        if (!path || !variant) throw hat::Error("null argument");
+        hat::Variant v;
+        if (!hat::variant_by_name(variant, &v))
+            throw hat::Error(std::string("unknown variant `") + variant + "` (hat-s, hat, hat-l)");
+        if (depths && n_depths > 0) v.depths.assign(depths, depths + n_depths);
+        hat::generate_weights(path, v, scale, seed);
+        return 0;
+    });
+}
+
+int hat_gpu_available(void)
+{
+    try {
+        std::string why;
+        return hat::gpu_available(&why) ? 1 : 0;
+    } catch (...) {
+        return 0;
+    }
+}
+
+hat_backend* hat_backend_new(const hat_weights* w, const char* device)
+{
+    hat_backend* out = nullptr;
+    guard([&] {
+        if (!w) throw hat::Error("null weights");
+        if (device && strcmp(device, "gpu") != 0)
+            throw hat::Error(std::string("device `") + device +
+                             "`: this library is the MI355X backend and has only `gpu`");
+        out = new hat_backend{std::unique_ptr<hat::GpuBackend>(new hat::GpuBackend(*w->w))};
+        return 0;
+    });
+    return out;
+}
+
+const char* hat_backend_name(const hat_backend* b) { return b ? b->b->name() : nullptr; }
+
+int hat_backend_forward(hat_backend* b, size_t h, size_t w, const float* in, float* out)
+{
+    return guard([&] {
+        if (!b || !in || !out) throw hat::Error("null argument");
+        b->b->forward((int)h, (int)w, in, out);
+        return 0;
+    });
+}
+
+int hat_backend_forward_device(hat_backend* b, size_t h, size_t w, const float* d_in, float* d_out)
+{
+    return guard([&] {
+        if (!b || !d_in || !d_out) throw hat::Error("null argument");
+        b->b->forward_device((int)h, (int)w, d_in, d_out);
+        return 0;
+    });
+}
+
+int hat_backend_synchronize(hat_backend* b)
+{
+    return guard([&] {
+        if (!b) throw hat::Error("null backend");
+        hat::Runtime& rt = hat::Runtime::get();
+        rt.check(rt.api().StreamSynchronize(b->b->stream()), "hipStreamSynchronize");
+        return 0;
+    });
+}
+
+size_t hat_backend_acts_bytes(const hat_backend* b) { return b ? b->b->acts_bytes() : 0; }
+size_t hat_backend_weight_bytes(const hat_backend* b) { return b ? b->b->weight_bytes() : 0; }
+void hat_backend_free(hat_backend* b) { delete b; }
+
+// main.rs:312-326 with the fixture format of fixture.rs:44-107.
+int hat_verify(const hat_weights* w, const char* device, const char* fixture_path)
+{
+    int rc = guard([&] {
+        if (!w || !fixture_path) throw hat::Error("null argument");
+        FILE* f = fopen(fixture_path, "rb");
+        if (!f) throw hat::Error(std::string(fixture_path) + ": " + strerror(errno));
+        std::vector<unsigned char> b;
+        unsigned char buf[65536];
+        size_t n;
+        while ((n = fread(buf, 1, sizeof buf, f)) > 0) b.insert(b.end(), buf, buf + n);
+        fclose(f);
+        auto u32 = [&](size_t off) {
+            uint32_t v;
+            memcpy(&v, &b[off], 4);
+            return v;
+        };
+        if (b.size() < 36 || memcmp(b.data(), "HATF", 4) != 0)
+            throw hat::Error(std::string(fixture_path) + ": not a hat fixture (want 4-byte magic HATF)");
+        const uint32_t version = u32(4), h = u32(8), wd = u32(12), c = u32(16), scale = u32(20),
+                       flags = u32(28);
+        if (version != 1) throw hat::Error("fixture version " + std::to_string(version) + ", this engine reads 1");
+        if (flags != 0) throw hat::Error("fixture flags are not zero");
+        const size_t need = 36 + 4 * ((size_t)h * wd * c + (size_t)h * scale * wd * scale * c);
+        if (b.size() != need)
+            throw hat::Error(std::string(fixture_path) + ": " + std::to_string(need) + " bytes expected, " +
+                             std::to_string(b.size()) + " present");
+        if ((int)scale != w->w->scale)
+            throw hat::Error(std::string(fixture_path) + " is a x" + std::to_string(scale) +
+                             " fixture but the model is x" + std::to_string(w->w->scale));
+        std::vector<float> in((size_t)h * wd * c), exp((size_t)h * scale * wd * scale * c);
+        memcpy(in.data(), &b[36], in.size() * 4);
+        memcpy(exp.data(), &b[36 + in.size() * 4], exp.size() * 4);
+        if (device && strcmp(device, "gpu") != 0) throw hat::Error("only the gpu device exists here");
+        hat::GpuBackend be(*w->w);
+        std::vector<float> got(exp.size());
+        be.forward((int)h, (int)wd, in.data(), got.data());
+        float worst = 0.f;
+        size_t at = 0;
+        double mean = 0;
+        for (size_t i = 0; i < got.size(); ++i) {
+            float d = std::fabs(exp[i] - got[i]);
+            mean += d;
+            if (d > worst || std::isnan(d)) {
+                worst = std::isnan(d) ? INFINITY : d;
+                at = i;
+            }
+        }
+        const size_t oh = (size_t)h * scale, ow = (size_t)wd * scale, plane = oh * ow;
+        printf("  verify worst |diff| %.3e at (y %zu, x %zu, ch %zu), mean |diff| %.3e\n", worst,
+               (at % plane) / ow, (at % plane) % ow, at / plane, mean / got.size());
+        if (worst > 1e-4f) {
+            char m[128];
+            snprintf(m, sizeof m, "worst |diff| %.3e exceeds 1e-4", worst);
+            g_err = m;
+            return 1;
+        }
+        printf("  ok\n");
+        return 0;
+    });
+    return rc;
+}
+
+int hat_gpu_selftest(void)
+{
+    return guard([&] {
+        std::string err;
+        int n = hat::gpu_selftest(&err);
+        if (n < 0) throw hat::Error(err);
+        return n;
+    });
+}
+
+int hat_op_swmsa(const float* x, float* out, int hp, int wp, int c, int heads, int shift,
+                 const float* qkv_w, const float* qkv_b, const float* proj_w, const float* proj_b,
+                 const float* table, int iters, float* ms, float* attn_ms)
+{
+    return guard([&] {
+        hat::op_swmsa(x, out, hp, wp, c, heads, shift, qkv_w, qkv_b, proj_w, proj_b, table, iters, ms,
+                      attn_ms);
+        return 0;
+    });
+}
+
+int hat_op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int mlp_ratio,
+                const float* n1w, const float* n1b, const float* qkv_w, const float* qkv_b,
+                const float* proj_w, const float* proj_b, const float* table, const float* n2w,
+                const float* n2b, const float* fc1_w, const float* fc1_b, const float* fc2_w,
+                const float* fc2_b, int iters, float* ms, float* attn_ms)
+{
+    return guard([&] {
+        hat::op_ocab(x, out, hp, wp, c, heads, mlp_ratio, n1w, n1b, qkv_w, qkv_b, proj_w, proj_b, table,
+                     n2w, n2b, fc1_w, fc1_b, fc2_w, fc2_b, iters, ms, attn_ms);
+        return 0;
+    });
+}
+
+void* hat_device_alloc(size_t bytes)
+{
+    void* p = nullptr;
+    guard([&] {
+        p = hat::Runtime::get().alloc(bytes);
+        return 0;
+    });
+    return p;
+}
+
+int hat_device_free(void* p)
+{
+    return guard([&] {
+        hat::Runtime::get().free(p);
+        return 0;
+    });
+}
+
+int hat_memcpy_h2d(void* dst, const void* src, size_t bytes)
+{
+    return guard([&] {
+        hat::Runtime::get().h2d(dst, src, bytes);
+        return 0;
+    });
+}
+
+int hat_memcpy_d2h(void* dst, const void* src, size_t bytes)
+{
+    return guard([&] {
+        hat::Runtime::get().d2h(dst, src, bytes);
+        return 0;
+    });
+}
+
+int hat_device_synchronize(void)
+{
+    return guard([&] {
+        hat::Runtime::get().sync();
+        return 0;
+    });
+}
+
+const char* hat_device_name(void)
+{
+    static std::string name;
+    guard([&] {
+        name = hat::Runtime::get().device_name();
+        return 0;
+    });
+    return name.c_str();
+}
+
+int hat_device_cu_count(void)
+{
+    int n = 0;
+    guard([&] {
+        n = hat::Runtime::get().cu_count();
+        return 0;
+    });
+    return n;
+}
+
+int hat_profile_begin(void)
+{
+    return guard([&] {
+        hat::Runtime::get();
+        hat::profile_begin();
+        return 0;
+    });
+}
+
+int hat_profile_end(void)
+{
+    return guard([&] {
+        hat::profile_end();
+        return 0;
+    });
+}
+
+int hat_profile_count(void) { return (int)hat::profile_stats().size(); }
+
+int hat_profile_get(int i, char* name, int cap, long* count, double* total_ms)
+{
+    return guard([&] {
+        std::vector<hat::KernelStat> st = hat::profile_stats();
+        if (i < 0 || i >= (int)st.size()) throw hat::Error("profile index out of range");
+        if (name && cap > 0) snprintf(name, (size_t)cap, "%s", st[i].name.c_str());
+        if (count) *count = st[i].count;
+        if (total_ms) *total_ms = st[i].total_ms;
+        return 0;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,648 @@
+#include "gpu.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "kargs.h"
+
+namespace hat {
+
+using namespace hatk;
+
+// ---------------------------------------------------------------------------
+// Weight repacking
+
+std::vector<float> pack_linear(const float* w, int N, int K, int* Kp)
+{
+    const int kp = (K + 15) / 16 * 16;
+    std::vector<float> out((size_t)N * kp, 0.0f);
+    for (int n = 0; n < N; ++n) memcpy(&out[(size_t)n * kp], w + (size_t)n * K, sizeof(float) * K);
+    *Kp = kp;
+    return out;
+}
+
+// [CO][CI][3][3] -> [CIp/16][9][COp][16]; with r > 0 the output channels are
+// permuted so that channel o = c*r*r + i*r + j lands at o' = (i*r + j)*Cf + c
+// (Cf = CO / r^2), which lets the conv store four consecutive o' as four
+// consecutive channels of one pixel of the shuffled plane.
+std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
+                             std::vector<float>* bias_out, int* CIp, int* COp)
+{
+    const int cip = (CI + 15) / 16 * 16, cop = (CO + 15) / 16 * 16;
+    const int Cf = r > 0 ? CO / (r * r) : 0;
+    auto src_channel = [&](int o2) -> int {
+        if (r <= 0) return o2;
+        const int sub = o2 / Cf, c = o2 % Cf;
+        const int i = sub / r, j = sub % r;
+        return c * r * r + i * r + j;
+    };
+    std::vector<float> out((size_t)cip * 9 * cop, 0.0f);
+    bias_out->assign(cop, 0.0f);
+    for (int o2 = 0; o2 < CO; ++o2) {
+        const int o = src_channel(o2);
+        (*bias_out)[o2] = b[o];
+        for (int ci = 0; ci < CI; ++ci)
+            for (int tap = 0; tap < 9; ++tap) {
+                const int cc = ci / 16, c16 = ci % 16;
+                out[(((size_t)cc * 9 + tap) * cop + o2) * 16 + c16] = w[((size_t)o * CI + ci) * 9 + tap];
+            }
+    }
+    *CIp = cip;
+    *COp = cop;
+    return out;
+}
+
+// ---------------------------------------------------------------------------
+// Launch helpers shared by the backend and the op entry points.
+
+namespace {
+
+const char* gemm_kernel(int N, int epi, bool ln)
+{
+    const bool n9 = N % 144 == 0;
+    switch (epi) {
+    case EPI_STORE: return n9 ? "hat_gemm_n9_store" : "hat_gemm_n6_store";
+    case EPI_GELU:
+        if (!ln) throw Error("GELU GEMM is only built with the LayerNorm prologue");
+        return n9 ? "hat_gemm_n9_gelu_ln" : "hat_gemm_n6_gelu_ln";
+    case EPI_QKV:
+        return ln ? (n9 ? "hat_gemm_n9_qkv_ln" : "hat_gemm_n6_qkv_ln")
+                  : (n9 ? "hat_gemm_n9_qkv" : "hat_gemm_n6_qkv");
+    case EPI_RESID: return n9 ? "hat_gemm_n9_resid" : "hat_gemm_n6_resid";
+    case EPI_HAB: return n9 ? "hat_gemm_n9_hab" : "hat_gemm_n6_hab";
+    }
+    throw Error("unknown GEMM epilogue");
+}
+
+void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M, float* out,
+              int ldo, int epi, const float* res, const float* aux, const float* gate,
+              const float* lnw, const float* lnb, int heads, int hdim, float cscale)
+{
+    if (L.K % 4 != 0 || lda % 4 != 0 || lda < L.K)
+        throw Error("GEMM: K and lda must be multiples of 4 with lda >= K");
+    if (M > 0x7fffffffL) throw Error("GEMM: too many rows");
+    GemmArgs p{};
+    p.a = a;
+    p.w = L.w;
+    p.bias = L.b;
+    p.out = out;
+    p.res = res;
+    p.aux = aux;
+    p.gate = gate;
+    p.lnw = lnw;
+    p.lnb = lnb;
+    p.M = (int)M;
+    p.N = L.N;
+    p.K = L.K;
+    p.Kp = L.Kp;
+    p.lda = lda;
+    p.ldo = ldo;
+    p.heads = heads;
+    p.hdim = hdim;
+    p.cscale = cscale;
+    p.eps = 1e-5f;
+    const int BN = L.N % 144 == 0 ? 144 : 96;
+    launch(s, gemm_kernel(L.N, epi, lnw != nullptr), (unsigned)((M + 127) / 128),
+           (unsigned)((L.N + BN - 1) / BN), 1, 256, p);
+}
+
+void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, int H, int W,
+              float* out, int co_stride, int epi, int act, const float* res, float* partial,
+              int crop_h, int crop_w, float img_range, const float* mean)
+{
+    if (H % 8 != 0 || W % 16 != 0) throw Error("conv: plane must be a multiple of 8x16");
+    if (cin_stride % 4 != 0 || cin_stride < C.CI) throw Error("conv: bad input channel stride");
+    const char* name = nullptr;
+    int BN = 16;
+    switch (epi) {
+    case CEPI_STORE:
+        if (C.CO <= 16) { name = "hat_conv_n1_store"; BN = 16; }
+        else if (C.CO <= 64) { name = "hat_conv_n4_store"; BN = 64; }
+        else { name = "hat_conv_n3_store"; BN = 48; }
+        break;
+    case CEPI_RESID: name = "hat_conv_n3_resid"; BN = 48; break;
+    case CEPI_COLSUM: name = "hat_conv_n3_colsum"; BN = 48; break;
+    case CEPI_SHUFFLE:
+        name = "hat_conv_n4_shuffle";
+        BN = 64;
+        if ((C.CO / (C.r * C.r)) % 4 != 0) throw Error("conv: shuffled width must be a multiple of 4");
+        break;
+    case CEPI_FINAL: name = "hat_conv_n1_final"; BN = 16; break;
+    default: throw Error("conv: unknown epilogue");
+    }
+    ConvArgs p{};
+    p.in = in;
+    p.w = C.w;
+    p.bias = C.b;
+    p.out = out;
+    p.res = res;
+    p.partial = partial;
+    p.H = H;
+    p.W = W;
+    p.CI = C.CI;
+    p.CIp = C.CIp;
+    p.cin_stride = cin_stride;
+    p.CO = C.CO;
+    p.COp = C.COp;
+    p.co_stride = co_stride;
+    p.act = act;
+    p.r = C.r;
+    p.crop_h = crop_h;
+    p.crop_w = crop_w;
+    p.img_range = img_range;
+    if (mean) {
+        p.mean0 = mean[0];
+        p.mean1 = mean[1];
+        p.mean2 = mean[2];
+    }
+    launch(s, name, (unsigned)((W / 16) * (H / 8)), (unsigned)((C.CO + BN - 1) / BN), 1, 256, p);
+}
+
+void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, const Plan& pl,
+              int heads, int D, bool oca, int shift)
+{
+    if (pl.win != 16 || pl.owin != 24)
+        throw Error("attention: the gfx950 kernels are built for window 16 / overlap window 24");
+    const char* name = nullptr;
+    if (D == 24) name = oca ? "hat_attn_oca_d24" : "hat_attn_sw_d24";
+    else if (D == 30) name = oca ? "hat_attn_oca_d30" : "hat_attn_sw_d30";
+    else throw Error("attention: head_dim " + std::to_string(D) + " has no kernel (24 and 30 do)");
+    AttnArgs p{};
+    p.qkv = qkv;
+    p.table = table;
+    p.out = out;
+    p.hp = pl.hp;
+    p.wp = pl.wp;
+    p.nx = pl.nx();
+    p.ny = pl.ny();
+    p.heads = heads;
+    p.D = D;
+    p.C = heads * D;
+    p.shift = shift;
+    p.owin = pl.owin;
+    p.opad = pl.opad();
+    p.T = (int)pl.tokens();
+    p.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+    launch(s, name, (unsigned)pl.nw(), (unsigned)heads, 1, 512, p);
+}
+
+void run_ln(hipStream_t s, const float* x, float* y, const float* w, const float* b, long rows, int C)
+{
+    if (C > 512) throw Error("layernorm: C > 512");
+    LnArgs p{x, y, w, b, (int)rows, C, 1e-5f};
+    launch(s, "hat_layernorm", (unsigned)((rows + 3) / 4), 1, 1, 256, p);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// GpuBackend
+
+float* GpuBackend::upload(const float* src, size_t n)
+{
+    Runtime& rt = Runtime::get();
+    float* d = (float*)rt.alloc(n * sizeof(float));
+    owned_.push_back(d);
+    rt.h2d(d, src, n * sizeof(float));
+    weight_bytes_ += n * sizeof(float);
+    return d;
+}
+
+void GpuBackend::upload_raw(const std::string& name)
+{
+    const TensorInfo& ti = wt_.info(name);
+    raw_[name] = upload(wt_.t(name), ti.numel());
+}
+
+void GpuBackend::upload_linear(const std::string& name)
+{
+    const TensorInfo& ti = wt_.info(name + ".weight");
+    DevLinear L;
+    L.N = (int)ti.shape[0];
+    L.K = (int)ti.shape[1];
+    std::vector<float> pk = pack_linear(wt_.t(name + ".weight"), L.N, L.K, &L.Kp);
+    L.w = upload(pk.data(), pk.size());
+    L.b = upload(wt_.t(name + ".bias"), L.N);
+    lin_[name] = L;
+}
+
+void GpuBackend::upload_conv(const std::string& name, int r)
+{
+    const TensorInfo& ti = wt_.info(name + ".weight");
+    DevConv C;
+    C.CO = (int)ti.shape[0];
+    C.CI = (int)ti.shape[1];
+    C.r = r;
+    std::vector<float> bias;
+    std::vector<float> pk = pack_conv(wt_.t(name + ".weight"), wt_.t(name + ".bias"), C.CO, C.CI, r,
+                                      &bias, &C.CIp, &C.COp);
+    C.w = upload(pk.data(), pk.size());
+    C.b = upload(bias.data(), bias.size());
+    conv_[name] = C;
+}
+
+// Gpu::new (gpu.rs:372-386): bring up the runtime, then upload every tensor.
+GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
+{
+    Runtime& rt = Runtime::get();
+    if (wt.window != 16 || wt.owin != 24)
+        throw Error("the gfx950 attention kernels are built for window 16 and overlap window 24");
+    if (wt.head_dim != 24 && wt.head_dim != 30)
+        throw Error("head_dim " + std::to_string(wt.head_dim) + " has no attention kernel (24, 30)");
+    if (wt.embed % 4 != 0 || wt.embed > 512) throw Error("embed_dim must be a multiple of 4, <= 512");
+    if (wt.squeezed > 64) throw Error("squeeze width above 64 is not supported");
+    if (wt.head_feat % 4 != 0) throw Error("head width must be a multiple of 4");
+    for (int d : wt.depths)
+        if (d < 1) throw Error("every stage needs at least one HAB");
+    rt.check(rt.api().StreamCreate(&stream_), "hipStreamCreate");
+    upload_conv("conv_first");
+    upload_raw("patch_embed.norm.weight");
+    upload_raw("patch_embed.norm.bias");
+    for (size_t s = 0; s < wt.depths.size(); ++s) {
+        const std::string L = "layers." + std::to_string(s);
+        for (int b = 0; b < wt.depths[s]; ++b) {
+            const std::string p = L + ".residual_group.blocks." + std::to_string(b);
+            for (const char* n : {".norm1.weight", ".norm1.bias", ".norm2.weight", ".norm2.bias",
+                                  ".attn.relative_position_bias_table",
+                                  ".conv_block.cab.3.attention.1.weight",
+                                  ".conv_block.cab.3.attention.1.bias",
+                                  ".conv_block.cab.3.attention.3.weight",
+                                  ".conv_block.cab.3.attention.3.bias"})
+                upload_raw(p + n);
+            upload_linear(p + ".attn.qkv");
+            upload_linear(p + ".attn.proj");
+            upload_linear(p + ".mlp.fc1");
+            upload_linear(p + ".mlp.fc2");
+            upload_conv(p + ".conv_block.cab.0");
+            upload_conv(p + ".conv_block.cab.2");
+        }
+        const std::string p = L + ".residual_group.overlap_attn";
+        for (const char* n : {".norm1.weight", ".norm1.bias", ".norm2.weight", ".norm2.bias",
+                              ".relative_position_bias_table"})
+            upload_raw(p + n);
+        upload_linear(p + ".qkv");
+        upload_linear(p + ".proj");
+        upload_linear(p + ".mlp.fc1");
+        upload_linear(p + ".mlp.fc2");
+        upload_conv(L + ".conv");
+    }
+    upload_raw("norm.weight");
+    upload_raw("norm.bias");
+    upload_conv("conv_after_body");
+    upload_conv("conv_before_upsample.0");
+    const auto blocks = wt.up_blocks();
+    for (size_t b = 0; b < blocks.size(); ++b)
+        upload_conv("upsample." + std::to_string(2 * b), blocks[b].first);
+    upload_conv("conv_last");
+}
+
+GpuBackend::~GpuBackend()
+{
+    try {
+        Runtime& rt = Runtime::get();
+        rt.api().StreamSynchronize(stream_);
+        free_plan();
+        for (void* p : owned_) rt.free(p);
+        rt.api().StreamDestroy(stream_);
+    } catch (...) {
+    }
+}
+
+void GpuBackend::free_plan()
+{
+    Runtime& rt = Runtime::get();
+    for (void* p : acts_) rt.free(p);
+    acts_.clear();
+    acts_bytes_ = 0;
+    have_plan_ = false;
+}
+
+// Acts::new (gpu.rs:293-334): one allocation set per plan, reused by every
+// forward at that size.
+void GpuBackend::ensure_plan(int h, int w)
+{
+    Plan p = Plan::make(h, w, wt_.window, wt_.embed);
+    if (have_plan_ && p == plan_) return;
+    free_plan();
+    plan_ = p;
+    Runtime& rt = Runtime::get();
+    const size_t T = (size_t)p.tokens(), C = wt_.embed;
+    auto A = [&](size_t floats) -> float* {
+        float* d = (float*)rt.alloc(floats * sizeof(float));
+        acts_.push_back(d);
+        acts_bytes_ += floats * sizeof(float);
+        return d;
+    };
+    t1_stride_ = (wt_.compressed + 3) / 4 * 4;
+    nblk_conv2_ = (p.wp / 16) * (p.hp / 8);
+    x0_ = A(T * 4);
+    body_ = A(T * C);
+    xa_ = A(T * C);
+    xb_ = A(T * C);
+    xn_ = A(T * C);
+    t1_ = A(T * t1_stride_);
+    t2_ = A(T * C);
+    partial_ = A((size_t)nblk_conv2_ * C);
+    gate_ = A(C);
+    qkv_ = A(3 * T * C);
+    ao_ = A(T * C);
+    hidden_ = A(T * C * wt_.mlp_ratio);
+    // Head ping-pong: the plane at each resolution goes to alternate buffers.
+    size_t need[2] = {T * (size_t)wt_.head_feat, 0};
+    size_t res = 1;
+    int which = 0;
+    for (auto& b : wt_.up_blocks()) {
+        res *= (size_t)b.first * b.first;
+        which ^= 1;
+        need[which] = std::max(need[which], T * res * (size_t)wt_.head_feat);
+    }
+    head0_ = A(need[0]);
+    head1_ = A(std::max<size_t>(need[1], 4));
+    const size_t s2 = (size_t)wt_.scale * wt_.scale;
+    din_ = A(3 * (size_t)h * w);
+    dout_ = A(3 * (size_t)h * w * s2);
+    have_plan_ = true;
+}
+
+void GpuBackend::layernorm(const float* x, float* y, const std::string& prefix, long rows)
+{
+    run_ln(stream_, x, y, raw_.at(prefix + ".weight"), raw_.at(prefix + ".bias"), rows, wt_.embed);
+}
+
+void GpuBackend::gemm(const DevLinear& L, const float* a, int lda, long M, float* out, int ldo,
+                      int epi, const float* res, const float* aux, const float* gate,
+                      const float* lnw, const float* lnb)
+{
+    run_gemm(stream_, L, a, lda, M, out, ldo, epi, res, aux, gate, lnw, lnb, wt_.heads,
+             wt_.head_dim, wt_.conv_scale);
+}
+
+void GpuBackend::conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
+                      int co_stride, int epi, int act, const float* res, float* partial,
+                      int crop_h, int crop_w)
+{
+    run_conv(stream_, C, in, cin_stride, H, W, out, co_stride, epi, act, res, partial, crop_h,
+             crop_w, wt_.img_range, wt_.mean);
+}
+
+void GpuBackend::attention(const std::string& table, bool oca, int shift)
+{
+    run_attn(stream_, qkv_, raw_.at(table), ao_, plan_, wt_.heads, wt_.head_dim, oca, shift);
+}
+
+// HAB.forward (hat_arch.py:266-309; cpu.rs:1090-1166):
+//   x = shortcut + attn(norm1 x) + conv_x * conv_scale;  x = x + mlp(norm2 x)
+void GpuBackend::hab(int stage, int block, float* x_in, float* x_out)
+{
+    const std::string p = "layers." + std::to_string(stage) + ".residual_group.blocks." +
+                          std::to_string(block);
+    const long T = plan_.tokens();
+    const int C = wt_.embed, H = plan_.hp, W = plan_.wp;
+    layernorm(x_in, xn_, p + ".norm1", T);
+    // CAB: conv3x3 -> GELU -> conv3x3 (+ per-block channel sums) -> gate.
+    conv(conv_.at(p + ".conv_block.cab.0"), xn_, C, H, W, t1_, t1_stride_, CEPI_STORE, 1);
+    conv(conv_.at(p + ".conv_block.cab.2"), t1_, t1_stride_, H, W, t2_, C, CEPI_COLSUM, 0, nullptr,
+         partial_);
+    SeArgs se{};
+    se.partial = partial_;
+    se.nblk = nblk_conv2_;
+    se.co_stride = C;
+    se.count = (float)T;
+    se.w1 = raw_.at(p + ".conv_block.cab.3.attention.1.weight");
+    se.b1 = raw_.at(p + ".conv_block.cab.3.attention.1.bias");
+    se.w2 = raw_.at(p + ".conv_block.cab.3.attention.3.weight");
+    se.b2 = raw_.at(p + ".conv_block.cab.3.attention.3.bias");
+    se.gate = gate_;
+    se.C = C;
+    se.sq = wt_.squeezed;
+    launch(stream_, "hat_se_gate", 1, 1, 1, 256, se);
+    // Window attention, the roll and the partition folded into its addressing.
+    gemm(lin_.at(p + ".attn.qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
+    attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0);
+    gemm(lin_.at(p + ".attn.proj"), ao_, C, T, x_out, C, EPI_HAB, x_in, t2_, gate_);
+    // MLP with norm2 as the fc1 prologue.
+    gemm(lin_.at(p + ".mlp.fc1"), x_out, C, T, hidden_, C * wt_.mlp_ratio, EPI_GELU, nullptr,
+         nullptr, nullptr, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"));
+    gemm(lin_.at(p + ".mlp.fc2"), hidden_, C * wt_.mlp_ratio, T, x_out, C, EPI_RESID, x_out);
+}
+
+// OCAB.forward (hat_arch.py:392-438; cpu.rs:1170-1198): x = proj(attn) + x;
+// x = x + mlp(norm2 x). norm1 is the qkv GEMM's prologue.
+void GpuBackend::ocab(int stage, float* x)
+{
+    const std::string p = "layers." + std::to_string(stage) + ".residual_group.overlap_attn";
+    const long T = plan_.tokens();
+    const int C = wt_.embed;
+    gemm(lin_.at(p + ".qkv"), x, C, T, qkv_, 0, EPI_QKV, nullptr, nullptr, nullptr,
+         raw_.at(p + ".norm1.weight"), raw_.at(p + ".norm1.bias"));
+    attention(p + ".relative_position_bias_table", true, 0);
+    gemm(lin_.at(p + ".proj"), ao_, C, T, x, C, EPI_RESID, x);
+    gemm(lin_.at(p + ".mlp.fc1"), x, C, T, hidden_, C * wt_.mlp_ratio, EPI_GELU, nullptr, nullptr,
+         nullptr, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"));
+    gemm(lin_.at(p + ".mlp.fc2"), hidden_, C * wt_.mlp_ratio, T, x, C, EPI_RESID, x);
+}
+
+// forward_planes (gpu.rs:714-748; cpu.rs:1318-1368) with Pre::adjust and finish
+// (backend.rs:71-109) folded into the first and last kernels.
+void GpuBackend::forward_device(int h, int w, const float* d_in, float* d_out)
+{
+    if (h <= 0 || w <= 0) throw Error(std::to_string(h) + "x" + std::to_string(w) + " is empty");
+    ensure_plan(h, w);
+    const long T = plan_.tokens();
+    const int C = wt_.embed, H = plan_.hp, W = plan_.wp;
+    PreArgs pa{d_in, x0_, h, w, H, W, 4, wt_.mean[0], wt_.mean[1], wt_.mean[2], wt_.img_range};
+    launch(stream_, "hat_pre", (unsigned)((T + 255) / 256), 1, 1, 256, pa);
+    conv(conv_.at("conv_first"), x0_, 4, H, W, body_, C, CEPI_STORE, 0);
+    layernorm(body_, xa_, "patch_embed.norm", T);
+    for (size_t s = 0; s < wt_.depths.size(); ++s) {
+        // RHAG (gpu.rs:592-610): conv3x3(blocks(x)) + x, with the stage input
+        // kept in xa_ and the blocks working in xb_.
+        for (int b = 0; b < wt_.depths[s]; ++b) hab((int)s, b, b == 0 ? xa_ : xb_, xb_);
+        ocab((int)s, xb_);
+        conv(conv_.at("layers." + std::to_string(s) + ".conv"), xb_, C, H, W, xa_, C, CEPI_RESID, 0,
+             xa_);
+    }
+    layernorm(xa_, xb_, "norm", T);
+    conv(conv_.at("conv_after_body"), xb_, C, H, W, xa_, C, CEPI_RESID, 0, body_);
+    // Head (gpu.rs:622-653): conv + LeakyReLU, [conv + PixelShuffle] per block, conv_last.
+    const int feat = wt_.head_feat;
+    conv(conv_.at("conv_before_upsample.0"), xa_, C, H, W, head0_, feat, CEPI_STORE, 2);
+    float* cur = head0_;
+    float* nxt = head1_;
+    int hh = H, ww = W;
+    const auto blocks = wt_.up_blocks();
+    for (size_t b = 0; b < blocks.size(); ++b) {
+        conv(conv_.at("upsample." + std::to_string(2 * b)), cur, feat, hh, ww, nxt, feat,
+             CEPI_SHUFFLE, 0);
+        hh *= blocks[b].first;
+        ww *= blocks[b].first;
+        std::swap(cur, nxt);
+    }
+    conv(conv_.at("conv_last"), cur, feat, hh, ww, d_out, 0, CEPI_FINAL, 0, nullptr, nullptr,
+         h * wt_.scale, w * wt_.scale);
+}
+
+// Backend::forward: host [3][h][w] in, host [3][h*s][w*s] out.
+void GpuBackend::forward(int h, int w, const float* in, float* out)
+{
+    if (h <= 0 || w <= 0) throw Error(std::to_string(h) + "x" + std::to_string(w) + " is empty");
+    ensure_plan(h, w);
+    Runtime& rt = Runtime::get();
+    const size_t s2 = (size_t)wt_.scale * wt_.scale;
+    rt.h2d(din_, in, 3 * (size_t)h * w * sizeof(float));
+    forward_device(h, w, din_, dout_);
+    rt.check(rt.api().StreamSynchronize(stream_), "forward");
+    rt.d2h(out, dout_, 3 * (size_t)h * w * s2 * sizeof(float));
+}
+
+// ---------------------------------------------------------------------------
+// Isolated ops.
+
+namespace {
+
+struct DevBuf {
+    float* p = nullptr;
+    DevBuf(size_t n) { p = (float*)Runtime::get().alloc(n * sizeof(float)); }
+    DevBuf(const float* src, size_t n) : DevBuf(n) { Runtime::get().h2d(p, src, n * sizeof(float)); }
+    ~DevBuf() { Runtime::get().free(p); }
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+};
+
+struct OpLinear {
+    DevBuf w, b;
+    DevLinear L;
+    OpLinear(const float* wt, const float* bias, int N, int K, std::vector<float> pk = {})
+        : w(1), b(bias, N)
+    {
+        L.N = N;
+        L.K = K;
+        pk = pack_linear(wt, N, K, &L.Kp);
+        Runtime::get().free(w.p);
+        w.p = (float*)Runtime::get().alloc(pk.size() * sizeof(float));
+        Runtime::get().h2d(w.p, pk.data(), pk.size() * sizeof(float));
+        L.w = w.p;
+        L.b = b.p;
+    }
+};
+
+struct Timer {
+    hipEvent_t a = nullptr, b = nullptr;
+    Timer()
+    {
+        const HipApi& api = Runtime::get().api();
+        api.EventCreate(&a);
+        api.EventCreate(&b);
+    }
+    ~Timer()
+    {
+        const HipApi& api = Runtime::get().api();
+        api.EventDestroy(a);
+        api.EventDestroy(b);
+    }
+};
+
+}  // namespace
+
+void op_swmsa(const float* x, float* out, int hp, int wp, int c, int heads, int shift,
+              const float* qkv_w, const float* qkv_b, const float* proj_w, const float* proj_b,
+              const float* table, int iters, float* ms, float* attn_ms)
+{
+    Runtime& rt = Runtime::get();
+    const HipApi& api = rt.api();
+    if (c % heads) throw Error("swmsa: c must be divisible by heads");
+    const int D = c / heads;
+    Plan pl = Plan::make(hp, wp, 16, c);
+    if (pl.hp != hp || pl.wp != wp) throw Error("swmsa: the plane must be a window multiple");
+    const size_t T = (size_t)hp * wp;
+    hipStream_t s = nullptr;
+    rt.check(api.StreamCreate(&s), "hipStreamCreate");
+    {
+        DevBuf dx(x, T * c), dq(3 * T * c), dao(T * c), dout(T * c), dtab(table, 961 * (size_t)heads);
+        OpLinear qkv(qkv_w, qkv_b, 3 * c, c), proj(proj_w, proj_b, c, c);
+        auto run = [&]() {
+            run_gemm(s, qkv.L, dx.p, c, (long)T, dq.p, 0, EPI_QKV, nullptr, nullptr, nullptr, nullptr,
+                     nullptr, heads, D, 0.f);
+            run_attn(s, dq.p, dtab.p, dao.p, pl, heads, D, false, shift);
+            run_gemm(s, proj.L, dao.p, c, (long)T, dout.p, c, EPI_STORE, nullptr, nullptr, nullptr,
+                     nullptr, nullptr, heads, D, 0.f);
+        };
+        run();
+        rt.check(api.StreamSynchronize(s), "swmsa");
+        if (iters > 0 && (ms || attn_ms)) {
+            Timer t, ta;
+            api.EventRecord(t.a, s);
+            for (int i = 0; i < iters; ++i) run();
+            api.EventRecord(t.b, s);
+            api.EventRecord(ta.a, s);
+            for (int i = 0; i < iters; ++i) run_attn(s, dq.p, dtab.p, dao.p, pl, heads, D, false, shift);
+            api.EventRecord(ta.b, s);
+            rt.check(api.EventSynchronize(ta.b), "swmsa timing");
+            float e = 0.f;
+            api.EventElapsedTime(&e, t.a, t.b);
+            if (ms) *ms = e / iters;
+            api.EventElapsedTime(&e, ta.a, ta.b);
+            if (attn_ms) *attn_ms = e / iters;
+        }
+        rt.d2h(out, dout.p, T * c * sizeof(float));
+    }
+    api.StreamDestroy(s);
+}
+
+void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int mlp_ratio,
+             const float* n1w, const float* n1b, const float* qkv_w, const float* qkv_b,
+             const float* proj_w, const float* proj_b, const float* table, const float* n2w,
+             const float* n2b, const float* fc1_w, const float* fc1_b, const float* fc2_w,
+             const float* fc2_b, int iters, float* ms, float* attn_ms)
+{
+    Runtime& rt = Runtime::get();
+    const HipApi& api = rt.api();
+    if (c % heads) throw Error("ocab: c must be divisible by heads");
+    const int D = c / heads;
+    Plan pl = Plan::make(hp, wp, 16, c);
+    if (pl.hp != hp || pl.wp != wp) throw Error("ocab: the plane must be a window multiple");
+    const size_t T = (size_t)hp * wp, hid = (size_t)c * mlp_ratio;
+    hipStream_t s = nullptr;
+    rt.check(api.StreamCreate(&s), "hipStreamCreate");
+    {
+        DevBuf dx(x, T * c), dwork(T * c), dq(3 * T * c), dao(T * c), dh(T * hid),
+            dtab(table, 1521 * (size_t)heads), d1w(n1w, c), d1b(n1b, c), d2w(n2w, c), d2b(n2b, c);
+        OpLinear qkv(qkv_w, qkv_b, 3 * c, c), proj(proj_w, proj_b, c, c),
+            fc1(fc1_w, fc1_b, (int)hid, c), fc2(fc2_w, fc2_b, c, (int)hid);
+        auto run = [&]() {
+            rt.check(api.MemcpyAsync(dwork.p, dx.p, T * c * sizeof(float), hipMemcpyDeviceToDevice, s),
+                     "copy");
+            run_gemm(s, qkv.L, dwork.p, c, (long)T, dq.p, 0, EPI_QKV, nullptr, nullptr, nullptr,
+                     d1w.p, d1b.p, heads, D, 0.f);
+            run_attn(s, dq.p, dtab.p, dao.p, pl, heads, D, true, 0);
+            run_gemm(s, proj.L, dao.p, c, (long)T, dwork.p, c, EPI_RESID, dwork.p, nullptr, nullptr,
+                     nullptr, nullptr, heads, D, 0.f);
+            run_gemm(s, fc1.L, dwork.p, c, (long)T, dh.p, (int)hid, EPI_GELU, nullptr, nullptr,
+                     nullptr, d2w.p, d2b.p, heads, D, 0.f);
+            run_gemm(s, fc2.L, dh.p, (int)hid, (long)T, dwork.p, c, EPI_RESID, dwork.p, nullptr,
+                     nullptr, nullptr, nullptr, heads, D, 0.f);
+        };
+        run();
+        rt.check(api.StreamSynchronize(s), "ocab");
+        rt.d2h(out, dwork.p, T * c * sizeof(float));
+        if (iters > 0 && (ms || attn_ms)) {
+            Timer t, ta;
+            api.EventRecord(t.a, s);
+            for (int i = 0; i < iters; ++i) run();
+            api.EventRecord(t.b, s);
+            api.EventRecord(ta.a, s);
+            for (int i = 0; i < iters; ++i) run_attn(s, dq.p, dtab.p, dao.p, pl, heads, D, true, 0);
+            api.EventRecord(ta.b, s);
+            rt.check(api.EventSynchronize(ta.b), "ocab timing");
+            float e = 0.f;
+            api.EventElapsedTime(&e, t.a, t.b);
+            if (ms) *ms = e / iters;
+            api.EventElapsedTime(&e, ta.a, ta.b);
+            if (attn_ms) *attn_ms = e / iters;
+        }
+    }
+    api.StreamDestroy(s);
+}
+
+}  // namespace hat

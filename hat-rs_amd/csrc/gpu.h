@@ -1,0 +1,108 @@
+// The MI355X backend behind the reference's Backend interface.
+//
+// Reference seam: `trait Backend { fn name(); fn forward(h, w, input) }`
+// (src/backend.rs:29-36) with `Gpu::new(&Weights)` (src/gpu.rs:372-386) and
+// `Gpu::forward` (src/gpu.rs:759-803). Input is [3][h][w] in [0,1] (not
+// mean-adjusted); output is [3][h*s][w*s] after denormalisation.
+#pragma once
+#include <map>
+#include <string>
+#include <vector>
+
+#include "hip_rt.h"
+#include "plan.h"
+#include "weights.h"
+
+namespace hat {
+
+class Backend {
+public:
+    virtual ~Backend() {}
+    virtual const char* name() const = 0;
+    virtual void forward(int h, int w, const float* in, float* out) = 0;
+};
+
+struct DevLinear {
+    float* w = nullptr;  // [N][Kp]
+    float* b = nullptr;  // [N]
+    int N = 0, K = 0, Kp = 0;
+};
+
+struct DevConv {
+    float* w = nullptr;  // [CIp/16][9][COp][16]
+    float* b = nullptr;  // [COp]
+    int CI = 0, CIp = 0, CO = 0, COp = 0, r = 0;
+};
+
+// Host-side repacking (also used by the selftest and the op entry points).
+std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
+std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
+                             std::vector<float>* bias_out, int* CIp, int* COp);
+
+class GpuBackend : public Backend {
+public:
+    explicit GpuBackend(const Weights& wt);
+    ~GpuBackend() override;
+    const char* name() const override { return "gpu"; }
+    void forward(int h, int w, const float* in, float* out) override;
+    // Device-resident variant: d_in [3][h][w], d_out [3][h*s][w*s].
+    void forward_device(int h, int w, const float* d_in, float* d_out);
+    size_t acts_bytes() const { return acts_bytes_; }
+    size_t weight_bytes() const { return weight_bytes_; }
+    hipStream_t stream() const { return stream_; }
+
+private:
+    const Weights& wt_;
+    hipStream_t stream_ = nullptr;
+    std::map<std::string, float*> raw_;
+    std::map<std::string, DevLinear> lin_;
+    std::map<std::string, DevConv> conv_;
+    std::vector<void*> owned_;
+    size_t weight_bytes_ = 0;
+
+    // per-plan buffers
+    Plan plan_;
+    bool have_plan_ = false;
+    std::vector<void*> acts_;
+    size_t acts_bytes_ = 0;
+    float *x0_ = nullptr, *body_ = nullptr, *xa_ = nullptr, *xb_ = nullptr, *xn_ = nullptr,
+          *t1_ = nullptr, *t2_ = nullptr, *partial_ = nullptr, *gate_ = nullptr, *qkv_ = nullptr,
+          *ao_ = nullptr, *hidden_ = nullptr, *head0_ = nullptr, *head1_ = nullptr,
+          *din_ = nullptr, *dout_ = nullptr;
+    int t1_stride_ = 0, nblk_conv2_ = 0;
+
+    float* upload(const float* src, size_t n);
+    void upload_raw(const std::string& name);
+    void upload_linear(const std::string& name);
+    void upload_conv(const std::string& name, int r = 0);
+    void ensure_plan(int h, int w);
+    void free_plan();
+
+    void layernorm(const float* x, float* y, const std::string& prefix, long rows);
+    void gemm(const DevLinear& L, const float* a, int lda, long M, float* out, int ldo, int epi,
+              const float* res = nullptr, const float* aux = nullptr, const float* gate = nullptr,
+              const float* lnw = nullptr, const float* lnb = nullptr);
+    void conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
+              int co_stride, int epi, int act, const float* res = nullptr, float* partial = nullptr,
+              int crop_h = 0, int crop_w = 0);
+    void attention(const std::string& table, bool oca, int shift);
+    void hab(int stage, int block, float* x_in, float* x_out);
+    void ocab(int stage, float* x);
+};
+
+// Isolated ops on host buffers (cfg2 / cfg3 of the benchmark plan). Each
+// uploads, runs `warmup + iters` times, downloads, and reports the mean device
+// time per run (HIP events on the op's stream) in *ms when ms is non-null.
+void op_swmsa(const float* x, float* out, int hp, int wp, int c, int heads, int shift,
+              const float* qkv_w, const float* qkv_b, const float* proj_w, const float* proj_b,
+              const float* table, int iters, float* ms, float* attn_ms);
+void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int mlp_ratio,
+             const float* n1w, const float* n1b, const float* qkv_w, const float* qkv_b,
+             const float* proj_w, const float* proj_b, const float* table, const float* n2w,
+             const float* n2b, const float* fc1_w, const float* fc1_b, const float* fc2_w,
+             const float* fc2_b, int iters, float* ms, float* attn_ms);
+
+// Selftest: every kernel against a host twin. Prints "  ok  <name>" per pass.
+int gpu_selftest(std::string* err);
+
+}  // namespace hat

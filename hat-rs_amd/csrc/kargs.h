@@ -1,0 +1,108 @@
+// Kernel argument blocks shared by the host runtime (g++) and the gfx950
+// kernels (hipcc). Every kernel takes exactly one of these structs by value,
+// so the host packs the kernarg segment by copying the struct: the layout is
+// plain C (pointers 8 bytes, int/float 4 bytes) and identical on both sides.
+#pragma once
+#include <stdint.h>
+
+namespace hatk {
+
+// Activation layout everywhere on the device: token-major NHWC, [pixel][channel],
+// pixels in image row-major order over the padded plane (hp x wp).
+
+// out[m][n] = epilogue( prologue(A)[m][:] . W[n][:] + bias[n] )
+enum GemmEpi : int {
+    EPI_STORE = 0,       // out[m][n] = v
+    EPI_GELU = 1,        // out[m][n] = gelu(v)
+    EPI_QKV = 2,         // head-major scatter: out[which][head][m][dim]
+    EPI_RESID = 3,       // out[m][n] = res[m][n] + v
+    EPI_HAB = 4,         // out[m][n] = (res[m][n] + v) + (aux[m][n] * gate[n]) * cscale
+};
+
+struct GemmArgs {
+    const float* a;      // [M][lda]
+    const float* w;      // [N][ldw] row-major, K contiguous (zero-padded to Kp)
+    const float* bias;   // [N]
+    float* out;
+    const float* res;    // residual input (EPI_RESID / EPI_HAB)
+    const float* aux;    // EPI_HAB: conv branch [M][N]
+    const float* gate;   // EPI_HAB: channel gate [N]
+    const float* lnw;    // LayerNorm prologue weight [K] (null = no LN)
+    const float* lnb;    // LayerNorm prologue bias [K]
+    int M, N, K;         // logical sizes
+    int Kp;              // K rounded up to 16 (W rows are Kp long)
+    int lda, ldo;        // row strides of A and out (floats)
+    int heads, hdim;     // EPI_QKV geometry (N = 3 * heads * hdim)
+    float cscale;        // EPI_HAB conv scale
+    float eps;           // LayerNorm eps
+};
+
+// Implicit-GEMM 3x3 convolution, stride 1, zero padding 1, NHWC.
+enum ConvEpi : int {
+    CEPI_STORE = 0,      // out[p][co] = v (+ act)
+    CEPI_RESID = 1,      // out[p][co] = v + res[p][co]
+    CEPI_SHUFFLE = 2,    // pixel shuffle by r into [H*r][W*r][co/(r*r)] (channels pre-permuted)
+    CEPI_FINAL = 3,      // planar [3][ch][cw] with crop, / img_range + mean
+    CEPI_COLSUM = 4,     // store + per-block column sums into partial[blk][co]
+};
+
+struct ConvArgs {
+    const float* in;     // [H][W][cin_stride]
+    const float* w;      // repacked: [CIp/16][9][COp][16] (chunk, tap, co, 16 ci)
+    const float* bias;   // [COp]
+    float* out;
+    const float* res;    // CEPI_RESID
+    float* partial;      // CEPI_COLSUM: [gridDim.x*gridDim.y][co_stride]
+    int H, W;
+    int CI, CIp, cin_stride;
+    int CO, COp, co_stride;   // co_stride = channel stride of out (NHWC)
+    int act;             // 0 none, 1 gelu, 2 leaky(0.01)
+    int r;               // CEPI_SHUFFLE factor
+    int crop_h, crop_w;  // CEPI_FINAL crop (output size)
+    float img_range;     // CEPI_FINAL: out = v / img_range + mean
+    float mean0, mean1, mean2;
+};
+
+// Fused window attention. One block per (window, head).
+struct AttnArgs {
+    const float* qkv;    // head-major [3][heads][T][D]
+    const float* table;  // relative-position bias table [rows][heads]
+    float* out;          // [T][C] token-major, image order
+    int hp, wp, nx, ny;  // padded plane and window grid
+    int heads, D, C;
+    int shift;           // SW: cyclic shift (0 or win/2); mask applied iff shift > 0
+    int owin, opad;      // OCA: unfold window and padding
+    int T;
+    float qscale;        // head_dim^-0.5 * log2(e)
+};
+
+struct LnArgs {
+    const float* x;
+    float* y;
+    const float* w;
+    const float* b;
+    int rows, C;
+    float eps;
+};
+
+struct PreArgs {
+    const float* in;     // [3][h][w]
+    float* out;          // [hp][wp][cstride], channels >= 3 zeroed
+    int h, w, hp, wp, cstride;
+    float m0, m1, m2, range;
+};
+
+// Squeeze-excite gate: gate[c] = sigmoid(b2 + W2 relu(b1 + W1 mean)).
+struct SeArgs {
+    const float* partial; // [nblk][co_stride]
+    int nblk, co_stride;
+    float count;          // pixel count (mean = sum / count)
+    const float* w1;      // [sq][C]
+    const float* b1;      // [sq]
+    const float* w2;      // [C][sq]
+    const float* b2;      // [C]
+    float* gate;          // [C]
+    int C, sq;
+};
+
+}  // namespace hatk

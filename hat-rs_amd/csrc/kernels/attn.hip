@@ -1,0 +1,232 @@
+// Fused window attention on FP32 MFMA: QK^T + relative-position bias + shift
+// mask + softmax + PV for one (window, head) per block.
+//
+// Replaces hat_attention_d24/_d30 (cuda/hat.cu:246-316) and, by folding them
+// into its load/store addressing, the launches around it in the reference
+// graph: lg_window_gather/lg_window_scatter with the cyclic roll (cuda.rs:
+// 298-319, plan.rs:129-151), hat_bias_gather (hat.cu:98-112), hat_mask_build
+// (hat.cu:137-152) and hat_unfold_kv (hat.cu:170-198). The arithmetic it
+// reproduces is src/cpu.rs:772-844 (window_attention) and :852-900
+// (overlap_attention):  s = (q.k)*scale + bias (+ mask), softmax, P.V.
+//
+// Two key sources:
+//  * SW (OCA = false): the 256 tokens of a 16x16 window taken at a cyclic shift
+//    (plan.rs:129-151); when shifted, the SW-MSA mask of the reference's
+//    calculate_mask (hat_arch.py:921-940) is applied as -100 between tokens of
+//    different regions. Only the last window row/column straddles regions, and
+//    there the region of a token is its (y >= 8, x >= 8) half, so the mask is
+//    two bit compares per score.
+//  * OCA (OCA = true): the 24x24 nn.Unfold(24, stride 16, padding 4) window of
+//    keys (hat_arch.py:373-410); keys outside the plane are zero and keep their
+//    bias (they are not masked: hat_arch.py:419-427, cpu.rs:866-875).
+//
+// Work split: 512 threads = 8 waves, wave w owns queries [32w, 32w+32). The
+// scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x2_f32: the
+// A operand is a 32-key tile of K from LDS, the B operand the wave's 32 queries
+// held in registers. Lane l owns query l%32 and, per 32-key tile, 16 of its
+// scores: exactly the B operand of the next product O^T += V^T P^T, so the
+// probabilities never leave registers. V^T is staged in LDS so that a lane's
+// four consecutive keys are one float4 read. The dot-product dimension is
+// split between the two lane halves: half h reduces dims [h*D/2, (h+1)*D/2),
+// so D = 24 and D = 30 both need no padding in QK^T.
+//
+// Softmax is computed in base 2 (q pre-scaled by scale*log2(e), the bias table
+// by log2(e)) over key chunks with a running max, which equals the reference's
+// row max subtraction up to rounding.
+#include "common.h"
+
+using namespace hatk;
+
+template <int D, bool OCA>
+__device__ __forceinline__ void attn_body(const AttnArgs& p)
+{
+    constexpr int HALF = D / 2;                 // dims per lane half
+    constexpr int HP = (HALF + 3) / 4 * 4;      // LDS offset of the second half
+    constexpr int RSK = 2 * HP + 4;             // K row stride in LDS (floats)
+    constexpr int NK = OCA ? 576 : 256;         // keys per window
+    constexpr int NKT = NK / 32;                // 32-key tiles
+    constexpr int CHT = OCA ? 3 : 4;            // tiles per softmax chunk
+    constexpr int NCH = NKT / CHT;
+    constexpr int RSV = NK + 4;                 // V^T row stride in LDS
+    constexpr int TROWS = OCA ? 1521 : 961;     // bias table rows
+    static_assert(NKT % CHT == 0, "chunking");
+
+    __shared__ float Kl[NK * RSK];
+    __shared__ float Vt[D * RSV];
+    __shared__ float Tb[TROWS];
+
+    const int wi = blockIdx.x;
+    const int head = blockIdx.y;
+    const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int hp = p.hp, wp = p.wp, T = p.T, heads = p.heads;
+    const int shift = OCA ? 0 : p.shift;
+
+    const float* Qg = p.qkv + (size_t)head * T * D;
+    const float* Kg = p.qkv + (size_t)(heads + head) * T * D;
+    const float* Vg = p.qkv + (size_t)(2 * heads + head) * T * D;
+
+    // ---- stage K (row-major, halves split) and V^T in LDS ----
+    for (int e = tid; e < NK * D; e += 512) {
+        const int k = e / D, d = e - (e / D) * D;
+        int pix;
+        if (OCA) {
+            const int ky = k / 24, kx = k - (k / 24) * 24;
+            const int y = wy * 16 - 4 + ky, x = wx * 16 - 4 + kx;
+            pix = (y >= 0 && y < hp && x >= 0 && x < wp) ? y * wp + x : -1;
+        } else {
+            int y = wy * 16 + (k >> 4) + shift, x = wx * 16 + (k & 15) + shift;
+            if (y >= hp) y -= hp;
+            if (x >= wp) x -= wp;
+            pix = y * wp + x;
+        }
+        float kv = 0.0f, vv = 0.0f;
+        if (pix >= 0) {
+            kv = Kg[(size_t)pix * D + d];
+            vv = Vg[(size_t)pix * D + d];
+        }
+        Kl[k * RSK + (d < HALF ? d : HP + d - HALF)] = kv;
+        Vt[d * RSV + k] = vv;
+    }
+    // Bias table for this head, in log2 units. For OCA the table is stored
+    // rotated so that the reference's negative-index wrap (plan.rs:397-416)
+    // becomes a plain offset: Tb[j] = table[(j - 880) mod 1521].
+    for (int i = tid; i < TROWS; i += 512) {
+        int row = i;
+        if (OCA) {
+            row = i - 880;
+            if (row < 0) row += 1521;
+        }
+        Tb[i] = p.table[(size_t)row * heads + head] * HAT_LOG2E;
+    }
+    __syncthreads();
+
+    // ---- this lane's query ----
+    const int ql = lane & 31, h = lane >> 5;
+    const int q = wave * 32 + ql;
+    const int qy = q >> 4, qx = q & 15;
+    int qpix;
+    {
+        int y = wy * 16 + qy + shift, x = wx * 16 + qx + shift;
+        if (y >= hp) y -= hp;
+        if (x >= wp) x -= wp;
+        qpix = y * wp + x;
+    }
+    float qv[HALF];
+#pragma unroll
+    for (int s = 0; s < HALF; ++s) qv[s] = Qg[(size_t)qpix * D + h * HALF + s] * p.qscale;
+
+    // Bias addressing. SW: idx = (qy-ky+15)*31 + (qx-kx+15) = sw_base - (ky*31+kx).
+    // OCA: idx = (ky*39+kx) - (qy*39+qx) + 600 on the rotated table.
+    const int sw_base = (qy + 15) * 31 + qx + 15 - 4 * h;
+    const int oca_base = 600 - (qy * 39 + qx);
+    // Mask addends (SW, shifted): a key differs in region from the query when
+    // its half (bit 3 of y or x) differs, in the last window row / column.
+    const float NEG = -100.0f * HAT_LOG2E;
+    const bool mrow = !OCA && shift > 0 && wy == p.ny - 1;
+    const bool mcol = !OCA && shift > 0 && wx == p.nx - 1;
+    const bool r_lo = mrow && (qy & 8), r_hi = mrow && !(qy & 8);
+    const bool c_lo = mcol && (qx & 8), c_hi = mcol && !(qx & 8);
+    const float madd[2][2] = {{(r_lo || c_lo) ? NEG : 0.0f, (r_lo || c_hi) ? NEG : 0.0f},
+                              {(r_hi || c_lo) ? NEG : 0.0f, (r_hi || c_hi) ? NEG : 0.0f}};
+
+    f32x16 o;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+    float mrun = -INFINITY, lrun = 0.0f;
+
+    // The OCA chunk loop stays rolled: unrolled, the compiler hoists the K
+    // operand reads of all 18 key tiles and spills.
+    constexpr int CH_UNROLL = OCA ? 1 : NCH;
+#pragma unroll CH_UNROLL
+    for (int ch = 0; ch < NCH; ++ch) {
+        f32x16 s[CHT];
+#pragma unroll
+        for (int t = 0; t < CHT; ++t) {
+            const int kt = ch * CHT + t;
+            const float* kp = Kl + (kt * 32 + ql) * RSK + h * HP;
+            f32x16 a;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) a[i] = 0.0f;
+#pragma unroll
+            for (int st = 0; st < HALF; ++st) a = mfma32(kp[st], qv[st], a);
+            s[t] = a;
+        }
+        // bias (+ mask), chunk max
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < CHT; ++t) {
+            const int kt = ch * CHT + t;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key0 = kt * 32 + (i >> 2) * 8 + (i & 3);  // key for h = 0
+                float v = s[t][i];
+                if (OCA) {
+                    // (ky*39 + kx) = key + 15*ky for a 24-wide key grid
+                    const int key = key0 + 4 * h;
+                    const int ky = (int)((unsigned)key / 24u);
+                    v += Tb[oca_base + key + 15 * ky];
+                } else {
+                    const int ky = key0 >> 4, kx = key0 & 15;
+                    v += Tb[sw_base - (ky * 31 + kx)];
+                    v += madd[(ky >> 3) & 1][(kx >> 3) & 1];
+                }
+                s[t][i] = v;
+                mx = fmaxf(mx, v);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(mrun, mx);
+        const float corr = fast_exp2(mrun - mnew);
+        lrun *= corr;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] *= corr;
+        mrun = mnew;
+#pragma unroll
+        for (int t = 0; t < CHT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float e = fast_exp2(s[t][i] - mnew);
+                s[t][i] = e;
+                lrun += e;
+            }
+        // O^T += V^T P^T
+#pragma unroll
+        for (int t = 0; t < CHT; ++t) {
+            const int kt = ch * CHT + t;
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                f32x4 vv = (f32x4){0.f, 0.f, 0.f, 0.f};
+                if (ql < D) vv = *(const f32x4*)(Vt + ql * RSV + kt * 32 + i4 * 8 + h * 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o = mfma32(vv[j], s[t][i4 * 4 + j], o);
+            }
+        }
+    }
+
+    const float ltot = lrun + __shfl_xor(lrun, 32, 64);
+    const float inv = 1.0f / ltot;
+    float* orow = p.out + (size_t)qpix * p.C + head * D;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+        const int d0 = 8 * i4 + 4 * h;
+        if (D % 4 == 0) {
+            if (d0 + 3 < D)
+                *(float4*)(orow + d0) = make_float4(o[i4 * 4] * inv, o[i4 * 4 + 1] * inv,
+                                                    o[i4 * 4 + 2] * inv, o[i4 * 4 + 3] * inv);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (d0 + j < D) orow[d0 + j] = o[i4 * 4 + j] * inv;
+        }
+    }
+}
+
+#define ATTN_INST(NAME, D, OCA)                                                              \
+    extern "C" __global__ __launch_bounds__(512) void NAME(AttnArgs p) { attn_body<D, OCA>(p); }
+
+ATTN_INST(hat_attn_sw_d24, 24, false)
+ATTN_INST(hat_attn_sw_d30, 30, false)
+ATTN_INST(hat_attn_oca_d24, 24, true)
+ATTN_INST(hat_attn_oca_d30, 30, true)

@@ -1,0 +1,212 @@
+// 3x3 convolution (stride 1, zero padding 1) as an implicit GEMM on FP32 MFMA,
+// NHWC in and out.
+//
+// Replaces lg_conv3x3_winograd (src/cuda.rs:88-106) at every call site of the
+// reference graph (CAB convs gpu.rs:426,429; RHAG conv :605; conv_first :722;
+// conv_after_body :742; head :636,643,650), and folds into the epilogue what
+// the reference runs as separate passes: GELU / LeakyReLU, the residual add,
+// the PixelShuffle (lg_pixel_shuffle, cuda.rs:516-522), the per-channel sums
+// of the channel-attention pool (lg_channel_mean, cuda.rs:259-272) and the
+// final crop + denormalisation (backend.rs:94-109).
+//
+// Tiling: 256 threads = 4 waves; a block owns an 8x16 pixel tile and 16*NT
+// output channels. Wave w owns pixel rows 2w and 2w+1 of the tile, one 16-pixel
+// MFMA tile each, so lane l%16 is the pixel's x. Input channels are walked in
+// chunks of 16: the (8+2)x(16+2) halo patch and the 9-tap weight slice of the
+// chunk are staged in LDS and every tap reads the same patch at an offset.
+// MFMA operands: weights (A, rows = output channels) and patch pixels (B,
+// columns = pixels); lane group g (= lane/16) reduces channels 4g..4g+3 of the
+// chunk, one float4 read each.
+#include "common.h"
+
+using namespace hatk;
+
+#define CV_TY 8
+#define CV_TX 16
+#define CV_PY (CV_TY + 2)
+#define CV_PX (CV_TX + 2)
+#define CV_CS 20  // 16 channels + 4 pad
+
+template <int NT, int EPI>
+__device__ __forceinline__ void conv_body(const ConvArgs& p)
+{
+    constexpr int BN = 16 * NT;
+    __shared__ float Ps[CV_PY * CV_PX * CV_CS];
+    __shared__ float Ws[9 * BN * CV_CS];
+    __shared__ float s_col[EPI == CEPI_COLSUM ? 4 * BN : 1];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int tiles_x = (p.W + CV_TX - 1) / CV_TX;
+    const int ty0 = (blockIdx.x / tiles_x) * CV_TY;
+    const int tx0 = (blockIdx.x % tiles_x) * CV_TX;
+    const int co0 = blockIdx.y * BN;
+    const int H = p.H, W = p.W;
+
+    f32x4 acc[2][NT];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    const int nchunks = p.CIp / 16;
+    for (int cc = 0; cc < nchunks; ++cc) {
+        const int ci0 = cc * 16;
+        __syncthreads();
+        // Halo patch: 180 pixels x 4 float4.
+        for (int idx = tid; idx < CV_PY * CV_PX * 4; idx += 256) {
+            const int pix = idx >> 2, c4 = (idx & 3) * 4;
+            const int py = pix / CV_PX, px = pix - py * CV_PX;
+            const int y = ty0 + py - 1, x = tx0 + px - 1;
+            const int ci = ci0 + c4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (y >= 0 && y < H && x >= 0 && x < W && ci < p.CI) {
+                const float* src = p.in + ((size_t)y * W + x) * p.cin_stride + ci;
+                if (ci + 3 < p.CI) {
+                    v = *(const float4*)src;
+                } else {
+                    // channels past CI are padding and read as zero
+                    v.x = src[0];
+                    if (ci + 1 < p.CI) v.y = src[1];
+                    if (ci + 2 < p.CI) v.z = src[2];
+                }
+            }
+            *(float4*)(Ps + pix * CV_CS + c4) = v;
+        }
+        // Weights: packed [chunk][tap][COp][16].
+        const float* wc = p.w + (size_t)cc * 9 * p.COp * 16;
+        for (int idx = tid; idx < 9 * BN * 4; idx += 256) {
+            const int row = idx >> 2, c4 = (idx & 3) * 4;
+            const int tap = row / BN, co = row - tap * BN;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (co0 + co < p.COp) v = *(const float4*)(wc + ((size_t)tap * p.COp + co0 + co) * 16 + c4);
+            *(float4*)(Ws + row * CV_CS + c4) = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const int dy = tap / 3, dx = tap - dy * 3;
+            f32x4 xv[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+                xv[mt] = *(const f32x4*)(Ps + ((wave * 2 + mt + dy) * CV_PX + lr + dx) * CV_CS + lg * 4);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const f32x4 wv = *(const f32x4*)(Ws + (tap * BN + nt * 16 + lr) * CV_CS + lg * 4);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16(wv[s], xv[mt][s], acc[mt][nt]);
+            }
+        }
+    }
+
+    // Epilogue: lane holds output channels co .. co+3 of pixel (y, x).
+    float colsum[NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) colsum[nt][j] = 0.0f;
+
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int y = ty0 + wave * 2 + mt;
+        const int x = tx0 + lr;
+        const bool live = y < H && x < W;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int co = co0 + nt * 16 + lg * 4;
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[j] = acc[mt][nt][j] + (co + j < p.COp ? p.bias[co + j] : 0.0f);
+                if (p.act == 1) v[j] = gelu(v[j]);
+                else if (p.act == 2) v[j] = v[j] < 0.0f ? v[j] * 0.01f : v[j];
+            }
+            if (!live || co >= p.CO) continue;
+            if (EPI == CEPI_STORE || EPI == CEPI_RESID || EPI == CEPI_COLSUM) {
+                float* o = p.out + ((size_t)y * W + x) * p.co_stride + co;
+                if (EPI == CEPI_RESID) {
+                    const float* r = p.res + ((size_t)y * W + x) * p.co_stride + co;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (co + j < p.CO) v[j] = v[j] + r[j];
+                }
+                if (EPI == CEPI_COLSUM) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (co + j < p.CO) colsum[nt][j] += v[j];
+                }
+                if (co + 3 < p.CO && (p.co_stride & 3) == 0) {
+                    *(float4*)o = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (co + j < p.CO) o[j] = v[j];
+                }
+            } else if (EPI == CEPI_SHUFFLE) {
+                // Channels were permuted at upload to o' = (i*r + j)*Cf + c.
+                const int r = p.r, Cf = p.CO / (r * r);
+                const int sub = co / Cf, c = co - sub * Cf;
+                const int i = sub / r, jj = sub - i * r;
+                float* o = p.out + ((size_t)(y * r + i) * (W * r) + x * r + jj) * p.co_stride + c;
+                *(float4*)o = make_float4(v[0], v[1], v[2], v[3]);
+            } else if (EPI == CEPI_FINAL) {
+                if (y < p.crop_h && x < p.crop_w) {
+                    const float mean[3] = {p.mean0, p.mean1, p.mean2};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int ch = co + j;
+                        if (ch < 3)
+                            p.out[((size_t)ch * p.crop_h + y) * p.crop_w + x] = v[j] / p.img_range + mean[ch];
+                    }
+                }
+            }
+        }
+    }
+
+    if (EPI == CEPI_COLSUM) {
+        // Reduce over the 16 pixels of each row tile (lanes with equal lg), then
+        // over the 4 waves through LDS; one partial row per block.
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float s = colsum[nt][j];
+                s += __shfl_xor(s, 1, 64);
+                s += __shfl_xor(s, 2, 64);
+                s += __shfl_xor(s, 4, 64);
+                s += __shfl_xor(s, 8, 64);
+                colsum[nt][j] = s;
+            }
+        if (lr == 0) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s_col[wave * BN + nt * 16 + lg * 4 + j] = colsum[nt][j];
+        }
+        __syncthreads();
+        const int blk = blockIdx.x;
+        for (int c = tid; c < BN; c += 256) {
+            const int co = co0 + c;
+            if (co < p.CO) {
+                float s = s_col[c] + s_col[BN + c] + s_col[2 * BN + c] + s_col[3 * BN + c];
+                p.partial[(size_t)blk * p.co_stride + co] = s;
+            }
+        }
+    }
+}
+
+#define CONV_INST(NAME, NT, EPI)                                                             \
+    extern "C" __global__ __launch_bounds__(256) void NAME(ConvArgs p) { conv_body<NT, EPI>(p); }
+
+CONV_INST(hat_conv_n1_store, 1, CEPI_STORE)
+CONV_INST(hat_conv_n3_store, 3, CEPI_STORE)
+CONV_INST(hat_conv_n4_store, 4, CEPI_STORE)
+CONV_INST(hat_conv_n3_resid, 3, CEPI_RESID)
+CONV_INST(hat_conv_n3_colsum, 3, CEPI_COLSUM)
+CONV_INST(hat_conv_n4_shuffle, 4, CEPI_SHUFFLE)
+CONV_INST(hat_conv_n1_final, 1, CEPI_FINAL)

@@ -1,0 +1,7 @@
+// The single gfx950 code object of the library: every kernel the runtime
+// launches, built with
+//   hipcc --offload-arch=gfx950 --offload-device-only --no-gpu-bundle-output
+#include "attn.hip"
+#include "conv.hip"
+#include "gemm.hip"
+#include "misc.hip"

@@ -1,0 +1,81 @@
+// Bandwidth kernels: LayerNorm, input preparation, squeeze-excite gate.
+#include "common.h"
+
+using namespace hatk;
+
+// LayerNorm over the channel axis of token-major rows (the reference's
+// layer_norm, cpu.rs:563-581, and lg_channel_layer_norm, cuda.rs:185-191):
+// two-pass mean then biased variance, y = (x - mean) * rstd * w + b.
+// One wave per row; y may alias x.
+extern "C" __global__ __launch_bounds__(256) void hat_layernorm(LnArgs p)
+{
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= p.rows) return;
+    const float* x = p.x + (size_t)row * p.C;
+    float* y = p.y + (size_t)row * p.C;
+    float v[8];
+    int n = 0;
+    float s = 0.0f;
+    for (int k = lane; k < p.C; k += 64) {
+        v[n] = x[k];
+        s += v[n];
+        ++n;
+    }
+    const float mean = wave_sum(s) / (float)p.C;
+    float q = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        const float d = v[i] - mean;
+        q += d * d;
+    }
+    const float var = wave_sum(q) / (float)p.C;
+    const float rstd = 1.0f / sqrtf(var + p.eps);
+    n = 0;
+    for (int k = lane; k < p.C; k += 64, ++n) y[k] = (v[n] - mean) * rstd * p.w[k] + p.b[k];
+}
+
+// Pre::adjust (backend.rs:71-89): edge-replicated padding to the window grid and
+// (x - mean) * img_range, written NHWC with a padded channel stride.
+extern "C" __global__ __launch_bounds__(256) void hat_pre(PreArgs p)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= p.hp * p.wp) return;
+    const int y = i / p.wp, x = i - (i / p.wp) * p.wp;
+    const int sy = y < p.h - 1 ? y : p.h - 1;
+    const int sx = x < p.w - 1 ? x : p.w - 1;
+    const size_t hw = (size_t)p.h * p.w;
+    const size_t src = (size_t)sy * p.w + sx;
+    float* o = p.out + (size_t)i * p.cstride;
+    o[0] = (p.in[src] - p.m0) * p.range;
+    o[1] = (p.in[hw + src] - p.m1) * p.range;
+    o[2] = (p.in[2 * hw + src] - p.m2) * p.range;
+    for (int c = 3; c < p.cstride; ++c) o[c] = 0.0f;
+}
+
+// The channel attention's gate (CAB, hat_arch.py:40-55; cpu.rs:940-955):
+// mean over the plane from the per-block column sums of the second CAB conv,
+// 1x1 squeeze + ReLU, 1x1 excite + sigmoid. One block; partial sums are added
+// in block order.
+extern "C" __global__ __launch_bounds__(256) void hat_se_gate(SeArgs p)
+{
+    __shared__ float s_mean[512];
+    __shared__ float s_sq[64];
+    const int tid = threadIdx.x;
+    for (int c = tid; c < p.C; c += 256) {
+        float acc = 0.0f;
+        for (int b = 0; b < p.nblk; ++b) acc += p.partial[(size_t)b * p.co_stride + c];
+        s_mean[c] = acc / p.count;
+    }
+    __syncthreads();
+    for (int j = tid; j < p.sq; j += 256) {
+        float acc = p.b1[j];
+        for (int c = 0; c < p.C; ++c) acc += s_mean[c] * p.w1[(size_t)j * p.C + c];
+        s_sq[j] = acc < 0.0f ? 0.0f : acc;
+    }
+    __syncthreads();
+    for (int c = tid; c < p.C; c += 256) {
+        float acc = p.b2[c];
+        for (int j = 0; j < p.sq; ++j) acc += s_sq[j] * p.w2[(size_t)c * p.sq + j];
+        p.gate[c] = 1.0f / (1.0f + __expf(-acc));
+    }
+}

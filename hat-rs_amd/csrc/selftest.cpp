@@ -1,0 +1,479 @@
+// The kernel selftest: every gfx950 kernel against a host twin on seeded
+// inputs, the contract of the reference's `--cuda-selftest` (src/selftest.rs:
+// 437-523). Movement and integer work is compared exactly; floating-point
+// kernels against a double-precision twin within a stated tolerance. The twins
+// use the reference's own geometry formulas (plan.rs: window_index with the
+// roll, unfold_index, the calculate_mask bands, rpi_sa, rpi_oca) rather than
+// the kernels' folded forms, so an addressing shortcut that is wrong fails here.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "gpu.h"
+#include "kargs.h"
+
+namespace hat {
+
+using namespace hatk;
+
+namespace {
+
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed * 0x9E3779B97F4A7C15ull + 1) {}
+    float uni()  // [-1, 1)
+    {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        return (float)((s >> 40) * (1.0 / 16777216.0)) * 2.0f - 1.0f;
+    }
+    std::vector<float> vec(size_t n, float scale)
+    {
+        std::vector<float> v(n);
+        for (auto& x : v) x = uni() * scale;
+        return v;
+    }
+};
+
+struct Dev {
+    float* p = nullptr;
+    size_t n = 0;
+    explicit Dev(size_t n_) : n(n_) { p = (float*)Runtime::get().alloc(n * sizeof(float)); }
+    Dev(const std::vector<float>& v) : Dev(v.size()) { Runtime::get().h2d(p, v.data(), n * sizeof(float)); }
+    ~Dev() { Runtime::get().free(p); }
+    std::vector<float> get() const
+    {
+        std::vector<float> v(n);
+        Runtime::get().sync();
+        Runtime::get().d2h(v.data(), p, n * sizeof(float));
+        return v;
+    }
+    Dev(const Dev&) = delete;
+};
+
+void check_close(const std::string& name, const std::vector<float>& got, const std::vector<double>& want,
+                 double tol)
+{
+    if (got.size() != want.size()) throw Error(name + ": size mismatch");
+    double worst = 0;
+    size_t at = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        double d = std::fabs((double)got[i] - want[i]);
+        if (!std::isfinite((double)got[i])) throw Error(name + ": non-finite value at " + std::to_string(i));
+        if (d > worst) {
+            worst = d;
+            at = i;
+        }
+    }
+    if (worst > tol) {
+        char b[256];
+        snprintf(b, sizeof b, "%s: worst |diff| %.3e at %zu (got %.9e, want %.9e), tolerance %.0e",
+                 name.c_str(), worst, at, got[at], want[at], tol);
+        throw Error(b);
+    }
+}
+
+// mask_label (plan.rs:300-334): region of pixel (y, x) from the three bands.
+int band(int v, int len, int win, int shift)
+{
+    const int a = len - win > 0 ? len - win : 0, b = len - shift > 0 ? len - shift : 0;
+    return v < a ? 0 : (v < b ? 1 : 2);
+}
+
+// Host twin of the fused attention, in double.
+std::vector<double> attn_twin(const std::vector<float>& qkv, const std::vector<float>& table,
+                              int hp, int wp, int heads, int D, bool oca, int shift)
+{
+    const int C = heads * D, T = hp * wp, nx = wp / 16, ny = hp / 16;
+    const int nk = oca ? 576 : 256;
+    std::vector<double> out((size_t)T * C, 0.0);
+    const double scale = 1.0 / std::sqrt((double)D);
+    auto Q = [&](int which, int hd, int pix, int d) { return (double)qkv[(((size_t)which * heads + hd) * T + pix) * D + d]; };
+    for (int wy = 0; wy < ny; ++wy)
+        for (int wx = 0; wx < nx; ++wx)
+            for (int hd = 0; hd < heads; ++hd)
+                for (int q = 0; q < 256; ++q) {
+                    const int qy = q / 16, qx = q % 16;
+                    const int qpy = (wy * 16 + qy + shift) % hp, qpx = (wx * 16 + qx + shift) % wp;
+                    const int qpix = qpy * wp + qpx;
+                    std::vector<double> s(nk);
+                    double mx = -1e300;
+                    for (int k = 0; k < nk; ++k) {
+                        int kpix = -1, bidx;
+                        if (oca) {
+                            const int ky = k / 24, kx = k % 24;
+                            const int y = wy * 16 - 4 + ky, x = wx * 16 - 4 + kx;
+                            if (y >= 0 && y < hp && x >= 0 && x < wp) kpix = y * wp + x;
+                            int raw = (ky - qy - 7) * 39 + (kx - qx - 7);
+                            bidx = ((raw % 1521) + 1521) % 1521;
+                        } else {
+                            const int ky = k / 16, kx = k % 16;
+                            kpix = ((wy * 16 + ky + shift) % hp) * wp + (wx * 16 + kx + shift) % wp;
+                            bidx = (qy - ky + 15) * 31 + (qx - kx + 15);
+                        }
+                        double dot = 0;
+                        if (kpix >= 0)
+                            for (int d = 0; d < D; ++d) dot += Q(0, hd, qpix, d) * Q(1, hd, kpix, d);
+                        double v = dot * scale + table[(size_t)bidx * heads + hd];
+                        if (!oca && shift > 0) {
+                            const int ky = k / 16, kx = k % 16;
+                            const int lq = band(wy * 16 + qy, hp, 16, shift) * 3 + band(wx * 16 + qx, wp, 16, shift);
+                            const int lk = band(wy * 16 + ky, hp, 16, shift) * 3 + band(wx * 16 + kx, wp, 16, shift);
+                            if (lq != lk) v -= 100.0;
+                        }
+                        s[k] = v;
+                        if (v > mx) mx = v;
+                    }
+                    double sum = 0;
+                    for (int k = 0; k < nk; ++k) sum += (s[k] = std::exp(s[k] - mx));
+                    for (int d = 0; d < D; ++d) {
+                        double acc = 0;
+                        for (int k = 0; k < nk; ++k) {
+                            int kpix = -1;
+                            if (oca) {
+                                const int y = wy * 16 - 4 + k / 24, x = wx * 16 - 4 + k % 24;
+                                if (y >= 0 && y < hp && x >= 0 && x < wp) kpix = y * wp + x;
+                            } else {
+                                kpix = ((wy * 16 + k / 16 + shift) % hp) * wp + (wx * 16 + k % 16 + shift) % wp;
+                            }
+                            if (kpix >= 0) acc += s[k] * Q(2, hd, kpix, d);
+                        }
+                        out[(size_t)qpix * C + hd * D + d] = acc / sum;
+                    }
+                }
+    return out;
+}
+
+double gelu_d(double v) { return 0.5 * v * (1.0 + std::erf(v / std::sqrt(2.0))); }
+
+}  // namespace
+
+int gpu_selftest(std::string* err)
+{
+    int passed = 0;
+    auto note = [&](const std::string& n) {
+        printf("  ok  %s\n", n.c_str());
+        fflush(stdout);
+        ++passed;
+    };
+    try {
+        Runtime& rt = Runtime::get();
+        hipStream_t s = nullptr;
+        printf("gpu selftest - every kernel against a host twin (%s, %d CUs, %zu kernels)\n",
+               rt.device_name().c_str(), rt.cu_count(), rt.kernel_names().size());
+        Rng rng(7);
+
+        // ---- attention: both head dims, SW plain / shifted (masked) and OCA,
+        // on a non-square 2 x 3 window grid and a single-window plane.
+        for (int D : {24, 30})
+            for (auto geo : {std::pair<int, int>{32, 48}, std::pair<int, int>{16, 16}})
+                for (int mode = 0; mode < 3; ++mode) {
+                    const int hp = geo.first, wp = geo.second, heads = 2, T = hp * wp;
+                    const bool oca = mode == 2;
+                    const int shift = mode == 1 ? 8 : 0;
+                    std::vector<float> qkv = rng.vec((size_t)3 * T * heads * D, 1.0f);
+                    std::vector<float> tab = rng.vec((size_t)(oca ? 1521 : 961) * heads, 0.5f);
+                    Dev dq(qkv), dt(tab), dout((size_t)T * heads * D);
+                    Plan pl = Plan::make(hp, wp, 16, heads * D);
+                    AttnArgs p{};
+                    p.qkv = dq.p;
+                    p.table = dt.p;
+                    p.out = dout.p;
+                    p.hp = hp;
+                    p.wp = wp;
+                    p.nx = pl.nx();
+                    p.ny = pl.ny();
+                    p.heads = heads;
+                    p.D = D;
+                    p.C = heads * D;
+                    p.shift = shift;
+                    p.owin = 24;
+                    p.opad = 4;
+                    p.T = T;
+                    p.qscale = (float)(1.0 / std::sqrt((double)D) * 1.4426950408889634);
+                    std::string k = std::string(oca ? "hat_attn_oca_d" : "hat_attn_sw_d") + std::to_string(D);
+                    launch(s, k.c_str(), pl.nw(), heads, 1, 512, p);
+                    std::vector<double> want = attn_twin(qkv, tab, hp, wp, heads, D, oca, shift);
+                    char nm[128];
+                    snprintf(nm, sizeof nm, "%s %dx%d shift %d", k.c_str(), hp, wp, shift);
+                    check_close(nm, dout.get(), want, 2e-5);
+                    note(nm);
+                }
+
+        // ---- GEMM epilogues (n9: N multiple of 144; n6: C = 180 family).
+        for (int C : {144, 180})
+            for (int epi = 0; epi < 5; ++epi)
+                for (int ln = 0; ln < 2; ++ln) {
+                    if (ln && !(epi == EPI_GELU || epi == EPI_QKV)) continue;
+                    if (!ln && epi == EPI_GELU) continue;
+                    const int heads = 6, hd = C / heads;
+                    const int M = 200;  // not a multiple of the 128-row tile
+                    int N = epi == EPI_QKV ? 3 * C : (epi == EPI_GELU ? 2 * C : C);
+                    int K = C;
+                    if (epi == EPI_RESID && !ln) K = 2 * C;  // the fc2 shape
+                    std::vector<float> a = rng.vec((size_t)M * K, 1.0f), w = rng.vec((size_t)N * K, 0.05f),
+                                       b = rng.vec(N, 0.1f), res = rng.vec((size_t)M * N, 1.0f),
+                                       aux = rng.vec((size_t)M * N, 1.0f), gate = rng.vec(N, 1.0f),
+                                       lnw = rng.vec(K, 1.0f), lnb = rng.vec(K, 0.1f);
+                    int Kp = 0;
+                    std::vector<float> pk = pack_linear(w.data(), N, K, &Kp);
+                    Dev da(a), dw(pk), db(b), dres(res), daux(aux), dg(gate), dlw(lnw), dlb(lnb),
+                        dout(epi == EPI_QKV ? (size_t)M * N : (size_t)M * N);
+                    GemmArgs p{};
+                    p.a = da.p;
+                    p.w = dw.p;
+                    p.bias = db.p;
+                    p.out = dout.p;
+                    p.res = dres.p;
+                    p.aux = daux.p;
+                    p.gate = dg.p;
+                    p.lnw = ln ? dlw.p : nullptr;
+                    p.lnb = ln ? dlb.p : nullptr;
+                    p.M = M;
+                    p.N = N;
+                    p.K = K;
+                    p.Kp = Kp;
+                    p.lda = K;
+                    p.ldo = N;
+                    p.heads = heads;
+                    p.hdim = hd;
+                    p.cscale = 0.01f;
+                    p.eps = 1e-5f;
+                    const bool n9 = N % 144 == 0;
+                    const char* names[5][2] = {{"store", "store"}, {"gelu_ln", "gelu_ln"}, {"qkv", "qkv_ln"},
+                                               {"resid", "resid"}, {"hab", "hab"}};
+                    std::string k = std::string(n9 ? "hat_gemm_n9_" : "hat_gemm_n6_") + names[epi][ln];
+                    launch(s, k.c_str(), (M + 127) / 128, (N + (n9 ? 143 : 95)) / (n9 ? 144 : 96), 1, 256, p);
+                    std::vector<double> want((size_t)M * N);
+                    for (int m = 0; m < M; ++m) {
+                        std::vector<double> row(K);
+                        double mean = 0, var = 0;
+                        for (int kk = 0; kk < K; ++kk) mean += a[(size_t)m * K + kk];
+                        mean /= K;
+                        for (int kk = 0; kk < K; ++kk) var += (a[(size_t)m * K + kk] - mean) * (a[(size_t)m * K + kk] - mean);
+                        var /= K;
+                        for (int kk = 0; kk < K; ++kk)
+                            row[kk] = ln ? (a[(size_t)m * K + kk] - mean) / std::sqrt(var + 1e-5) * lnw[kk] + lnb[kk]
+                                         : a[(size_t)m * K + kk];
+                        for (int n = 0; n < N; ++n) {
+                            double v = b[n];
+                            for (int kk = 0; kk < K; ++kk) v += row[kk] * w[(size_t)n * K + kk];
+                            const size_t o = (size_t)m * N + n;
+                            if (epi == EPI_GELU) v = gelu_d(v);
+                            if (epi == EPI_RESID) v = res[o] + v;
+                            if (epi == EPI_HAB) v = (res[o] + v) + aux[o] * gate[n] * 0.01;
+                            if (epi == EPI_QKV) {
+                                const int which = n / C, rem = n % C, h = rem / hd, d = rem % hd;
+                                want[(((size_t)which * heads + h) * M + m) * hd + d] = v;
+                            } else {
+                                want[o] = v;
+                            }
+                        }
+                    }
+                    check_close(k + " C " + std::to_string(C), dout.get(), want, 3e-5);
+                    note(k + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
+                }
+
+        // ---- convolutions (all epilogues) on a non-square plane.
+        struct CCase { int CI, CO, epi, act, r; const char* what; };
+        const CCase cases[] = {
+            {144, 6, CEPI_STORE, 1, 0, "cab conv1 144->6 + gelu"},
+            {180, 60, CEPI_STORE, 1, 0, "cab conv1 180->60 + gelu"},
+            {6, 144, CEPI_COLSUM, 0, 0, "cab conv2 6->144 + column sums"},
+            {144, 144, CEPI_RESID, 0, 0, "rhag conv 144->144 + residual"},
+            {3, 144, CEPI_STORE, 0, 0, "conv_first 3->144"},
+            {144, 64, CEPI_STORE, 2, 0, "conv_before_upsample 144->64 + leaky"},
+            {64, 256, CEPI_SHUFFLE, 0, 2, "upsample 64->256 + shuffle 2"},
+            {64, 576, CEPI_SHUFFLE, 0, 3, "upsample 64->576 + shuffle 3"},
+            {64, 3, CEPI_FINAL, 0, 0, "conv_last 64->3 + crop/denorm"},
+        };
+        for (const CCase& cc : cases) {
+            const int H = 32, W = 48, HW = H * W;
+            const int cin_stride = (cc.CI + 3) / 4 * 4;
+            std::vector<float> in((size_t)HW * cin_stride, 0.0f);
+            for (int p = 0; p < HW; ++p)
+                for (int c = 0; c < cc.CI; ++c) in[(size_t)p * cin_stride + c] = rng.uni();
+            std::vector<float> w = rng.vec((size_t)cc.CO * cc.CI * 9, 0.05f), b = rng.vec(cc.CO, 0.1f);
+            std::vector<float> res = rng.vec((size_t)HW * cc.CO, 1.0f);
+            std::vector<float> bias;
+            int CIp = 0, COp = 0;
+            std::vector<float> pk = pack_conv(w.data(), b.data(), cc.CO, cc.CI, cc.r, &bias, &CIp, &COp);
+            const int nblk = (W / 16) * (H / 8);
+            const int crop_h = 30, crop_w = 41;
+            size_t out_n = cc.epi == CEPI_FINAL ? (size_t)3 * crop_h * crop_w : (size_t)HW * cc.CO;
+            Dev din(in), dw(pk), db(bias), dres(res), dout(out_n), dpart((size_t)nblk * cc.CO);
+            DevConv C;
+            C.w = dw.p;
+            C.b = db.p;
+            C.CI = cc.CI;
+            C.CIp = CIp;
+            C.CO = cc.CO;
+            C.COp = COp;
+            C.r = cc.r;
+            const float mean[3] = {0.4488f, 0.4371f, 0.4040f};
+            ConvArgs p{};
+            p.in = din.p;
+            p.w = dw.p;
+            p.bias = db.p;
+            p.out = dout.p;
+            p.res = dres.p;
+            p.partial = dpart.p;
+            p.H = H;
+            p.W = W;
+            p.CI = cc.CI;
+            p.CIp = CIp;
+            p.cin_stride = cin_stride;
+            p.CO = cc.CO;
+            p.COp = COp;
+            p.co_stride = cc.epi == CEPI_SHUFFLE ? cc.CO / (cc.r * cc.r) : cc.CO;
+            p.act = cc.act;
+            p.r = cc.r;
+            p.crop_h = crop_h;
+            p.crop_w = crop_w;
+            p.img_range = 1.0f;
+            p.mean0 = mean[0];
+            p.mean1 = mean[1];
+            p.mean2 = mean[2];
+            const char* name = nullptr;
+            int BN = 16;
+            switch (cc.epi) {
+            case CEPI_STORE:
+                name = cc.CO <= 16 ? "hat_conv_n1_store" : cc.CO <= 64 ? "hat_conv_n4_store" : "hat_conv_n3_store";
+                BN = cc.CO <= 16 ? 16 : cc.CO <= 64 ? 64 : 48;
+                break;
+            case CEPI_RESID: name = "hat_conv_n3_resid"; BN = 48; break;
+            case CEPI_COLSUM: name = "hat_conv_n3_colsum"; BN = 48; break;
+            case CEPI_SHUFFLE: name = "hat_conv_n4_shuffle"; BN = 64; break;
+            case CEPI_FINAL: name = "hat_conv_n1_final"; BN = 16; break;
+            }
+            launch(s, name, nblk, (cc.CO + BN - 1) / BN, 1, 256, p);
+            std::vector<double> full((size_t)HW * cc.CO);
+            for (int y = 0; y < H; ++y)
+                for (int x = 0; x < W; ++x)
+                    for (int o = 0; o < cc.CO; ++o) {
+                        double v = b[o];
+                        for (int ci = 0; ci < cc.CI; ++ci)
+                            for (int dy = 0; dy < 3; ++dy)
+                                for (int dx = 0; dx < 3; ++dx) {
+                                    const int yy = y + dy - 1, xx = x + dx - 1;
+                                    if (yy < 0 || yy >= H || xx < 0 || xx >= W) continue;
+                                    v += (double)in[((size_t)yy * W + xx) * cin_stride + ci] *
+                                         w[((size_t)o * cc.CI + ci) * 9 + dy * 3 + dx];
+                                }
+                        if (cc.act == 1) v = gelu_d(v);
+                        if (cc.act == 2 && v < 0) v *= 0.01;
+                        full[((size_t)y * W + x) * cc.CO + o] = v;
+                    }
+            std::vector<double> want(out_n);
+            if (cc.epi == CEPI_STORE || cc.epi == CEPI_COLSUM) want = full;
+            else if (cc.epi == CEPI_RESID)
+                for (size_t i = 0; i < want.size(); ++i) want[i] = full[i] + res[i];
+            else if (cc.epi == CEPI_SHUFFLE) {
+                // PixelShuffle (cpu.rs:1285-1301): channel c*r*r + i*r + j -> (r*y+i, r*x+j).
+                const int r = cc.r, Cf = cc.CO / (r * r);
+                for (int y = 0; y < H; ++y)
+                    for (int x = 0; x < W; ++x)
+                        for (int c = 0; c < Cf; ++c)
+                            for (int i = 0; i < r; ++i)
+                                for (int j = 0; j < r; ++j)
+                                    want[((size_t)(r * y + i) * (W * r) + r * x + j) * Cf + c] =
+                                        full[((size_t)y * W + x) * cc.CO + c * r * r + i * r + j];
+            } else if (cc.epi == CEPI_FINAL) {
+                for (int c = 0; c < 3; ++c)
+                    for (int y = 0; y < crop_h; ++y)
+                        for (int x = 0; x < crop_w; ++x)
+                            want[((size_t)c * crop_h + y) * crop_w + x] = full[((size_t)y * W + x) * 3 + c] + mean[c];
+            }
+            check_close(name + std::string(" ") + cc.what, dout.get(), want, 5e-5);
+            if (cc.epi == CEPI_COLSUM) {
+                std::vector<double> ps((size_t)nblk * cc.CO, 0.0);
+                const int tiles_x = W / 16;
+                for (int y = 0; y < H; ++y)
+                    for (int x = 0; x < W; ++x) {
+                        const int blk = (y / 8) * tiles_x + x / 16;
+                        for (int o = 0; o < cc.CO; ++o) ps[(size_t)blk * cc.CO + o] += full[((size_t)y * W + x) * cc.CO + o];
+                    }
+                check_close(std::string(name) + " partial sums", dpart.get(), ps, 5e-4);
+            }
+            note(std::string(name) + "  " + cc.what + "  32x48");
+        }
+
+        // ---- LayerNorm, input preparation, squeeze-excite.
+        {
+            const int rows = 300, C = 180;
+            std::vector<float> x = rng.vec((size_t)rows * C, 2.0f), w = rng.vec(C, 1.0f), b = rng.vec(C, 0.5f);
+            Dev dx(x), dw(w), db(b), dy((size_t)rows * C);
+            LnArgs p{dx.p, dy.p, dw.p, db.p, rows, C, 1e-5f};
+            launch(s, "hat_layernorm", (rows + 3) / 4, 1, 1, 256, p);
+            std::vector<double> want((size_t)rows * C);
+            for (int r = 0; r < rows; ++r) {
+                double mean = 0, var = 0;
+                for (int c = 0; c < C; ++c) mean += x[(size_t)r * C + c];
+                mean /= C;
+                for (int c = 0; c < C; ++c) var += (x[(size_t)r * C + c] - mean) * (x[(size_t)r * C + c] - mean);
+                var /= C;
+                for (int c = 0; c < C; ++c)
+                    want[(size_t)r * C + c] = (x[(size_t)r * C + c] - mean) / std::sqrt(var + 1e-5) * w[c] + b[c];
+            }
+            check_close("hat_layernorm", dy.get(), want, 1e-5);
+            note("hat_layernorm 300x180");
+        }
+        {
+            const int h = 21, w = 35, hp = 32, wp = 48;
+            std::vector<float> in = rng.vec((size_t)3 * h * w, 1.0f);
+            Dev din(in), dout((size_t)hp * wp * 4);
+            PreArgs p{din.p, dout.p, h, w, hp, wp, 4, 0.4488f, 0.4371f, 0.4040f, 1.0f};
+            launch(s, "hat_pre", (hp * wp + 255) / 256, 1, 1, 256, p);
+            std::vector<float> got = dout.get();
+            const float m[3] = {0.4488f, 0.4371f, 0.4040f};
+            for (int y = 0; y < hp; ++y)
+                for (int x = 0; x < wp; ++x)
+                    for (int c = 0; c < 4; ++c) {
+                        const int sy = y < h - 1 ? y : h - 1, sx = x < w - 1 ? x : w - 1;
+                        const float want = c < 3 ? (in[(size_t)c * h * w + sy * w + sx] - m[c]) * 1.0f : 0.0f;
+                        if (got[((size_t)y * wp + x) * 4 + c] != want)
+                            throw Error("hat_pre: mismatch at (" + std::to_string(y) + ", " + std::to_string(x) + ")");
+                    }
+            note("hat_pre 21x35 -> 32x48 (exact)");
+        }
+        {
+            const int C = 144, sq = 6, nblk = 37;
+            std::vector<float> part = rng.vec((size_t)nblk * C, 10.0f), w1 = rng.vec((size_t)sq * C, 0.1f),
+                               b1 = rng.vec(sq, 0.1f), w2 = rng.vec((size_t)C * sq, 0.1f), b2 = rng.vec(C, 0.1f);
+            Dev dp(part), d1(w1), db1(b1), d2(w2), db2(b2), dg(C);
+            SeArgs p{dp.p, nblk, C, 4096.0f, d1.p, db1.p, d2.p, db2.p, dg.p, C, sq};
+            launch(s, "hat_se_gate", 1, 1, 1, 256, p);
+            std::vector<double> mean(C), hid(sq), want(C);
+            for (int c = 0; c < C; ++c) {
+                double a = 0;
+                for (int b = 0; b < nblk; ++b) a += part[(size_t)b * C + c];
+                mean[c] = a / 4096.0;
+            }
+            for (int j = 0; j < sq; ++j) {
+                double a = b1[j];
+                for (int c = 0; c < C; ++c) a += mean[c] * w1[(size_t)j * C + c];
+                hid[j] = a < 0 ? 0 : a;
+            }
+            for (int c = 0; c < C; ++c) {
+                double a = b2[c];
+                for (int j = 0; j < sq; ++j) a += hid[j] * w2[(size_t)c * sq + j];
+                want[c] = 1.0 / (1.0 + std::exp(-a));
+            }
+            check_close("hat_se_gate", dg.get(), want, 1e-6);
+            note("hat_se_gate C 144 sq 6");
+        }
+        printf("  gpu selftest: %d checks passed\n", passed);
+        fflush(stdout);
+    } catch (const Error& e) {
+        if (err) *err = e.msg;
+        printf("  FAIL %s\n", e.msg.c_str());
+        fflush(stdout);
+        return -1;
+    }
+    return passed;
+}
+
+}  // namespace hat

@@ -1,0 +1,146 @@
+/*
+ * hat.h - the C ABI of the MI355X HAT backend (libhat.so).
+ *
+ * A drop-in for the reference's GPU backend (jacobsparts/hat-rs). Every entry
+ * point names the reference interface it replaces. Plain pointers and sizes
+ * only; no GPU runtime types cross this boundary. Errors: functions returning
+ * int give 0 on success (or a count, where stated) and a negative value on
+ * failure; functions returning a pointer give NULL on failure. In both cases
+ * hat_last_error() holds the message (thread-local), the counterpart of the
+ * reference's `Result<_, String>` printed as `hat: <msg>` (src/main.rs:189-195).
+ */
+#ifndef HAT_H
+#define HAT_H
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct hat_weights hat_weights;
+typedef struct hat_backend hat_backend;
+
+/* Library version string (the reference's hat::VERSION, src/lib.rs). */
+const char *hat_version(void);
+
+/* The last error message on this thread, or "" (main.rs:189-195). */
+const char *hat_last_error(void);
+
+/* ---- Weights (src/weights.rs) ------------------------------------------ */
+
+/* Weights::load (weights.rs:60-129): mmap a converted .safetensors file, read
+ * the architecture from __metadata__, validate every tensor shape
+ * (weights.rs:133-265). */
+hat_weights *hat_weights_open(const char *path);
+void hat_weights_close(hat_weights *w);
+
+/* The architecture fields of `Weights` (weights.rs:28-57). */
+typedef struct {
+    int scale, window, owin, embed, heads, head_dim, mlp_ratio;
+    int n_stages;
+    int depths[32];
+    int compressed, squeezed, head_feat;
+    float conv_scale, img_range;
+    float mean[3];
+} hat_model_info;
+int hat_weights_info(const hat_weights *w, hat_model_info *out);
+
+/* Tensor listing and access (weights.rs:270-272 `t`, `--list-weights`). */
+int hat_weights_count(const hat_weights *w);
+const char *hat_weights_name(const hat_weights *w, int i);
+/* F32 tensor data (owned by the weights object) and its element count. */
+const float *hat_weights_tensor(const hat_weights *w, const char *name, size_t *numel);
+/* Weights::i64 (weights.rs:331-346): copies up to n int64 values; returns the
+ * element count. */
+long hat_weights_index_i64(const hat_weights *w, const char *name, long long *out, size_t n);
+
+/* A seeded checkpoint in tools/convert.py's format (convert.py:205-250): every
+ * weight, bias and bias table ~ N(0, 0.02), LayerNorm weight 1 / bias 0, the
+ * int64 relative-position index buffers from their closed forms. `variant` is
+ * "hat-s", "hat" or "hat-l"; `depths` (may be NULL) overrides the variant's
+ * per-stage block counts. No reference counterpart: the reference ships
+ * converted checkpoints, and this writes the synthetic ones the benchmarks
+ * and parity tests use. */
+int hat_weights_generate(const char *path, const char *variant, int scale, unsigned long long seed,
+                         const int *depths, int n_depths);
+
+/* ---- Backend (src/backend.rs:29-36, src/gpu.rs:372-803) ------------------ */
+
+/* 1 if the HIP runtime and a device can be brought up, else 0 (the probe
+ * behind main.rs:148-174 `resolve_device`). Never fails. */
+int hat_gpu_available(void);
+
+/* Gpu::new (gpu.rs:372-386): brings up the runtime, checks that every kernel
+ * resolves (cuda.rs:558-563) and uploads every weight. `device` must be "gpu"
+ * (or NULL): this library has no CPU path, and asking for one is an error
+ * rather than a silent fallback. The weights must outlive the backend. */
+hat_backend *hat_backend_new(const hat_weights *w, const char *device);
+/* Backend::name (backend.rs:30). */
+const char *hat_backend_name(const hat_backend *b);
+/* Backend::forward (backend.rs:32-35): in = [3][h][w] in [0,1] host memory;
+ * out = caller-allocated [3][h*scale][w*scale] host memory. Synchronous. */
+int hat_backend_forward(hat_backend *b, size_t h, size_t w, const float *in, float *out);
+/* The same pass on device-resident buffers (from hat_device_alloc);
+ * asynchronous on the backend's stream until hat_backend_synchronize. */
+int hat_backend_forward_device(hat_backend *b, size_t h, size_t w, const float *d_in, float *d_out);
+int hat_backend_synchronize(hat_backend *b);
+/* Device bytes of the per-plan buffers and of the uploaded weights
+ * (Acts/footprint, gpu.rs:78-290). */
+size_t hat_backend_acts_bytes(const hat_backend *b);
+size_t hat_backend_weight_bytes(const hat_backend *b);
+void hat_backend_free(hat_backend *b);
+
+/* ---- Contracts (src/main.rs:312-326, src/selftest.rs:437-523) ----------- */
+
+/* `--verify`: load a HATF v1 fixture (fixture.rs:44-78), run the backend,
+ * print "  verify worst |diff| ... at (y, x, ch), mean |diff| ..." and return
+ * 0 if the worst difference is within 1e-4, 1 if it is not, -1 on error. */
+int hat_verify(const hat_weights *w, const char *device, const char *fixture_path);
+
+/* `--cuda-selftest`: every gfx950 kernel against a host twin; prints
+ * "  ok  <name>" per check and returns the number passed, or -1. */
+int hat_gpu_selftest(void);
+
+/* ---- Isolated ops (benchmark configs 2 and 3; host buffers) -------------- */
+
+/* Shifted-window self-attention, the attention branch of HAB.forward
+ * (hat_arch.py:266-309; cpu.rs:1117-1130): gather with the cyclic shift,
+ * qkv linear, attention with relative-position bias and (shift > 0) the
+ * SW-MSA mask, proj linear, scatter. x/out are token-major [hp*wp][c]; table is
+ * [961][heads]. `iters` > 0 times that many extra runs: *ms = mean device time
+ * of the op, *attn_ms = of its attention kernel alone (either may be NULL). */
+int hat_op_swmsa(const float *x, float *out, int hp, int wp, int c, int heads, int shift,
+                 const float *qkv_w, const float *qkv_b, const float *proj_w, const float *proj_b,
+                 const float *table, int iters, float *ms, float *attn_ms);
+
+/* The OCAB block (hat_arch.py:392-438; cpu.rs:1170-1198): norm1, qkv,
+ * 24x24 unfold (stride 16, pad 4), attention with the [1521][heads] bias on
+ * all 576 keys, proj + shortcut, norm2, GELU MLP + residual. */
+int hat_op_ocab(const float *x, float *out, int hp, int wp, int c, int heads, int mlp_ratio,
+                const float *n1w, const float *n1b, const float *qkv_w, const float *qkv_b,
+                const float *proj_w, const float *proj_b, const float *table, const float *n2w,
+                const float *n2b, const float *fc1_w, const float *fc1_b, const float *fc2_w,
+                const float *fc2_b, int iters, float *ms, float *attn_ms);
+
+/* ---- Device memory and timing (lightgpu::vm DevBuf, src/cuda.rs:528-555) -- */
+void *hat_device_alloc(size_t bytes);
+int hat_device_free(void *p);
+int hat_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int hat_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int hat_device_synchronize(void);
+/* Device name and compute-unit count; "" / 0 when no device. */
+const char *hat_device_name(void);
+int hat_device_cu_count(void);
+
+/* Per-kernel HIP-event timing of every launch between begin and end, on the
+ * stream each kernel is launched on. hat_profile_get returns 0 and fills the
+ * i-th kernel's name, launch count and total milliseconds. */
+int hat_profile_begin(void);
+int hat_profile_end(void);
+int hat_profile_count(void);
+int hat_profile_get(int i, char *name, int cap, long *count, double *total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
