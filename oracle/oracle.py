@@ -222,7 +222,8 @@ class OracleModel:
         with safe_open(str(path), framework="numpy") as f:
             meta = f.metadata()
         tensors = load_file(str(path))
-        self.arrays = {k: f32(v) for k, v in tensors.items() if v.dtype == np.float32}
+        self.arrays = {k: np.array(v, dtype=np.float32, copy=True)
+                       for k, v in tensors.items() if v.dtype == np.float32}
         m = Model()
         self.scale = m.scale = int(meta["scale"])
         m.window = int(meta["window_size"])
