@@ -113,6 +113,28 @@ def main():
                 "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
                 "flop_per_launch": attn_flop, "mean_launch_ms": round(attn_ms, 5), "traffic": None}
 
+    # HBM reference: the library's plain copy kernel over 1 GiB (read + write),
+    # timed with events; rocprof counter runs of this script also see it, which
+    # is what scales their FETCH_SIZE / WRITE_SIZE readings to bytes.
+    nb = 1 << 30
+    c_src = hat_amd.DeviceBuffer(nb)
+    c_dst = hat_amd.DeviceBuffer(nb)
+    hat_amd.device_copy(c_dst, c_src, nb)
+    hat_amd.synchronize()
+    hat_amd.profile_begin()
+    for _ in range(3):
+        hat_amd.device_copy(c_dst, c_src, nb)
+    hat_amd.synchronize()
+    cstat = hat_amd.profile_end()["hat_copy"]
+    copy_gbps = 2 * nb / (cstat[1] / cstat[0] / 1e3) / 1e9
+    c_src.free()
+    c_dst.free()
+
+    traffic_file = os.path.join(REPO, "profiles", "traffic_hat_attn_sw_d24_hats512.json")
+    if os.path.exists(traffic_file) and attn_name == "hat_attn_sw_d24" and h == 512:
+        with open(traffic_file) as f:
+            roofline["traffic"] = json.load(f)["bytes_per_launch"]
+
     # One forward with the PCIe copies, as the reference's Backend::forward does.
     t2 = time.perf_counter()
     be.forward(h, w, img)
@@ -155,6 +177,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "wall_ms_incl_pcie": round(wall_ms, 3),
+        "copy_kernel_gbps": round(copy_gbps, 1),
         "acts_gib": round(be.acts_bytes() / 2**30, 3),
         "weights_mib": round(be.weight_bytes() / 2**20, 2),
         "device": hat_amd.device_name(),

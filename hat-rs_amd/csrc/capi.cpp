@@ -1,7 +1,9 @@
 // The C ABI (include/hat.h): the boundary a Rust (or any FFI) caller binds.
 #include "../../include/hat.h"
 
+#include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -10,6 +12,7 @@
 
 #include "gpu.h"
 #include "hip_rt.h"
+#include "kargs.h"
 #include "weights.h"
 
 struct hat_weights {
@@ -315,6 +318,18 @@ int hat_memcpy_d2h(void* dst, const void* src, size_t bytes)
 {
     return guard([&] {
         hat::Runtime::get().d2h(dst, src, bytes);
+        return 0;
+    });
+}
+
+int hat_device_copy(void* dst, const void* src, size_t bytes)
+{
+    return guard([&] {
+        if (!dst || !src || bytes % 16 != 0 || ((uintptr_t)dst | (uintptr_t)src) % 16 != 0)
+            throw hat::Error("hat_device_copy: 16-byte aligned pointers and a multiple of 16 bytes");
+        hatk::CopyArgs p{(const float*)src, (float*)dst, (long)(bytes / 16)};
+        const long blocks = std::min<long>((p.n4 + 255) / 256, 256L * 64);
+        hat::launch(nullptr, "hat_copy", (unsigned)std::max<long>(blocks, 1), 1, 1, 256, p);
         return 0;
     });
 }

@@ -58,40 +58,55 @@ std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int
 
 namespace {
 
-const char* gemm_kernel(int N, int epi, bool ln)
+// Column-block width of the GEMM for an output width N: 144 for the C = 144
+// family, 192 for C = 180 (N = 180, 360, 540 in 1, 2, 3 blocks).
+int gemm_bn(int N) { return N % 144 == 0 ? 144 : 192; }
+
+const char* gemm_kernel(int N, int epi)
 {
-    const bool n9 = N % 144 == 0;
+    const bool n9 = gemm_bn(N) == 144;
     switch (epi) {
-    case EPI_STORE: return n9 ? "hat_gemm_n9_store" : "hat_gemm_n6_store";
-    case EPI_GELU:
-        if (!ln) throw Error("GELU GEMM is only built with the LayerNorm prologue");
-        return n9 ? "hat_gemm_n9_gelu_ln" : "hat_gemm_n6_gelu_ln";
-    case EPI_QKV:
-        return ln ? (n9 ? "hat_gemm_n9_qkv_ln" : "hat_gemm_n6_qkv_ln")
-                  : (n9 ? "hat_gemm_n9_qkv" : "hat_gemm_n6_qkv");
-    case EPI_RESID: return n9 ? "hat_gemm_n9_resid" : "hat_gemm_n6_resid";
-    case EPI_HAB: return n9 ? "hat_gemm_n9_hab" : "hat_gemm_n6_hab";
+    case EPI_STORE: return n9 ? "hat_gemm_n9_store" : "hat_gemm_n12_store";
+    case EPI_GELU: return n9 ? "hat_gemm_n9_gelu" : "hat_gemm_n12_gelu";
+    case EPI_QKV: return n9 ? "hat_gemm_n9_qkv" : "hat_gemm_n12_qkv";
+    case EPI_RESID: return n9 ? "hat_gemm_n9_resid" : "hat_gemm_n12_resid";
+    case EPI_RESID_LN: return n9 ? "hat_gemm_n9_resid_ln" : "hat_gemm_n12_resid_ln";
+    case EPI_HAB_LN: return n9 ? "hat_gemm_n9_hab_ln" : "hat_gemm_n12_hab_ln";
     }
     throw Error("unknown GEMM epilogue");
 }
 
+struct GemmEpilogue {
+    const float* res = nullptr;   // residual
+    const float* aux = nullptr;   // conv branch (HAB)
+    const float* gate = nullptr;  // channel gate (HAB)
+    float* xn = nullptr;          // LayerNorm output of the result rows
+    const float* nw = nullptr;
+    const float* nb = nullptr;
+};
+
 void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M, float* out,
-              int ldo, int epi, const float* res, const float* aux, const float* gate,
-              const float* lnw, const float* lnb, int heads, int hdim, float cscale)
+              int ldo, int epi, const GemmEpilogue& e, int heads, int hdim, float cscale)
 {
     if (L.K % 4 != 0 || lda % 4 != 0 || lda < L.K)
         throw Error("GEMM: K and lda must be multiples of 4 with lda >= K");
+    if (L.N % 4 != 0 || (epi != EPI_QKV && (ldo % 4 != 0 || ldo < L.N)))
+        throw Error("GEMM: N and ldo must be multiples of 4 with ldo >= N");
     if (M > 0x7fffffffL) throw Error("GEMM: too many rows");
+    const int BN = gemm_bn(L.N);
+    if ((epi == EPI_RESID_LN || epi == EPI_HAB_LN) && L.N > BN)
+        throw Error("GEMM: a LayerNorm epilogue needs whole rows in one block");
     GemmArgs p{};
     p.a = a;
     p.w = L.w;
     p.bias = L.b;
     p.out = out;
-    p.res = res;
-    p.aux = aux;
-    p.gate = gate;
-    p.lnw = lnw;
-    p.lnb = lnb;
+    p.res = e.res;
+    p.aux = e.aux;
+    p.gate = e.gate;
+    p.xn = e.xn;
+    p.nw = e.nw;
+    p.nb = e.nb;
     p.M = (int)M;
     p.N = L.N;
     p.K = L.K;
@@ -102,9 +117,32 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
     p.hdim = hdim;
     p.cscale = cscale;
     p.eps = 1e-5f;
-    const int BN = L.N % 144 == 0 ? 144 : 96;
-    launch(s, gemm_kernel(L.N, epi, lnw != nullptr), (unsigned)((M + 127) / 128),
-           (unsigned)((L.N + BN - 1) / BN), 1, 256, p);
+    launch(s, gemm_kernel(L.N, epi), (unsigned)((M + 127) / 128), (unsigned)((L.N + BN - 1) / BN), 1,
+           256, p);
+}
+
+// The channel-attention gate from the CAB conv's per-tile column sums:
+// reduce in fixed row blocks, then squeeze-excite.
+void run_se(hipStream_t s, const float* partial, int nblk, int C, float* red, float count,
+            const float* w1, const float* b1, const float* w2, const float* b2, int sq, float* gate)
+{
+    const int rows_per = 32;
+    const int nred = (nblk + rows_per - 1) / rows_per;
+    ReduceArgs r{partial, red, nblk, C, C, rows_per};
+    launch(s, "hat_colsum_reduce", (unsigned)nred, 1, 1, 256, r);
+    SeArgs se{};
+    se.partial = red;
+    se.nblk = nred;
+    se.co_stride = C;
+    se.count = count;
+    se.w1 = w1;
+    se.b1 = b1;
+    se.w2 = w2;
+    se.b2 = b2;
+    se.gate = gate;
+    se.C = C;
+    se.sq = sq;
+    launch(s, "hat_se_gate", 1, 1, 1, 256, se);
 }
 
 void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, int H, int W,
@@ -344,6 +382,7 @@ void GpuBackend::ensure_plan(int h, int w)
     t1_ = A(T * t1_stride_);
     t2_ = A(T * C);
     partial_ = A((size_t)nblk_conv2_ * C);
+    red_ = A((size_t)((nblk_conv2_ + 31) / 32) * C);
     gate_ = A(C);
     qkv_ = A(3 * T * C);
     ao_ = A(T * C);
@@ -371,11 +410,19 @@ void GpuBackend::layernorm(const float* x, float* y, const std::string& prefix, 
 }
 
 void GpuBackend::gemm(const DevLinear& L, const float* a, int lda, long M, float* out, int ldo,
-                      int epi, const float* res, const float* aux, const float* gate,
-                      const float* lnw, const float* lnb)
+                      int epi, const float* res, const float* aux, const float* gate, float* xn,
+                      const std::string& norm)
 {
-    run_gemm(stream_, L, a, lda, M, out, ldo, epi, res, aux, gate, lnw, lnb, wt_.heads,
-             wt_.head_dim, wt_.conv_scale);
+    GemmEpilogue e;
+    e.res = res;
+    e.aux = aux;
+    e.gate = gate;
+    e.xn = xn;
+    if (!norm.empty()) {
+        e.nw = raw_.at(norm + ".weight");
+        e.nb = raw_.at(norm + ".bias");
+    }
+    run_gemm(stream_, L, a, lda, M, out, ldo, epi, e, wt_.heads, wt_.head_dim, wt_.conv_scale);
 }
 
 void GpuBackend::conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
@@ -393,53 +440,46 @@ void GpuBackend::attention(const std::string& table, bool oca, int shift)
 
 // HAB.forward (hat_arch.py:266-309; cpu.rs:1090-1166):
 //   x = shortcut + attn(norm1 x) + conv_x * conv_scale;  x = x + mlp(norm2 x)
-void GpuBackend::hab(int stage, int block, float* x_in, float* x_out)
+// On entry xn_ holds norm1(x_in); on exit x_out holds the block's result and
+// xn_ holds next_norm(x_out), the input of whatever block follows.
+void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std::string& next_norm)
 {
     const std::string p = "layers." + std::to_string(stage) + ".residual_group.blocks." +
                           std::to_string(block);
     const long T = plan_.tokens();
     const int C = wt_.embed, H = plan_.hp, W = plan_.wp;
-    layernorm(x_in, xn_, p + ".norm1", T);
-    // CAB: conv3x3 -> GELU -> conv3x3 (+ per-block channel sums) -> gate.
+    // CAB: conv3x3 -> GELU -> conv3x3 (+ per-tile channel sums) -> gate.
     conv(conv_.at(p + ".conv_block.cab.0"), xn_, C, H, W, t1_, t1_stride_, CEPI_STORE, 1);
     conv(conv_.at(p + ".conv_block.cab.2"), t1_, t1_stride_, H, W, t2_, C, CEPI_COLSUM, 0, nullptr,
          partial_);
-    SeArgs se{};
-    se.partial = partial_;
-    se.nblk = nblk_conv2_;
-    se.co_stride = C;
-    se.count = (float)T;
-    se.w1 = raw_.at(p + ".conv_block.cab.3.attention.1.weight");
-    se.b1 = raw_.at(p + ".conv_block.cab.3.attention.1.bias");
-    se.w2 = raw_.at(p + ".conv_block.cab.3.attention.3.weight");
-    se.b2 = raw_.at(p + ".conv_block.cab.3.attention.3.bias");
-    se.gate = gate_;
-    se.C = C;
-    se.sq = wt_.squeezed;
-    launch(stream_, "hat_se_gate", 1, 1, 1, 256, se);
-    // Window attention, the roll and the partition folded into its addressing.
+    run_se(stream_, partial_, nblk_conv2_, C, red_, (float)T,
+           raw_.at(p + ".conv_block.cab.3.attention.1.weight"),
+           raw_.at(p + ".conv_block.cab.3.attention.1.bias"),
+           raw_.at(p + ".conv_block.cab.3.attention.3.weight"),
+           raw_.at(p + ".conv_block.cab.3.attention.3.bias"), wt_.squeezed, gate_);
+    // Window attention, the roll and the partition folded into its addressing;
+    // proj's epilogue adds the shortcut and the gated conv branch, then norm2.
     gemm(lin_.at(p + ".attn.qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
     attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0);
-    gemm(lin_.at(p + ".attn.proj"), ao_, C, T, x_out, C, EPI_HAB, x_in, t2_, gate_);
-    // MLP with norm2 as the fc1 prologue.
-    gemm(lin_.at(p + ".mlp.fc1"), x_out, C, T, hidden_, C * wt_.mlp_ratio, EPI_GELU, nullptr,
-         nullptr, nullptr, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"));
-    gemm(lin_.at(p + ".mlp.fc2"), hidden_, C * wt_.mlp_ratio, T, x_out, C, EPI_RESID, x_out);
+    gemm(lin_.at(p + ".attn.proj"), ao_, C, T, x_out, C, EPI_HAB_LN, x_in, t2_, gate_, xn_,
+         p + ".norm2");
+    gemm(lin_.at(p + ".mlp.fc1"), xn_, C, T, hidden_, C * wt_.mlp_ratio, EPI_GELU);
+    gemm(lin_.at(p + ".mlp.fc2"), hidden_, C * wt_.mlp_ratio, T, x_out, C, EPI_RESID_LN, x_out,
+         nullptr, nullptr, xn_, next_norm);
 }
 
 // OCAB.forward (hat_arch.py:392-438; cpu.rs:1170-1198): x = proj(attn) + x;
-// x = x + mlp(norm2 x). norm1 is the qkv GEMM's prologue.
+// x = x + mlp(norm2 x). On entry xn_ holds norm1(x).
 void GpuBackend::ocab(int stage, float* x)
 {
     const std::string p = "layers." + std::to_string(stage) + ".residual_group.overlap_attn";
     const long T = plan_.tokens();
     const int C = wt_.embed;
-    gemm(lin_.at(p + ".qkv"), x, C, T, qkv_, 0, EPI_QKV, nullptr, nullptr, nullptr,
-         raw_.at(p + ".norm1.weight"), raw_.at(p + ".norm1.bias"));
+    gemm(lin_.at(p + ".qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
     attention(p + ".relative_position_bias_table", true, 0);
-    gemm(lin_.at(p + ".proj"), ao_, C, T, x, C, EPI_RESID, x);
-    gemm(lin_.at(p + ".mlp.fc1"), x, C, T, hidden_, C * wt_.mlp_ratio, EPI_GELU, nullptr, nullptr,
-         nullptr, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"));
+    gemm(lin_.at(p + ".proj"), ao_, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, xn_,
+         p + ".norm2");
+    gemm(lin_.at(p + ".mlp.fc1"), xn_, C, T, hidden_, C * wt_.mlp_ratio, EPI_GELU);
     gemm(lin_.at(p + ".mlp.fc2"), hidden_, C * wt_.mlp_ratio, T, x, C, EPI_RESID, x);
 }
 
@@ -457,8 +497,16 @@ void GpuBackend::forward_device(int h, int w, const float* d_in, float* d_out)
     layernorm(body_, xa_, "patch_embed.norm", T);
     for (size_t s = 0; s < wt_.depths.size(); ++s) {
         // RHAG (gpu.rs:592-610): conv3x3(blocks(x)) + x, with the stage input
-        // kept in xa_ and the blocks working in xb_.
-        for (int b = 0; b < wt_.depths[s]; ++b) hab((int)s, b, b == 0 ? xa_ : xb_, xb_);
+        // kept in xa_ and the blocks working in xb_. Each block's last GEMM
+        // leaves the next block's norm1 in xn_; the first needs its own pass.
+        const std::string L = "layers." + std::to_string(s) + ".residual_group.";
+        layernorm(xa_, xn_, L + "blocks.0.norm1", T);
+        for (int b = 0; b < wt_.depths[s]; ++b) {
+            const std::string next = b + 1 < wt_.depths[s]
+                                         ? L + "blocks." + std::to_string(b + 1) + ".norm1"
+                                         : L + "overlap_attn.norm1";
+            hab((int)s, b, b == 0 ? xa_ : xb_, xb_, next);
+        }
         ocab((int)s, xb_);
         conv(conv_.at("layers." + std::to_string(s) + ".conv"), xb_, C, H, W, xa_, C, CEPI_RESID, 0,
              xa_);
@@ -561,12 +609,11 @@ void op_swmsa(const float* x, float* out, int hp, int wp, int c, int heads, int 
     {
         DevBuf dx(x, T * c), dq(3 * T * c), dao(T * c), dout(T * c), dtab(table, 961 * (size_t)heads);
         OpLinear qkv(qkv_w, qkv_b, 3 * c, c), proj(proj_w, proj_b, c, c);
+        const GemmEpilogue none;
         auto run = [&]() {
-            run_gemm(s, qkv.L, dx.p, c, (long)T, dq.p, 0, EPI_QKV, nullptr, nullptr, nullptr, nullptr,
-                     nullptr, heads, D, 0.f);
+            run_gemm(s, qkv.L, dx.p, c, (long)T, dq.p, 0, EPI_QKV, none, heads, D, 0.f);
             run_attn(s, dq.p, dtab.p, dao.p, pl, heads, D, false, shift);
-            run_gemm(s, proj.L, dao.p, c, (long)T, dout.p, c, EPI_STORE, nullptr, nullptr, nullptr,
-                     nullptr, nullptr, heads, D, 0.f);
+            run_gemm(s, proj.L, dao.p, c, (long)T, dout.p, c, EPI_STORE, none, heads, D, 0.f);
         };
         run();
         rt.check(api.StreamSynchronize(s), "swmsa");
@@ -606,22 +653,27 @@ void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int m
     hipStream_t s = nullptr;
     rt.check(api.StreamCreate(&s), "hipStreamCreate");
     {
-        DevBuf dx(x, T * c), dwork(T * c), dq(3 * T * c), dao(T * c), dh(T * hid),
+        DevBuf dx(x, T * c), dwork(T * c), dxn(T * c), dq(3 * T * c), dao(T * c), dh(T * hid),
             dtab(table, 1521 * (size_t)heads), d1w(n1w, c), d1b(n1b, c), d2w(n2w, c), d2b(n2b, c);
         OpLinear qkv(qkv_w, qkv_b, 3 * c, c), proj(proj_w, proj_b, c, c),
             fc1(fc1_w, fc1_b, (int)hid, c), fc2(fc2_w, fc2_b, c, (int)hid);
+        const GemmEpilogue none;
+        GemmEpilogue resid_ln;
+        resid_ln.res = dx.p;
+        resid_ln.xn = dxn.p;
+        resid_ln.nw = d2w.p;
+        resid_ln.nb = d2b.p;
+        GemmEpilogue resid;
+        resid.res = dwork.p;
+        // The backend's OCAB sequence: norm1, qkv, attention, proj + shortcut
+        // (whose epilogue also writes norm2), GELU fc1, fc2 + residual.
         auto run = [&]() {
-            rt.check(api.MemcpyAsync(dwork.p, dx.p, T * c * sizeof(float), hipMemcpyDeviceToDevice, s),
-                     "copy");
-            run_gemm(s, qkv.L, dwork.p, c, (long)T, dq.p, 0, EPI_QKV, nullptr, nullptr, nullptr,
-                     d1w.p, d1b.p, heads, D, 0.f);
+            run_ln(s, dx.p, dxn.p, d1w.p, d1b.p, (long)T, c);
+            run_gemm(s, qkv.L, dxn.p, c, (long)T, dq.p, 0, EPI_QKV, none, heads, D, 0.f);
             run_attn(s, dq.p, dtab.p, dao.p, pl, heads, D, true, 0);
-            run_gemm(s, proj.L, dao.p, c, (long)T, dwork.p, c, EPI_RESID, dwork.p, nullptr, nullptr,
-                     nullptr, nullptr, heads, D, 0.f);
-            run_gemm(s, fc1.L, dwork.p, c, (long)T, dh.p, (int)hid, EPI_GELU, nullptr, nullptr,
-                     nullptr, d2w.p, d2b.p, heads, D, 0.f);
-            run_gemm(s, fc2.L, dh.p, (int)hid, (long)T, dwork.p, c, EPI_RESID, dwork.p, nullptr,
-                     nullptr, nullptr, nullptr, heads, D, 0.f);
+            run_gemm(s, proj.L, dao.p, c, (long)T, dwork.p, c, EPI_RESID_LN, resid_ln, heads, D, 0.f);
+            run_gemm(s, fc1.L, dxn.p, c, (long)T, dh.p, (int)hid, EPI_GELU, none, heads, D, 0.f);
+            run_gemm(s, fc2.L, dh.p, (int)hid, (long)T, dwork.p, c, EPI_RESID, resid, heads, D, 0.f);
         };
         run();
         rt.check(api.StreamSynchronize(s), "ocab");

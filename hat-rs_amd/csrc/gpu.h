@@ -66,7 +66,8 @@ private:
     std::vector<void*> acts_;
     size_t acts_bytes_ = 0;
     float *x0_ = nullptr, *body_ = nullptr, *xa_ = nullptr, *xb_ = nullptr, *xn_ = nullptr,
-          *t1_ = nullptr, *t2_ = nullptr, *partial_ = nullptr, *gate_ = nullptr, *qkv_ = nullptr,
+          *t1_ = nullptr, *t2_ = nullptr, *partial_ = nullptr, *red_ = nullptr, *gate_ = nullptr,
+          *qkv_ = nullptr,
           *ao_ = nullptr, *hidden_ = nullptr, *head0_ = nullptr, *head1_ = nullptr,
           *din_ = nullptr, *dout_ = nullptr;
     int t1_stride_ = 0, nblk_conv2_ = 0;
@@ -81,12 +82,12 @@ private:
     void layernorm(const float* x, float* y, const std::string& prefix, long rows);
     void gemm(const DevLinear& L, const float* a, int lda, long M, float* out, int ldo, int epi,
               const float* res = nullptr, const float* aux = nullptr, const float* gate = nullptr,
-              const float* lnw = nullptr, const float* lnb = nullptr);
+              float* xn = nullptr, const std::string& norm = "");
     void conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
               int co_stride, int epi, int act, const float* res = nullptr, float* partial = nullptr,
               int crop_h = 0, int crop_w = 0);
     void attention(const std::string& table, bool oca, int shift);
-    void hab(int stage, int block, float* x_in, float* x_out);
+    void hab(int stage, int block, float* x_in, float* x_out, const std::string& next_norm);
     void ocab(int stage, float* x);
 };
 

@@ -16,11 +16,13 @@ const std::vector<std::string>& required_kernels()
     static const std::vector<std::string> k = {
         "hat_attn_sw_d24",     "hat_attn_sw_d30",     "hat_attn_oca_d24",   "hat_attn_oca_d30",
         "hat_conv_n1_store",   "hat_conv_n3_store",   "hat_conv_n4_store",  "hat_conv_n3_resid",
-        "hat_conv_n3_colsum",  "hat_conv_n4_shuffle", "hat_conv_n1_final",  "hat_gemm_n9_store",
-        "hat_gemm_n9_gelu_ln", "hat_gemm_n9_qkv",     "hat_gemm_n9_qkv_ln", "hat_gemm_n9_resid",
-        "hat_gemm_n9_hab",     "hat_gemm_n6_store",   "hat_gemm_n6_gelu_ln", "hat_gemm_n6_qkv",
-        "hat_gemm_n6_qkv_ln",  "hat_gemm_n6_resid",   "hat_gemm_n6_hab",    "hat_layernorm",
-        "hat_pre",             "hat_se_gate",
+        "hat_conv_n3_colsum",  "hat_conv_n4_shuffle", "hat_conv_n1_final",
+        "hat_gemm_n9_store",   "hat_gemm_n9_gelu",    "hat_gemm_n9_qkv",    "hat_gemm_n9_resid",
+        "hat_gemm_n9_resid_ln", "hat_gemm_n9_hab_ln",
+        "hat_gemm_n12_store",  "hat_gemm_n12_gelu",   "hat_gemm_n12_qkv",   "hat_gemm_n12_resid",
+        "hat_gemm_n12_resid_ln", "hat_gemm_n12_hab_ln",
+        "hat_layernorm",       "hat_pre",             "hat_colsum_reduce",  "hat_se_gate",
+        "hat_copy",
     };
     return k;
 }
@@ -148,6 +150,9 @@ std::string Runtime::device_name() const
 {
     char buf[256] = {0};
     if (api_.DeviceGetName(buf, sizeof buf, 0) != hipSuccess) return "?";
+    // Some boards report no marketing name; the code object only loads on
+    // gfx950, so that is what the device is.
+    if (buf[0] == '\0') return "gfx950";
     return buf;
 }
 

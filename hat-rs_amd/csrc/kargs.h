@@ -10,30 +10,33 @@ namespace hatk {
 // Activation layout everywhere on the device: token-major NHWC, [pixel][channel],
 // pixels in image row-major order over the padded plane (hp x wp).
 
-// out[m][n] = epilogue( prologue(A)[m][:] . W[n][:] + bias[n] )
+// out[m][n] = epilogue( A[m][:] . W[n][:] + bias[n] )
 enum GemmEpi : int {
     EPI_STORE = 0,       // out[m][n] = v
     EPI_GELU = 1,        // out[m][n] = gelu(v)
     EPI_QKV = 2,         // head-major scatter: out[which][head][m][dim]
     EPI_RESID = 3,       // out[m][n] = res[m][n] + v
     EPI_HAB = 4,         // out[m][n] = (res[m][n] + v) + (aux[m][n] * gate[n]) * cscale
+    EPI_RESID_LN = 5,    // EPI_RESID, and xn[m][:] = LayerNorm(out[m][:]) (full rows)
+    EPI_HAB_LN = 6,      // EPI_HAB, and xn[m][:] = LayerNorm(out[m][:]) (full rows)
 };
 
 struct GemmArgs {
     const float* a;      // [M][lda]
-    const float* w;      // [N][ldw] row-major, K contiguous (zero-padded to Kp)
+    const float* w;      // [N][Kp] row-major, K contiguous, zero-padded to Kp
     const float* bias;   // [N]
     float* out;
-    const float* res;    // residual input (EPI_RESID / EPI_HAB)
-    const float* aux;    // EPI_HAB: conv branch [M][N]
-    const float* gate;   // EPI_HAB: channel gate [N]
-    const float* lnw;    // LayerNorm prologue weight [K] (null = no LN)
-    const float* lnb;    // LayerNorm prologue bias [K]
+    const float* res;    // residual input (EPI_RESID*, EPI_HAB*)
+    const float* aux;    // EPI_HAB*: conv branch [M][N]
+    const float* gate;   // EPI_HAB*: channel gate [N]
+    float* xn;           // EPI_*_LN: LayerNorm of the output rows [M][ldo]
+    const float* nw;     // EPI_*_LN: LayerNorm weight [N]
+    const float* nb;     // EPI_*_LN: LayerNorm bias [N]
     int M, N, K;         // logical sizes
     int Kp;              // K rounded up to 16 (W rows are Kp long)
     int lda, ldo;        // row strides of A and out (floats)
     int heads, hdim;     // EPI_QKV geometry (N = 3 * heads * hdim)
-    float cscale;        // EPI_HAB conv scale
+    float cscale;        // EPI_HAB* conv scale
     float eps;           // LayerNorm eps
 };
 
@@ -90,6 +93,21 @@ struct PreArgs {
     float* out;          // [hp][wp][cstride], channels >= 3 zeroed
     int h, w, hp, wp, cstride;
     float m0, m1, m2, range;
+};
+
+// dst[i] = src[i] for n4 float4 (16-byte aligned buffers).
+struct CopyArgs {
+    const float* src;
+    float* dst;
+    long n4;
+};
+
+// Column sums of a [nrows][stride] matrix in row blocks: out[blk][c] = sum of
+// rows [blk*rows_per, blk*rows_per + rows_per) of column c.
+struct ReduceArgs {
+    const float* in;
+    float* out;
+    int nrows, C, stride, rows_per;
 };
 
 // Squeeze-excite gate: gate[c] = sigmoid(b2 + W2 relu(b1 + W1 mean)).

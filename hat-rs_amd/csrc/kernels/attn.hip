@@ -45,7 +45,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p)
     constexpr int RSK = 2 * HP + 4;             // K row stride in LDS (floats)
     constexpr int NK = OCA ? 576 : 256;         // keys per window
     constexpr int NKT = NK / 32;                // 32-key tiles
-    constexpr int CHT = OCA ? 3 : 4;            // tiles per softmax chunk
+    constexpr int CHT = OCA ? 3 : 2;            // tiles per softmax chunk
     constexpr int NCH = NKT / CHT;
     constexpr int RSV = NK + 4;                 // V^T row stride in LDS
     constexpr int TROWS = OCA ? 1521 : 961;     // bias table rows
@@ -136,10 +136,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p)
     for (int i = 0; i < 16; ++i) o[i] = 0.0f;
     float mrun = -INFINITY, lrun = 0.0f;
 
-    // The OCA chunk loop stays rolled: unrolled, the compiler hoists the K
-    // operand reads of all 18 key tiles and spills.
-    constexpr int CH_UNROLL = OCA ? 1 : NCH;
-#pragma unroll CH_UNROLL
+    // The chunk loop stays rolled: unrolled, the compiler hoists the K operand
+    // reads of every key tile ahead of the MFMAs and spills.
+#pragma unroll 1
     for (int ch = 0; ch < NCH; ++ch) {
         f32x16 s[CHT];
 #pragma unroll
@@ -223,8 +222,14 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p)
     }
 }
 
+// SW kernels are asked for 4 waves per SIMD (2 blocks per CU, <= 128 VGPRs), so
+// one block's K/V staging
+// overlaps the other's MFMA work; the OCA block's LDS allows only one block.
 #define ATTN_INST(NAME, D, OCA)                                                              \
-    extern "C" __global__ __launch_bounds__(512) void NAME(AttnArgs p) { attn_body<D, OCA>(p); }
+    extern "C" __global__ __launch_bounds__(512, OCA ? 2 : 4) void NAME(AttnArgs p)          \
+    {                                                                                        \
+        attn_body<D, OCA>(p);                                                                \
+    }
 
 ATTN_INST(hat_attn_sw_d24, 24, false)
 ATTN_INST(hat_attn_sw_d30, 30, false)

@@ -52,10 +52,41 @@ extern "C" __global__ __launch_bounds__(256) void hat_pre(PreArgs p)
     for (int c = 3; c < p.cstride; ++c) o[c] = 0.0f;
 }
 
+// A plain copy of n float4 (the HBM reference point the traffic counters of the
+// other kernels are scaled by; also the library's device-to-device copy).
+extern "C" __global__ __launch_bounds__(256) void hat_copy(CopyArgs p)
+{
+    const float4* src = (const float4*)p.src;
+    float4* dst = (float4*)p.dst;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < p.n4; i += (long)gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+// First stage of the channel-attention pool (lg_channel_mean, cuda.rs:259-272):
+// the per-tile column sums of the second CAB conv, summed over row blocks in
+// a fixed order (deterministic). One block per row block, one thread per column.
+extern "C" __global__ __launch_bounds__(256) void hat_colsum_reduce(ReduceArgs p)
+{
+    const int r0 = blockIdx.x * p.rows_per;
+    const int r1 = min(r0 + p.rows_per, p.nrows);
+    for (int c = threadIdx.x; c < p.C; c += 256) {
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        int r = r0;
+        for (; r + 3 < r1; r += 4) {
+            a0 += p.in[(size_t)r * p.stride + c];
+            a1 += p.in[(size_t)(r + 1) * p.stride + c];
+            a2 += p.in[(size_t)(r + 2) * p.stride + c];
+            a3 += p.in[(size_t)(r + 3) * p.stride + c];
+        }
+        for (; r < r1; ++r) a0 += p.in[(size_t)r * p.stride + c];
+        p.out[(size_t)blockIdx.x * p.C + c] = (a0 + a1) + (a2 + a3);
+    }
+}
+
 // The channel attention's gate (CAB, hat_arch.py:40-55; cpu.rs:940-955):
-// mean over the plane from the per-block column sums of the second CAB conv,
-// 1x1 squeeze + ReLU, 1x1 excite + sigmoid. One block; partial sums are added
-// in block order.
+// mean over the plane from the column sums of the second CAB conv, 1x1 squeeze
+// + ReLU, 1x1 excite + sigmoid. One block; partial sums are added in block
+// order.
 extern "C" __global__ __launch_bounds__(256) void hat_se_gate(SeArgs p)
 {
     __shared__ float s_mean[512];

@@ -203,79 +203,80 @@ int gpu_selftest(std::string* err)
                     note(nm);
                 }
 
-        // ---- GEMM epilogues (n9: N multiple of 144; n6: C = 180 family).
+        // ---- GEMM epilogues (n9: the C = 144 family; n12: C = 180). The
+        // LayerNorm epilogues also check the normalised rows they write.
+        const int epis[6] = {EPI_STORE, EPI_GELU, EPI_QKV, EPI_RESID, EPI_RESID_LN, EPI_HAB_LN};
+        const char* enames[7] = {"store", "gelu", "qkv", "resid", "", "resid_ln", "hab_ln"};
         for (int C : {144, 180})
-            for (int epi = 0; epi < 5; ++epi)
-                for (int ln = 0; ln < 2; ++ln) {
-                    if (ln && !(epi == EPI_GELU || epi == EPI_QKV)) continue;
-                    if (!ln && epi == EPI_GELU) continue;
-                    const int heads = 6, hd = C / heads;
-                    const int M = 200;  // not a multiple of the 128-row tile
-                    int N = epi == EPI_QKV ? 3 * C : (epi == EPI_GELU ? 2 * C : C);
-                    int K = C;
-                    if (epi == EPI_RESID && !ln) K = 2 * C;  // the fc2 shape
-                    std::vector<float> a = rng.vec((size_t)M * K, 1.0f), w = rng.vec((size_t)N * K, 0.05f),
-                                       b = rng.vec(N, 0.1f), res = rng.vec((size_t)M * N, 1.0f),
-                                       aux = rng.vec((size_t)M * N, 1.0f), gate = rng.vec(N, 1.0f),
-                                       lnw = rng.vec(K, 1.0f), lnb = rng.vec(K, 0.1f);
-                    int Kp = 0;
-                    std::vector<float> pk = pack_linear(w.data(), N, K, &Kp);
-                    Dev da(a), dw(pk), db(b), dres(res), daux(aux), dg(gate), dlw(lnw), dlb(lnb),
-                        dout(epi == EPI_QKV ? (size_t)M * N : (size_t)M * N);
-                    GemmArgs p{};
-                    p.a = da.p;
-                    p.w = dw.p;
-                    p.bias = db.p;
-                    p.out = dout.p;
-                    p.res = dres.p;
-                    p.aux = daux.p;
-                    p.gate = dg.p;
-                    p.lnw = ln ? dlw.p : nullptr;
-                    p.lnb = ln ? dlb.p : nullptr;
-                    p.M = M;
-                    p.N = N;
-                    p.K = K;
-                    p.Kp = Kp;
-                    p.lda = K;
-                    p.ldo = N;
-                    p.heads = heads;
-                    p.hdim = hd;
-                    p.cscale = 0.01f;
-                    p.eps = 1e-5f;
-                    const bool n9 = N % 144 == 0;
-                    const char* names[5][2] = {{"store", "store"}, {"gelu_ln", "gelu_ln"}, {"qkv", "qkv_ln"},
-                                               {"resid", "resid"}, {"hab", "hab"}};
-                    std::string k = std::string(n9 ? "hat_gemm_n9_" : "hat_gemm_n6_") + names[epi][ln];
-                    launch(s, k.c_str(), (M + 127) / 128, (N + (n9 ? 143 : 95)) / (n9 ? 144 : 96), 1, 256, p);
-                    std::vector<double> want((size_t)M * N);
-                    for (int m = 0; m < M; ++m) {
-                        std::vector<double> row(K);
-                        double mean = 0, var = 0;
-                        for (int kk = 0; kk < K; ++kk) mean += a[(size_t)m * K + kk];
-                        mean /= K;
-                        for (int kk = 0; kk < K; ++kk) var += (a[(size_t)m * K + kk] - mean) * (a[(size_t)m * K + kk] - mean);
-                        var /= K;
-                        for (int kk = 0; kk < K; ++kk)
-                            row[kk] = ln ? (a[(size_t)m * K + kk] - mean) / std::sqrt(var + 1e-5) * lnw[kk] + lnb[kk]
-                                         : a[(size_t)m * K + kk];
-                        for (int n = 0; n < N; ++n) {
-                            double v = b[n];
-                            for (int kk = 0; kk < K; ++kk) v += row[kk] * w[(size_t)n * K + kk];
-                            const size_t o = (size_t)m * N + n;
-                            if (epi == EPI_GELU) v = gelu_d(v);
-                            if (epi == EPI_RESID) v = res[o] + v;
-                            if (epi == EPI_HAB) v = (res[o] + v) + aux[o] * gate[n] * 0.01;
-                            if (epi == EPI_QKV) {
-                                const int which = n / C, rem = n % C, h = rem / hd, d = rem % hd;
-                                want[(((size_t)which * heads + h) * M + m) * hd + d] = v;
-                            } else {
-                                want[o] = v;
-                            }
+            for (int epi : epis) {
+                const int heads = 6, hd = C / heads;
+                const int M = 200;  // not a multiple of the 128-row tile
+                const int N = epi == EPI_QKV ? 3 * C : (epi == EPI_GELU ? 2 * C : C);
+                const int K = epi == EPI_RESID ? 2 * C : C;  // RESID at the fc2 shape
+                const bool lnout = epi == EPI_RESID_LN || epi == EPI_HAB_LN;
+                std::vector<float> a = rng.vec((size_t)M * K, 1.0f), w = rng.vec((size_t)N * K, 0.05f),
+                                   b = rng.vec(N, 0.1f), res = rng.vec((size_t)M * N, 1.0f),
+                                   aux = rng.vec((size_t)M * N, 1.0f), gate = rng.vec(N, 1.0f),
+                                   nw = rng.vec(N, 1.0f), nb = rng.vec(N, 0.1f);
+                int Kp = 0;
+                std::vector<float> pk = pack_linear(w.data(), N, K, &Kp);
+                Dev da(a), dw(pk), db(b), dres(res), daux(aux), dg(gate), dnw(nw), dnb(nb),
+                    dout((size_t)M * N), dxn((size_t)M * N);
+                GemmArgs p{};
+                p.a = da.p;
+                p.w = dw.p;
+                p.bias = db.p;
+                p.out = dout.p;
+                p.res = dres.p;
+                p.aux = daux.p;
+                p.gate = dg.p;
+                p.xn = dxn.p;
+                p.nw = dnw.p;
+                p.nb = dnb.p;
+                p.M = M;
+                p.N = N;
+                p.K = K;
+                p.Kp = Kp;
+                p.lda = K;
+                p.ldo = N;
+                p.heads = heads;
+                p.hdim = hd;
+                p.cscale = 0.01f;
+                p.eps = 1e-5f;
+                const bool n9 = N % 144 == 0;
+                const int BN = n9 ? 144 : 192;
+                std::string k = std::string(n9 ? "hat_gemm_n9_" : "hat_gemm_n12_") + enames[epi];
+                launch(s, k.c_str(), (M + 127) / 128, (N + BN - 1) / BN, 1, 256, p);
+                std::vector<double> want((size_t)M * N), wxn((size_t)M * N);
+                for (int m = 0; m < M; ++m) {
+                    for (int n = 0; n < N; ++n) {
+                        double v = b[n];
+                        for (int kk = 0; kk < K; ++kk) v += (double)a[(size_t)m * K + kk] * w[(size_t)n * K + kk];
+                        const size_t o = (size_t)m * N + n;
+                        if (epi == EPI_GELU) v = gelu_d(v);
+                        if (epi == EPI_RESID || epi == EPI_RESID_LN) v = res[o] + v;
+                        if (epi == EPI_HAB_LN) v = (res[o] + v) + aux[o] * gate[n] * 0.01;
+                        if (epi == EPI_QKV) {
+                            const int which = n / C, rem = n % C, h = rem / hd, d = rem % hd;
+                            want[(((size_t)which * heads + h) * M + m) * hd + d] = v;
+                        } else {
+                            want[o] = v;
                         }
                     }
-                    check_close(k + " C " + std::to_string(C), dout.get(), want, 3e-5);
-                    note(k + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
+                    if (lnout) {
+                        double mean = 0, var = 0;
+                        for (int n = 0; n < N; ++n) mean += want[(size_t)m * N + n];
+                        mean /= N;
+                        for (int n = 0; n < N; ++n) var += (want[(size_t)m * N + n] - mean) * (want[(size_t)m * N + n] - mean);
+                        var /= N;
+                        for (int n = 0; n < N; ++n)
+                            wxn[(size_t)m * N + n] = (want[(size_t)m * N + n] - mean) / std::sqrt(var + 1e-5) * nw[n] + nb[n];
+                    }
                 }
+                check_close(k + " C " + std::to_string(C), dout.get(), want, 3e-5);
+                if (lnout) check_close(k + " C " + std::to_string(C) + " layernorm", dxn.get(), wxn, 5e-5);
+                note(k + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
+            }
 
         // ---- convolutions (all epilogues) on a non-square plane.
         struct CCase { int CI, CO, epi, act, r; const char* what; };
@@ -438,6 +439,18 @@ int gpu_selftest(std::string* err)
                             throw Error("hat_pre: mismatch at (" + std::to_string(y) + ", " + std::to_string(x) + ")");
                     }
             note("hat_pre 21x35 -> 32x48 (exact)");
+        }
+        {
+            const int nrows = 2048 + 17, C = 180, rows_per = 32, nred = (nrows + rows_per - 1) / rows_per;
+            std::vector<float> in = rng.vec((size_t)nrows * C, 4.0f);
+            Dev din(in), dout((size_t)nred * C);
+            ReduceArgs p{din.p, dout.p, nrows, C, C, rows_per};
+            launch(s, "hat_colsum_reduce", nred, 1, 1, 256, p);
+            std::vector<double> want((size_t)nred * C, 0.0);
+            for (int r = 0; r < nrows; ++r)
+                for (int c = 0; c < C; ++c) want[(size_t)(r / rows_per) * C + c] += in[(size_t)r * C + c];
+            check_close("hat_colsum_reduce", dout.get(), want, 1e-4);
+            note("hat_colsum_reduce 2065x180 in blocks of 32 rows");
         }
         {
             const int C = 144, sq = 6, nblk = 37;

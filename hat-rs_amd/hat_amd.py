@@ -75,6 +75,7 @@ def lib():
         "hat_device_free": (C.c_int, [C.c_void_p]),
         "hat_memcpy_h2d": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
         "hat_memcpy_d2h": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+        "hat_device_copy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
         "hat_device_synchronize": (C.c_int, []),
         "hat_device_name": (C.c_char_p, []),
         "hat_device_cu_count": (C.c_int, []),
@@ -304,6 +305,13 @@ class DeviceBuffer:
 
 def synchronize():
     _check(lib().hat_device_synchronize(), "synchronize")
+
+
+def device_copy(dst, src, nbytes):
+    """Device-to-device copy with the library's copy kernel (DeviceBuffer or raw pointers)."""
+    d = dst.ptr if isinstance(dst, DeviceBuffer) else dst
+    s = src.ptr if isinstance(src, DeviceBuffer) else src
+    _check(lib().hat_device_copy(d, s, nbytes), "device_copy")
 
 
 def device_name():

@@ -127,6 +127,10 @@ void *hat_device_alloc(size_t bytes);
 int hat_device_free(void *p);
 int hat_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int hat_memcpy_d2h(void *dst, const void *src, size_t bytes);
+/* Device-to-device copy with the library's plain copy kernel (bytes a multiple
+ * of 16, 16-byte aligned pointers); asynchronous on the library's stream. It is
+ * also the HBM reference point the benchmark scales traffic counters by. */
+int hat_device_copy(void *dst, const void *src, size_t bytes);
 int hat_device_synchronize(void);
 /* Device name and compute-unit count; "" / 0 when no device. */
 const char *hat_device_name(void);
