@@ -76,6 +76,20 @@ const char* gemm_kernel(int N, int epi)
     throw Error("unknown GEMM epilogue");
 }
 
+// The weight-stationary kernel covers K = 144 (the whole weight row slice sits
+// in LDS) and N a multiple of 144, for the epilogues the C = 144 blocks use.
+const char* gemm_ws_kernel(const DevLinear& L, int epi)
+{
+    if (L.K != 144 || L.Kp != 144 || L.N % 144 != 0) return nullptr;
+    switch (epi) {
+    case EPI_QKV: return "hat_gemmws_qkv";
+    case EPI_GELU: return "hat_gemmws_gelu";
+    case EPI_RESID_LN: return "hat_gemmws_resid_ln";
+    case EPI_HAB_LN: return "hat_gemmws_hab_ln";
+    }
+    return nullptr;
+}
+
 struct GemmEpilogue {
     const float* res = nullptr;   // residual
     const float* aux = nullptr;   // conv branch (HAB)
@@ -117,6 +131,20 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
     p.hdim = hdim;
     p.cscale = cscale;
     p.eps = 1e-5f;
+    if (const char* ws = gemm_ws_kernel(L, epi)) {
+        // One 512-thread block per CU (its 85 KB weight slice fills the LDS),
+        // the CUs split evenly over the column slices; each block walks the
+        // 256-row tiles of its slice. Fewest blocks for the same number of
+        // rounds, so no CU gets a tile more than the others need.
+        static const int cus = std::max(1, Runtime::get().cu_count());
+        const long ntiles = (M + 255) / 256;
+        const int slices = L.N / 144;
+        const long per = std::max(1, cus / slices);
+        const long rounds = (ntiles + per - 1) / per;
+        const long g = std::max(1L, (ntiles + rounds - 1) / rounds);
+        launch(s, ws, (unsigned)g, (unsigned)slices, 1, 512, p);
+        return;
+    }
     launch(s, gemm_kernel(L.N, epi), (unsigned)((M + 127) / 128), (unsigned)((L.N + BN - 1) / BN), 1,
            256, p);
 }

@@ -23,6 +23,114 @@ using namespace hatk;
 #define GEMM_BK 16
 #define GEMM_LDS_STRIDE 20  // 16 + 4 floats: conflict-free float4 rows
 
+// EPI_QKV: for the block's columns n0 .. n0+BN-1, the head-major destination
+// ((which*heads + head) << 8) | dim, so the epilogue scatters with no division.
+template <int BN, int EPI>
+__device__ __forceinline__ void build_colmap(const GemmArgs& p, int n0, int* colmap)
+{
+    if (EPI != EPI_QKV) return;
+    const int C = p.heads * p.hdim;
+    for (int j = threadIdx.x; j < BN; j += blockDim.x) {
+        const int n = n0 + j;
+        const int which = n / C, rem = n - which * C;
+        const int hd = rem / p.hdim, dim = rem - hd * p.hdim;
+        colmap[j] = ((which * p.heads + hd) << 8) | dim;
+    }
+}
+
+// Epilogue shared by both GEMM kernels: lane (lr, lg) holds out[m][n .. n+3]
+// for m = mbase + 16*mt + lr and n = n0 + 16*nt + 4*lg.
+template <int NT, int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[2][NT], int mbase,
+                                              int n0, int lr, int lg, const int* colmap)
+{
+    const int M = p.M, N = p.N;
+    constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = mbase + mt * 16 + lr;
+        const bool mlive = m < M;
+        // Values (bias + residual combine) in place. N is a multiple of 4, so a
+        // lane's four columns are all live or all padding: whole float4 accesses.
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int n = n0 + nt * 16 + lg * 4;
+            const bool live = mlive && n < N;
+            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+            if (live) {
+                const float4 b4 = *(const float4*)(p.bias + n);
+                v = acc[mt][nt] + (f32x4){b4.x, b4.y, b4.z, b4.w};
+                if (EPI == EPI_GELU) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) v[j] = gelu(v[j]);
+                }
+                if (EPI == EPI_RESID || EPI == EPI_RESID_LN || EPI == EPI_HAB || EPI == EPI_HAB_LN) {
+                    const float4 r4 = *(const float4*)(p.res + (size_t)m * p.ldo + n);
+                    v = (f32x4){r4.x, r4.y, r4.z, r4.w} + v;
+                }
+                if (EPI == EPI_HAB || EPI == EPI_HAB_LN) {
+                    const float4 a4 = *(const float4*)(p.aux + (size_t)m * p.ldo + n);
+                    const float4 g4 = *(const float4*)(p.gate + n);
+                    v[0] = v[0] + (a4.x * g4.x) * p.cscale;
+                    v[1] = v[1] + (a4.y * g4.y) * p.cscale;
+                    v[2] = v[2] + (a4.z * g4.z) * p.cscale;
+                    v[3] = v[3] + (a4.w * g4.w) * p.cscale;
+                }
+            }
+            acc[mt][nt] = v;
+        }
+        float mean = 0.0f, rstd = 0.0f;
+        if (LNOUT) {
+            // Row statistics over the 4 lanes that share the row: two-pass mean
+            // then biased variance, as the reference's layer_norm (cpu.rs:563-581).
+            float s = 0.0f;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s += acc[mt][nt][j];
+            s += __shfl_xor(s, 16, 64);
+            s += __shfl_xor(s, 32, 64);
+            mean = s / (float)N;
+            float q = 0.0f;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int n = n0 + nt * 16 + lg * 4 + j;
+                    const float d = n < N ? acc[mt][nt][j] - mean : 0.0f;
+                    q += d * d;
+                }
+            q += __shfl_xor(q, 16, 64);
+            q += __shfl_xor(q, 32, 64);
+            rstd = 1.0f / sqrtf(q / (float)N + p.eps);
+        }
+        if (!mlive) continue;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int n = n0 + nt * 16 + lg * 4;
+            if (n >= N) continue;
+            const f32x4 v = acc[mt][nt];
+            if (EPI == EPI_QKV) {
+                // colmap[n - n0] = ((which*heads + head) << 8) | dim, built per block
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int cm = colmap[n - n0 + j];
+                    p.out[((size_t)(cm >> 8) * M + m) * p.hdim + (cm & 255)] = v[j];
+                }
+                continue;
+            }
+            *(float4*)(p.out + (size_t)m * p.ldo + n) = make_float4(v[0], v[1], v[2], v[3]);
+            if (LNOUT) {
+                const float4 w4 = *(const float4*)(p.nw + n);
+                const float4 b4 = *(const float4*)(p.nb + n);
+                *(float4*)(p.xn + (size_t)m * p.ldo + n) =
+                    make_float4((v[0] - mean) * rstd * w4.x + b4.x, (v[1] - mean) * rstd * w4.y + b4.y,
+                                (v[2] - mean) * rstd * w4.z + b4.z, (v[3] - mean) * rstd * w4.w + b4.w);
+            }
+        }
+    }
+}
+
 template <int NT, int EPI>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p)
 {
@@ -30,6 +138,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
     constexpr int ABUF = GEMM_BM * GEMM_LDS_STRIDE, WBUF = BN * GEMM_LDS_STRIDE;
     __shared__ float As[2 * ABUF];
     __shared__ float Ws[2 * WBUF];
+    __shared__ int s_colmap[EPI == EPI_QKV ? BN : 1];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -96,6 +205,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
         }
     };
 
+    build_colmap<BN, EPI>(p, n0, s_colmap);
     load_chunk(0);
     store_chunk(0);
     __syncthreads();
@@ -121,98 +231,106 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
         __syncthreads();
     }
 
-    // Epilogue: lane holds out[m][n .. n+3] for n = n0 + 16*nt + 4*lg.
-    constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const int m = m0 + wave * 32 + mt * 16 + lr;
-        const bool mlive = m < M;
-        // Values (bias + residual combine) in place. N is a multiple of 4, so a
-        // lane's four columns are all live or all padding: whole float4 accesses.
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const int n = n0 + nt * 16 + lg * 4;
-            const bool live = mlive && n < N;
-            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-            if (live) {
-                const float4 b4 = *(const float4*)(p.bias + n);
-                v = acc[mt][nt] + (f32x4){b4.x, b4.y, b4.z, b4.w};
-                if (EPI == EPI_GELU) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) v[j] = gelu(v[j]);
-                }
-                if (EPI == EPI_RESID || EPI == EPI_RESID_LN || EPI == EPI_HAB || EPI == EPI_HAB_LN) {
-                    const float4 r4 = *(const float4*)(p.res + (size_t)m * p.ldo + n);
-                    v = (f32x4){r4.x, r4.y, r4.z, r4.w} + v;
-                }
-                if (EPI == EPI_HAB || EPI == EPI_HAB_LN) {
-                    const float4 a4 = *(const float4*)(p.aux + (size_t)m * p.ldo + n);
-                    const float4 g4 = *(const float4*)(p.gate + n);
-                    v[0] = v[0] + (a4.x * g4.x) * p.cscale;
-                    v[1] = v[1] + (a4.y * g4.y) * p.cscale;
-                    v[2] = v[2] + (a4.z * g4.z) * p.cscale;
-                    v[3] = v[3] + (a4.w * g4.w) * p.cscale;
-                }
-            }
-            acc[mt][nt] = v;
-        }
-        float mean = 0.0f, rstd = 0.0f;
-        if (LNOUT) {
-            // Row statistics over the 4 lanes that share the row: two-pass mean
-            // then biased variance, as the reference's layer_norm (cpu.rs:563-581).
-            float s = 0.0f;
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) s += acc[mt][nt][j];
-            s += __shfl_xor(s, 16, 64);
-            s += __shfl_xor(s, 32, 64);
-            mean = s / (float)N;
-            float q = 0.0f;
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int n = n0 + nt * 16 + lg * 4 + j;
-                    const float d = n < N ? acc[mt][nt][j] - mean : 0.0f;
-                    q += d * d;
-                }
-            q += __shfl_xor(q, 16, 64);
-            q += __shfl_xor(q, 32, 64);
-            rstd = 1.0f / sqrtf(q / (float)N + p.eps);
-        }
-        if (!mlive) continue;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const int n = n0 + nt * 16 + lg * 4;
-            if (n >= N) continue;
-            const f32x4 v = acc[mt][nt];
-            if (EPI == EPI_QKV) {
-                const int C = p.heads * p.hdim;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int nn = n + j;
-                    if (nn >= N) break;
-                    const int which = nn / C, rem = nn - which * C;
-                    const int hd = rem / p.hdim, dim = rem - hd * p.hdim;
-                    p.out[((size_t)(which * p.heads + hd) * M + m) * p.hdim + dim] = v[j];
-                }
-                continue;
-            }
-            *(float4*)(p.out + (size_t)m * p.ldo + n) = make_float4(v[0], v[1], v[2], v[3]);
-            if (LNOUT) {
-                const float4 w4 = *(const float4*)(p.nw + n);
-                const float4 b4 = *(const float4*)(p.nb + n);
-                *(float4*)(p.xn + (size_t)m * p.ldo + n) =
-                    make_float4((v[0] - mean) * rstd * w4.x + b4.x, (v[1] - mean) * rstd * w4.y + b4.y,
-                                (v[2] - mean) * rstd * w4.z + b4.z, (v[3] - mean) * rstd * w4.w + b4.w);
-            }
-        }
-    }
+    gemm_epilogue<NT, EPI>(p, acc, m0 + wave * 32, n0, lr, lg, s_colmap);
 }
 
 #define GEMM_INST(NAME, NT, EPI)                                                             \
     extern "C" __global__ __launch_bounds__(256) void NAME(GemmArgs p) { gemm_body<NT, EPI>(p); }
+
+// ---------------------------------------------------------------------------
+// Weight-stationary variant for K = 144 (the C = 144 family's qkv, proj and fc1).
+//
+// A block holds the 144 x 144 weight slice of its column block in LDS for the
+// whole kernel and loops over 256-row tiles (persistent: gridDim.x blocks per
+// column slice, gridDim.y slices). Each of the 8 waves owns 32 rows of a tile
+// and streams its A rows from global memory straight into registers - all nine
+// K-chunks of the tile are in flight at once - so the K loop has no barrier
+// and no LDS traffic for A. The MFMA arrangement and the epilogue are the ones
+// of gemm_body (a lane's four accumulators are four consecutive columns).
+#define WS_K 144
+#define WS_KS (WS_K + 4)  // LDS row stride of the weight slice
+#define WS_ROWS 256
+
+template <int EPI>
+__device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
+{
+    constexpr int NT = 9, BN = 144, NCH = WS_K / 16;
+    __shared__ float Wsm[BN * WS_KS];
+    __shared__ int s_colmap[EPI == EPI_QKV ? BN : 1];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int n0 = blockIdx.y * BN;
+    const int M = p.M, N = p.N;
+
+    // The weight slice, once: BN rows x 36 float4.
+    for (int idx = tid; idx < BN * (WS_K / 4); idx += 512) {
+        const int r = idx / (WS_K / 4), c4 = (idx - r * (WS_K / 4)) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (n0 + r < N) v = *(const float4*)(p.w + (size_t)(n0 + r) * p.Kp + c4);
+        *(float4*)(Wsm + r * WS_KS + c4) = v;
+    }
+    build_colmap<BN, EPI>(p, n0, s_colmap);
+    __syncthreads();
+
+    const int ntiles = (M + WS_ROWS - 1) / WS_ROWS;
+    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int mbase = tile * WS_ROWS + wave * 32;
+        const float* arow[2];
+        bool alive[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int m = mbase + mt * 16 + lr;
+            alive[mt] = m < M;
+            arow[mt] = p.a + (size_t)(alive[mt] ? m : 0) * p.lda + lg * 4;
+        }
+        // A operands in three register slots, streamed three chunks ahead of
+        // the MFMAs that use them (the chunk loop is rolled over groups of 3 so
+        // the slots are fixed registers).
+        f32x4 xa[3][2];
+        auto load_a = [&](int slot, int kc) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+                if (alive[mt]) v = *(const f32x4*)(arow[mt] + kc * 16);
+                xa[slot][mt] = v;
+            }
+        };
+#pragma unroll
+        for (int s = 0; s < 3; ++s) load_a(s, s);
+        f32x4 acc[2][NT];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int kg = 0; kg < NCH; kg += 3) {
+#pragma unroll
+            for (int slot = 0; slot < 3; ++slot) {
+                const int kc = kg + slot;
+                f32x4 cur[2] = {xa[slot][0], xa[slot][1]};
+                if (kc + 3 < NCH) load_a(slot, kc + 3);
+                const float* wrow = Wsm + lr * WS_KS + kc * 16 + lg * 4;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const f32x4 wv = *(const f32x4*)(wrow + nt * 16 * WS_KS);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int mt = 0; mt < 2; ++mt)
+                            acc[mt][nt] = mfma16(wv[s], cur[mt][s], acc[mt][nt]);
+                }
+            }
+        }
+        gemm_epilogue<NT, EPI>(p, acc, mbase, n0, lr, lg, s_colmap);
+    }
+}
+
+#define GEMM_WS_INST(NAME, EPI)                                                              \
+    extern "C" __global__ __launch_bounds__(512) void NAME(GemmArgs p) { gemm_ws_body<EPI>(p); }
 
 // NT = 9: 144-wide column blocks (HAT-S: N = 144, 288, 432 divide exactly).
 GEMM_INST(hat_gemm_n9_store, 9, EPI_STORE)
@@ -228,3 +346,10 @@ GEMM_INST(hat_gemm_n12_qkv, 12, EPI_QKV)
 GEMM_INST(hat_gemm_n12_resid, 12, EPI_RESID)
 GEMM_INST(hat_gemm_n12_resid_ln, 12, EPI_RESID_LN)
 GEMM_INST(hat_gemm_n12_hab_ln, 12, EPI_HAB_LN)
+
+// K = 144 weight-stationary instances (HAT-S: qkv N = 432, fc1 N = 288, attention
+// proj and OCAB proj N = 144).
+GEMM_WS_INST(hat_gemmws_qkv, EPI_QKV)
+GEMM_WS_INST(hat_gemmws_gelu, EPI_GELU)
+GEMM_WS_INST(hat_gemmws_resid_ln, EPI_RESID_LN)
+GEMM_WS_INST(hat_gemmws_hab_ln, EPI_HAB_LN)

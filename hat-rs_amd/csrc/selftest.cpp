@@ -207,10 +207,12 @@ int gpu_selftest(std::string* err)
         // LayerNorm epilogues also check the normalised rows they write.
         const int epis[6] = {EPI_STORE, EPI_GELU, EPI_QKV, EPI_RESID, EPI_RESID_LN, EPI_HAB_LN};
         const char* enames[7] = {"store", "gelu", "qkv", "resid", "", "resid_ln", "hab_ln"};
-        for (int C : {144, 180})
-            for (int epi : epis) {
+        // ws: the weight-stationary K = 144 kernel, on 600 rows (three 256-row
+        // tiles, the last one partial) with two blocks per column slice, so one
+        // block walks two tiles.
+        auto gemm_case = [&](int C, int epi, bool ws) {
                 const int heads = 6, hd = C / heads;
-                const int M = 200;  // not a multiple of the 128-row tile
+                const int M = ws ? 600 : 200;  // not a multiple of the row tile
                 const int N = epi == EPI_QKV ? 3 * C : (epi == EPI_GELU ? 2 * C : C);
                 const int K = epi == EPI_RESID ? 2 * C : C;  // RESID at the fc2 shape
                 const bool lnout = epi == EPI_RESID_LN || epi == EPI_HAB_LN;
@@ -245,8 +247,14 @@ int gpu_selftest(std::string* err)
                 p.eps = 1e-5f;
                 const bool n9 = N % 144 == 0;
                 const int BN = n9 ? 144 : 192;
-                std::string k = std::string(n9 ? "hat_gemm_n9_" : "hat_gemm_n12_") + enames[epi];
-                launch(s, k.c_str(), (M + 127) / 128, (N + BN - 1) / BN, 1, 256, p);
+                std::string k;
+                if (ws) {
+                    k = std::string("hat_gemmws_") + enames[epi];
+                    launch(s, k.c_str(), 2, N / 144, 1, 512, p);
+                } else {
+                    k = std::string(n9 ? "hat_gemm_n9_" : "hat_gemm_n12_") + enames[epi];
+                    launch(s, k.c_str(), (M + 127) / 128, (N + BN - 1) / BN, 1, 256, p);
+                }
                 std::vector<double> want((size_t)M * N), wxn((size_t)M * N);
                 for (int m = 0; m < M; ++m) {
                     for (int n = 0; n < N; ++n) {
@@ -276,7 +284,10 @@ int gpu_selftest(std::string* err)
                 check_close(k + " C " + std::to_string(C), dout.get(), want, 3e-5);
                 if (lnout) check_close(k + " C " + std::to_string(C) + " layernorm", dxn.get(), wxn, 5e-5);
                 note(k + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
-            }
+        };
+        for (int C : {144, 180})
+            for (int epi : epis) gemm_case(C, epi, false);
+        for (int epi : {EPI_QKV, EPI_GELU, EPI_RESID_LN, EPI_HAB_LN}) gemm_case(144, epi, true);
 
         // ---- convolutions (all epilogues) on a non-square plane.
         struct CCase { int CI, CO, epi, act, r; const char* what; };

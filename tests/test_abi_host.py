@@ -40,7 +40,7 @@ def _kernel_sources():
         if not fn.endswith(".hip"):
             continue
         src = open(os.path.join(PKG, "csrc", "kernels", fn)).read()
-        names |= set(re.findall(r"^(?:GEMM|CONV|ATTN)_INST\((\w+),", src, flags=re.M))
+        names |= set(re.findall(r"^[A-Z_]+_INST\((\w+),", src, flags=re.M))
         names |= set(re.findall(r'extern "C" __global__[^\n]*?\bvoid (hat_\w+)\(', src))
     return names
 
