@@ -21,6 +21,15 @@ enum GemmEpi : int {
     EPI_HAB_LN = 6,      // EPI_HAB, and xn[m][:] = LayerNorm(out[m][:]) (full rows)
 };
 
+// Weight-stationary K = 144 GEMM launch geometry per epilogue: ws_waves waves
+// per block, each owning ws_mt 16-row MFMA tiles of a ws_rows-row tile. One
+// 16-row tile per wave keeps the plain epilogues at 4 waves per SIMD, so one
+// wave's stores overlap the others' MFMAs; the LayerNorm epilogues need the
+// registers of 2 waves per SIMD.
+constexpr int ws_mt(int /*epi*/) { return 1; }
+constexpr int ws_waves(int epi) { return epi == EPI_RESID_LN || epi == EPI_HAB_LN ? 8 : 16; }
+constexpr int ws_rows(int epi) { return ws_waves(epi) * 16 * ws_mt(epi); }
+
 struct GemmArgs {
     const float* a;      // [M][lda]
     const float* w;      // [N][Kp] row-major, K contiguous, zero-padded to Kp

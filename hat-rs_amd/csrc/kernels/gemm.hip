@@ -40,14 +40,14 @@ __device__ __forceinline__ void build_colmap(const GemmArgs& p, int n0, int* col
 
 // Epilogue shared by both GEMM kernels: lane (lr, lg) holds out[m][n .. n+3]
 // for m = mbase + 16*mt + lr and n = n0 + 16*nt + 4*lg.
-template <int NT, int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[2][NT], int mbase,
+template <int MT, int NT, int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[MT][NT], int mbase,
                                               int n0, int lr, int lg, const int* colmap)
 {
     const int M = p.M, N = p.N;
     constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
         const int m = mbase + mt * 16 + lr;
         const bool mlive = m < M;
         // Values (bias + residual combine) in place. N is a multiple of 4, so a
@@ -111,7 +111,15 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[2]
             if (n >= N) continue;
             const f32x4 v = acc[mt][nt];
             if (EPI == EPI_QKV) {
-                // colmap[n - n0] = ((which*heads + head) << 8) | dim, built per block
+                // colmap[n - n0] = ((which*heads + head) << 8) | dim, built per block.
+                // With hdim % 4 == 0 the four columns n .. n+3 (n % 4 == 0) are one
+                // head's dims d .. d+3, d % 4 == 0: one aligned 16-byte store.
+                if ((p.hdim & 3) == 0) {
+                    const int cm = colmap[n - n0];
+                    *(float4*)(p.out + ((size_t)(cm >> 8) * M + m) * p.hdim + (cm & 255)) =
+                        make_float4(v[0], v[1], v[2], v[3]);
+                    continue;
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int cm = colmap[n - n0 + j];
@@ -231,7 +239,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
         __syncthreads();
     }
 
-    gemm_epilogue<NT, EPI>(p, acc, m0 + wave * 32, n0, lr, lg, s_colmap);
+    gemm_epilogue<2, NT, EPI>(p, acc, m0 + wave * 32, n0, lr, lg, s_colmap);
 }
 
 #define GEMM_INST(NAME, NT, EPI)                                                             \
@@ -241,19 +249,21 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
 // Weight-stationary variant for K = 144 (the C = 144 family's qkv, proj and fc1).
 //
 // A block holds the 144 x 144 weight slice of its column block in LDS for the
-// whole kernel and loops over 256-row tiles (persistent: gridDim.x blocks per
-// column slice, gridDim.y slices). Each of the 8 waves owns 32 rows of a tile
-// and streams its A rows from global memory straight into registers - all nine
-// K-chunks of the tile are in flight at once - so the K loop has no barrier
-// and no LDS traffic for A. The MFMA arrangement and the epilogue are the ones
-// of gemm_body (a lane's four accumulators are four consecutive columns).
+// whole kernel and loops over row tiles (persistent: gridDim.x blocks per
+// column slice, gridDim.y slices). Each of the WAVES waves owns 16*MT rows of
+// a tile and streams its A rows from global memory straight into registers,
+// three K-chunks ahead of the MFMAs, so the K loop has no barrier and no LDS
+// traffic for A; waves drift apart freely, and one wave's epilogue stores
+// overlap the other waves' MFMAs. The MFMA arrangement and the epilogue are
+// the ones of gemm_body (a lane's four accumulators are four consecutive
+// columns).
 #define WS_K 144
 #define WS_KS (WS_K + 4)  // LDS row stride of the weight slice
-#define WS_ROWS 256
 
-template <int EPI>
+template <int EPI, int MT, int WAVES>
 __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 {
+    constexpr int ROWS = WAVES * 16 * MT;  // rows per tile
     constexpr int NT = 9, BN = 144, NCH = WS_K / 16;
     __shared__ float Wsm[BN * WS_KS];
     __shared__ int s_colmap[EPI == EPI_QKV ? BN : 1];
@@ -267,7 +277,7 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
     const int M = p.M, N = p.N;
 
     // The weight slice, once: BN rows x 36 float4.
-    for (int idx = tid; idx < BN * (WS_K / 4); idx += 512) {
+    for (int idx = tid; idx < BN * (WS_K / 4); idx += WAVES * 64) {
         const int r = idx / (WS_K / 4), c4 = (idx - r * (WS_K / 4)) * 4;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (n0 + r < N) v = *(const float4*)(p.w + (size_t)(n0 + r) * p.Kp + c4);
@@ -276,13 +286,13 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
     build_colmap<BN, EPI>(p, n0, s_colmap);
     __syncthreads();
 
-    const int ntiles = (M + WS_ROWS - 1) / WS_ROWS;
+    const int ntiles = (M + ROWS - 1) / ROWS;
     for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int mbase = tile * WS_ROWS + wave * 32;
-        const float* arow[2];
-        bool alive[2];
+        const int mbase = tile * ROWS + wave * 16 * MT;
+        const float* arow[MT];
+        bool alive[MT];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
             const int m = mbase + mt * 16 + lr;
             alive[mt] = m < M;
             arow[mt] = p.a + (size_t)(alive[mt] ? m : 0) * p.lda + lg * 4;
@@ -290,10 +300,10 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         // A operands in three register slots, streamed three chunks ahead of
         // the MFMAs that use them (the chunk loop is rolled over groups of 3 so
         // the slots are fixed registers).
-        f32x4 xa[3][2];
+        f32x4 xa[3][MT];
         auto load_a = [&](int slot, int kc) {
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
+            for (int mt = 0; mt < MT; ++mt) {
                 f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
                 if (alive[mt]) v = *(const f32x4*)(arow[mt] + kc * 16);
                 xa[slot][mt] = v;
@@ -301,7 +311,7 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         };
 #pragma unroll
         for (int s = 0; s < 3; ++s) load_a(s, s);
-        f32x4 acc[2][NT];
+        f32x4 acc[MT][NT];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -311,7 +321,9 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 #pragma unroll
             for (int slot = 0; slot < 3; ++slot) {
                 const int kc = kg + slot;
-                f32x4 cur[2] = {xa[slot][0], xa[slot][1]};
+                f32x4 cur[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) cur[mt] = xa[slot][mt];
                 if (kc + 3 < NCH) load_a(slot, kc + 3);
                 const float* wrow = Wsm + lr * WS_KS + kc * 16 + lg * 4;
 #pragma unroll
@@ -320,17 +332,20 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
 #pragma unroll
-                        for (int mt = 0; mt < 2; ++mt)
+                        for (int mt = 0; mt < MT; ++mt)
                             acc[mt][nt] = mfma16(wv[s], cur[mt][s], acc[mt][nt]);
                 }
             }
         }
-        gemm_epilogue<NT, EPI>(p, acc, mbase, n0, lr, lg, s_colmap);
+        gemm_epilogue<MT, NT, EPI>(p, acc, mbase, n0, lr, lg, s_colmap);
     }
 }
 
 #define GEMM_WS_INST(NAME, EPI)                                                              \
-    extern "C" __global__ __launch_bounds__(512) void NAME(GemmArgs p) { gemm_ws_body<EPI>(p); }
+    extern "C" __global__ __launch_bounds__(ws_waves(EPI) * 64) void NAME(GemmArgs p)          \
+    {                                                                                          \
+        gemm_ws_body<EPI, ws_mt(EPI), ws_waves(EPI)>(p);                                       \
+    }
 
 // NT = 9: 144-wide column blocks (HAT-S: N = 144, 288, 432 divide exactly).
 GEMM_INST(hat_gemm_n9_store, 9, EPI_STORE)

@@ -207,9 +207,9 @@ int gpu_selftest(std::string* err)
         // LayerNorm epilogues also check the normalised rows they write.
         const int epis[6] = {EPI_STORE, EPI_GELU, EPI_QKV, EPI_RESID, EPI_RESID_LN, EPI_HAB_LN};
         const char* enames[7] = {"store", "gelu", "qkv", "resid", "", "resid_ln", "hab_ln"};
-        // ws: the weight-stationary K = 144 kernel, on 600 rows (three 256-row
-        // tiles, the last one partial) with two blocks per column slice, so one
-        // block walks two tiles.
+        // ws: the weight-stationary K = 144 kernel, on 600 rows (3 or 5 row
+        // tiles, the last one partial) with two blocks per column slice, so a
+        // block walks several tiles.
         auto gemm_case = [&](int C, int epi, bool ws) {
                 const int heads = 6, hd = C / heads;
                 const int M = ws ? 600 : 200;  // not a multiple of the row tile
@@ -250,7 +250,7 @@ int gpu_selftest(std::string* err)
                 std::string k;
                 if (ws) {
                     k = std::string("hat_gemmws_") + enames[epi];
-                    launch(s, k.c_str(), 2, N / 144, 1, 512, p);
+                    launch(s, k.c_str(), 2, N / 144, 1, ws_waves(epi) * 64, p);
                 } else {
                     k = std::string(n9 ? "hat_gemm_n9_" : "hat_gemm_n12_") + enames[epi];
                     launch(s, k.c_str(), (M + 127) / 128, (N + BN - 1) / BN, 1, 256, p);
