@@ -149,6 +149,44 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
            256, p);
 }
 
+// The MLP of one block: x_out = res + fc2(gelu(fc1(a))), for EPI_RESID_LN also
+// xn = LayerNorm(x_out). One fused kernel for the C = 144 family (hidden 288),
+// else fc1 and fc2 as two GEMMs through the hidden buffer.
+void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const float* a, long M,
+             const float* res, float* out, int epi, const GemmEpilogue& ln, float* hidden)
+{
+    if (epi != EPI_RESID && epi != EPI_RESID_LN) throw Error("MLP: bad epilogue");
+    if (fc1.K == MLP_C && fc1.Kp == MLP_C && fc1.N == MLP_H && fc2.K == MLP_H && fc2.Kp == MLP_H &&
+        fc2.N == MLP_C) {
+        if (M > 0x7fffffffL) throw Error("MLP: too many rows");
+        MlpArgs p{};
+        p.a = a;
+        p.w1 = fc1.w;
+        p.b1 = fc1.b;
+        p.w2 = fc2.w;
+        p.b2 = fc2.b;
+        p.res = res;
+        p.out = out;
+        p.xn = ln.xn;
+        p.nw = ln.nw;
+        p.nb = ln.nb;
+        p.M = (int)M;
+        p.eps = 1e-5f;
+        // One block per CU (117 KB of LDS), persistent over the 128-row tiles.
+        static const int cus = std::max(1, Runtime::get().cu_count());
+        const long ntiles = (M + MLP_ROWS - 1) / MLP_ROWS;
+        const long rounds = (ntiles + cus - 1) / cus;
+        const long g = std::max(1L, (ntiles + rounds - 1) / rounds);
+        launch(s, epi == EPI_RESID_LN ? "hat_mlp_resid_ln" : "hat_mlp_resid", (unsigned)g, 1, 1,
+               MLP_WAVES * 64, p);
+        return;
+    }
+    GemmEpilogue e = ln;
+    e.res = res;
+    run_gemm(s, fc1, a, fc1.K, M, hidden, fc1.N, EPI_GELU, GemmEpilogue{}, 0, 0, 0.f);
+    run_gemm(s, fc2, hidden, fc1.N, M, out, fc2.N, epi, e, 0, 0, 0.f);
+}
+
 // The channel-attention gate from the CAB conv's per-tile column sums:
 // reduce in fixed row blocks, then squeeze-excite.
 void run_se(hipStream_t s, const float* partial, int nblk, int C, float* red, float count,
@@ -453,6 +491,19 @@ void GpuBackend::gemm(const DevLinear& L, const float* a, int lda, long M, float
     run_gemm(stream_, L, a, lda, M, out, ldo, epi, e, wt_.heads, wt_.head_dim, wt_.conv_scale);
 }
 
+// x = x + fc2(gelu(fc1(xn_))), in place; with a norm also xn_ = norm(x).
+void GpuBackend::mlp(const std::string& prefix, float* x, int epi, const std::string& norm)
+{
+    GemmEpilogue e;
+    if (!norm.empty()) {
+        e.xn = xn_;
+        e.nw = raw_.at(norm + ".weight");
+        e.nb = raw_.at(norm + ".bias");
+    }
+    run_mlp(stream_, lin_.at(prefix + ".fc1"), lin_.at(prefix + ".fc2"), xn_, plan_.tokens(), x, x, epi,
+            e, hidden_);
+}
+
 void GpuBackend::conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
                       int co_stride, int epi, int act, const float* res, float* partial,
                       int crop_h, int crop_w)
@@ -491,9 +542,7 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
     attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0);
     gemm(lin_.at(p + ".attn.proj"), ao_, C, T, x_out, C, EPI_HAB_LN, x_in, t2_, gate_, xn_,
          p + ".norm2");
-    gemm(lin_.at(p + ".mlp.fc1"), xn_, C, T, hidden_, C * wt_.mlp_ratio, EPI_GELU);
-    gemm(lin_.at(p + ".mlp.fc2"), hidden_, C * wt_.mlp_ratio, T, x_out, C, EPI_RESID_LN, x_out,
-         nullptr, nullptr, xn_, next_norm);
+    mlp(p + ".mlp", x_out, EPI_RESID_LN, next_norm);
 }
 
 // OCAB.forward (hat_arch.py:392-438; cpu.rs:1170-1198): x = proj(attn) + x;
@@ -507,8 +556,7 @@ void GpuBackend::ocab(int stage, float* x)
     attention(p + ".relative_position_bias_table", true, 0);
     gemm(lin_.at(p + ".proj"), ao_, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, xn_,
          p + ".norm2");
-    gemm(lin_.at(p + ".mlp.fc1"), xn_, C, T, hidden_, C * wt_.mlp_ratio, EPI_GELU);
-    gemm(lin_.at(p + ".mlp.fc2"), hidden_, C * wt_.mlp_ratio, T, x, C, EPI_RESID, x);
+    mlp(p + ".mlp", x, EPI_RESID, "");
 }
 
 // forward_planes (gpu.rs:714-748; cpu.rs:1318-1368) with Pre::adjust and finish
@@ -691,17 +739,14 @@ void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int m
         resid_ln.xn = dxn.p;
         resid_ln.nw = d2w.p;
         resid_ln.nb = d2b.p;
-        GemmEpilogue resid;
-        resid.res = dwork.p;
         // The backend's OCAB sequence: norm1, qkv, attention, proj + shortcut
-        // (whose epilogue also writes norm2), GELU fc1, fc2 + residual.
+        // (whose epilogue also writes norm2), then the MLP + residual.
         auto run = [&]() {
             run_ln(s, dx.p, dxn.p, d1w.p, d1b.p, (long)T, c);
             run_gemm(s, qkv.L, dxn.p, c, (long)T, dq.p, 0, EPI_QKV, none, heads, D, 0.f);
             run_attn(s, dq.p, dtab.p, dao.p, pl, heads, D, true, 0);
             run_gemm(s, proj.L, dao.p, c, (long)T, dwork.p, c, EPI_RESID_LN, resid_ln, heads, D, 0.f);
-            run_gemm(s, fc1.L, dxn.p, c, (long)T, dh.p, (int)hid, EPI_GELU, none, heads, D, 0.f);
-            run_gemm(s, fc2.L, dh.p, (int)hid, (long)T, dwork.p, c, EPI_RESID, resid, heads, D, 0.f);
+            run_mlp(s, fc1.L, fc2.L, dxn.p, (long)T, dwork.p, dwork.p, EPI_RESID, none, dh.p);
         };
         run();
         rt.check(api.StreamSynchronize(s), "ocab");

@@ -4,4 +4,5 @@
 #include "attn.hip"
 #include "conv.hip"
 #include "gemm.hip"
+#include "mlp.hip"
 #include "misc.hip"

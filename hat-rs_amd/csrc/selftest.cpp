@@ -289,6 +289,57 @@ int gpu_selftest(std::string* err)
             for (int epi : epis) gemm_case(C, epi, false);
         for (int epi : {EPI_QKV, EPI_GELU, EPI_RESID_LN, EPI_HAB_LN}) gemm_case(144, epi, true);
 
+        // ---- fused MLP (C = 144, hidden 288), in place as the backend runs it:
+        // out aliases the residual, the LayerNorm output aliases the input.
+        // 600 rows = 5 tiles of 128 (the last partial) over 2 blocks.
+        for (int epi : {EPI_RESID, EPI_RESID_LN}) {
+            const int M = 600, C = MLP_C, H = MLP_H;
+            std::vector<float> a = rng.vec((size_t)M * C, 1.0f), w1 = rng.vec((size_t)H * C, 0.08f),
+                               b1 = rng.vec(H, 0.1f), w2 = rng.vec((size_t)C * H, 0.06f), b2 = rng.vec(C, 0.1f),
+                               res = rng.vec((size_t)M * C, 1.0f), nw = rng.vec(C, 1.0f), nb = rng.vec(C, 0.1f);
+            int K1 = 0, K2 = 0;
+            std::vector<float> p1 = pack_linear(w1.data(), H, C, &K1), p2 = pack_linear(w2.data(), C, H, &K2);
+            Dev da(a), dw1(p1), db1(b1), dw2(p2), db2(b2), dx(res), dnw(nw), dnb(nb);
+            MlpArgs p{};
+            p.a = da.p;
+            p.w1 = dw1.p;
+            p.b1 = db1.p;
+            p.w2 = dw2.p;
+            p.b2 = db2.p;
+            p.res = dx.p;
+            p.out = dx.p;
+            p.xn = epi == EPI_RESID_LN ? da.p : nullptr;
+            p.nw = dnw.p;
+            p.nb = dnb.p;
+            p.M = M;
+            p.eps = 1e-5f;
+            const char* k = epi == EPI_RESID_LN ? "hat_mlp_resid_ln" : "hat_mlp_resid";
+            launch(s, k, 2, 1, 1, MLP_WAVES * 64, p);
+            std::vector<double> want((size_t)M * C), wxn((size_t)M * C), hid(H);
+            for (int m = 0; m < M; ++m) {
+                for (int j = 0; j < H; ++j) {
+                    double v = b1[j];
+                    for (int c = 0; c < C; ++c) v += (double)a[(size_t)m * C + c] * w1[(size_t)j * C + c];
+                    hid[j] = gelu_d(v);
+                }
+                double mean = 0, var = 0;
+                for (int n = 0; n < C; ++n) {
+                    double v = b2[n];
+                    for (int j = 0; j < H; ++j) v += hid[j] * w2[(size_t)n * H + j];
+                    want[(size_t)m * C + n] = res[(size_t)m * C + n] + v;
+                    mean += want[(size_t)m * C + n];
+                }
+                mean /= C;
+                for (int n = 0; n < C; ++n) var += (want[(size_t)m * C + n] - mean) * (want[(size_t)m * C + n] - mean);
+                var /= C;
+                for (int n = 0; n < C; ++n)
+                    wxn[(size_t)m * C + n] = (want[(size_t)m * C + n] - mean) / std::sqrt(var + 1e-5) * nw[n] + nb[n];
+            }
+            check_close(std::string(k), dx.get(), want, 5e-5);
+            if (epi == EPI_RESID_LN) check_close(std::string(k) + " layernorm", da.get(), wxn, 5e-5);
+            note(std::string(k) + " M 600 (in place)");
+        }
+
         // ---- convolutions (all epilogues) on a non-square plane.
         struct CCase { int CI, CO, epi, act, r; const char* what; };
         const CCase cases[] = {
