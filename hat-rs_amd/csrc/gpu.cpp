@@ -53,6 +53,16 @@ std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int
     return out;
 }
 
+std::vector<float> pack_cab_conv1(const float* w)
+{
+    std::vector<float> out((size_t)64 * CAB_C, 0.0f);
+    for (int co = 0; co < CAB_CC; ++co)
+        for (int ci = 0; ci < CAB_C; ++ci)
+            for (int tap = 0; tap < 9; ++tap)
+                out[(size_t)(tap * CAB_CC + co) * CAB_C + ci] = w[((size_t)co * CAB_C + ci) * 9 + tap];
+    return out;
+}
+
 // ---------------------------------------------------------------------------
 // Launch helpers shared by the backend and the op entry points.
 
@@ -185,6 +195,75 @@ void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const fl
     e.res = res;
     run_gemm(s, fc1, a, fc1.K, M, hidden, fc1.N, EPI_GELU, GemmEpilogue{}, 0, 0, 0.f);
     run_gemm(s, fc2, hidden, fc1.N, M, out, fc2.N, epi, e, 0, 0, 0.f);
+}
+
+// Folded CAB, first half: t1 = gelu(conv1(xn)) with its per-tile sums, then
+// the gate and the gate-scaled conv2 weights (w2g) and combined bias (bias2 =
+// bproj + cscale * gate * b2) for the projection GEMM.
+void run_cab(hipStream_t s, const DevCab& cb, const float* xn, int H, int W, const float* bproj,
+             float cscale, int sq, float* t1, float* partial, float* w2g, float* bias2, float* gate)
+{
+    if (H % 16 != 0 || W % 16 != 0 || H < 16 || W < 16) throw Error("CAB: plane must be 16-aligned");
+    if (sq < 1 || sq > 64) throw Error("CAB: squeeze width must be 1..64");
+    const int tiles = (H / 16) * (W / 16);
+    static const int cus = std::max(1, Runtime::get().cu_count());
+    CabConvArgs a{xn, cb.w1, cb.b1, t1, partial, H, W};
+    // Two blocks per CU (73 KB of LDS each), persistent over the 16 x 16 tiles.
+    launch(s, "hat_cab_conv1", (unsigned)std::min(tiles, 2 * cus), 1, 1, 256, a);
+    CabGateArgs g{};
+    g.partial = partial;
+    g.t1 = t1;
+    g.tiles = tiles;
+    g.H = H;
+    g.W = W;
+    g.w2 = cb.w2;
+    g.b2 = cb.b2;
+    g.wa = cb.wa;
+    g.ba = cb.ba;
+    g.wb = cb.wb;
+    g.bb = cb.bb;
+    g.bproj = bproj;
+    g.w2g = w2g;
+    g.bias2 = bias2;
+    g.gate = gate;
+    g.cscale = cscale;
+    g.sq = sq;
+    launch(s, "hat_cab_gate", 1, 1, 1, 1024, g);
+}
+
+// Folded CAB, second half: out = res + a . proj^T + conv2-segment + bias2,
+// xn = LayerNorm(out) (norm2).
+void run_proj_cab(hipStream_t s, const DevLinear& L, const float* a, long M, float* out,
+                  const float* res, float* xn, const float* nw, const float* nb, const float* bias2,
+                  const float* t1, const float* w2g, int H, int W)
+{
+    if (L.K != CAB_C || L.Kp != CAB_C || L.N != CAB_C) throw Error("CAB projection: needs 144 x 144");
+    if ((long)H * W != M) throw Error("CAB projection: rows must be the H x W plane");
+    GemmArgs p{};
+    p.a = a;
+    p.w = L.w;
+    p.bias = bias2;
+    p.out = out;
+    p.res = res;
+    p.xn = xn;
+    p.nw = nw;
+    p.nb = nb;
+    p.M = (int)M;
+    p.N = L.N;
+    p.K = L.K;
+    p.Kp = L.Kp;
+    p.lda = CAB_C;
+    p.ldo = CAB_C;
+    p.eps = 1e-5f;
+    p.t1 = t1;
+    p.w2g = w2g;
+    p.H = H;
+    p.W = W;
+    static const int cus = std::max(1, Runtime::get().cu_count());
+    const long ntiles = (M + ws_rows(EPI_RESID_LN) - 1) / ws_rows(EPI_RESID_LN);
+    const long rounds = (ntiles + cus - 1) / cus;
+    const long g = std::max(1L, (ntiles + rounds - 1) / rounds);
+    launch(s, "hat_gemmws_cab_ln", (unsigned)g, 1, 1, ws_waves(EPI_RESID_LN) * 64, p);
 }
 
 // The channel-attention gate from the CAB conv's per-tile column sums:
@@ -359,6 +438,7 @@ GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
     if (wt.head_feat % 4 != 0) throw Error("head width must be a multiple of 4");
     for (int d : wt.depths)
         if (d < 1) throw Error("every stage needs at least one HAB");
+    cab_fold_ = wt.embed == CAB_C && wt.compressed == CAB_CC;
     rt.check(rt.api().StreamCreate(&stream_), "hipStreamCreate");
     upload_conv("conv_first");
     upload_raw("patch_embed.norm.weight");
@@ -378,8 +458,24 @@ GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
             upload_linear(p + ".attn.proj");
             upload_linear(p + ".mlp.fc1");
             upload_linear(p + ".mlp.fc2");
-            upload_conv(p + ".conv_block.cab.0");
-            upload_conv(p + ".conv_block.cab.2");
+            if (cab_fold_) {
+                const std::string c = p + ".conv_block.cab.";
+                for (const char* n : {"0.bias", "2.weight", "2.bias"}) upload_raw(c + n);
+                std::vector<float> w1 = pack_cab_conv1(wt.t(c + "0.weight"));
+                DevCab cb;
+                cb.w1 = upload(w1.data(), w1.size());
+                cb.b1 = raw_.at(c + "0.bias");
+                cb.w2 = raw_.at(c + "2.weight");
+                cb.b2 = raw_.at(c + "2.bias");
+                cb.wa = raw_.at(c + "3.attention.1.weight");
+                cb.ba = raw_.at(c + "3.attention.1.bias");
+                cb.wb = raw_.at(c + "3.attention.3.weight");
+                cb.bb = raw_.at(c + "3.attention.3.bias");
+                cab_[p] = cb;
+            } else {
+                upload_conv(p + ".conv_block.cab.0");
+                upload_conv(p + ".conv_block.cab.2");
+            }
         }
         const std::string p = L + ".residual_group.overlap_attn";
         for (const char* n : {".norm1.weight", ".norm1.bias", ".norm2.weight", ".norm2.bias",
@@ -446,9 +542,15 @@ void GpuBackend::ensure_plan(int h, int w)
     xb_ = A(T * C);
     xn_ = A(T * C);
     t1_ = A(T * t1_stride_);
-    t2_ = A(T * C);
-    partial_ = A((size_t)nblk_conv2_ * C);
-    red_ = A((size_t)((nblk_conv2_ + 31) / 32) * C);
+    if (cab_fold_) {
+        cab_part_ = A((size_t)(p.hp / 16) * (p.wp / 16) * CAB_NSUM * CAB_CS);
+        w2g_ = A((size_t)C * CAB_K2);
+        bias2_ = A(C);
+    } else {
+        t2_ = A(T * C);
+        partial_ = A((size_t)nblk_conv2_ * C);
+        red_ = A((size_t)((nblk_conv2_ + 31) / 32) * C);
+    }
     gate_ = A(C);
     qkv_ = A(3 * T * C);
     ao_ = A(T * C);
@@ -527,6 +629,18 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
                           std::to_string(block);
     const long T = plan_.tokens();
     const int C = wt_.embed, H = plan_.hp, W = plan_.wp;
+    if (cab_fold_) {
+        // CAB, folded: conv1 + GELU and the gate here; conv2 runs inside proj.
+        const DevLinear& proj = lin_.at(p + ".attn.proj");
+        run_cab(stream_, cab_.at(p), xn_, H, W, proj.b, wt_.conv_scale, wt_.squeezed, t1_, cab_part_,
+                w2g_, bias2_, gate_);
+        gemm(lin_.at(p + ".attn.qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
+        attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0);
+        run_proj_cab(stream_, proj, ao_, T, x_out, x_in, xn_, raw_.at(p + ".norm2.weight"),
+                     raw_.at(p + ".norm2.bias"), bias2_, t1_, w2g_, H, W);
+        mlp(p + ".mlp", x_out, EPI_RESID_LN, next_norm);
+        return;
+    }
     // CAB: conv3x3 -> GELU -> conv3x3 (+ per-tile channel sums) -> gate.
     conv(conv_.at(p + ".conv_block.cab.0"), xn_, C, H, W, t1_, t1_stride_, CEPI_STORE, 1);
     conv(conv_.at(p + ".conv_block.cab.2"), t1_, t1_stride_, H, W, t2_, C, CEPI_COLSUM, 0, nullptr,

@@ -28,6 +28,23 @@ struct DevLinear {
     int N = 0, K = 0, Kp = 0;
 };
 
+// The CAB of the compress-to-6 family, in the folded form (conv1 per-tap
+// weights; conv2 and the channel attention as raw tensors for the gate kernel).
+struct DevCab {
+    float* w1 = nullptr;  // [64][144], row tap*6 + co
+    float* b1 = nullptr;  // [6]
+    float* w2 = nullptr;  // [144][6][3][3]
+    float* b2 = nullptr;  // [144]
+    float* wa = nullptr;  // [sq][144]
+    float* ba = nullptr;
+    float* wb = nullptr;  // [144][sq]
+    float* bb = nullptr;
+};
+
+// conv1 weight [6][144][3][3] -> [64][144]: row tap*6 + co holds w[co][:][tap],
+// rows 54..63 zero.
+std::vector<float> pack_cab_conv1(const float* w);
+
 struct DevConv {
     float* w = nullptr;  // [CIp/16][9][COp][16]
     float* b = nullptr;  // [COp]
@@ -57,6 +74,8 @@ private:
     std::map<std::string, float*> raw_;
     std::map<std::string, DevLinear> lin_;
     std::map<std::string, DevConv> conv_;
+    std::map<std::string, DevCab> cab_;
+    bool cab_fold_ = false;  // the C = 144, 6-channel CAB runs folded
     std::vector<void*> owned_;
     size_t weight_bytes_ = 0;
 
@@ -70,6 +89,7 @@ private:
           *qkv_ = nullptr,
           *ao_ = nullptr, *hidden_ = nullptr, *head0_ = nullptr, *head1_ = nullptr,
           *din_ = nullptr, *dout_ = nullptr;
+    float *cab_part_ = nullptr, *w2g_ = nullptr, *bias2_ = nullptr;
     int t1_stride_ = 0, nblk_conv2_ = 0;
 
     float* upload(const float* src, size_t n);

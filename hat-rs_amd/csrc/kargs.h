@@ -47,6 +47,47 @@ struct GemmArgs {
     int heads, hdim;     // EPI_QKV geometry (N = 3 * heads * hdim)
     float cscale;        // EPI_HAB* conv scale
     float eps;           // LayerNorm eps
+    // hat_gemmws_cab_ln only: the CAB's second conv as an extra K segment,
+    // A = 3x3 neighbourhood of t1 on the H x W plane, W = w2g [144][CAB_K2].
+    const float* t1;     // [H*W][CAB_CS]
+    const float* w2g;    // [N][CAB_K2]
+    int H, W;
+};
+
+// CAB of the compress-to-6 family (HAT-S: 144 -> 6 -> 144), restated by the
+// linearity of its second conv: conv2 becomes a K segment of the attention
+// projection GEMM and its pixel mean comes from per-tile sums of conv1's output.
+#define CAB_C 144
+#define CAB_CC 6             // compressed channels
+#define CAB_CS 8             // t1 channel stride (channels 6, 7 are zero)
+#define CAB_K2 80            // 9 taps x 8 channel slots, padded to 5 x 16
+#define CAB_NSUM 5           // per-tile sums: whole tile, row 0, row H-1, col 0, col W-1
+
+struct CabConvArgs {
+    const float* xn;     // [H*W][144]
+    const float* w;      // [64][144]: row tap*6 + co = conv1 weight[co][:][tap]; rows 54.. zero
+    const float* bias;   // [6]
+    float* t1;           // [H*W][8]: gelu(conv1(xn))
+    float* partial;      // [CAB_NSUM * 8][tiles] (value-major)
+    int H, W;            // multiples of 16
+};
+
+struct CabGateArgs {
+    const float* partial;  // [CAB_NSUM * 8][tiles] (value-major)
+    const float* t1;       // corner pixels
+    int tiles, H, W;
+    const float* w2;     // conv2 weight [144][6][3][3]
+    const float* b2;     // [144]
+    const float* wa;     // channel attention squeeze [sq][144]
+    const float* ba;     // [sq]
+    const float* wb;     // excite [144][sq]
+    const float* bb;     // [144]
+    const float* bproj;  // attention projection bias [144]
+    float* w2g;          // out: cscale * gate[c] * conv2 weight, [144][CAB_K2] (k = tap*8 + ci)
+    float* bias2;        // out: bproj + cscale * gate * b2, [144]
+    float* gate;         // out: the gate itself [144]
+    float cscale;
+    int sq;
 };
 
 // Implicit-GEMM 3x3 convolution, stride 1, zero padding 1, NHWC.

@@ -1,0 +1,220 @@
+// The channel-attention block (CAB) of the compress-to-6 family (HAT-S):
+//   CAB(x) = gate * conv2(gelu(conv1(x))),  gate = sigmoid(Wb relu(Wa mean_p conv2(..) + ba) + bb)
+// (hat_arch.py CAB / ChannelAttention; cpu.rs cab, 1090-1120; the reference's
+// GPU path runs it as lg_conv3x3 x2, a column mean and the squeeze-excite,
+// src/cuda.rs:171-183, 201-214).
+//
+// conv2 is linear, so two of its three uses need no conv2 output at all:
+//   * its pixel mean is b2 + (1/HW) sum_{tap,ci} w2[c][ci][tap] * S[tap][ci],
+//     S[tap][ci] = sum of t1[.][ci] over the plane shifted by the tap (zero
+//     padding): the whole-plane sum minus the row / column the shift pushes out,
+//     plus the corner counted twice. hat_cab_conv1 leaves per-tile sums of t1
+//     over the tile and over its pixels on the four border lines;
+//   * gate[c] * conv2(t1)[p][c] * cscale is a GEMM of the 3x3 neighbourhood of
+//     t1 at p (9 taps x 8 channel slots) with weights cscale * gate[c] * w2 -
+//     hat_cab_gate folds them, and the attention projection GEMM
+//     (hat_gemmws_cab_ln) runs them as 80 more K.
+// So conv2's T x 144 output is never written or read back.
+#include "common.h"
+
+using namespace hatk;
+
+// ---------------------------------------------------------------------------
+// conv1 (144 -> 6, 3x3, zero padding) + GELU, one 16 x 16 output tile at a time.
+//
+// Per-tap products: for each pixel q of the tile's 18 x 18 halo, P[q][tap*6+co]
+// = sum_ci xn[q][ci] * w[co][ci][tap] is a 144-deep product with 54 (padded to
+// 64) outputs - one MFMA row tile of 16 halo pixels x 4 column tiles. The conv
+// output at p is then sum over the 9 taps of P[p + d(tap)][tap*6 + co], read
+// from LDS. The weights (64 x 144) stay in registers for the whole kernel, so a
+// block streams its tiles with no weight traffic; two blocks share a CU.
+#define CC1_HS 18                       // halo side
+#define CC1_HP (CC1_HS * CC1_HS)        // 324 halo pixels
+#define CC1_RT ((CC1_HP + 15) / 16)     // 21 row tiles of 16 pixels
+#define CC1_PS 56                       // LDS row stride of P (54 used)
+
+extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p)
+{
+    __shared__ float Ps[CC1_HP * CC1_PS];
+    __shared__ float red[4][CAB_NSUM * CAB_CC];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int H = p.H, W = p.W;
+    const int ntx = W / 16;
+    const int ntiles = ntx * (H / 16);
+
+    f32x4 wreg[4][CAB_C / 16];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int kc = 0; kc < CAB_C / 16; ++kc)
+            wreg[nt][kc] = *(const f32x4*)(p.w + (nt * 16 + lr) * CAB_C + kc * 16 + lg * 4);
+    float bias[CAB_CC];
+#pragma unroll
+    for (int co = 0; co < CAB_CC; ++co) bias[co] = p.bias[co];
+
+    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int ty = tile / ntx, tx = tile - ty * ntx;
+        const int y0 = ty * 16, x0 = tx * 16;
+
+        for (int rt = wave; rt < CC1_RT; rt += 4) {
+            const int hi = rt * 16 + lr;
+            const int hy = hi / CC1_HS, hx = hi - hy * CC1_HS;
+            const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
+            const bool valid = hi < CC1_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
+            const float* src = p.xn + (size_t)(valid ? gy * W + gx : 0) * CAB_C + lg * 4;
+            f32x4 a[CAB_C / 16];
+#pragma unroll
+            for (int kc = 0; kc < CAB_C / 16; ++kc) {
+                f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+                if (valid) v = *(const f32x4*)(src + kc * 16);
+                a[kc] = v;
+            }
+            f32x4 acc[4];
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) acc[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < CAB_C / 16; ++kc)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16(wreg[nt][kc][s], a[kc][s], acc[nt]);
+            // lane (lr, lg) holds P[hi][16nt + 4lg .. +3]; columns 56.. are not stored
+            if (hi < CC1_HP) {
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt)
+                    if (nt * 16 + lg * 4 < CC1_PS) *(f32x4*)(Ps + hi * CC1_PS + nt * 16 + lg * 4) = acc[nt];
+            }
+        }
+        __syncthreads();
+
+        // One output pixel per thread: the 9 taps from the halo products.
+        const int oy = tid >> 4, ox = tid & 15;
+        float v[CAB_CC];
+#pragma unroll
+        for (int co = 0; co < CAB_CC; ++co) v[co] = bias[co];
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                const float* q = Ps + ((oy + ky) * CC1_HS + ox + kx) * CC1_PS + (ky * 3 + kx) * CAB_CC;
+#pragma unroll
+                for (int j = 0; j < CAB_CC / 2; ++j) {
+                    const float2 t = *(const float2*)(q + 2 * j);
+                    v[2 * j] += t.x;
+                    v[2 * j + 1] += t.y;
+                }
+            }
+#pragma unroll
+        for (int co = 0; co < CAB_CC; ++co) v[co] = gelu(v[co]);
+        const int gy = y0 + oy, gx = x0 + ox;
+        float* dst = p.t1 + ((size_t)gy * W + gx) * CAB_CS;
+        *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4*)(dst + 4) = make_float4(v[4], v[5], 0.f, 0.f);
+
+        // Per-tile sums: the tile, and its pixels on row 0, row H-1, col 0, col W-1.
+        const bool line[CAB_NSUM] = {true, gy == 0, gy == H - 1, gx == 0, gx == W - 1};
+#pragma unroll
+        for (int l = 0; l < CAB_NSUM; ++l)
+#pragma unroll
+            for (int co = 0; co < CAB_CC; ++co) {
+                const float s = wave_sum(line[l] ? v[co] : 0.0f);
+                if (lane == 0) red[wave][l * CAB_CC + co] = s;
+            }
+        __syncthreads();
+        if (tid < CAB_NSUM * CAB_CS) {
+            const int l = tid / CAB_CS, co = tid - l * CAB_CS;
+            float s = 0.0f;
+            if (co < CAB_CC) {
+                const int i = l * CAB_CC + co;
+                s = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
+            }
+            p.partial[(size_t)tid * ntiles + tile] = s;  // value-major: [40][tiles]
+        }
+        // The next tile's P stores come after this barrier; every read of Ps
+        // and red above precedes it.
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The gate, and conv2 folded with it: one block of 16 waves. Every reduction
+// is a fixed-order per-lane sum followed by a fixed shuffle tree, so the
+// result does not depend on timing.
+#define CG_WAVES 16
+
+extern "C" __global__ __launch_bounds__(CG_WAVES * 64) void hat_cab_gate(CabGateArgs p)
+{
+    constexpr int NV = CAB_NSUM * CAB_CS;  // 40 sums per tile
+    __shared__ float s_sum[NV];
+    __shared__ float s_S[9 * CAB_CC];
+    __shared__ float s_mean[CAB_C];
+    __shared__ float s_z[64];
+    __shared__ float s_gate[CAB_C];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+
+    // Tile sums: partial is value-major, so a wave reads 64 tiles per load.
+    for (int v = wave; v < NV; v += CG_WAVES) {
+        const float* src = p.partial + (size_t)v * p.tiles;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int t = lane; t < p.tiles; t += 64) acc += src[t];
+        acc = wave_sum(acc);
+        if (lane == 0) s_sum[v] = acc;
+    }
+    __syncthreads();
+    const int H = p.H, W = p.W;
+    if (tid < 9 * CAB_CC) {
+        const int tap = tid / CAB_CC, ci = tid - tap * CAB_CC;
+        const int dy = tap / 3 - 1, dx = tap % 3 - 1;
+        float s = s_sum[0 * CAB_CS + ci];
+        if (dy == 1) s -= s_sum[1 * CAB_CS + ci];   // source rows 1 .. H-1: row 0 is out
+        if (dy == -1) s -= s_sum[2 * CAB_CS + ci];  // rows 0 .. H-2: row H-1 is out
+        if (dx == 1) s -= s_sum[3 * CAB_CS + ci];
+        if (dx == -1) s -= s_sum[4 * CAB_CS + ci];
+        if (dy != 0 && dx != 0)  // the corner both lines removed
+            s += p.t1[((size_t)(dy == 1 ? 0 : H - 1) * W + (dx == 1 ? 0 : W - 1)) * CAB_CS + ci];
+        s_S[tid] = s;
+    }
+    __syncthreads();
+    const float inv = 1.0f / ((float)H * (float)W);
+    if (tid < CAB_C) {
+        const int c = tid;
+        float acc = 0.0f;
+#pragma unroll
+        for (int ci = 0; ci < CAB_CC; ++ci)
+#pragma unroll
+            for (int tap = 0; tap < 9; ++tap) acc += p.w2[(c * CAB_CC + ci) * 9 + tap] * s_S[tap * CAB_CC + ci];
+        s_mean[c] = p.b2[c] + acc * inv;
+    }
+    __syncthreads();
+    for (int j = wave; j < p.sq; j += CG_WAVES) {
+        float acc = 0.0f;
+        for (int c = lane; c < CAB_C; c += 64) acc += s_mean[c] * p.wa[j * CAB_C + c];
+        acc = wave_sum(acc) + p.ba[j];
+        if (lane == 0) s_z[j] = acc < 0.0f ? 0.0f : acc;
+    }
+    __syncthreads();
+    if (tid < CAB_C) {
+        const int c = tid;
+        float acc = p.bb[c];
+        for (int j = 0; j < p.sq; ++j) acc += s_z[j] * p.wb[c * p.sq + j];
+        const float g = 1.0f / (1.0f + __expf(-acc));
+        s_gate[c] = g;
+        p.gate[c] = g;
+        p.bias2[c] = p.bproj[c] + (p.cscale * g) * p.b2[c];
+    }
+    __syncthreads();
+    for (int i = tid; i < CAB_C * CAB_K2; i += CG_WAVES * 64) {
+        const int c = i / CAB_K2, k = i - c * CAB_K2;
+        const int tap = k / CAB_CS, ci = k - tap * CAB_CS;
+        float v = 0.0f;
+        if (tap < 9 && ci < CAB_CC) v = (p.cscale * s_gate[c]) * p.w2[(c * CAB_CC + ci) * 9 + tap];
+        p.w2g[i] = v;
+    }
+}

@@ -260,12 +260,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
 #define WS_K 144
 #define WS_KS (WS_K + 4)  // LDS row stride of the weight slice
 
-template <int EPI, int MT, int WAVES>
+template <int EPI, int MT, int WAVES, bool CAB>
 __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 {
     constexpr int ROWS = WAVES * 16 * MT;  // rows per tile
     constexpr int NT = 9, BN = 144, NCH = WS_K / 16;
+    constexpr int S2 = CAB_K2 + 4;         // LDS row stride of the conv2 slice
     __shared__ float Wsm[BN * WS_KS];
+    __shared__ float W2s[CAB ? BN * S2 : 1];
     __shared__ int s_colmap[EPI == EPI_QKV ? BN : 1];
 
     const int tid = threadIdx.x;
@@ -282,6 +284,14 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (n0 + r < N) v = *(const float4*)(p.w + (size_t)(n0 + r) * p.Kp + c4);
         *(float4*)(Wsm + r * WS_KS + c4) = v;
+    }
+    if (CAB) {
+        for (int idx = tid; idx < BN * (CAB_K2 / 4); idx += WAVES * 64) {
+            const int r = idx / (CAB_K2 / 4), c4 = (idx - r * (CAB_K2 / 4)) * 4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (n0 + r < N) v = *(const float4*)(p.w2g + (size_t)(n0 + r) * CAB_K2 + c4);
+            *(float4*)(W2s + r * S2 + c4) = v;
+        }
     }
     build_colmap<BN, EPI>(p, n0, s_colmap);
     __syncthreads();
@@ -311,9 +321,28 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         };
 #pragma unroll
         for (int s = 0; s < 3; ++s) load_a(s, s);
+        // CAB: the 3x3 neighbourhood of t1 at each row's pixel, k = tap*8 + ci;
+        // chunk kc2 holds taps 2*kc2 (lane groups 0, 1) and 2*kc2 + 1 (2, 3).
+        f32x4 xg[CAB ? MT : 1][CAB_K2 / 16];
+        if (CAB) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = mbase + mt * 16 + lr;
+                const int y = m / p.W, x = m - y * p.W;
+#pragma unroll
+                for (int kc2 = 0; kc2 < CAB_K2 / 16; ++kc2) {
+                    const int tap = 2 * kc2 + (lg >> 1), ci0 = (lg & 1) * 4;
+                    const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
+                    f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    if (alive[mt] && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W)
+                        v = *(const f32x4*)(p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci0);
+                    xg[mt][kc2] = v;
+                }
+            }
+        }
         f32x4 acc[MT][NT];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
@@ -337,6 +366,24 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 }
             }
         }
+        if (CAB) {
+#pragma unroll
+            for (int kc2 = 0; kc2 < CAB_K2 / 16; ++kc2) {
+                // keep each chunk's weight reads next to its MFMAs (hoisting
+                // all five chunks' reads costs more registers than there are)
+                __builtin_amdgcn_sched_barrier(0);
+                const float* wrow = W2s + lr * S2 + kc2 * 16 + lg * 4;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const f32x4 wv = *(const f32x4*)(wrow + nt * 16 * S2);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            acc[mt][nt] = mfma16(wv[s], xg[mt][kc2][s], acc[mt][nt]);
+                }
+            }
+        }
         gemm_epilogue<MT, NT, EPI>(p, acc, mbase, n0, lr, lg, s_colmap);
     }
 }
@@ -344,7 +391,7 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 #define GEMM_WS_INST(NAME, EPI)                                                              \
     extern "C" __global__ __launch_bounds__(ws_waves(EPI) * 64) void NAME(GemmArgs p)          \
     {                                                                                          \
-        gemm_ws_body<EPI, ws_mt(EPI), ws_waves(EPI)>(p);                                       \
+        gemm_ws_body<EPI, ws_mt(EPI), ws_waves(EPI), false>(p);                                \
     }
 
 // NT = 9: 144-wide column blocks (HAT-S: N = 144, 288, 432 divide exactly).
@@ -368,3 +415,10 @@ GEMM_WS_INST(hat_gemmws_qkv, EPI_QKV)
 GEMM_WS_INST(hat_gemmws_gelu, EPI_GELU)
 GEMM_WS_INST(hat_gemmws_resid_ln, EPI_RESID_LN)
 GEMM_WS_INST(hat_gemmws_hab_ln, EPI_HAB_LN)
+
+// HAB attention projection with the CAB's conv2 folded in as 80 more K (the
+// block input as residual, bias = proj bias + folded conv2 bias), then norm2.
+extern "C" __global__ __launch_bounds__(ws_waves(EPI_RESID_LN) * 64) void hat_gemmws_cab_ln(GemmArgs p)
+{
+    gemm_ws_body<EPI_RESID_LN, ws_mt(EPI_RESID_LN), ws_waves(EPI_RESID_LN), true>(p);
+}

@@ -5,4 +5,5 @@
 #include "conv.hip"
 #include "gemm.hip"
 #include "mlp.hip"
+#include "cab.hip"
 #include "misc.hip"

@@ -340,6 +340,139 @@ int gpu_selftest(std::string* err)
             note(std::string(k) + " M 600 (in place)");
         }
 
+        // ---- folded CAB (144 -> 6 -> 144) against the unfolded computation:
+        // conv1 + GELU, conv2 in full, its pixel mean, squeeze-excite, gate, and
+        // shortcut + proj + gated conv2 * cscale + LayerNorm - in double. A 32 x 48
+        // plane (6 tiles over 2 blocks, so tiles on every border line and corner).
+        {
+            const int H = 32, W = 48, T = H * W, C = CAB_C, CC = CAB_CC, sq = 6;
+            const float cscale = 0.01f;
+            std::vector<float> xn = rng.vec((size_t)T * C, 1.0f), w1 = rng.vec((size_t)CC * C * 9, 0.05f),
+                               b1 = rng.vec(CC, 0.1f), w2 = rng.vec((size_t)C * CC * 9, 0.2f),
+                               b2 = rng.vec(C, 0.1f), wa = rng.vec((size_t)sq * C, 0.2f), ba = rng.vec(sq, 0.1f),
+                               wb = rng.vec((size_t)C * sq, 0.5f), bb = rng.vec(C, 0.1f),
+                               ao = rng.vec((size_t)T * C, 1.0f), wp = rng.vec((size_t)C * C, 0.05f),
+                               bp = rng.vec(C, 0.1f), res = rng.vec((size_t)T * C, 1.0f),
+                               nw = rng.vec(C, 1.0f), nb = rng.vec(C, 0.1f);
+            std::vector<float> w1p = pack_cab_conv1(w1.data());
+            int Kp = 0;
+            std::vector<float> wpp = pack_linear(wp.data(), C, C, &Kp);
+            const int tiles = (H / 16) * (W / 16);
+            Dev dxn(xn), dw1(w1p), db1(b1), dw2(w2), db2(b2), dwa(wa), dba(ba), dwb(wb), dbb(bb), dao(ao),
+                dwp(wpp), dbp(bp), dres(res), dnw(nw), dnb(nb), dt1((size_t)T * CAB_CS),
+                dpart((size_t)tiles * CAB_NSUM * CAB_CS), dw2g((size_t)C * CAB_K2), dbias2(C), dgate(C),
+                dout((size_t)T * C), dxo((size_t)T * C);
+            CabConvArgs ca{dxn.p, dw1.p, db1.p, dt1.p, dpart.p, H, W};
+            launch(s, "hat_cab_conv1", 2, 1, 1, 256, ca);
+            CabGateArgs ga{};
+            ga.partial = dpart.p;
+            ga.t1 = dt1.p;
+            ga.tiles = tiles;
+            ga.H = H;
+            ga.W = W;
+            ga.w2 = dw2.p;
+            ga.b2 = db2.p;
+            ga.wa = dwa.p;
+            ga.ba = dba.p;
+            ga.wb = dwb.p;
+            ga.bb = dbb.p;
+            ga.bproj = dbp.p;
+            ga.w2g = dw2g.p;
+            ga.bias2 = dbias2.p;
+            ga.gate = dgate.p;
+            ga.cscale = cscale;
+            ga.sq = sq;
+            launch(s, "hat_cab_gate", 1, 1, 1, 1024, ga);
+            GemmArgs gp{};
+            gp.a = dao.p;
+            gp.w = dwp.p;
+            gp.bias = dbias2.p;
+            gp.out = dout.p;
+            gp.res = dres.p;
+            gp.xn = dxo.p;
+            gp.nw = dnw.p;
+            gp.nb = dnb.p;
+            gp.M = T;
+            gp.N = C;
+            gp.K = C;
+            gp.Kp = Kp;
+            gp.lda = C;
+            gp.ldo = C;
+            gp.eps = 1e-5f;
+            gp.t1 = dt1.p;
+            gp.w2g = dw2g.p;
+            gp.H = H;
+            gp.W = W;
+            launch(s, "hat_gemmws_cab_ln", 3, 1, 1, ws_waves(EPI_RESID_LN) * 64, gp);
+
+            auto inb = [&](int y, int x) { return y >= 0 && y < H && x >= 0 && x < W; };
+            std::vector<double> t1((size_t)T * CAB_CS, 0.0), y2((size_t)T * C);
+            for (int y = 0; y < H; ++y)
+                for (int x = 0; x < W; ++x)
+                    for (int co = 0; co < CC; ++co) {
+                        double v = b1[co];
+                        for (int tap = 0; tap < 9; ++tap) {
+                            const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
+                            if (!inb(yy, xx)) continue;
+                            for (int ci = 0; ci < C; ++ci)
+                                v += (double)w1[((size_t)co * C + ci) * 9 + tap] * xn[((size_t)yy * W + xx) * C + ci];
+                        }
+                        t1[((size_t)y * W + x) * CAB_CS + co] = gelu_d(v);
+                    }
+            std::vector<double> mean2(C, 0.0);
+            for (int y = 0; y < H; ++y)
+                for (int x = 0; x < W; ++x)
+                    for (int c = 0; c < C; ++c) {
+                        double v = b2[c];
+                        for (int tap = 0; tap < 9; ++tap) {
+                            const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
+                            if (!inb(yy, xx)) continue;
+                            for (int ci = 0; ci < CC; ++ci)
+                                v += (double)w2[((size_t)c * CC + ci) * 9 + tap] * t1[((size_t)yy * W + xx) * CAB_CS + ci];
+                        }
+                        y2[((size_t)y * W + x) * C + c] = v;
+                        mean2[c] += v / T;
+                    }
+            std::vector<double> z(sq), gate(C), bias2(C), w2g((size_t)C * CAB_K2, 0.0);
+            for (int j = 0; j < sq; ++j) {
+                double v = ba[j];
+                for (int c = 0; c < C; ++c) v += (double)wa[(size_t)j * C + c] * mean2[c];
+                z[j] = v < 0 ? 0 : v;
+            }
+            for (int c = 0; c < C; ++c) {
+                double v = bb[c];
+                for (int j = 0; j < sq; ++j) v += (double)wb[(size_t)c * sq + j] * z[j];
+                gate[c] = 1.0 / (1.0 + std::exp(-v));
+                bias2[c] = bp[c] + cscale * gate[c] * b2[c];
+                for (int tap = 0; tap < 9; ++tap)
+                    for (int ci = 0; ci < CC; ++ci)
+                        w2g[(size_t)c * CAB_K2 + tap * CAB_CS + ci] = cscale * gate[c] * w2[((size_t)c * CC + ci) * 9 + tap];
+            }
+            std::vector<double> want((size_t)T * C), wxn((size_t)T * C);
+            for (int m = 0; m < T; ++m) {
+                double mean = 0, var = 0;
+                for (int c = 0; c < C; ++c) {
+                    double v = bp[c];
+                    for (int k = 0; k < C; ++k) v += (double)ao[(size_t)m * C + k] * wp[(size_t)c * C + k];
+                    v = res[(size_t)m * C + c] + v + y2[(size_t)m * C + c] * gate[c] * cscale;
+                    want[(size_t)m * C + c] = v;
+                    mean += v / C;
+                }
+                for (int c = 0; c < C; ++c) var += (want[(size_t)m * C + c] - mean) * (want[(size_t)m * C + c] - mean) / C;
+                for (int c = 0; c < C; ++c)
+                    wxn[(size_t)m * C + c] = (want[(size_t)m * C + c] - mean) / std::sqrt(var + 1e-5) * nw[c] + nb[c];
+            }
+            check_close("hat_cab_conv1 t1", dt1.get(), t1, 2e-5);
+            note("hat_cab_conv1 144->6 + gelu, 32x48");
+            check_close("hat_cab_gate gate", dgate.get(), gate, 2e-6);
+            check_close("hat_cab_gate bias2", dbias2.get(), bias2, 2e-6);
+            check_close("hat_cab_gate w2g", dw2g.get(), w2g, 1e-7);
+            note("hat_cab_gate (mean by linearity) vs conv2 in full");
+            check_close("hat_gemmws_cab_ln", dout.get(), want, 5e-5);
+            check_close("hat_gemmws_cab_ln layernorm", dxo.get(), wxn, 5e-5);
+            note("hat_gemmws_cab_ln proj + folded conv2 + norm2");
+        }
+
         // ---- convolutions (all epilogues) on a non-square plane.
         struct CCase { int CI, CO, epi, act, r; const char* what; };
         const CCase cases[] = {
