@@ -37,23 +37,34 @@
 
 using namespace hatk;
 
+// MASKED: the block's window is in the last row or column of a shifted SW
+// grid, so its scores get the region mask; every other block runs the loop
+// without it.
 template <int D, bool OCA>
-__device__ __forceinline__ void attn_body(const AttnArgs& p)
+struct AttnShape {
+    static constexpr int HALF = D / 2;                 // dims per lane half
+    static constexpr int HP = (HALF + 3) / 4 * 4;      // LDS offset of the second half
+    static constexpr int RSK = 2 * HP + 4;             // K row stride in LDS (floats)
+    static constexpr int NK = OCA ? 576 : 256;         // keys per window
+    static constexpr int RSV = NK + 4;                 // V^T row stride in LDS
+    static constexpr int TROWS = OCA ? 1521 : 961;     // bias table rows
+    static constexpr int LDS = NK * RSK + 32 * RSV + TROWS;  // floats
+};
+
+template <int D, bool OCA, bool MASKED>
+__device__ __forceinline__ void attn_body(const AttnArgs& p, float* lds)
 {
-    constexpr int HALF = D / 2;                 // dims per lane half
-    constexpr int HP = (HALF + 3) / 4 * 4;      // LDS offset of the second half
-    constexpr int RSK = 2 * HP + 4;             // K row stride in LDS (floats)
-    constexpr int NK = OCA ? 576 : 256;         // keys per window
+    using S = AttnShape<D, OCA>;
+    constexpr int HALF = S::HALF, HP = S::HP, RSK = S::RSK, NK = S::NK, RSV = S::RSV;
+    constexpr int TROWS = S::TROWS;
     constexpr int NKT = NK / 32;                // 32-key tiles
     constexpr int CHT = OCA ? 3 : 2;            // tiles per softmax chunk
     constexpr int NCH = NKT / CHT;
-    constexpr int RSV = NK + 4;                 // V^T row stride in LDS
-    constexpr int TROWS = OCA ? 1521 : 961;     // bias table rows
     static_assert(NKT % CHT == 0, "chunking");
 
-    __shared__ float Kl[NK * RSK];
-    __shared__ float Vt[D * RSV];
-    __shared__ float Tb[TROWS];
+    float* Kl = lds;                   // [NK][RSK]
+    float* Vt = Kl + NK * RSK;         // [32][RSV]: V^T, then row D ones, rows D+1.. zeros
+    float* Tb = Vt + 32 * RSV;         // [TROWS]
 
     const int wi = blockIdx.x;
     const int head = blockIdx.y;
@@ -68,26 +79,52 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p)
     const float* Vg = p.qkv + (size_t)(2 * heads + head) * T * D;
 
     // ---- stage K (row-major, halves split) and V^T in LDS ----
-    for (int e = tid; e < NK * D; e += 512) {
-        const int k = e / D, d = e - (e / D) * D;
-        int pix;
+    auto key_pixel = [&](int k) -> int {
         if (OCA) {
             const int ky = k / 24, kx = k - (k / 24) * 24;
             const int y = wy * 16 - 4 + ky, x = wx * 16 - 4 + kx;
-            pix = (y >= 0 && y < hp && x >= 0 && x < wp) ? y * wp + x : -1;
-        } else {
-            int y = wy * 16 + (k >> 4) + shift, x = wx * 16 + (k & 15) + shift;
-            if (y >= hp) y -= hp;
-            if (x >= wp) x -= wp;
-            pix = y * wp + x;
+            return (y >= 0 && y < hp && x >= 0 && x < wp) ? y * wp + x : -1;
         }
-        float kv = 0.0f, vv = 0.0f;
-        if (pix >= 0) {
-            kv = Kg[(size_t)pix * D + d];
-            vv = Vg[(size_t)pix * D + d];
+        int y = wy * 16 + (k >> 4) + shift, x = wx * 16 + (k & 15) + shift;
+        if (y >= hp) y -= hp;
+        if (x >= wp) x -= wp;
+        return y * wp + x;
+    };
+    if constexpr (D % 4 == 0 && HP == HALF) {
+        // Rows of D floats are whole float4s and the halves need no gap, so K
+        // goes to LDS as float4s in place; V^T takes four scalar stores.
+        for (int e = tid; e < NK * (D / 4); e += 512) {
+            const int k = e / (D / 4), d = (e - k * (D / 4)) * 4;
+            const int pix = key_pixel(k);
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (pix >= 0) {
+                kv = *(const float4*)(Kg + (size_t)pix * D + d);
+                vv = *(const float4*)(Vg + (size_t)pix * D + d);
+            }
+            *(float4*)(Kl + k * RSK + d) = kv;
+            Vt[(d + 0) * RSV + k] = vv.x;
+            Vt[(d + 1) * RSV + k] = vv.y;
+            Vt[(d + 2) * RSV + k] = vv.z;
+            Vt[(d + 3) * RSV + k] = vv.w;
         }
-        Kl[k * RSK + (d < HALF ? d : HP + d - HALF)] = kv;
-        Vt[d * RSV + k] = vv;
+    } else {
+        for (int e = tid; e < NK * D; e += 512) {
+            const int k = e / D, d = e - (e / D) * D;
+            const int pix = key_pixel(k);
+            float kv = 0.0f, vv = 0.0f;
+            if (pix >= 0) {
+                kv = Kg[(size_t)pix * D + d];
+                vv = Vg[(size_t)pix * D + d];
+            }
+            Kl[k * RSK + (d < HALF ? d : HP + d - HALF)] = kv;
+            Vt[d * RSV + k] = vv;
+        }
+    }
+    // The V^T rows past D fill the 32-row MFMA tile: row D all ones (it sums
+    // the probabilities, see below), the rest zero.
+    for (int e = tid; e < (32 - D) * NK; e += 512) {
+        const int r = D + e / NK, k = e - (e / NK) * NK;
+        Vt[r * RSV + k] = r == D ? 1.0f : 0.0f;
     }
     // Bias table for this head, in log2 units. For OCA the table is stored
     // rotated so that the reference's negative-index wrap (plan.rs:397-416)
@@ -114,8 +151,19 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p)
         qpix = y * wp + x;
     }
     float qv[HALF];
+    if constexpr (HALF % 4 == 0) {
 #pragma unroll
-    for (int s = 0; s < HALF; ++s) qv[s] = Qg[(size_t)qpix * D + h * HALF + s] * p.qscale;
+        for (int s4 = 0; s4 < HALF; s4 += 4) {
+            const float4 v = *(const float4*)(Qg + (size_t)qpix * D + h * HALF + s4);
+            qv[s4] = v.x * p.qscale;
+            qv[s4 + 1] = v.y * p.qscale;
+            qv[s4 + 2] = v.z * p.qscale;
+            qv[s4 + 3] = v.w * p.qscale;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < HALF; ++s) qv[s] = Qg[(size_t)qpix * D + h * HALF + s] * p.qscale;
+    }
 
     // Bias addressing. SW: idx = (qy-ky+15)*31 + (qx-kx+15) = sw_base - (ky*31+kx).
     // OCA: idx = (ky*39+kx) - (qy*39+qx) + 600 on the rotated table.
@@ -124,17 +172,24 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p)
     // Mask addends (SW, shifted): a key differs in region from the query when
     // its half (bit 3 of y or x) differs, in the last window row / column.
     const float NEG = -100.0f * HAT_LOG2E;
-    const bool mrow = !OCA && shift > 0 && wy == p.ny - 1;
-    const bool mcol = !OCA && shift > 0 && wx == p.nx - 1;
+    const bool mrow = MASKED && wy == p.ny - 1;
+    const bool mcol = MASKED && wx == p.nx - 1;
     const bool r_lo = mrow && (qy & 8), r_hi = mrow && !(qy & 8);
     const bool c_lo = mcol && (qx & 8), c_hi = mcol && !(qx & 8);
     const float madd[2][2] = {{(r_lo || c_lo) ? NEG : 0.0f, (r_lo || c_hi) ? NEG : 0.0f},
                               {(r_hi || c_lo) ? NEG : 0.0f, (r_hi || c_hi) ? NEG : 0.0f}};
 
+    // Row D of the 32-row V^T tile is padding; it holds ones, so row D of
+    // O^T accumulates the softmax denominator sum_k P[k][q] - rescaled along
+    // with the rest of O - inside the PV products. In the MFMA output layout
+    // it is register RR of lane half RH.
+    static_assert(D < 32, "a spare V^T row is needed");
+    constexpr int RH = (D % 8) / 4, RR = (D / 8) * 4 + D % 4;
+
     f32x16 o;
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[i] = 0.0f;
-    float mrun = -INFINITY, lrun = 0.0f;
+    float mrun = -INFINITY;
 
     // The chunk loop stays rolled: unrolled, the compiler hoists the K operand
     // reads of every key tile ahead of the MFMAs and spills.
@@ -145,66 +200,61 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p)
         for (int t = 0; t < CHT; ++t) {
             const int kt = ch * CHT + t;
             const float* kp = Kl + (kt * 32 + ql) * RSK + h * HP;
+            // The scores accumulate onto their bias (+ mask): S = bias + K Q^T.
             f32x16 a;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) a[i] = 0.0f;
-#pragma unroll
-            for (int st = 0; st < HALF; ++st) a = mfma32(kp[st], qv[st], a);
-            s[t] = a;
-        }
-        // bias (+ mask), chunk max
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < CHT; ++t) {
-            const int kt = ch * CHT + t;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int key0 = kt * 32 + (i >> 2) * 8 + (i & 3);  // key for h = 0
-                float v = s[t][i];
+                float b;
                 if (OCA) {
                     // (ky*39 + kx) = key + 15*ky for a 24-wide key grid
                     const int key = key0 + 4 * h;
                     const int ky = (int)((unsigned)key / 24u);
-                    v += Tb[oca_base + key + 15 * ky];
+                    b = Tb[oca_base + key + 15 * ky];
                 } else {
                     const int ky = key0 >> 4, kx = key0 & 15;
-                    v += Tb[sw_base - (ky * 31 + kx)];
-                    v += madd[(ky >> 3) & 1][(kx >> 3) & 1];
+                    b = Tb[sw_base - (ky * 31 + kx)];
+                    if (MASKED) b += madd[(ky >> 3) & 1][(kx >> 3) & 1];
                 }
-                s[t][i] = v;
-                mx = fmaxf(mx, v);
+                a[i] = b;
             }
+#pragma unroll
+            for (int st = 0; st < HALF; ++st) a = mfma32(kp[st], qv[st], a);
+            s[t] = a;
         }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < CHT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[t][i]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mnew = fmaxf(mrun, mx);
         const float corr = fast_exp2(mrun - mnew);
-        lrun *= corr;
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[i] *= corr;
         mrun = mnew;
 #pragma unroll
         for (int t = 0; t < CHT; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float e = fast_exp2(s[t][i] - mnew);
-                s[t][i] = e;
-                lrun += e;
-            }
+            for (int i = 0; i < 16; ++i) s[t][i] = fast_exp2(s[t][i] - mnew);
         // O^T += V^T P^T
 #pragma unroll
         for (int t = 0; t < CHT; ++t) {
             const int kt = ch * CHT + t;
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
-                f32x4 vv = (f32x4){0.f, 0.f, 0.f, 0.f};
-                if (ql < D) vv = *(const f32x4*)(Vt + ql * RSV + kt * 32 + i4 * 8 + h * 4);
+                // The padding rows come from LDS for OCA; for SW (more blocks per
+                // CU, LDS-bound in this phase) the idle lanes skip the read.
+                f32x4 vv;
+                if (OCA || ql < D) vv = *(const f32x4*)(Vt + ql * RSV + kt * 32 + i4 * 8 + h * 4);
+                else vv = ql == D ? (f32x4){1.f, 1.f, 1.f, 1.f} : (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) o = mfma32(vv[j], s[t][i4 * 4 + j], o);
             }
         }
     }
 
-    const float ltot = lrun + __shfl_xor(lrun, 32, 64);
+    const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
     const float inv = 1.0f / ltot;
     float* orow = p.out + (size_t)qpix * p.C + head * D;
 #pragma unroll
@@ -228,7 +278,12 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p)
 #define ATTN_INST(NAME, D, OCA)                                                              \
     extern "C" __global__ __launch_bounds__(512, OCA ? 2 : 4) void NAME(AttnArgs p)          \
     {                                                                                        \
-        attn_body<D, OCA>(p);                                                                \
+        __shared__ __attribute__((aligned(16))) float lds[AttnShape<D, OCA>::LDS];           \
+        const int wi = blockIdx.x;                                                           \
+        if (!OCA && p.shift > 0 && (wi / p.nx == p.ny - 1 || wi % p.nx == p.nx - 1))         \
+            attn_body<D, OCA, true>(p, lds);                                                 \
+        else                                                                                 \
+            attn_body<D, OCA, false>(p, lds);                                                \
     }
 
 ATTN_INST(hat_attn_sw_d24, 24, false)
