@@ -38,11 +38,13 @@ __device__ __forceinline__ void build_colmap(const GemmArgs& p, int n0, int* col
     }
 }
 
-// Epilogue shared by both GEMM kernels: lane (lr, lg) holds out[m][n .. n+3]
-// for m = mbase + 16*mt + lr and n = n0 + 16*nt + 4*lg.
+// Epilogue shared by the GEMM kernels: lane (lr, lg) holds out[m][n .. n+3]
+// for m = mbase + 16*mt + lr and n = n0 + 16*nt + 4*lg. With pres, the
+// residual values were loaded ahead by the caller (same layout as acc).
 template <int MT, int NT, int EPI>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[MT][NT], int mbase,
-                                              int n0, int lr, int lg, const int* colmap)
+                                              int n0, int lr, int lg, const int* colmap,
+                                              const f32x4 (*pres)[NT] = nullptr)
 {
     const int M = p.M, N = p.N;
     constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN;
@@ -65,8 +67,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[MT
                     for (int j = 0; j < 4; ++j) v[j] = gelu(v[j]);
                 }
                 if (EPI == EPI_RESID || EPI == EPI_RESID_LN || EPI == EPI_HAB || EPI == EPI_HAB_LN) {
-                    const float4 r4 = *(const float4*)(p.res + (size_t)m * p.ldo + n);
-                    v = (f32x4){r4.x, r4.y, r4.z, r4.w} + v;
+                    if (pres) {
+                        v = pres[mt][nt] + v;
+                    } else {
+                        const float4 r4 = *(const float4*)(p.res + (size_t)m * p.ldo + n);
+                        v = (f32x4){r4.x, r4.y, r4.z, r4.w} + v;
+                    }
                 }
                 if (EPI == EPI_HAB || EPI == EPI_HAB_LN) {
                     const float4 a4 = *(const float4*)(p.aux + (size_t)m * p.ldo + n);

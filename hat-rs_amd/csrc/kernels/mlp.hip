@@ -115,6 +115,7 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     for (; tile < ntiles; tile += gridDim.x) {
         const bool last_tile = tile + (int)gridDim.x >= ntiles;
         f32x4 acc2[1][MLP_C / 16];
+        f32x4 rres[1][MLP_C / 16];
 #pragma unroll
         for (int j = 0; j < MLP_C / 16; ++j) acc2[0][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
@@ -122,6 +123,17 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             const float* B = Wb + (c & 1) * MLP_BUF;
             const bool more = c + 1 < MLP_NCH || !last_tile;  // block-uniform
             if (more) fetch(c + 1 < MLP_NCH ? c + 1 : 0);
+            // The residual rows for the epilogue, one chunk ahead of it.
+            if (c == MLP_NCH - 1) {
+                const int m = tile * MLP_ROWS + wave * 16 + lr;
+                const float* rrow = p.res + (size_t)(m < M ? m : 0) * MLP_C + lg * 4;
+#pragma unroll
+                for (int n2 = 0; n2 < MLP_C / 16; ++n2) {
+                    f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    if (m < M) v = *(const f32x4*)(rrow + n2 * 16);
+                    rres[0][n2] = v;
+                }
+            }
 
             // fc1 for this chunk: h[16 rows][48] = a . w1[chunk]^T
             f32x4 h[MLP_HC / 16];
@@ -159,7 +171,7 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             if (more) stash((c + 1) & 1);
             __syncthreads();
         }
-        gemm_epilogue<1, MLP_C / 16, EPI>(g, acc2, tile * MLP_ROWS + wave * 16, 0, lr, lg, nullptr);
+        gemm_epilogue<1, MLP_C / 16, EPI>(g, acc2, tile * MLP_ROWS + wave * 16, 0, lr, lg, nullptr, rres);
     }
 }
 
