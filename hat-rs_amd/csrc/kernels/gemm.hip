@@ -346,6 +346,23 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 }
             }
         }
+        // The residual for the epilogue, loaded now so its latency hides under
+        // the K loop.
+        constexpr bool PRE = EPI == EPI_RESID_LN || EPI == EPI_RESID;
+        f32x4 rres[PRE ? MT : 1][NT];
+        if (PRE) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = mbase + mt * 16 + lr;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int n = n0 + nt * 16 + lg * 4;
+                    f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    if (alive[mt] && n < N) v = *(const f32x4*)(p.res + (size_t)m * p.ldo + n);
+                    rres[mt][nt] = v;
+                }
+            }
+        }
         f32x4 acc[MT][NT];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
@@ -390,7 +407,7 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 }
             }
         }
-        gemm_epilogue<MT, NT, EPI>(p, acc, mbase, n0, lr, lg, s_colmap);
+        gemm_epilogue<MT, NT, EPI>(p, acc, mbase, n0, lr, lg, s_colmap, PRE ? rres : nullptr);
     }
 }
 
