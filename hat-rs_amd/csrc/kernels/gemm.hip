@@ -38,12 +38,25 @@ __device__ __forceinline__ void build_colmap(const GemmArgs& p, int n0, int* col
     }
 }
 
+// Column constants of a block's n0.. columns, indexed from n0 (global memory
+// or an LDS copy).
+struct EpiConsts {
+    const float* bias;
+    const float* nw;
+    const float* nb;
+};
+
+__device__ __forceinline__ EpiConsts global_consts(const GemmArgs& p, int n0)
+{
+    return EpiConsts{p.bias + n0, p.nw ? p.nw + n0 : nullptr, p.nb ? p.nb + n0 : nullptr};
+}
+
 // Epilogue shared by the GEMM kernels: lane (lr, lg) holds out[m][n .. n+3]
 // for m = mbase + 16*mt + lr and n = n0 + 16*nt + 4*lg. With pres, the
 // residual values were loaded ahead by the caller (same layout as acc).
 template <int MT, int NT, int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[MT][NT], int mbase,
-                                              int n0, int lr, int lg, const int* colmap,
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts& k, f32x4 (&acc)[MT][NT],
+                                              int mbase, int n0, int lr, int lg, const int* colmap,
                                               const f32x4 (*pres)[NT] = nullptr)
 {
     const int M = p.M, N = p.N;
@@ -60,7 +73,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[MT
             const bool live = mlive && n < N;
             f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
             if (live) {
-                const float4 b4 = *(const float4*)(p.bias + n);
+                const float4 b4 = *(const float4*)(k.bias + (n - n0));
                 v = acc[mt][nt] + (f32x4){b4.x, b4.y, b4.z, b4.w};
                 if (EPI == EPI_GELU) {
 #pragma unroll
@@ -135,8 +148,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, f32x4 (&acc)[MT
             }
             *(float4*)(p.out + (size_t)m * p.ldo + n) = make_float4(v[0], v[1], v[2], v[3]);
             if (LNOUT) {
-                const float4 w4 = *(const float4*)(p.nw + n);
-                const float4 b4 = *(const float4*)(p.nb + n);
+                const float4 w4 = *(const float4*)(k.nw + (n - n0));
+                const float4 b4 = *(const float4*)(k.nb + (n - n0));
                 *(float4*)(p.xn + (size_t)m * p.ldo + n) =
                     make_float4((v[0] - mean) * rstd * w4.x + b4.x, (v[1] - mean) * rstd * w4.y + b4.y,
                                 (v[2] - mean) * rstd * w4.z + b4.z, (v[3] - mean) * rstd * w4.w + b4.w);
@@ -245,7 +258,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
         __syncthreads();
     }
 
-    gemm_epilogue<2, NT, EPI>(p, acc, m0 + wave * 32, n0, lr, lg, s_colmap);
+    gemm_epilogue<2, NT, EPI>(p, global_consts(p, n0), acc, m0 + wave * 32, n0, lr, lg, s_colmap);
 }
 
 #define GEMM_INST(NAME, NT, EPI)                                                             \
@@ -275,6 +288,9 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
     __shared__ float Wsm[BN * WS_KS];
     __shared__ float W2s[CAB ? BN * S2 : 1];
     __shared__ int s_colmap[EPI == EPI_QKV ? BN : 1];
+    constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN;
+    // bias (+ LayerNorm weight and bias) of the block's columns
+    __shared__ __attribute__((aligned(16))) float Cs[(LNOUT ? 3 : 1) * BN];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -300,6 +316,12 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         }
     }
     build_colmap<BN, EPI>(p, n0, s_colmap);
+    for (int i = tid; i < (LNOUT ? 3 : 1) * BN; i += WAVES * 64) {
+        const int j = i % BN, n = n0 + j;
+        const float* src = i < BN ? p.bias : (i < 2 * BN ? p.nw : p.nb);
+        Cs[i] = n < N ? src[n] : 0.0f;
+    }
+    const EpiConsts kc{Cs, LNOUT ? Cs + BN : nullptr, LNOUT ? Cs + 2 * BN : nullptr};
     __syncthreads();
 
     const int ntiles = (M + ROWS - 1) / ROWS;
@@ -407,7 +429,7 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 }
             }
         }
-        gemm_epilogue<MT, NT, EPI>(p, acc, mbase, n0, lr, lg, s_colmap, PRE ? rres : nullptr);
+        gemm_epilogue<MT, NT, EPI>(p, kc, acc, mbase, n0, lr, lg, s_colmap, PRE ? rres : nullptr);
     }
 }
 

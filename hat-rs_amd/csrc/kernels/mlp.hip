@@ -35,6 +35,9 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
 {
     static_assert(MLP_NCH % 2 == 0, "chunk parity must repeat across tiles");
     __shared__ float Wb[2 * MLP_BUF];
+    // The per-column constants, read in every chunk and every epilogue, from
+    // LDS rather than through the cache hierarchy: b1, then b2, nw, nb.
+    __shared__ __attribute__((aligned(16))) float Cs[MLP_H + 3 * MLP_C];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -48,7 +51,8 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
 
     // This thread's share of a chunk: global offset (relative to the chunk) and
     // LDS offset of each of its float4, for the fc1 rows then the fc2 columns.
-    int goff[MLP_PER], loff[MLP_PER];
+    unsigned goff[MLP_PER];
+    int loff[MLP_PER];
 #pragma unroll
     for (int i = 0; i < MLP_PER; ++i) {
         const int idx = tid + i * MLP_THREADS;
@@ -65,14 +69,17 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     }
     float4 stg[MLP_PER];
     auto fetch = [&](int c) {
+        // uniform chunk bases + 32-bit per-thread offsets
+        const float* w1c = p.w1 + c * MLP_HC * MLP_C;
+        const float* w2c = p.w2 + c * MLP_HC;
 #pragma unroll
         for (int i = 0; i < MLP_PER; ++i) {
             const int idx = tid + i * MLP_THREADS;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (idx < MLP_W1F4)
-                v = *(const float4*)(p.w1 + (size_t)c * MLP_HC * MLP_C + goff[i]);
+                v = *(const float4*)(w1c + goff[i]);
             else if (idx < MLP_F4)
-                v = *(const float4*)(p.w2 + c * MLP_HC + goff[i]);
+                v = *(const float4*)(w2c + goff[i]);
             stg[i] = v;
         }
     };
@@ -95,13 +102,20 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
         }
     };
 
+    for (int i = tid; i < MLP_H + 3 * MLP_C; i += MLP_THREADS) {
+        float v;
+        if (i < MLP_H) v = p.b1[i];
+        else if (i < MLP_H + MLP_C) v = p.b2[i - MLP_H];
+        else if (EPI != EPI_RESID_LN) v = 0.0f;
+        else if (i < MLP_H + 2 * MLP_C) v = p.nw[i - MLP_H - MLP_C];
+        else v = p.nb[i - MLP_H - 2 * MLP_C];
+        Cs[i] = v;
+    }
     GemmArgs g{};
-    g.bias = p.b2;
     g.out = p.out;
     g.res = p.res;
     g.xn = p.xn;
-    g.nw = p.nw;
-    g.nb = p.nb;
+    const EpiConsts kc{Cs + MLP_H, Cs + MLP_H + MLP_C, Cs + MLP_H + 2 * MLP_C};
     g.M = M;
     g.N = MLP_C;
     g.ldo = MLP_C;
@@ -152,7 +166,7 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             if (c == MLP_NCH - 1 && !last_tile) load_a(tile + gridDim.x);
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt) {
-                const float4 b4 = *(const float4*)(p.b1 + c * MLP_HC + nt * 16 + lg * 4);
+                const float4 b4 = *(const float4*)(Cs + c * MLP_HC + nt * 16 + lg * 4);
                 h[nt][0] = gelu(h[nt][0] + b4.x);
                 h[nt][1] = gelu(h[nt][1] + b4.y);
                 h[nt][2] = gelu(h[nt][2] + b4.z);
@@ -171,7 +185,7 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             if (more) stash((c + 1) & 1);
             __syncthreads();
         }
-        gemm_epilogue<1, MLP_C / 16, EPI>(g, acc2, tile * MLP_ROWS + wave * 16, 0, lr, lg, nullptr, rres);
+        gemm_epilogue<1, MLP_C / 16, EPI>(g, kc, acc2, tile * MLP_ROWS + wave * 16, 0, lr, lg, nullptr, rres);
     }
 }
 
