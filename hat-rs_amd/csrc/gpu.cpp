@@ -342,6 +342,43 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
     launch(s, name, (unsigned)((W / 16) * (H / 8)), (unsigned)((C.CO + BN - 1) / BN), 1, 256, p);
 }
 
+// A C -> 144 3x3 conv with every output channel in one block and a GEMM
+// epilogue: EPI_STORE_LN (out, xn = LN(out)), EPI_RESID_LN (out = conv + res,
+// xn = LN(out)) or EPI_RESID. out may alias res; in, out and xn must not overlap.
+bool convw_fits(const DevConv& C) { return C.CO == 144 && C.COp == 144 && C.r == 0; }
+
+void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride, int H, int W,
+               float* out, int epi, const float* res, float* xn, const float* nw, const float* nb)
+{
+    if (!convw_fits(C)) throw Error("convw: needs 144 output channels");
+    if (H % 16 != 0 || W % 16 != 0) throw Error("convw: plane must be 16-aligned");
+    if (cin_stride % 4 != 0 || cin_stride < C.CI) throw Error("convw: bad input channel stride");
+    const char* name = epi == EPI_STORE_LN   ? "hat_convw_n9_store_ln"
+                       : epi == EPI_RESID_LN ? "hat_convw_n9_resid_ln"
+                       : epi == EPI_RESID    ? "hat_convw_n9_resid"
+                                             : nullptr;
+    if (!name) throw Error("convw: bad epilogue");
+    ConvArgs p{};
+    p.in = in;
+    p.w = C.w;
+    p.bias = C.b;
+    p.out = out;
+    p.res = res;
+    p.H = H;
+    p.W = W;
+    p.CI = C.CI;
+    p.CIp = C.CIp;
+    p.cin_stride = cin_stride;
+    p.CO = C.CO;
+    p.COp = C.COp;
+    p.co_stride = C.CO;
+    p.xn = xn;
+    p.nw = nw;
+    p.nb = nb;
+    p.eps = 1e-5f;
+    launch(s, name, (unsigned)((W / 16) * (H / 16)), 1, 1, 512, p);
+}
+
 void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, const Plan& pl,
               int heads, int D, bool oca, int shift)
 {
@@ -683,14 +720,24 @@ void GpuBackend::forward_device(int h, int w, const float* d_in, float* d_out)
     const int C = wt_.embed, H = plan_.hp, W = plan_.wp;
     PreArgs pa{d_in, x0_, h, w, H, W, 4, wt_.mean[0], wt_.mean[1], wt_.mean[2], wt_.img_range};
     launch(stream_, "hat_pre", (unsigned)((T + 255) / 256), 1, 1, 256, pa);
-    conv(conv_.at("conv_first"), x0_, 4, H, W, body_, C, CEPI_STORE, 0);
-    layernorm(body_, xa_, "patch_embed.norm", T);
-    for (size_t s = 0; s < wt_.depths.size(); ++s) {
+    const DevConv& cf = conv_.at("conv_first");
+    // With 144 channels the trunk convs carry the LayerNorm that follows them.
+    const bool fused = convw_fits(cf);
+    if (fused) {
+        run_convw(stream_, cf, x0_, 4, H, W, body_, EPI_STORE_LN, nullptr, xa_,
+                  raw_.at("patch_embed.norm.weight"), raw_.at("patch_embed.norm.bias"));
+    } else {
+        conv(cf, x0_, 4, H, W, body_, C, CEPI_STORE, 0);
+        layernorm(body_, xa_, "patch_embed.norm", T);
+    }
+    const size_t S = wt_.depths.size();
+    for (size_t s = 0; s < S; ++s) {
         // RHAG (gpu.rs:592-610): conv3x3(blocks(x)) + x, with the stage input
         // kept in xa_ and the blocks working in xb_. Each block's last GEMM
-        // leaves the next block's norm1 in xn_; the first needs its own pass.
+        // leaves the next block's norm1 in xn_; the first block's comes from
+        // the previous stage's conv (or its own pass).
         const std::string L = "layers." + std::to_string(s) + ".residual_group.";
-        layernorm(xa_, xn_, L + "blocks.0.norm1", T);
+        if (!fused || s == 0) layernorm(xa_, xn_, L + "blocks.0.norm1", T);
         for (int b = 0; b < wt_.depths[s]; ++b) {
             const std::string next = b + 1 < wt_.depths[s]
                                          ? L + "blocks." + std::to_string(b + 1) + ".norm1"
@@ -698,11 +745,25 @@ void GpuBackend::forward_device(int h, int w, const float* d_in, float* d_out)
             hab((int)s, b, b == 0 ? xa_ : xb_, xb_, next);
         }
         ocab((int)s, xb_);
-        conv(conv_.at("layers." + std::to_string(s) + ".conv"), xb_, C, H, W, xa_, C, CEPI_RESID, 0,
-             xa_);
+        const DevConv& rc = conv_.at("layers." + std::to_string(s) + ".conv");
+        if (fused) {
+            // x = conv(blocks) + x, then the next stage's norm1 or the final
+            // norm into xn_ (xb_, the conv's input, is still being read).
+            const std::string nn = s + 1 < S ? "layers." + std::to_string(s + 1) + ".residual_group.blocks.0.norm1"
+                                             : std::string("norm");
+            run_convw(stream_, rc, xb_, C, H, W, xa_, EPI_RESID_LN, xa_, xn_, raw_.at(nn + ".weight"),
+                      raw_.at(nn + ".bias"));
+        } else {
+            conv(rc, xb_, C, H, W, xa_, C, CEPI_RESID, 0, xa_);
+        }
     }
-    layernorm(xa_, xb_, "norm", T);
-    conv(conv_.at("conv_after_body"), xb_, C, H, W, xa_, C, CEPI_RESID, 0, body_);
+    if (fused) {
+        run_convw(stream_, conv_.at("conv_after_body"), xn_, C, H, W, xa_, EPI_RESID, body_, nullptr,
+                  nullptr, nullptr);
+    } else {
+        layernorm(xa_, xb_, "norm", T);
+        conv(conv_.at("conv_after_body"), xb_, C, H, W, xa_, C, CEPI_RESID, 0, body_);
+    }
     // Head (gpu.rs:622-653): conv + LeakyReLU, [conv + PixelShuffle] per block, conv_last.
     const int feat = wt_.head_feat;
     conv(conv_.at("conv_before_upsample.0"), xa_, C, H, W, head0_, feat, CEPI_STORE, 2);

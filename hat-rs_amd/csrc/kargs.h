@@ -19,6 +19,7 @@ enum GemmEpi : int {
     EPI_HAB = 4,         // out[m][n] = (res[m][n] + v) + (aux[m][n] * gate[n]) * cscale
     EPI_RESID_LN = 5,    // EPI_RESID, and xn[m][:] = LayerNorm(out[m][:]) (full rows)
     EPI_HAB_LN = 6,      // EPI_HAB, and xn[m][:] = LayerNorm(out[m][:]) (full rows)
+    EPI_STORE_LN = 7,    // EPI_STORE, and xn[m][:] = LayerNorm(out[m][:]) (full rows)
 };
 
 // Weight-stationary K = 144 GEMM launch geometry per epilogue: ws_waves waves
@@ -114,6 +115,11 @@ struct ConvArgs {
     int crop_h, crop_w;  // CEPI_FINAL crop (output size)
     float img_range;     // CEPI_FINAL: out = v / img_range + mean
     float mean0, mean1, mean2;
+    // hat_convw_* (all output channels per block, GEMM epilogues):
+    float* xn;           // LayerNorm of the output rows [H*W][co_stride]
+    const float* nw;
+    const float* nb;
+    float eps;
 };
 
 // Fused window attention. One block per (window, head).

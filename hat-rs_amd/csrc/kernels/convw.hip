@@ -1,0 +1,172 @@
+// 3x3 convolution (stride 1, zero padding 1) over NHWC with all BN = 16*NT
+// output channels of a column block in one block, so that for BN = C the
+// GEMM epilogues apply: bias + residual and the LayerNorm of whole rows.
+//
+// Used for the C -> C convs of the trunk: conv_first (+ patch_embed.norm), the
+// RHAG conv (+ stage input, + the next stage's norm1 or the final norm) and
+// conv_after_body (+ the conv_first skip) - lg_conv3x3_winograd at gpu.rs:605,
+// 722, 742 with the lg_add and lg_channel_layer_norm passes that follow them
+// (cuda.rs:227-248, 185-191).
+//
+// A block owns a 16x16 pixel tile; 8 waves, wave w owns tile rows 2w and 2w+1
+// (two 16-pixel MFMA tiles, lane l%16 is the pixel's x). Input channels are
+// walked in chunks of 16: the chunk's 18x18 halo patch and its [9 taps][BN][16]
+// weight slice are staged in LDS (with BN = 144: 20.7 KB + 83 KB), the next
+// chunk's data travelling through registers while this chunk's MFMAs run, and
+// every tap reads the patch at an offset. The input is read once per column
+// block (the C -> C convs have one), the weights once per 256 pixels.
+//
+// Included after gemm.hip (gemm_epilogue) in the one translation unit.
+
+#define CW_T 16                        // output tile side
+#define CW_P (CW_T + 2)                // halo side
+#define CW_PX (CW_P * CW_P)            // 324 halo pixels
+#define CW_WAVES 8
+#define CW_THREADS (CW_WAVES * 64)
+
+template <int NT, int EPI>
+__device__ __forceinline__ void convw_body(const ConvArgs& p)
+{
+    constexpr int BN = 16 * NT;
+    constexpr int PF4 = CW_PX * 4;                 // patch float4 per chunk
+    constexpr int WF4 = 9 * BN * 4;                // weight float4 per chunk
+    constexpr int PPER = (PF4 + CW_THREADS - 1) / CW_THREADS;
+    constexpr int WPER = (WF4 + CW_THREADS - 1) / CW_THREADS;
+    __shared__ __attribute__((aligned(16))) float Ps[CW_PX * 16];
+    __shared__ __attribute__((aligned(16))) float Ws[9 * BN * 16];
+    __shared__ __attribute__((aligned(16))) float Cs[3 * BN];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int H = p.H, W = p.W;
+    const int tiles_x = W / CW_T;
+    const int ty0 = (blockIdx.x / tiles_x) * CW_T;
+    const int tx0 = (blockIdx.x % tiles_x) * CW_T;
+    const int co0 = blockIdx.y * BN;
+    constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_STORE_LN;
+
+    // Column constants (bias, LayerNorm weight and bias) of the block.
+    for (int i = tid; i < (LNOUT ? 3 : 1) * BN; i += CW_THREADS) {
+        const int j = i % BN, co = co0 + j;
+        const float* src = i < BN ? p.bias : (i < 2 * BN ? p.nw : p.nb);
+        Cs[i] = co < p.CO ? src[co] : 0.0f;
+    }
+
+    float4 pst[PPER], wst[WPER];
+    auto fetch = [&](int cc) {
+        const int ci0 = cc * 16;
+#pragma unroll
+        for (int i = 0; i < PPER; ++i) {
+            const int idx = tid + i * CW_THREADS;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (idx < PF4) {
+                const int pix = idx >> 2, c4 = (idx & 3) * 4;
+                const int py = pix / CW_P, px = pix - py * CW_P;
+                const int y = ty0 + py - 1, x = tx0 + px - 1;
+                const int ci = ci0 + c4;
+                if (y >= 0 && y < H && x >= 0 && x < W && ci < p.CI) {
+                    const float* src = p.in + ((size_t)y * W + x) * p.cin_stride + ci;
+                    if (ci + 3 < p.CI) {
+                        v = *(const float4*)src;
+                    } else {
+                        // channels past CI are padding and read as zero
+                        v.x = src[0];
+                        if (ci + 1 < p.CI) v.y = src[1];
+                        if (ci + 2 < p.CI) v.z = src[2];
+                    }
+                }
+            }
+            pst[i] = v;
+        }
+        // packed weights [chunk][tap][COp][16]: this block's BN rows of each tap
+        const float* wc = p.w + (size_t)cc * 9 * p.COp * 16;
+#pragma unroll
+        for (int i = 0; i < WPER; ++i) {
+            const int idx = tid + i * CW_THREADS;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (idx < WF4) {
+                const int row = idx >> 2, c4 = (idx & 3) * 4;
+                const int tap = row / BN, co = row - tap * BN;
+                if (co0 + co < p.COp) v = *(const float4*)(wc + ((size_t)tap * p.COp + co0 + co) * 16 + c4);
+            }
+            wst[i] = v;
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < PPER; ++i) {
+            const int idx = tid + i * CW_THREADS;
+            if (idx < PF4) *(float4*)(Ps + idx * 4) = pst[i];
+        }
+#pragma unroll
+        for (int i = 0; i < WPER; ++i) {
+            const int idx = tid + i * CW_THREADS;
+            if (idx < WF4) *(float4*)(Ws + idx * 4) = wst[i];
+        }
+    };
+
+    f32x4 acc[2][NT];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    const int nchunks = p.CIp / 16;
+    fetch(0);
+#pragma unroll 1
+    for (int cc = 0; cc < nchunks; ++cc) {
+        __syncthreads();  // every read of the previous chunk is done
+        stash();
+        __syncthreads();
+        if (cc + 1 < nchunks) fetch(cc + 1);
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const int dy = tap / 3, dx = tap - dy * 3;
+            f32x4 xv[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+                xv[mt] = *(const f32x4*)(Ps + ((wave * 2 + mt + dy) * CW_P + lr + dx) * 16 + lg * 4);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const f32x4 wv = *(const f32x4*)(Ws + (tap * BN + nt * 16 + lr) * 16 + lg * 4);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16(wv[s], xv[mt][s], acc[mt][nt]);
+            }
+        }
+    }
+
+    // Rows of the epilogue are pixels: m = y*W + x, 16 consecutive per tile row.
+    GemmArgs g{};
+    g.out = p.out;
+    g.res = p.res;
+    g.xn = p.xn;
+    g.M = H * W;
+    g.N = p.CO;
+    g.ldo = p.co_stride;
+    g.eps = p.eps;
+    const EpiConsts kc{Cs, LNOUT ? Cs + BN : nullptr, LNOUT ? Cs + 2 * BN : nullptr};
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        f32x4 a1[1][NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) a1[0][nt] = acc[mt][nt];
+        const int y = ty0 + wave * 2 + mt;
+        gemm_epilogue<1, NT, EPI>(g, kc, a1, y * W + tx0, co0, lr, lg, nullptr);
+    }
+}
+
+#define CONVW_INST(NAME, NT, EPI)                                                            \
+    extern "C" __global__ __launch_bounds__(CW_THREADS) void NAME(ConvArgs p)                \
+    {                                                                                        \
+        convw_body<NT, EPI>(p);                                                              \
+    }
+
+// C = 144 (NT = 9) trunk convs.
+CONVW_INST(hat_convw_n9_store_ln, 9, EPI_STORE_LN)
+CONVW_INST(hat_convw_n9_resid_ln, 9, EPI_RESID_LN)
+CONVW_INST(hat_convw_n9_resid, 9, EPI_RESID)

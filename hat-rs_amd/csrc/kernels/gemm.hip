@@ -60,7 +60,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts
                                               const f32x4 (*pres)[NT] = nullptr)
 {
     const int M = p.M, N = p.N;
-    constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN;
+    constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN || EPI == EPI_STORE_LN;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         const int m = mbase + mt * 16 + lr;

@@ -6,4 +6,5 @@
 #include "gemm.hip"
 #include "mlp.hip"
 #include "cab.hip"
+#include "convw.hip"
 #include "misc.hip"

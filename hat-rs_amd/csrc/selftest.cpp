@@ -473,6 +473,73 @@ int gpu_selftest(std::string* err)
             note("hat_gemmws_cab_ln proj + folded conv2 + norm2");
         }
 
+        // ---- trunk convs with every output channel in a block (C -> 144):
+        // residual (in place) + LayerNorm, conv_first's 3-channel input +
+        // LayerNorm, and a plain residual; 32 x 48 plane = 6 tiles.
+        {
+            struct WCase { int CI, cin_stride, epi; const char* k; };
+            const WCase wc[] = {{144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln"},
+                                {3, 4, EPI_STORE_LN, "hat_convw_n9_store_ln"},
+                                {144, 144, EPI_RESID, "hat_convw_n9_resid"}};
+            for (const WCase& c : wc) {
+                const int H = 32, W = 48, HW = H * W, CO = 144;
+                std::vector<float> in((size_t)HW * c.cin_stride, 0.0f);
+                for (int q = 0; q < HW; ++q)
+                    for (int ci = 0; ci < c.CI; ++ci) in[(size_t)q * c.cin_stride + ci] = rng.uni();
+                std::vector<float> w = rng.vec((size_t)CO * c.CI * 9, 0.05f), b = rng.vec(CO, 0.1f),
+                                   res = rng.vec((size_t)HW * CO, 1.0f), nw = rng.vec(CO, 1.0f),
+                                   nb = rng.vec(CO, 0.1f);
+                std::vector<float> bias;
+                int CIp = 0, COp = 0;
+                std::vector<float> pk = pack_conv(w.data(), b.data(), CO, c.CI, 0, &bias, &CIp, &COp);
+                Dev din(in), dw(pk), db(bias), dres(res), dnw(nw), dnb(nb), dxn((size_t)HW * CO);
+                ConvArgs p{};
+                p.in = din.p;
+                p.w = dw.p;
+                p.bias = db.p;
+                p.out = dres.p;  // in place over the residual
+                p.res = c.epi == EPI_STORE_LN ? nullptr : dres.p;
+                p.H = H;
+                p.W = W;
+                p.CI = c.CI;
+                p.CIp = CIp;
+                p.cin_stride = c.cin_stride;
+                p.CO = CO;
+                p.COp = COp;
+                p.co_stride = CO;
+                p.xn = dxn.p;
+                p.nw = dnw.p;
+                p.nb = dnb.p;
+                p.eps = 1e-5f;
+                launch(s, c.k, (W / 16) * (H / 16), 1, 1, 512, p);
+                std::vector<double> want((size_t)HW * CO), wxn((size_t)HW * CO);
+                for (int y = 0; y < H; ++y)
+                    for (int x = 0; x < W; ++x) {
+                        const size_t o = ((size_t)y * W + x) * CO;
+                        double mean = 0, var = 0;
+                        for (int co = 0; co < CO; ++co) {
+                            double v = b[co];
+                            for (int tap = 0; tap < 9; ++tap) {
+                                const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
+                                if (yy < 0 || yy >= H || xx < 0 || xx >= W) continue;
+                                for (int ci = 0; ci < c.CI; ++ci)
+                                    v += (double)w[((size_t)co * c.CI + ci) * 9 + tap] *
+                                         in[((size_t)yy * W + xx) * c.cin_stride + ci];
+                            }
+                            if (c.epi != EPI_STORE_LN) v += res[o + co];
+                            want[o + co] = v;
+                            mean += v / CO;
+                        }
+                        for (int co = 0; co < CO; ++co) var += (want[o + co] - mean) * (want[o + co] - mean) / CO;
+                        for (int co = 0; co < CO; ++co)
+                            wxn[o + co] = (want[o + co] - mean) / std::sqrt(var + 1e-5) * nw[co] + nb[co];
+                    }
+                check_close(c.k, dres.get(), want, 5e-5);
+                if (c.epi != EPI_RESID) check_close(std::string(c.k) + " layernorm", dxn.get(), wxn, 5e-5);
+                note(std::string(c.k) + " " + std::to_string(c.CI) + "->144, 32x48");
+            }
+        }
+
         // ---- convolutions (all epilogues) on a non-square plane.
         struct CCase { int CI, CO, epi, act, r; const char* what; };
         const CCase cases[] = {
