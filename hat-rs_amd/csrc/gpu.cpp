@@ -296,6 +296,19 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
 {
     if (H % 8 != 0 || W % 16 != 0) throw Error("conv: plane must be a multiple of 8x16");
     if (cin_stride % 4 != 0 || cin_stride < C.CI) throw Error("conv: bad input channel stride");
+    // The wide-tile kernel (16x16 pixels, a whole 64- or 128-channel column
+    // block per block) for the head convs and the 60-channel CAB conv.
+    const char* wide = nullptr;
+    int wbn = 0;
+    if (H % 16 == 0 && W % 16 == 0 && C.CO % 4 == 0 && co_stride % 4 == 0) {
+        if (epi == CEPI_STORE && C.CO > 16 && C.CO <= 64) {
+            wide = "hat_convw_n4_store";
+            wbn = 64;
+        } else if (epi == CEPI_SHUFFLE) {
+            wide = "hat_convw_n8_shuffle";
+            wbn = 128;
+        }
+    }
     const char* name = nullptr;
     int BN = 16;
     switch (epi) {
@@ -338,6 +351,10 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
         p.mean0 = mean[0];
         p.mean1 = mean[1];
         p.mean2 = mean[2];
+    }
+    if (wide) {
+        launch(s, wide, (unsigned)((W / 16) * (H / 16)), (unsigned)((C.CO + wbn - 1) / wbn), 1, 512, p);
+        return;
     }
     launch(s, name, (unsigned)((W / 16) * (H / 8)), (unsigned)((C.CO + BN - 1) / BN), 1, 256, p);
 }

@@ -24,7 +24,10 @@
 #define CW_WAVES 8
 #define CW_THREADS (CW_WAVES * 64)
 
-template <int NT, int EPI>
+// HEAD selects a head epilogue instead of a GEMM one: CEPI_SHUFFLE (store
+// into the PixelShuffle'd plane, channels pre-permuted at upload) or
+// CEPI_STORE (bias + activation); -1 = none (EPI applies).
+template <int NT, int EPI, int HEAD>
 __device__ __forceinline__ void convw_body(const ConvArgs& p)
 {
     constexpr int BN = 16 * NT;
@@ -140,6 +143,39 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
         }
     }
 
+    if (HEAD == CEPI_SHUFFLE || HEAD == CEPI_STORE) {
+        // Lane (lr, lg) holds channels co .. co+3 of pixel (y, x), x = tx0 + lr.
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int y = ty0 + wave * 2 + mt, x = tx0 + lr;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int j0 = nt * 16 + lg * 4, co = co0 + j0;
+                if (co >= p.CO) continue;
+                const float4 b4 = *(const float4*)(Cs + j0);
+                f32x4 v = acc[mt][nt] + (f32x4){b4.x, b4.y, b4.z, b4.w};
+                if (HEAD == CEPI_STORE) {
+                    if (p.act == 2) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) v[j] = v[j] < 0.0f ? v[j] * 0.01f : v[j];
+                    } else if (p.act == 1) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) v[j] = gelu(v[j]);
+                    }
+                    *(float4*)(p.out + ((size_t)y * W + x) * p.co_stride + co) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+                    // o' = (i*r + jj)*Cf + c lands at pixel (y*r + i, x*r + jj), channel c
+                    const int r = p.r, Cf = p.CO / (r * r);
+                    const int sub = co / Cf, c = co - sub * Cf;
+                    const int i = sub / r, jj = sub - i * r;
+                    *(float4*)(p.out + ((size_t)(y * r + i) * (W * r) + x * r + jj) * p.co_stride + c) =
+                        make_float4(v[0], v[1], v[2], v[3]);
+                }
+            }
+        }
+        return;
+    }
+
     // Rows of the epilogue are pixels: m = y*W + x, 16 consecutive per tile row.
     GemmArgs g{};
     g.out = p.out;
@@ -160,13 +196,17 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
     }
 }
 
-#define CONVW_INST(NAME, NT, EPI)                                                            \
+#define CONVW_INST(NAME, NT, EPI, HEAD)                                                      \
     extern "C" __global__ __launch_bounds__(CW_THREADS) void NAME(ConvArgs p)                \
     {                                                                                        \
-        convw_body<NT, EPI>(p);                                                              \
+        convw_body<NT, EPI, HEAD>(p);                                                        \
     }
 
 // C = 144 (NT = 9) trunk convs.
-CONVW_INST(hat_convw_n9_store_ln, 9, EPI_STORE_LN)
-CONVW_INST(hat_convw_n9_resid_ln, 9, EPI_RESID_LN)
-CONVW_INST(hat_convw_n9_resid, 9, EPI_RESID)
+CONVW_INST(hat_convw_n9_store_ln, 9, EPI_STORE_LN, -1)
+CONVW_INST(hat_convw_n9_resid_ln, 9, EPI_RESID_LN, -1)
+CONVW_INST(hat_convw_n9_resid, 9, EPI_RESID, -1)
+// Head: conv_before_upsample (-> 64, LeakyReLU) and the upsample convs
+// (64 -> 4*64 or 9*64 in 128-channel column blocks, + PixelShuffle).
+CONVW_INST(hat_convw_n4_store, 4, EPI_STORE, CEPI_STORE)
+CONVW_INST(hat_convw_n8_shuffle, 8, EPI_STORE, CEPI_SHUFFLE)

@@ -662,6 +662,18 @@ int gpu_selftest(std::string* err)
                 check_close(std::string(name) + " partial sums", dpart.get(), ps, 5e-4);
             }
             note(std::string(name) + "  " + cc.what + "  32x48");
+            // The wide-tile kernel serves the same store / shuffle cases.
+            const char* wide = cc.epi == CEPI_STORE && cc.CO > 16 && cc.CO <= 64 ? "hat_convw_n4_store"
+                               : cc.epi == CEPI_SHUFFLE                           ? "hat_convw_n8_shuffle"
+                                                                                  : nullptr;
+            if (wide) {
+                const int wbn = cc.epi == CEPI_SHUFFLE ? 128 : 64;
+                Dev dout2(out_n);
+                p.out = dout2.p;
+                launch(s, wide, (W / 16) * (H / 16), (cc.CO + wbn - 1) / wbn, 1, 512, p);
+                check_close(std::string(wide) + " " + cc.what, dout2.get(), want, 5e-5);
+                note(std::string(wide) + "  " + cc.what + "  32x48");
+            }
         }
 
         // ---- LayerNorm, input preparation, squeeze-excite.
