@@ -61,34 +61,54 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
         const int ty = tile / ntx, tx = tile - ty * ntx;
         const int y0 = ty * 16, x0 = tx * 16;
 
-        for (int rt = wave; rt < CC1_RT; rt += 4) {
-            const int hi = rt * 16 + lr;
+        // This wave's halo row tiles rt = wave, wave + 4, ... are walked as one
+        // stream of 16-channel chunks (9 per row tile), the input rows held in
+        // three register slots loaded three chunks ahead of their MFMAs, across
+        // row-tile boundaries.
+        const int nrt = (CC1_RT - wave + 3) / 4;
+        auto src_of = [&](int i) -> const float* {  // lane's input row of row tile i, or null
+            const int hi = (wave + 4 * i) * 16 + lr;
             const int hy = hi / CC1_HS, hx = hi - hy * CC1_HS;
             const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
-            const bool valid = hi < CC1_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
-            const float* src = p.xn + (size_t)(valid ? gy * W + gx : 0) * CAB_C + lg * 4;
-            f32x4 a[CAB_C / 16];
+            const bool valid = i < nrt && hi < CC1_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
+            return valid ? p.xn + (size_t)(gy * W + gx) * CAB_C + lg * 4 : nullptr;
+        };
+        f32x4 xa[3];
+        auto load = [&](int slot, const float* src, int kc) {
+            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+            if (src) v = *(const f32x4*)(src + kc * 16);
+            xa[slot] = v;
+        };
+        const float* cur = src_of(0);
+        const float* nxt = src_of(1);
 #pragma unroll
-            for (int kc = 0; kc < CAB_C / 16; ++kc) {
-                f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-                if (valid) v = *(const f32x4*)(src + kc * 16);
-                a[kc] = v;
-            }
+        for (int s = 0; s < 3; ++s) load(s, cur, s);
+#pragma unroll 1
+        for (int i = 0; i < nrt; ++i) {
             f32x4 acc[4];
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) acc[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kc = 0; kc < CAB_C / 16; ++kc)
+            for (int kc = 0; kc < CAB_C / 16; ++kc) {
+                const int slot = kc % 3;
+                const f32x4 a = xa[slot];
+                // chunk kc + 3 of this row tile, or chunk kc - 6 of the next
+                if (kc + 3 < CAB_C / 16) load(slot, cur, kc + 3);
+                else load(slot, nxt, kc + 3 - CAB_C / 16);
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
 #pragma unroll
-                    for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16(wreg[nt][kc][s], a[kc][s], acc[nt]);
+                    for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16(wreg[nt][kc][s], a[s], acc[nt]);
+            }
             // lane (lr, lg) holds P[hi][16nt + 4lg .. +3]; columns 56.. are not stored
+            const int hi = (wave + 4 * i) * 16 + lr;
             if (hi < CC1_HP) {
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt)
                     if (nt * 16 + lg * 4 < CC1_PS) *(f32x4*)(Ps + hi * CC1_PS + nt * 16 + lg * 4) = acc[nt];
             }
+            cur = nxt;
+            nxt = src_of(i + 2);
         }
         __syncthreads();
 
@@ -116,20 +136,24 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
         *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
         *(float4*)(dst + 4) = make_float4(v[4], v[5], 0.f, 0.f);
 
-        // Per-tile sums: the tile, and its pixels on row 0, row H-1, col 0, col W-1.
+        // Per-tile sums: the tile, and its pixels on row 0, row H-1, col 0,
+        // col W-1 - only tiles on the plane's border have any of the latter.
+        const bool border = y0 == 0 || y0 + 16 == H || x0 == 0 || x0 + 16 == W;  // tile-uniform
         const bool line[CAB_NSUM] = {true, gy == 0, gy == H - 1, gx == 0, gx == W - 1};
 #pragma unroll
-        for (int l = 0; l < CAB_NSUM; ++l)
+        for (int l = 0; l < CAB_NSUM; ++l) {
+            if (l > 0 && !border) break;
 #pragma unroll
             for (int co = 0; co < CAB_CC; ++co) {
                 const float s = wave_sum(line[l] ? v[co] : 0.0f);
                 if (lane == 0) red[wave][l * CAB_CC + co] = s;
             }
+        }
         __syncthreads();
         if (tid < CAB_NSUM * CAB_CS) {
             const int l = tid / CAB_CS, co = tid - l * CAB_CS;
             float s = 0.0f;
-            if (co < CAB_CC) {
+            if (co < CAB_CC && (l == 0 || border)) {
                 const int i = l * CAB_CC + co;
                 s = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
             }
