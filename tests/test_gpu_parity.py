@@ -200,3 +200,48 @@ def test_hat_s_512_full_size(hl, weights_dir):
     assert np.isfinite(y1).all()
     assert np.array_equal(y1, y2)
     assert abs(float(y1.mean()) - float(img.mean())) < 0.2
+
+
+def test_cfg4_hat_full_depth(hl, weights_dir):
+    """Benchmark config 4's network, HAT x4 (C = 180, 6 stages x 6 HABs, the
+    compress-3 CAB on the unfolded path): the full depth against the oracle at
+    32x48, then the config's own size, 256x256, through the size-independent
+    properties of the 512x512 test."""
+    import oracle
+    wp = make_weights(weights_dir, "hat", 4, 4, None)
+    be = hl.Backend(hl.Weights(wp))
+    rng = np.random.default_rng(44)
+    small = rng.random((3, 32, 48), dtype=np.float32)
+    _say("forward HAT x4 32x48 (full depth) vs oracle")
+    got = be.forward(32, 48, small)
+    orc = oracle.OracleModel(wp).forward(32, 48, small)
+    worst = np.abs(got - orc).max()
+    _say(f"  worst |diff| vs oracle {worst:.3e}")
+    assert worst < FWD_TOL
+    img = rng.random((3, 256, 256), dtype=np.float32)
+    _say("forward HAT x4 256x256 (cfg4)")
+    y1 = be.forward(256, 256, img)
+    y2 = be.forward(256, 256, img)
+    assert y1.shape == (3, 1024, 1024)
+    assert np.isfinite(y1).all()
+    assert np.array_equal(y1, y2)
+    assert abs(float(y1.mean()) - float(img.mean())) < 0.2
+
+
+def test_cfg5_hat_l_512_single_pass(hl, weights_dir):
+    """Benchmark config 5: HAT-L x4 (12 stages) at 512x512 in a single pass.
+    Finite, bit-exact on a second run, the image mean preserved; the per-plan
+    working set is reported (the reference's buffers: 7.8 GiB, README.md:141)."""
+    wp = make_weights(weights_dir, "hat-l", 4, 5, None)
+    W = hl.Weights(wp)
+    be = hl.Backend(W)
+    img = np.random.default_rng(55).random((3, 512, 512), dtype=np.float32)
+    _say("forward HAT-L x4 512x512 (cfg5)")
+    y1 = be.forward(512, 512, img)
+    _say(f"  per-plan buffers {be.acts_bytes() / 2**30:.2f} GiB, weights {be.weight_bytes() / 2**20:.1f} MiB")
+    y2 = be.forward(512, 512, img)
+    assert y1.shape == (3, 2048, 2048)
+    assert np.isfinite(y1).all()
+    assert np.array_equal(y1, y2)
+    assert abs(float(y1.mean()) - float(img.mean())) < 0.2
+    assert be.acts_bytes() < 8 * 2**30
