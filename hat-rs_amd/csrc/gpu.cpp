@@ -428,7 +428,9 @@ void run_ln(hipStream_t s, const float* x, float* y, const float* w, const float
 {
     if (C > 512) throw Error("layernorm: C > 512");
     LnArgs p{x, y, w, b, (int)rows, C, 1e-5f};
-    launch(s, "hat_layernorm", (unsigned)((rows + 3) / 4), 1, 1, 256, p);
+    // 16 rows per block when C % 4 == 0 and C <= 192, else 4 (one per wave)
+    const long per = (C % 4 == 0 && C <= 192) ? 16 : 4;
+    launch(s, "hat_layernorm", (unsigned)((rows + per - 1) / per), 1, 1, 256, p);
 }
 
 }  // namespace

@@ -3,35 +3,77 @@
 
 using namespace hatk;
 
-// LayerNorm over the channel axis of token-major rows (the reference's
-// layer_norm, cpu.rs:563-581, and lg_channel_layer_norm, cuda.rs:185-191):
-// two-pass mean then biased variance, y = (x - mean) * rstd * w + b.
-// One wave per row; y may alias x.
+// LayerNorm over C channels of each row (lg_channel_layer_norm, cuda.rs:185-191;
+// cpu.rs:563-581): two-pass mean then biased variance, y = (x - mean) * rstd *
+// w + b; y may alias x. For C % 4 == 0, C <= 192 (the models' 144 and 180): a
+// row per 16 lanes, four rows per wave, each lane holding up to three float4 of
+// its row, the sums reduced within the 16 lanes. Otherwise one wave per row.
 extern "C" __global__ __launch_bounds__(256) void hat_layernorm(LnArgs p)
 {
     const int lane = threadIdx.x & 63;
+    const int C = p.C;
+    if ((C & 3) == 0 && C <= 192) {
+        const int g = lane & 15;
+        const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+        if (row >= p.rows) return;  // whole 16-lane groups leave together
+        const int n4 = C >> 2;
+        const float4* x = (const float4*)(p.x + (size_t)row * C);
+        float4 v[3];
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            const int k = g + 16 * t;
+            v[t] = k < n4 ? x[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+            s += (v[t].x + v[t].y) + (v[t].z + v[t].w);
+        }
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+        const float mean = s / (float)C;
+        float q = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            if (g + 16 * t < n4) {
+                const float a = v[t].x - mean, b = v[t].y - mean, c = v[t].z - mean, d = v[t].w - mean;
+                q += (a * a + b * b) + (c * c + d * d);
+            }
+        }
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
+        const float rstd = 1.0f / sqrtf(q / (float)C + p.eps);
+        float4* y = (float4*)(p.y + (size_t)row * C);
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            const int k = g + 16 * t;
+            if (k < n4) {
+                const float4 w = ((const float4*)p.w)[k], b = ((const float4*)p.b)[k];
+                y[k] = make_float4((v[t].x - mean) * rstd * w.x + b.x, (v[t].y - mean) * rstd * w.y + b.y,
+                                   (v[t].z - mean) * rstd * w.z + b.z, (v[t].w - mean) * rstd * w.w + b.w);
+            }
+        }
+        return;
+    }
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= p.rows) return;
-    const float* x = p.x + (size_t)row * p.C;
-    float* y = p.y + (size_t)row * p.C;
+    const float* x = p.x + (size_t)row * C;
+    float* y = p.y + (size_t)row * C;
     float v[8];
     int n = 0;
     float s = 0.0f;
-    for (int k = lane; k < p.C; k += 64) {
+    for (int k = lane; k < C; k += 64) {
         v[n] = x[k];
         s += v[n];
         ++n;
     }
-    const float mean = wave_sum(s) / (float)p.C;
+    const float mean = wave_sum(s) / (float)C;
     float q = 0.0f;
     for (int i = 0; i < n; ++i) {
         const float d = v[i] - mean;
         q += d * d;
     }
-    const float var = wave_sum(q) / (float)p.C;
+    const float var = wave_sum(q) / (float)C;
     const float rstd = 1.0f / sqrtf(var + p.eps);
     n = 0;
-    for (int k = lane; k < p.C; k += 64, ++n) y[k] = (v[n] - mean) * rstd * p.w[k] + p.b[k];
+    for (int k = lane; k < C; k += 64, ++n) y[k] = (v[n] - mean) * rstd * p.w[k] + p.b[k];
 }
 
 // Pre::adjust (backend.rs:71-89): edge-replicated padding to the window grid and

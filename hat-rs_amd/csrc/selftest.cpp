@@ -677,12 +677,16 @@ int gpu_selftest(std::string* err)
         }
 
         // ---- LayerNorm, input preparation, squeeze-excite.
-        {
-            const int rows = 300, C = 180;
+        // C = 144 and 180 take the 16-lanes-per-row path (16 rows per block),
+        // C = 196 the one-wave-per-row path (4 rows per block); 300 rows leave
+        // partial blocks in both.
+        for (int C : {144, 180, 196}) {
+            const int rows = 300;
             std::vector<float> x = rng.vec((size_t)rows * C, 2.0f), w = rng.vec(C, 1.0f), b = rng.vec(C, 0.5f);
             Dev dx(x), dw(w), db(b), dy((size_t)rows * C);
             LnArgs p{dx.p, dy.p, dw.p, db.p, rows, C, 1e-5f};
-            launch(s, "hat_layernorm", (rows + 3) / 4, 1, 1, 256, p);
+            const int per = (C % 4 == 0 && C <= 192) ? 16 : 4;
+            launch(s, "hat_layernorm", (rows + per - 1) / per, 1, 1, 256, p);
             std::vector<double> want((size_t)rows * C);
             for (int r = 0; r < rows; ++r) {
                 double mean = 0, var = 0;
@@ -693,8 +697,8 @@ int gpu_selftest(std::string* err)
                 for (int c = 0; c < C; ++c)
                     want[(size_t)r * C + c] = (x[(size_t)r * C + c] - mean) / std::sqrt(var + 1e-5) * w[c] + b[c];
             }
-            check_close("hat_layernorm", dy.get(), want, 1e-5);
-            note("hat_layernorm 300x180");
+            check_close("hat_layernorm C " + std::to_string(C), dy.get(), want, 1e-5);
+            note("hat_layernorm 300x" + std::to_string(C));
         }
         {
             const int h = 21, w = 35, hp = 32, wp = 48;
