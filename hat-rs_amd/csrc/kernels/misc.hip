@@ -96,12 +96,21 @@ extern "C" __global__ __launch_bounds__(256) void hat_pre(PreArgs p)
 
 // A plain copy of n float4 (the HBM reference point the traffic counters of the
 // other kernels are scaled by; also the library's device-to-device copy).
+// Four loads in flight per thread, each warp-contiguous.
 extern "C" __global__ __launch_bounds__(256) void hat_copy(CopyArgs p)
 {
     const float4* src = (const float4*)p.src;
     float4* dst = (float4*)p.dst;
-    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < p.n4; i += (long)gridDim.x * 256)
-        dst[i] = src[i];
+    const long stride = (long)gridDim.x * 256;
+    long i = (long)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < p.n4; i += 4 * stride) {
+        const float4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        dst[i] = a;
+        dst[i + stride] = b;
+        dst[i + 2 * stride] = c;
+        dst[i + 3 * stride] = d;
+    }
+    for (; i < p.n4; i += stride) dst[i] = src[i];
 }
 
 // First stage of the channel-attention pool (lg_channel_mean, cuda.rs:259-272):

@@ -245,3 +245,21 @@ def test_cfg5_hat_l_512_single_pass(hl, weights_dir):
     assert np.array_equal(y1, y2)
     assert abs(float(y1.mean()) - float(img.mean())) < 0.2
     assert be.acts_bytes() < 8 * 2**30
+
+
+@pytest.mark.parametrize("n4", [1, 257, 4 * 256 * 16384 + 5, 9 * 256 * 16384 + 3])
+def test_device_copy_exact(hl, n4):
+    """The library's copy kernel (bench.py's HBM reference): bit-exact at sizes
+    below one block, past whole unrolled sweeps of the 16384-block grid, and
+    with a tail; the bytes after the copied range are untouched."""
+    rng = np.random.default_rng(n4)
+    src = rng.standard_normal(4 * n4 + 8).astype(np.float32)
+    ds, dd = hl.DeviceBuffer(src.nbytes), hl.DeviceBuffer(src.nbytes)
+    ds.upload(src)
+    guard = np.full_like(src, 7.0)
+    dd.upload(guard)
+    hl.device_copy(dd, ds, 16 * n4)
+    hl.synchronize()
+    got = dd.download(np.empty_like(src))
+    assert np.array_equal(got[: 4 * n4], src[: 4 * n4])
+    assert np.array_equal(got[4 * n4:], guard[4 * n4:])
