@@ -362,7 +362,7 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
 // A C -> 144 3x3 conv with every output channel in one block and a GEMM
 // epilogue: EPI_STORE_LN (out, xn = LN(out)), EPI_RESID_LN (out = conv + res,
 // xn = LN(out)) or EPI_RESID. out may alias res; in, out and xn must not overlap.
-bool convw_fits(const DevConv& C) { return C.CO == 144 && C.COp == 144 && C.r == 0; }
+bool convw_fits(const DevConv& C) { return C.r == 0 && C.CO == 144 && C.COp == 144; }
 
 void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride, int H, int W,
                float* out, int epi, const float* res, float* xn, const float* nw, const float* nb)

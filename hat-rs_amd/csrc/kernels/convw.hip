@@ -8,8 +8,8 @@
 // 722, 742 with the lg_add and lg_channel_layer_norm passes that follow them
 // (cuda.rs:227-248, 185-191).
 //
-// A block owns a 16x16 pixel tile; 8 waves, wave w owns tile rows 2w and 2w+1
-// (two 16-pixel MFMA tiles, lane l%16 is the pixel's x). Input channels are
+// A block owns a 16x16 pixel tile; 8 waves owning two tile rows each; a tile
+// row is one 16-pixel MFMA tile, lane l%16 the pixel's x. Input channels are
 // walked in chunks of 16: the chunk's 18x18 halo patch and its [9 taps][BN][16]
 // weight slice are staged in LDS (with BN = 144: 20.7 KB + 83 KB), the next
 // chunk's data travelling through registers while this chunk's MFMAs run, and
@@ -21,15 +21,16 @@
 #define CW_T 16                        // output tile side
 #define CW_P (CW_T + 2)                // halo side
 #define CW_PX (CW_P * CW_P)            // 324 halo pixels
-#define CW_WAVES 8
-#define CW_THREADS (CW_WAVES * 64)
 
 // HEAD selects a head epilogue instead of a GEMM one: CEPI_SHUFFLE (store
 // into the PixelShuffle'd plane, channels pre-permuted at upload) or
 // CEPI_STORE (bias + activation); -1 = none (EPI applies).
-template <int NT, int EPI, int HEAD>
+template <int NT, int EPI, int HEAD, int WAVES>
 __device__ __forceinline__ void convw_body(const ConvArgs& p)
 {
+    constexpr int MT = CW_T / WAVES;               // tile rows per wave
+    constexpr int CW_THREADS = WAVES * 64;
+    static_assert(MT * WAVES == CW_T, "waves must split the tile rows");
     constexpr int BN = 16 * NT;
     constexpr int PF4 = CW_PX * 4;                 // patch float4 per chunk
     constexpr int WF4 = 9 * BN * 4;                // weight float4 per chunk
@@ -111,9 +112,9 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
         }
     };
 
-    f32x4 acc[2][NT];
+    f32x4 acc[MT][NT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
@@ -128,17 +129,17 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
 #pragma unroll
         for (int tap = 0; tap < 9; ++tap) {
             const int dy = tap / 3, dx = tap - dy * 3;
-            f32x4 xv[2];
+            f32x4 xv[MT];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-                xv[mt] = *(const f32x4*)(Ps + ((wave * 2 + mt + dy) * CW_P + lr + dx) * 16 + lg * 4);
+            for (int mt = 0; mt < MT; ++mt)
+                xv[mt] = *(const f32x4*)(Ps + ((wave * MT + mt + dy) * CW_P + lr + dx) * 16 + lg * 4);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const f32x4 wv = *(const f32x4*)(Ws + (tap * BN + nt * 16 + lr) * 16 + lg * 4);
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
 #pragma unroll
-                    for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16(wv[s], xv[mt][s], acc[mt][nt]);
+                    for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16(wv[s], xv[mt][s], acc[mt][nt]);
             }
         }
     }
@@ -146,8 +147,8 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
     if (HEAD == CEPI_SHUFFLE || HEAD == CEPI_STORE) {
         // Lane (lr, lg) holds channels co .. co+3 of pixel (y, x), x = tx0 + lr.
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const int y = ty0 + wave * 2 + mt, x = tx0 + lr;
+        for (int mt = 0; mt < MT; ++mt) {
+            const int y = ty0 + wave * MT + mt, x = tx0 + lr;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const int j0 = nt * 16 + lg * 4, co = co0 + j0;
@@ -187,19 +188,23 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
     g.eps = p.eps;
     const EpiConsts kc{Cs, LNOUT ? Cs + BN : nullptr, LNOUT ? Cs + 2 * BN : nullptr};
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
         f32x4 a1[1][NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) a1[0][nt] = acc[mt][nt];
-        const int y = ty0 + wave * 2 + mt;
+        const int y = ty0 + wave * MT + mt;
         gemm_epilogue<1, NT, EPI>(g, kc, a1, y * W + tx0, co0, lr, lg, nullptr);
     }
 }
 
+// Waves per block: 8, two tile rows each (the instances here have at most
+// 144 channels; wider blocks would need one row per wave).
+constexpr int convw_waves(int nt) { return nt > 9 ? 16 : 8; }
+
 #define CONVW_INST(NAME, NT, EPI, HEAD)                                                      \
-    extern "C" __global__ __launch_bounds__(CW_THREADS) void NAME(ConvArgs p)                \
+    extern "C" __global__ __launch_bounds__(convw_waves(NT) * 64) void NAME(ConvArgs p)      \
     {                                                                                        \
-        convw_body<NT, EPI, HEAD>(p);                                                        \
+        convw_body<NT, EPI, HEAD, convw_waves(NT)>(p);                                       \
     }
 
 // C = 144 (NT = 9) trunk convs.

@@ -477,12 +477,12 @@ int gpu_selftest(std::string* err)
         // residual (in place) + LayerNorm, conv_first's 3-channel input +
         // LayerNorm, and a plain residual; 32 x 48 plane = 6 tiles.
         {
-            struct WCase { int CI, cin_stride, epi; const char* k; };
-            const WCase wc[] = {{144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln"},
-                                {3, 4, EPI_STORE_LN, "hat_convw_n9_store_ln"},
-                                {144, 144, EPI_RESID, "hat_convw_n9_resid"}};
+            struct WCase { int CI, cin_stride, CO, epi; const char* k; };
+            const WCase wc[] = {{144, 144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln"},
+                                {3, 4, 144, EPI_STORE_LN, "hat_convw_n9_store_ln"},
+                                {144, 144, 144, EPI_RESID, "hat_convw_n9_resid"}};
             for (const WCase& c : wc) {
-                const int H = 32, W = 48, HW = H * W, CO = 144;
+                const int H = 32, W = 48, HW = H * W, CO = c.CO;
                 std::vector<float> in((size_t)HW * c.cin_stride, 0.0f);
                 for (int q = 0; q < HW; ++q)
                     for (int ci = 0; ci < c.CI; ++ci) in[(size_t)q * c.cin_stride + ci] = rng.uni();
@@ -536,7 +536,7 @@ int gpu_selftest(std::string* err)
                     }
                 check_close(c.k, dres.get(), want, 5e-5);
                 if (c.epi != EPI_RESID) check_close(std::string(c.k) + " layernorm", dxn.get(), wxn, 5e-5);
-                note(std::string(c.k) + " " + std::to_string(c.CI) + "->144, 32x48");
+                note(std::string(c.k) + " " + std::to_string(c.CI) + "->" + std::to_string(CO) + ", 32x48");
             }
         }
 
