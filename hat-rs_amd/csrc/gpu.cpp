@@ -86,16 +86,21 @@ const char* gemm_kernel(int N, int epi)
     throw Error("unknown GEMM epilogue");
 }
 
-// The weight-stationary kernel covers K = 144 (the whole weight row slice sits
-// in LDS) and N a multiple of 144, for the epilogues the C = 144 blocks use.
-const char* gemm_ws_kernel(const DevLinear& L, int epi)
+// The weight-stationary kernels hold a block's whole weight row slice in LDS:
+// K = 144 with 144-wide column blocks (N a multiple of 144), and K = 180
+// (rows padded to 192) with 192-wide blocks, for the epilogues the blocks use.
+// Returns the kernel and sets *bn to its column-block width.
+const char* gemm_ws_kernel(const DevLinear& L, int epi, int* bn)
 {
-    if (L.K != 144 || L.Kp != 144 || L.N % 144 != 0) return nullptr;
+    const bool k144 = L.K == 144 && L.Kp == 144 && L.N % 144 == 0;
+    const bool k180 = L.K == 180 && L.Kp == 192;
+    if (!k144 && !k180) return nullptr;
+    *bn = k144 ? 144 : 192;
     switch (epi) {
-    case EPI_QKV: return "hat_gemmws_qkv";
-    case EPI_GELU: return "hat_gemmws_gelu";
-    case EPI_RESID_LN: return "hat_gemmws_resid_ln";
-    case EPI_HAB_LN: return "hat_gemmws_hab_ln";
+    case EPI_QKV: return k144 ? "hat_gemmws_qkv" : "hat_gemmws12_qkv";
+    case EPI_GELU: return k144 ? "hat_gemmws_gelu" : "hat_gemmws12_gelu";
+    case EPI_RESID_LN: return k144 ? "hat_gemmws_resid_ln" : "hat_gemmws12_resid_ln";
+    case EPI_HAB_LN: return k144 ? "hat_gemmws_hab_ln" : "hat_gemmws12_hab_ln";
     }
     return nullptr;
 }
@@ -141,14 +146,15 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
     p.hdim = hdim;
     p.cscale = cscale;
     p.eps = 1e-5f;
-    if (const char* ws = gemm_ws_kernel(L, epi)) {
-        // One block per CU (its 85 KB weight slice fills the LDS), the CUs
+    int wbn = 0;
+    if (const char* ws = gemm_ws_kernel(L, epi, &wbn)) {
+        // One block per CU (its 85 or 150 KB weight slice fills the LDS), the CUs
         // split evenly over the column slices; each block walks the row tiles
         // of its slice. Fewest blocks for the same number of rounds, so no CU
         // gets a tile more than the others need.
         static const int cus = std::max(1, Runtime::get().cu_count());
         const long ntiles = (M + ws_rows(epi) - 1) / ws_rows(epi);
-        const int slices = L.N / 144;
+        const int slices = (L.N + wbn - 1) / wbn;
         const long per = std::max(1, cus / slices);
         const long rounds = (ntiles + per - 1) / per;
         const long g = std::max(1L, (ntiles + rounds - 1) / rounds);

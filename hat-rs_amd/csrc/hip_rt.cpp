@@ -22,6 +22,7 @@ const std::vector<std::string>& required_kernels()
         "hat_gemm_n12_store",  "hat_gemm_n12_gelu",   "hat_gemm_n12_qkv",   "hat_gemm_n12_resid",
         "hat_gemm_n12_resid_ln", "hat_gemm_n12_hab_ln",
         "hat_gemmws_qkv",      "hat_gemmws_gelu",     "hat_gemmws_resid_ln", "hat_gemmws_hab_ln",
+        "hat_gemmws12_qkv",    "hat_gemmws12_gelu",   "hat_gemmws12_resid_ln", "hat_gemmws12_hab_ln",
         "hat_mlp_resid",       "hat_mlp_resid_ln",    "hat_gemmws_cab_ln",  "hat_cab_conv1",
         "hat_cab_gate",        "hat_convw_n9_store_ln", "hat_convw_n9_resid_ln", "hat_convw_n9_resid",
         "hat_convw_n4_store",  "hat_convw_n8_shuffle",

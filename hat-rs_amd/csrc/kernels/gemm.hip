@@ -276,14 +276,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
 // overlap the other waves' MFMAs. The MFMA arrangement and the epilogue are
 // the ones of gemm_body (a lane's four accumulators are four consecutive
 // columns).
-#define WS_K 144
-#define WS_KS (WS_K + 4)  // LDS row stride of the weight slice
-
-template <int EPI, int MT, int WAVES, bool CAB>
+// KP: the weight rows' padded K (144, or 192 for K = 180), a multiple of 48;
+// NT: 16-column tiles per block (9, or 12 for the C = 180 family).
+template <int EPI, int MT, int WAVES, bool CAB, int KP, int NT>
 __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 {
     constexpr int ROWS = WAVES * 16 * MT;  // rows per tile
-    constexpr int NT = 9, BN = 144, NCH = WS_K / 16;
+    constexpr int BN = 16 * NT, NCH = KP / 16;
+    constexpr int WS_K = KP, WS_KS = KP + 4;  // LDS row stride of the weight slice
+    static_assert(NCH % 3 == 0, "the K loop walks groups of three chunks");
+    static_assert(!CAB || (KP == 144 && NT == 9), "the folded CAB is the C = 144 family's");
     constexpr int S2 = CAB_K2 + 4;         // LDS row stride of the conv2 slice
     __shared__ float Wsm[BN * WS_KS];
     __shared__ float W2s[CAB ? BN * S2 : 1];
@@ -339,11 +341,14 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         // the MFMAs that use them (the chunk loop is rolled over groups of 3 so
         // the slots are fixed registers).
         f32x4 xa[3][MT];
+        // k beyond K (K = 180 in 192) reads as zero: past it lies the next row
+        const bool kin_last = (NCH - 1) * 16 + lg * 4 < p.K;
         auto load_a = [&](int slot, int kc) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-                if (alive[mt]) v = *(const f32x4*)(arow[mt] + kc * 16);
+                if (alive[mt] && (KP == 144 || kc < NCH - 1 || kin_last))
+                    v = *(const f32x4*)(arow[mt] + kc * 16);
                 xa[slot][mt] = v;
             }
         };
@@ -433,10 +438,10 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
     }
 }
 
-#define GEMM_WS_INST(NAME, EPI)                                                              \
+#define GEMM_WS_INST(NAME, EPI, KP, NT)                                                      \
     extern "C" __global__ __launch_bounds__(ws_waves(EPI) * 64) void NAME(GemmArgs p)          \
     {                                                                                          \
-        gemm_ws_body<EPI, ws_mt(EPI), ws_waves(EPI), false>(p);                                \
+        gemm_ws_body<EPI, ws_mt(EPI), ws_waves(EPI), false, KP, NT>(p);                        \
     }
 
 // NT = 9: 144-wide column blocks (HAT-S: N = 144, 288, 432 divide exactly).
@@ -456,14 +461,20 @@ GEMM_INST(hat_gemm_n12_hab_ln, 12, EPI_HAB_LN)
 
 // K = 144 weight-stationary instances (HAT-S: qkv N = 432, fc1 N = 288, attention
 // proj and OCAB proj N = 144).
-GEMM_WS_INST(hat_gemmws_qkv, EPI_QKV)
-GEMM_WS_INST(hat_gemmws_gelu, EPI_GELU)
-GEMM_WS_INST(hat_gemmws_resid_ln, EPI_RESID_LN)
-GEMM_WS_INST(hat_gemmws_hab_ln, EPI_HAB_LN)
+GEMM_WS_INST(hat_gemmws_qkv, EPI_QKV, 144, 9)
+GEMM_WS_INST(hat_gemmws_gelu, EPI_GELU, 144, 9)
+GEMM_WS_INST(hat_gemmws_resid_ln, EPI_RESID_LN, 144, 9)
+GEMM_WS_INST(hat_gemmws_hab_ln, EPI_HAB_LN, 144, 9)
+// K = 180 (padded to 192), 192-wide column blocks: the C = 180 family's qkv
+// (N = 540 in 3 blocks), fc1 (N = 360 in 2) and projections (N = 180).
+GEMM_WS_INST(hat_gemmws12_qkv, EPI_QKV, 192, 12)
+GEMM_WS_INST(hat_gemmws12_gelu, EPI_GELU, 192, 12)
+GEMM_WS_INST(hat_gemmws12_resid_ln, EPI_RESID_LN, 192, 12)
+GEMM_WS_INST(hat_gemmws12_hab_ln, EPI_HAB_LN, 192, 12)
 
 // HAB attention projection with the CAB's conv2 folded in as 80 more K (the
 // block input as residual, bias = proj bias + folded conv2 bias), then norm2.
 extern "C" __global__ __launch_bounds__(ws_waves(EPI_RESID_LN) * 64) void hat_gemmws_cab_ln(GemmArgs p)
 {
-    gemm_ws_body<EPI_RESID_LN, ws_mt(EPI_RESID_LN), ws_waves(EPI_RESID_LN), true>(p);
+    gemm_ws_body<EPI_RESID_LN, ws_mt(EPI_RESID_LN), ws_waves(EPI_RESID_LN), true, 144, 9>(p);
 }

@@ -207,9 +207,10 @@ int gpu_selftest(std::string* err)
         // LayerNorm epilogues also check the normalised rows they write.
         const int epis[6] = {EPI_STORE, EPI_GELU, EPI_QKV, EPI_RESID, EPI_RESID_LN, EPI_HAB_LN};
         const char* enames[7] = {"store", "gelu", "qkv", "resid", "", "resid_ln", "hab_ln"};
-        // ws: the weight-stationary K = 144 kernel, on 600 rows (3 or 5 row
-        // tiles, the last one partial) with two blocks per column slice, so a
-        // block walks several tiles.
+        // ws: the weight-stationary kernels (K = 144; K = 180 padded to 192, whose
+        // last K chunk must not read past a row's 180 values), on 600 rows (3 or
+        // 5 row tiles, the last one partial) with two blocks per column slice, so
+        // a block walks several tiles.
         auto gemm_case = [&](int C, int epi, bool ws) {
                 const int heads = 6, hd = C / heads;
                 const int M = ws ? 600 : 200;  // not a multiple of the row tile
@@ -249,8 +250,9 @@ int gpu_selftest(std::string* err)
                 const int BN = n9 ? 144 : 192;
                 std::string k;
                 if (ws) {
-                    k = std::string("hat_gemmws_") + enames[epi];
-                    launch(s, k.c_str(), 2, N / 144, 1, ws_waves(epi) * 64, p);
+                    const int wbn = C == 144 ? 144 : 192;
+                    k = std::string(C == 144 ? "hat_gemmws_" : "hat_gemmws12_") + enames[epi];
+                    launch(s, k.c_str(), 2, (N + wbn - 1) / wbn, 1, ws_waves(epi) * 64, p);
                 } else {
                     k = std::string(n9 ? "hat_gemm_n9_" : "hat_gemm_n12_") + enames[epi];
                     launch(s, k.c_str(), (M + 127) / 128, (N + BN - 1) / BN, 1, 256, p);
@@ -287,7 +289,8 @@ int gpu_selftest(std::string* err)
         };
         for (int C : {144, 180})
             for (int epi : epis) gemm_case(C, epi, false);
-        for (int epi : {EPI_QKV, EPI_GELU, EPI_RESID_LN, EPI_HAB_LN}) gemm_case(144, epi, true);
+        for (int C : {144, 180})
+            for (int epi : {EPI_QKV, EPI_GELU, EPI_RESID_LN, EPI_HAB_LN}) gemm_case(C, epi, true);
 
         // ---- fused MLP (C = 144, hidden 288), in place as the backend runs it:
         // out aliases the residual, the LayerNorm output aliases the input.
