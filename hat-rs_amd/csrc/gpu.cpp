@@ -166,14 +166,16 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
 }
 
 // The MLP of one block: x_out = res + fc2(gelu(fc1(a))), for EPI_RESID_LN also
-// xn = LayerNorm(x_out). One fused kernel for the C = 144 family (hidden 288),
-// else fc1 and fc2 as two GEMMs through the hidden buffer.
+// xn = LayerNorm(x_out). One fused kernel for C = 144 (hidden 288) and
+// C = 180 (hidden 360), else fc1 and fc2 as two GEMMs through the hidden buffer.
 void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const float* a, long M,
              const float* res, float* out, int epi, const GemmEpilogue& ln, float* hidden)
 {
     if (epi != EPI_RESID && epi != EPI_RESID_LN) throw Error("MLP: bad epilogue");
-    if (fc1.K == MLP_C && fc1.Kp == MLP_C && fc1.N == MLP_H && fc2.K == MLP_H && fc2.Kp == MLP_H &&
-        fc2.N == MLP_C) {
+    // the fused kernels: C = 144 (hidden 288) and C = 180 (hidden 360)
+    const bool c144 = fc1.K == 144 && fc1.Kp == 144 && fc1.N == 288 && fc2.K == 288 && fc2.N == 144;
+    const bool c180 = fc1.K == 180 && fc1.Kp == 192 && fc1.N == 360 && fc2.K == 360 && fc2.N == 180;
+    if (c144 || c180) {
         if (M > 0x7fffffffL) throw Error("MLP: too many rows");
         MlpArgs p{};
         p.a = a;
@@ -188,13 +190,19 @@ void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const fl
         p.nb = ln.nb;
         p.M = (int)M;
         p.eps = 1e-5f;
-        // One block per CU (117 KB of LDS), persistent over the 128-row tiles.
+        p.K = fc1.K;
+        p.H = fc1.N;
+        p.N = fc2.N;
+        p.ldw1 = fc1.Kp;
+        p.ldw2 = fc2.Kp;
+        // One block per CU (120 or 159 KB of LDS), persistent over the 128-row tiles.
         static const int cus = std::max(1, Runtime::get().cu_count());
         const long ntiles = (M + MLP_ROWS - 1) / MLP_ROWS;
         const long rounds = (ntiles + cus - 1) / cus;
         const long g = std::max(1L, (ntiles + rounds - 1) / rounds);
-        launch(s, epi == EPI_RESID_LN ? "hat_mlp_resid_ln" : "hat_mlp_resid", (unsigned)g, 1, 1,
-               MLP_WAVES * 64, p);
+        const char* name = epi == EPI_RESID_LN ? (c144 ? "hat_mlp_resid_ln" : "hat_mlp12_resid_ln")
+                                               : (c144 ? "hat_mlp_resid" : "hat_mlp12_resid");
+        launch(s, name, (unsigned)g, 1, 1, MLP_WAVES * 64, p);
         return;
     }
     GemmEpilogue e = ln;

@@ -135,26 +135,26 @@ struct AttnArgs {
     float qscale;        // head_dim^-0.5 * log2(e)
 };
 
-// Fused MLP of the C = 144 family (hidden 288):
+// Fused MLP (C = 144, hidden 288; C = 180, hidden 360):
 //   out[m][:] = res[m][:] + fc2(gelu(fc1(a[m][:])))   (+ xn = LayerNorm(out) for EPI_RESID_LN)
-#define MLP_C 144
-#define MLP_H 288
 #define MLP_WAVES 8
 #define MLP_ROWS (MLP_WAVES * 16)
 
 struct MlpArgs {
-    const float* a;      // [M][144]
-    const float* w1;     // [288][144]
-    const float* b1;     // [288]
-    const float* w2;     // [144][288]
-    const float* b2;     // [144]
-    const float* res;    // [M][144] (may alias out)
-    float* out;          // [M][144]
-    float* xn;           // EPI_RESID_LN: [M][144] (may alias a)
+    const float* a;      // [M][K]
+    const float* w1;     // [H][ldw1] (K used)
+    const float* b1;     // [H]
+    const float* w2;     // [N][ldw2] (H used)
+    const float* b2;     // [N]
+    const float* res;    // [M][N] (may alias out)
+    float* out;          // [M][N]
+    float* xn;           // EPI_RESID_LN: [M][N] (may alias a)
     const float* nw;
     const float* nb;
     int M;
     float eps;
+    int K, H, N;         // input width (= N), hidden width, output width
+    int ldw1, ldw2;      // packed weight row strides
 };
 
 struct LnArgs {

@@ -292,11 +292,13 @@ int gpu_selftest(std::string* err)
         for (int C : {144, 180})
             for (int epi : {EPI_QKV, EPI_GELU, EPI_RESID_LN, EPI_HAB_LN}) gemm_case(C, epi, true);
 
-        // ---- fused MLP (C = 144, hidden 288), in place as the backend runs it:
-        // out aliases the residual, the LayerNorm output aliases the input.
-        // 600 rows = 5 tiles of 128 (the last partial) over 2 blocks.
+        // ---- fused MLP (C = 144, hidden 288; C = 180, hidden 360 padded to
+        // 384), in place as the backend runs it: out aliases the residual, the
+        // LayerNorm output aliases the input. 600 rows = 5 tiles of 128 (the
+        // last partial) over 2 blocks.
+        for (int C : {144, 180})
         for (int epi : {EPI_RESID, EPI_RESID_LN}) {
-            const int M = 600, C = MLP_C, H = MLP_H;
+            const int M = 600, H = 2 * C;
             std::vector<float> a = rng.vec((size_t)M * C, 1.0f), w1 = rng.vec((size_t)H * C, 0.08f),
                                b1 = rng.vec(H, 0.1f), w2 = rng.vec((size_t)C * H, 0.06f), b2 = rng.vec(C, 0.1f),
                                res = rng.vec((size_t)M * C, 1.0f), nw = rng.vec(C, 1.0f), nb = rng.vec(C, 0.1f);
@@ -316,7 +318,13 @@ int gpu_selftest(std::string* err)
             p.nb = dnb.p;
             p.M = M;
             p.eps = 1e-5f;
-            const char* k = epi == EPI_RESID_LN ? "hat_mlp_resid_ln" : "hat_mlp_resid";
+            p.K = C;
+            p.H = H;
+            p.N = C;
+            p.ldw1 = K1;
+            p.ldw2 = K2;
+            const char* k = epi == EPI_RESID_LN ? (C == 144 ? "hat_mlp_resid_ln" : "hat_mlp12_resid_ln")
+                                                : (C == 144 ? "hat_mlp_resid" : "hat_mlp12_resid");
             launch(s, k, 2, 1, 1, MLP_WAVES * 64, p);
             std::vector<double> want((size_t)M * C), wxn((size_t)M * C), hid(H);
             for (int m = 0; m < M; ++m) {
@@ -340,7 +348,7 @@ int gpu_selftest(std::string* err)
             }
             check_close(std::string(k), dx.get(), want, 5e-5);
             if (epi == EPI_RESID_LN) check_close(std::string(k) + " layernorm", da.get(), wxn, 5e-5);
-            note(std::string(k) + " M 600 (in place)");
+            note(std::string(k) + " C " + std::to_string(C) + " M 600 (in place)");
         }
 
         // ---- folded CAB (144 -> 6 -> 144) against the unfolded computation:
