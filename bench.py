@@ -12,6 +12,9 @@ Also reported on the same JSON line:
     4 * T * 256 * C (QK^T + PV, head_dim unpadded) over its mean launch time,
     measured with HIP events on the launch stream in a second pass of --steps
     steps; peak = 157.3 TFLOP/s (MI355X dense FP32 MFMA);
+  * norm_roofline: the standalone LayerNorm kernel against HBM peak (8 TB/s),
+    8*C bytes per token over its mean launch time (the other LayerNorms run in
+    GEMM and conv epilogues);
   * kernels: the same per-kernel event times for every kernel of the forward;
   * cpu_baseline: the CPU oracle (a C restatement of the reference's src/cpu.rs,
     kind "port") timed on this host's cores on a bounded sample (one HAT-S x4
@@ -130,6 +133,19 @@ def main():
     c_src.free()
     c_dst.free()
 
+    # The standalone LayerNorm (the forward's one norm kernel outside a GEMM or
+    # conv epilogue) against HBM: 8*C bytes per token (read x, write y) + the
+    # 8*C bytes of weight and bias.
+    norm = None
+    if "hat_layernorm" in stats:
+        n_l, t_l = stats["hat_layernorm"]
+        ln_ms = t_l / n_l
+        ln_bytes = 8.0 * C * T + 8.0 * C
+        gbps = ln_bytes / (ln_ms / 1e3) / 1e9
+        norm = {"kernel": "hat_layernorm", "bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM,
+                "unit": "GB/s", "frac": round(gbps / PEAK_HBM, 4), "bytes_per_launch": ln_bytes,
+                "mean_launch_ms": round(ln_ms, 5)}
+
     traffic_file = os.path.join(REPO, "profiles", "traffic_hat_attn_sw_d24_hats512.json")
     if os.path.exists(traffic_file) and attn_name == "hat_attn_sw_d24" and h == 512:
         with open(traffic_file) as f:
@@ -175,6 +191,7 @@ def main():
                    "input": f"{h}x{w}x3", "output": f"{h*scale}x{w*scale}x3",
                    "weights": "seeded, tools/convert.py format", "parallelism": "none (1 GPU)"},
         "roofline": roofline,
+        "norm_roofline": norm,
         "cpu_baseline": cpu,
         "wall_ms_incl_pcie": round(wall_ms, 3),
         "copy_kernel_gbps": round(copy_gbps, 1),
