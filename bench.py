@@ -53,7 +53,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU strip sharding is a design, not a build - see DESIGN.md)",
+              "(every GPU box here has one GPU; sharding by strips of window rows is designed, not built)",
               file=sys.stderr)
         sys.exit(2)
 
