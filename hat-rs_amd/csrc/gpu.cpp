@@ -435,7 +435,13 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
     p.opad = pl.opad();
     p.T = (int)pl.tokens();
     p.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
-    launch(s, name, (unsigned)pl.nw(), (unsigned)heads, 1, 512, p);
+    if (attn_persistent(D, oca)) {
+        static const int cus = std::max(1, Runtime::get().cu_count());
+        const long items = (long)pl.nw() * heads;
+        launch(s, name, (unsigned)std::min<long>(items, cus), 1, 1, 512, p);
+    } else {
+        launch(s, name, (unsigned)pl.nw(), (unsigned)heads, 1, 512, p);
+    }
 }
 
 void run_ln(hipStream_t s, const float* x, float* y, const float* w, const float* b, long rows, int C)

@@ -122,7 +122,10 @@ struct ConvArgs {
     float eps;
 };
 
-// Fused window attention. One block per (window, head).
+// Fused window attention: one block per (window, head) (grid nw x heads), or,
+// for OCA with head_dim 24, persistent blocks walking the (window, head) items
+// head-major (grid: at most one block per CU, gridDim.y = 1).
+constexpr bool attn_persistent(int D, bool oca) { return oca && D == 24; }
 struct AttnArgs {
     const float* qkv;    // head-major [3][heads][T][D]
     const float* table;  // relative-position bias table [rows][heads]

@@ -37,9 +37,15 @@
 
 using namespace hatk;
 
-// MASKED: the block's window is in the last row or column of a shifted SW
-// grid, so its scores get the region mask; every other block runs the loop
-// without it.
+template <bool B, class T, class F>
+struct pick_t {
+    using type = T;
+};
+template <class T, class F>
+struct pick_t<false, T, F> {
+    using type = F;
+};
+
 template <int D, bool OCA>
 struct AttnShape {
     static constexpr int HALF = D / 2;                 // dims per lane half
@@ -49,112 +55,125 @@ struct AttnShape {
     static constexpr int RSV = NK + 4;                 // V^T row stride in LDS
     static constexpr int TROWS = OCA ? 1521 : 961;     // bias table rows
     static constexpr int LDS = NK * RSK + 32 * RSV + TROWS;  // floats
+    // K and V move global -> registers -> LDS in units of U floats (float4 for
+    // D = 24, float2 for D = 30), NE units of each per thread.
+    static constexpr int U = D % 4 == 0 ? 4 : 2;
+    static constexpr int NE = (NK * D / U + 511) / 512;
+    using vec = typename pick_t<U == 4, float4, float2>::type;
 };
 
-template <int D, bool OCA, bool MASKED>
-__device__ __forceinline__ void attn_body(const AttnArgs& p, float* lds)
+// Pixel of key k of window wi (SW: the window at the cyclic shift, plan.rs:
+// 129-151; OCA: the 24x24 unfold with padding 4, -1 outside the plane).
+template <bool OCA>
+__device__ __forceinline__ int attn_key_pixel(const AttnArgs& p, int wi, int k)
+{
+    const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
+    if (OCA) {
+        const int ky = k / 24, kx = k - (k / 24) * 24;
+        const int y = wy * 16 - 4 + ky, x = wx * 16 - 4 + kx;
+        return (y >= 0 && y < p.hp && x >= 0 && x < p.wp) ? y * p.wp + x : -1;
+    }
+    int y = wy * 16 + (k >> 4) + p.shift, x = wx * 16 + (k & 15) + p.shift;
+    if (y >= p.hp) y -= p.hp;
+    if (x >= p.wp) x -= p.wp;
+    return y * p.wp + x;
+}
+
+// This thread's share of item (wi, head)'s K and V, into registers.
+template <int D, bool OCA>
+__device__ __forceinline__ void attn_fetch(const AttnArgs& p, int wi, int head,
+                                           typename AttnShape<D, OCA>::vec (&ks)[AttnShape<D, OCA>::NE],
+                                           typename AttnShape<D, OCA>::vec (&vs)[AttnShape<D, OCA>::NE])
 {
     using S = AttnShape<D, OCA>;
-    constexpr int HALF = S::HALF, HP = S::HP, RSK = S::RSK, NK = S::NK, RSV = S::RSV;
-    constexpr int TROWS = S::TROWS;
-    constexpr int NKT = NK / 32;                // 32-key tiles
-    constexpr int CHT = OCA ? 3 : 2;            // tiles per softmax chunk
-    constexpr int NCH = NKT / CHT;
-    static_assert(NKT % CHT == 0, "chunking");
-
-    float* Kl = lds;                   // [NK][RSK]
-    float* Vt = Kl + NK * RSK;         // [32][RSV]: V^T, then row D ones, rows D+1.. zeros
-    float* Tb = Vt + 32 * RSV;         // [TROWS]
-
-    const int wi = blockIdx.x;
-    const int head = blockIdx.y;
-    const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int hp = p.hp, wp = p.wp, T = p.T, heads = p.heads;
-    const int shift = OCA ? 0 : p.shift;
-
-    const float* Qg = p.qkv + (size_t)head * T * D;
-    const float* Kg = p.qkv + (size_t)(heads + head) * T * D;
-    const float* Vg = p.qkv + (size_t)(2 * heads + head) * T * D;
-
-    // ---- stage K (row-major, halves split) and V^T in LDS ----
-    auto key_pixel = [&](int k) -> int {
-        if (OCA) {
-            const int ky = k / 24, kx = k - (k / 24) * 24;
-            const int y = wy * 16 - 4 + ky, x = wx * 16 - 4 + kx;
-            return (y >= 0 && y < hp && x >= 0 && x < wp) ? y * wp + x : -1;
-        }
-        int y = wy * 16 + (k >> 4) + shift, x = wx * 16 + (k & 15) + shift;
-        if (y >= hp) y -= hp;
-        if (x >= wp) x -= wp;
-        return y * wp + x;
-    };
-    if constexpr (D % 4 == 0 && HP == HALF) {
-        // Rows of D floats are whole float4s and the halves need no gap, so K
-        // goes to LDS as float4s in place; V^T takes four scalar stores.
-        for (int e = tid; e < NK * (D / 4); e += 512) {
-            const int k = e / (D / 4), d = (e - k * (D / 4)) * 4;
-            const int pix = key_pixel(k);
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+    using vec = typename S::vec;
+    constexpr int PER_KEY = D / S::U;
+    const float* Kg = p.qkv + (size_t)(p.heads + head) * p.T * D;
+    const float* Vg = p.qkv + (size_t)(2 * p.heads + head) * p.T * D;
+#pragma unroll
+    for (int i = 0; i < S::NE; ++i) {
+        const int e = threadIdx.x + i * 512;
+        vec kv{}, vv{};
+        if (e < S::NK * PER_KEY) {
+            const int k = e / PER_KEY, d = (e - k * PER_KEY) * S::U;
+            const int pix = attn_key_pixel<OCA>(p, wi, k);
             if (pix >= 0) {
-                kv = *(const float4*)(Kg + (size_t)pix * D + d);
-                vv = *(const float4*)(Vg + (size_t)pix * D + d);
+                kv = *(const vec*)(Kg + (size_t)pix * D + d);
+                vv = *(const vec*)(Vg + (size_t)pix * D + d);
             }
-            *(float4*)(Kl + k * RSK + d) = kv;
-            Vt[(d + 0) * RSV + k] = vv.x;
-            Vt[(d + 1) * RSV + k] = vv.y;
-            Vt[(d + 2) * RSV + k] = vv.z;
-            Vt[(d + 3) * RSV + k] = vv.w;
         }
-    } else {
-        for (int e = tid; e < NK * D; e += 512) {
-            const int k = e / D, d = e - (e / D) * D;
-            const int pix = key_pixel(k);
-            float kv = 0.0f, vv = 0.0f;
-            if (pix >= 0) {
-                kv = Kg[(size_t)pix * D + d];
-                vv = Vg[(size_t)pix * D + d];
+        ks[i] = kv;
+        vs[i] = vv;
+    }
+}
+
+// The registers of attn_fetch into LDS: K row-major with the head_dim halves
+// at 0 and HP, V transposed.
+template <int D, bool OCA>
+__device__ __forceinline__ void attn_stash(float* Kl, float* Vt,
+                                           const typename AttnShape<D, OCA>::vec (&ks)[AttnShape<D, OCA>::NE],
+                                           const typename AttnShape<D, OCA>::vec (&vs)[AttnShape<D, OCA>::NE])
+{
+    using S = AttnShape<D, OCA>;
+    constexpr int PER_KEY = D / S::U;
+#pragma unroll
+    for (int i = 0; i < S::NE; ++i) {
+        const int e = threadIdx.x + i * 512;
+        if (e < S::NK * PER_KEY) {
+            const int k = e / PER_KEY, d = (e - k * PER_KEY) * S::U;
+            if constexpr (S::U == 4) {
+                static_assert(S::HP == S::HALF, "float4 rows need no gap between the halves");
+                *(float4*)(Kl + k * S::RSK + d) = ks[i];
+                Vt[(d + 0) * S::RSV + k] = vs[i].x;
+                Vt[(d + 1) * S::RSV + k] = vs[i].y;
+                Vt[(d + 2) * S::RSV + k] = vs[i].z;
+                Vt[(d + 3) * S::RSV + k] = vs[i].w;
+            } else {
+                Kl[k * S::RSK + (d < S::HALF ? d : S::HP + d - S::HALF)] = ks[i].x;
+                Kl[k * S::RSK + (d + 1 < S::HALF ? d + 1 : S::HP + d + 1 - S::HALF)] = ks[i].y;
+                Vt[(d + 0) * S::RSV + k] = vs[i].x;
+                Vt[(d + 1) * S::RSV + k] = vs[i].y;
             }
-            Kl[k * RSK + (d < HALF ? d : HP + d - HALF)] = kv;
-            Vt[d * RSV + k] = vv;
         }
     }
-    // The V^T rows past D fill the 32-row MFMA tile: row D all ones (it sums
-    // the probabilities, see below), the rest zero.
-    for (int e = tid; e < (32 - D) * NK; e += 512) {
-        const int r = D + e / NK, k = e - (e / NK) * NK;
-        Vt[r * RSV + k] = r == D ? 1.0f : 0.0f;
-    }
-    // Bias table for this head, in log2 units. For OCA the table is stored
-    // rotated so that the reference's negative-index wrap (plan.rs:397-416)
-    // becomes a plain offset: Tb[j] = table[(j - 880) mod 1521].
-    for (int i = tid; i < TROWS; i += 512) {
+}
+
+// Bias table of a head, in log2 units. For OCA the table is stored rotated so
+// that the reference's negative-index wrap (plan.rs:397-416) becomes a plain
+// offset: Tb[j] = table[(j - 880) mod 1521].
+template <int D, bool OCA>
+__device__ __forceinline__ void attn_table(const AttnArgs& p, float* Tb, int head)
+{
+    for (int i = threadIdx.x; i < AttnShape<D, OCA>::TROWS; i += 512) {
         int row = i;
         if (OCA) {
             row = i - 880;
             if (row < 0) row += 1521;
         }
-        Tb[i] = p.table[(size_t)row * heads + head] * HAT_LOG2E;
+        Tb[i] = p.table[(size_t)row * p.heads + head] * HAT_LOG2E;
     }
-    __syncthreads();
+}
 
-    // ---- this lane's query ----
+// This lane's query of item (wi, head): its pixel and its half of q, scaled
+// by head_dim^-0.5 * log2(e).
+template <int D>
+__device__ __forceinline__ int attn_query(const AttnArgs& p, int wi, int head, float (&qv)[D / 2], bool oca)
+{
+    constexpr int HALF = D / 2;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ql = lane & 31, h = lane >> 5;
-    const int q = wave * 32 + ql;
-    const int qy = q >> 4, qx = q & 15;
-    int qpix;
-    {
-        int y = wy * 16 + qy + shift, x = wx * 16 + qx + shift;
-        if (y >= hp) y -= hp;
-        if (x >= wp) x -= wp;
-        qpix = y * wp + x;
-    }
-    float qv[HALF];
+    const int q = wave * 32 + ql, qy = q >> 4, qx = q & 15;
+    const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
+    const int shift = oca ? 0 : p.shift;
+    int y = wy * 16 + qy + shift, x = wx * 16 + qx + shift;
+    if (y >= p.hp) y -= p.hp;
+    if (x >= p.wp) x -= p.wp;
+    const int qpix = y * p.wp + x;
+    const float* Qg = p.qkv + (size_t)head * p.T * D + (size_t)qpix * D + h * HALF;
     if constexpr (HALF % 4 == 0) {
 #pragma unroll
         for (int s4 = 0; s4 < HALF; s4 += 4) {
-            const float4 v = *(const float4*)(Qg + (size_t)qpix * D + h * HALF + s4);
+            const float4 v = *(const float4*)(Qg + s4);
             qv[s4] = v.x * p.qscale;
             qv[s4 + 1] = v.y * p.qscale;
             qv[s4 + 2] = v.z * p.qscale;
@@ -162,8 +181,34 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, float* lds)
         }
     } else {
 #pragma unroll
-        for (int s = 0; s < HALF; ++s) qv[s] = Qg[(size_t)qpix * D + h * HALF + s] * p.qscale;
+        for (int s = 0; s < HALF; ++s) qv[s] = Qg[s] * p.qscale;
     }
+    return qpix;
+}
+
+// The attention of one staged item. MASKED: the window is in the last row or
+// column of a shifted SW grid, so its scores get the region mask; every other
+// window runs the loop without it.
+template <int D, bool OCA, bool MASKED>
+__device__ __forceinline__ void attn_compute(const AttnArgs& p, const float* lds, int wi, int head,
+                                             const float (&qv)[D / 2], int qpix)
+{
+    using S = AttnShape<D, OCA>;
+    constexpr int HALF = S::HALF, HP = S::HP, RSK = S::RSK, NK = S::NK, RSV = S::RSV;
+    constexpr int NKT = NK / 32;                // 32-key tiles
+    constexpr int CHT = OCA ? 3 : 2;            // tiles per softmax chunk
+    constexpr int NCH = NKT / CHT;
+    static_assert(NKT % CHT == 0, "chunking");
+
+    const float* Kl = lds;                      // [NK][RSK]
+    const float* Vt = Kl + NK * RSK;            // [32][RSV]: V^T, then row D ones, rows D+1.. zeros
+    const float* Tb = Vt + 32 * RSV;            // [TROWS]
+
+    const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ql = lane & 31, h = lane >> 5;
+    const int q = wave * 32 + ql;
+    const int qy = q >> 4, qx = q & 15;
 
     // Bias addressing. SW: idx = (qy-ky+15)*31 + (qx-kx+15) = sw_base - (ky*31+kx).
     // OCA: idx = (ky*39+kx) - (qy*39+qx) + 600 on the rotated table.
@@ -272,18 +317,98 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, float* lds)
     }
 }
 
-// SW kernels are asked for 4 waves per SIMD (2 blocks per CU, <= 128 VGPRs), so
-// one block's K/V staging
-// overlaps the other's MFMA work; the OCA block's LDS allows only one block.
+// One (window, head) per block (grid nw x heads). SW runs 4 waves per SIMD (2
+// blocks per CU, <= 128 VGPRs), so one block's K/V staging overlaps the
+// other's MFMA work; its V^T padding rows are not read (the idle lanes
+// substitute them). OCA with head_dim 30 also runs this way (its staging
+// registers do not fit the persistent form).
+template <int D, bool OCA>
+__device__ __forceinline__ void attn_item_kernel(const AttnArgs& p, float* lds)
+{
+    using S = AttnShape<D, OCA>;
+    float* Vt = lds + S::NK * S::RSK;
+    const int wi = blockIdx.x, head = blockIdx.y;
+    {
+        typename S::vec ks[S::NE], vs[S::NE];
+        attn_fetch<D, OCA>(p, wi, head, ks, vs);
+        attn_stash<D, OCA>(lds, Vt, ks, vs);
+    }
+    if (OCA) {
+        // V^T rows past D: row D all ones (it sums the probabilities), the rest zero.
+        for (int e = threadIdx.x; e < (32 - D) * S::NK; e += 512) {
+            const int r = D + e / S::NK, k = e - (e / S::NK) * S::NK;
+            Vt[r * S::RSV + k] = r == D ? 1.0f : 0.0f;
+        }
+    }
+    attn_table<D, OCA>(p, Vt + 32 * S::RSV, head);
+    float qv[D / 2];
+    const int qpix = attn_query<D>(p, wi, head, qv, OCA);
+    __syncthreads();
+    if (!OCA && p.shift > 0 && (wi / p.nx == p.ny - 1 || wi % p.nx == p.nx - 1))
+        attn_compute<D, OCA, true>(p, lds, wi, head, qv, qpix);
+    else
+        attn_compute<D, OCA, false>(p, lds, wi, head, qv, qpix);
+}
+
+// OCA, head_dim 24: the LDS holds one block per CU, so the kernel is
+// persistent (grid: one block per CU at most) over the (window, head) items, head-major (a block's consecutive items mostly share
+// the bias table): the next item's K, V and q travel through registers while
+// this item computes, and go to LDS between two barriers.
+template <int D>
+__device__ __forceinline__ void attn_oca_kernel(const AttnArgs& p, float* lds)
+{
+    using S = AttnShape<D, true>;
+    float* Kl = lds;
+    float* Vt = Kl + S::NK * S::RSK;
+    float* Tb = Vt + 32 * S::RSV;
+    const int nw = p.nx * p.ny, nitems = nw * p.heads;
+    int item = blockIdx.x;
+    if (item >= nitems) return;  // whole block, before any barrier
+    // V^T rows past D: row D all ones (it sums the probabilities), the rest zero.
+    for (int e = threadIdx.x; e < (32 - D) * S::NK; e += 512) {
+        const int r = D + e / S::NK, k = e - (e / S::NK) * S::NK;
+        Vt[r * S::RSV + k] = r == D ? 1.0f : 0.0f;
+    }
+    typename S::vec ks[S::NE], vs[S::NE];
+    float qn[D / 2];
+    int head = item / nw, wi = item - head * nw;
+    attn_fetch<D, true>(p, wi, head, ks, vs);
+    int qpix_n = attn_query<D>(p, wi, head, qn, true);
+    int table_head = -1;
+    while (true) {
+        __syncthreads();  // every read of the previous item's LDS is done
+        attn_stash<D, true>(Kl, Vt, ks, vs);
+        if (head != table_head) {  // block-uniform
+            attn_table<D, true>(p, Tb, head);
+            table_head = head;
+        }
+        float qv[D / 2];
+#pragma unroll
+        for (int s = 0; s < D / 2; ++s) qv[s] = qn[s];
+        const int qpix = qpix_n;
+        __syncthreads();
+        const int next = item + gridDim.x;
+        const int nhead = next / nw, nwi = next - nhead * nw;
+        if (next < nitems) {
+            attn_fetch<D, true>(p, nwi, nhead, ks, vs);
+            qpix_n = attn_query<D>(p, nwi, nhead, qn, true);
+        }
+        attn_compute<D, true, false>(p, lds, wi, head, qv, qpix);
+        if (next >= nitems) break;
+        item = next;
+        head = nhead;
+        wi = nwi;
+    }
+}
+
 #define ATTN_INST(NAME, D, OCA)                                                              \
     extern "C" __global__ __launch_bounds__(512, OCA ? 2 : 4) void NAME(AttnArgs p)          \
     {                                                                                        \
         __shared__ __attribute__((aligned(16))) float lds[AttnShape<D, OCA>::LDS];           \
-        const int wi = blockIdx.x;                                                           \
-        if (!OCA && p.shift > 0 && (wi / p.nx == p.ny - 1 || wi % p.nx == p.nx - 1))         \
-            attn_body<D, OCA, true>(p, lds);                                                 \
+        if (attn_persistent(D, OCA))                                                         \
+            attn_oca_kernel<D>(p, lds);                                                      \
         else                                                                                 \
-            attn_body<D, OCA, false>(p, lds);                                                \
+            attn_item_kernel<D, OCA>(p, lds);                                                \
     }
 
 ATTN_INST(hat_attn_sw_d24, 24, false)

@@ -195,7 +195,10 @@ int gpu_selftest(std::string* err)
                     p.T = T;
                     p.qscale = (float)(1.0 / std::sqrt((double)D) * 1.4426950408889634);
                     std::string k = std::string(oca ? "hat_attn_oca_d" : "hat_attn_sw_d") + std::to_string(D);
-                    launch(s, k.c_str(), pl.nw(), heads, 1, 512, p);
+                    if (attn_persistent(D, oca))  // 3 blocks, so a block walks several items
+                        launch(s, k.c_str(), 3, 1, 1, 512, p);
+                    else
+                        launch(s, k.c_str(), pl.nw(), heads, 1, 512, p);
                     std::vector<double> want = attn_twin(qkv, tab, hp, wp, heads, D, oca, shift);
                     char nm[128];
                     snprintf(nm, sizeof nm, "%s %dx%d shift %d", k.c_str(), hp, wp, shift);
