@@ -328,7 +328,8 @@ int hat_device_copy(void* dst, const void* src, size_t bytes)
         if (!dst || !src || bytes % 16 != 0 || ((uintptr_t)dst | (uintptr_t)src) % 16 != 0)
             throw hat::Error("hat_device_copy: 16-byte aligned pointers and a multiple of 16 bytes");
         hatk::CopyArgs p{(const float*)src, (float*)dst, (long)(bytes / 16)};
-        const long blocks = std::min<long>((p.n4 + 255) / 256, 256L * 64);
+        const long blocks = (p.n4 + 1023) / 1024;
+        if (blocks > 0x7fffffffL) throw hat::Error("hat_device_copy: too large");
         hat::launch(nullptr, "hat_copy", (unsigned)std::max<long>(blocks, 1), 1, 1, 256, p);
         return 0;
     });

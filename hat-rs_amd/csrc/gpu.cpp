@@ -148,17 +148,12 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
     p.eps = 1e-5f;
     int wbn = 0;
     if (const char* ws = gemm_ws_kernel(L, epi, &wbn)) {
-        // One block per CU (its 85 or 150 KB weight slice fills the LDS), the CUs
-        // split evenly over the column slices; each block walks the row tiles
-        // of its slice. Fewest blocks for the same number of rounds, so no CU
-        // gets a tile more than the others need.
+        // One block per CU (its 85 or 150 KB weight slice fills the LDS); the
+        // (column slice, row tile) units are dealt out round-robin over the blocks.
         static const int cus = std::max(1, Runtime::get().cu_count());
         const long ntiles = (M + ws_rows(epi) - 1) / ws_rows(epi);
-        const int slices = (L.N + wbn - 1) / wbn;
-        const long per = std::max(1, cus / slices);
-        const long rounds = (ntiles + per - 1) / per;
-        const long g = std::max(1L, (ntiles + rounds - 1) / rounds);
-        launch(s, ws, (unsigned)g, (unsigned)slices, 1, ws_waves(epi) * 64, p);
+        const long units = ntiles * ((L.N + wbn - 1) / wbn);
+        launch(s, ws, (unsigned)std::max(1L, std::min<long>(units, cus)), 1, 1, ws_waves(epi) * 64, p);
         return;
     }
     launch(s, gemm_kernel(L.N, epi), (unsigned)((M + 127) / 128), (unsigned)((L.N + BN - 1) / BN), 1,

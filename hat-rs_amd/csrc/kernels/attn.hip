@@ -354,32 +354,34 @@ __device__ __forceinline__ void attn_item_kernel(const AttnArgs& p, float* lds)
 // persistent (grid: one block per CU at most) over the (window, head) items, head-major (a block's consecutive items mostly share
 // the bias table): the next item's K, V and q travel through registers while
 // this item computes, and go to LDS between two barriers.
-template <int D>
-__device__ __forceinline__ void attn_oca_kernel(const AttnArgs& p, float* lds)
+template <int D, bool OCA>
+__device__ __forceinline__ void attn_persistent_kernel(const AttnArgs& p, float* lds)
 {
-    using S = AttnShape<D, true>;
+    using S = AttnShape<D, OCA>;
     float* Kl = lds;
     float* Vt = Kl + S::NK * S::RSK;
     float* Tb = Vt + 32 * S::RSV;
     const int nw = p.nx * p.ny, nitems = nw * p.heads;
     int item = blockIdx.x;
     if (item >= nitems) return;  // whole block, before any barrier
-    // V^T rows past D: row D all ones (it sums the probabilities), the rest zero.
-    for (int e = threadIdx.x; e < (32 - D) * S::NK; e += 512) {
-        const int r = D + e / S::NK, k = e - (e / S::NK) * S::NK;
-        Vt[r * S::RSV + k] = r == D ? 1.0f : 0.0f;
+    if (OCA) {
+        // V^T rows past D: row D all ones (it sums the probabilities), the rest zero.
+        for (int e = threadIdx.x; e < (32 - D) * S::NK; e += 512) {
+            const int r = D + e / S::NK, k = e - (e / S::NK) * S::NK;
+            Vt[r * S::RSV + k] = r == D ? 1.0f : 0.0f;
+        }
     }
     typename S::vec ks[S::NE], vs[S::NE];
     float qn[D / 2];
     int head = item / nw, wi = item - head * nw;
-    attn_fetch<D, true>(p, wi, head, ks, vs);
-    int qpix_n = attn_query<D>(p, wi, head, qn, true);
+    attn_fetch<D, OCA>(p, wi, head, ks, vs);
+    int qpix_n = attn_query<D>(p, wi, head, qn, OCA);
     int table_head = -1;
     while (true) {
         __syncthreads();  // every read of the previous item's LDS is done
-        attn_stash<D, true>(Kl, Vt, ks, vs);
+        attn_stash<D, OCA>(Kl, Vt, ks, vs);
         if (head != table_head) {  // block-uniform
-            attn_table<D, true>(p, Tb, head);
+            attn_table<D, OCA>(p, Tb, head);
             table_head = head;
         }
         float qv[D / 2];
@@ -390,10 +392,13 @@ __device__ __forceinline__ void attn_oca_kernel(const AttnArgs& p, float* lds)
         const int next = item + gridDim.x;
         const int nhead = next / nw, nwi = next - nhead * nw;
         if (next < nitems) {
-            attn_fetch<D, true>(p, nwi, nhead, ks, vs);
-            qpix_n = attn_query<D>(p, nwi, nhead, qn, true);
+            attn_fetch<D, OCA>(p, nwi, nhead, ks, vs);
+            qpix_n = attn_query<D>(p, nwi, nhead, qn, OCA);
         }
-        attn_compute<D, true, false>(p, lds, wi, head, qv, qpix);
+        if (!OCA && p.shift > 0 && (wi / p.nx == p.ny - 1 || wi % p.nx == p.nx - 1))
+            attn_compute<D, OCA, true>(p, lds, wi, head, qv, qpix);
+        else
+            attn_compute<D, OCA, false>(p, lds, wi, head, qv, qpix);
         if (next >= nitems) break;
         item = next;
         head = nhead;
@@ -406,7 +411,7 @@ __device__ __forceinline__ void attn_oca_kernel(const AttnArgs& p, float* lds)
     {                                                                                        \
         __shared__ __attribute__((aligned(16))) float lds[AttnShape<D, OCA>::LDS];           \
         if (attn_persistent(D, OCA))                                                         \
-            attn_oca_kernel<D>(p, lds);                                                      \
+            attn_persistent_kernel<D, OCA>(p, lds);                                          \
         else                                                                                 \
             attn_item_kernel<D, OCA>(p, lds);                                                \
     }

@@ -267,9 +267,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
 // ---------------------------------------------------------------------------
 // Weight-stationary variant for K = 144 (the C = 144 family's qkv, proj and fc1).
 //
-// A block holds the 144 x 144 weight slice of its column block in LDS for the
-// whole kernel and loops over row tiles (persistent: gridDim.x blocks per
-// column slice, gridDim.y slices). Each of the WAVES waves owns 16*MT rows of
+// A block holds a 144 x 144 weight slice (one column block) in LDS and loops
+// over row tiles. The work is the sequence of (column slice, row tile) units,
+// slice-major; block b takes units b, b + G, b + 2G, ... (G = gridDim.x, one
+// block per CU), so every CU gets the same number of tiles to within one and
+// the blocks running at one time work on neighbouring rows; a block reloads the
+// weights where its units cross into the next slice (slices - 1 times at most).
+// Each of the WAVES waves owns 16*MT rows of
 // a tile and streams its A rows from global memory straight into registers,
 // three K-chunks ahead of the MFMAs, so the K loop has no barrier and no LDS
 // traffic for A; waves drift apart freely, and one wave's epilogue stores
@@ -299,35 +303,46 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
     const int lane = tid & 63;
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    const int n0 = blockIdx.y * BN;
     const int M = p.M, N = p.N;
 
-    // The weight slice, once: BN rows x 36 float4.
-    for (int idx = tid; idx < BN * (WS_K / 4); idx += WAVES * 64) {
-        const int r = idx / (WS_K / 4), c4 = (idx - r * (WS_K / 4)) * 4;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (n0 + r < N) v = *(const float4*)(p.w + (size_t)(n0 + r) * p.Kp + c4);
-        *(float4*)(Wsm + r * WS_KS + c4) = v;
-    }
-    if (CAB) {
-        for (int idx = tid; idx < BN * (CAB_K2 / 4); idx += WAVES * 64) {
-            const int r = idx / (CAB_K2 / 4), c4 = (idx - r * (CAB_K2 / 4)) * 4;
+    // The weight slice of the columns from n0: BN rows x KP/4 float4, with the
+    // conv2 slice, the QKV column map and the epilogue constants.
+    auto load_slice = [&](int n0) {
+        for (int idx = tid; idx < BN * (WS_K / 4); idx += WAVES * 64) {
+            const int r = idx / (WS_K / 4), c4 = (idx - r * (WS_K / 4)) * 4;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (n0 + r < N) v = *(const float4*)(p.w2g + (size_t)(n0 + r) * CAB_K2 + c4);
-            *(float4*)(W2s + r * S2 + c4) = v;
+            if (n0 + r < N) v = *(const float4*)(p.w + (size_t)(n0 + r) * p.Kp + c4);
+            *(float4*)(Wsm + r * WS_KS + c4) = v;
         }
-    }
-    build_colmap<BN, EPI>(p, n0, s_colmap);
-    for (int i = tid; i < (LNOUT ? 3 : 1) * BN; i += WAVES * 64) {
-        const int j = i % BN, n = n0 + j;
-        const float* src = i < BN ? p.bias : (i < 2 * BN ? p.nw : p.nb);
-        Cs[i] = n < N ? src[n] : 0.0f;
-    }
+        if (CAB) {
+            for (int idx = tid; idx < BN * (CAB_K2 / 4); idx += WAVES * 64) {
+                const int r = idx / (CAB_K2 / 4), c4 = (idx - r * (CAB_K2 / 4)) * 4;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (n0 + r < N) v = *(const float4*)(p.w2g + (size_t)(n0 + r) * CAB_K2 + c4);
+                *(float4*)(W2s + r * S2 + c4) = v;
+            }
+        }
+        build_colmap<BN, EPI>(p, n0, s_colmap);
+        for (int i = tid; i < (LNOUT ? 3 : 1) * BN; i += WAVES * 64) {
+            const int j = i % BN, n = n0 + j;
+            const float* src = i < BN ? p.bias : (i < 2 * BN ? p.nw : p.nb);
+            Cs[i] = n < N ? src[n] : 0.0f;
+        }
+    };
     const EpiConsts kc{Cs, LNOUT ? Cs + BN : nullptr, LNOUT ? Cs + 2 * BN : nullptr};
-    __syncthreads();
 
     const int ntiles = (M + ROWS - 1) / ROWS;
-    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const long units = (long)ntiles * ((N + BN - 1) / BN);
+    int slice = -1;
+    for (long u = blockIdx.x; u < units; u += gridDim.x) {
+        const int us = (int)(u / ntiles), tile = (int)(u - (long)us * ntiles);
+        if (us != slice) {  // block-uniform
+            if (slice >= 0) __syncthreads();  // every wave is done with the old slice
+            load_slice(us * BN);
+            __syncthreads();
+            slice = us;
+        }
+        const int n0 = slice * BN;
         const int mbase = tile * ROWS + wave * 16 * MT;
         const float* arow[MT];
         bool alive[MT];
