@@ -57,44 +57,46 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
 #pragma unroll
     for (int co = 0; co < CAB_CC; ++co) bias[co] = p.bias[co];
 
+    // This wave's halo row tiles rt = wave, wave + 4, ... of the block's tiles
+    // are walked as one stream of 16-channel chunks (9 per row tile), the input
+    // rows held in nine register slots: chunk kc of the next row tile (of this
+    // tile, or the first of the block's next tile) is loaded as soon as chunk kc
+    // of this one has gone to its MFMAs, a whole row tile (144 MFMAs) ahead.
+    const int nrt = (CC1_RT - wave + 3) / 4;
+    auto src_of = [&](int tl, int i) -> const float* {  // lane's input row of row tile i of tile tl, or null
+        if (tl >= ntiles) return nullptr;
+        const int ty = tl / ntx, tx = tl - ty * ntx;
+        const int hi = (wave + 4 * i) * 16 + lr;
+        const int hy = hi / CC1_HS, hx = hi - hy * CC1_HS;
+        const int gy = ty * 16 - 1 + hy, gx = tx * 16 - 1 + hx;
+        const bool valid = hi < CC1_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
+        return valid ? p.xn + (size_t)(gy * W + gx) * CAB_C + lg * 4 : nullptr;
+    };
+    f32x4 xa[CAB_C / 16];
+    auto load = [&](int slot, const float* src, int kc) {
+        f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+        if (src) v = *(const f32x4*)(src + kc * 16);
+        xa[slot] = v;
+    };
+    {
+        const float* first = src_of(blockIdx.x, 0);
+#pragma unroll
+        for (int s = 0; s < CAB_C / 16; ++s) load(s, first, s);
+    }
+
     for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int ty = tile / ntx, tx = tile - ty * ntx;
         const int y0 = ty * 16, x0 = tx * 16;
-
-        // This wave's halo row tiles rt = wave, wave + 4, ... are walked as one
-        // stream of 16-channel chunks (9 per row tile), the input rows held in
-        // three register slots loaded three chunks ahead of their MFMAs, across
-        // row-tile boundaries.
-        const int nrt = (CC1_RT - wave + 3) / 4;
-        auto src_of = [&](int i) -> const float* {  // lane's input row of row tile i, or null
-            const int hi = (wave + 4 * i) * 16 + lr;
-            const int hy = hi / CC1_HS, hx = hi - hy * CC1_HS;
-            const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
-            const bool valid = i < nrt && hi < CC1_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
-            return valid ? p.xn + (size_t)(gy * W + gx) * CAB_C + lg * 4 : nullptr;
-        };
-        f32x4 xa[3];
-        auto load = [&](int slot, const float* src, int kc) {
-            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-            if (src) v = *(const f32x4*)(src + kc * 16);
-            xa[slot] = v;
-        };
-        const float* cur = src_of(0);
-        const float* nxt = src_of(1);
-#pragma unroll
-        for (int s = 0; s < 3; ++s) load(s, cur, s);
 #pragma unroll 1
         for (int i = 0; i < nrt; ++i) {
+            const float* nxt = i + 1 < nrt ? src_of(tile, i + 1) : src_of(tile + gridDim.x, 0);
             f32x4 acc[4];
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) acc[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kc = 0; kc < CAB_C / 16; ++kc) {
-                const int slot = kc % 3;
-                const f32x4 a = xa[slot];
-                // chunk kc + 3 of this row tile, or chunk kc - 6 of the next
-                if (kc + 3 < CAB_C / 16) load(slot, cur, kc + 3);
-                else load(slot, nxt, kc + 3 - CAB_C / 16);
+                const f32x4 a = xa[kc];
+                load(kc, nxt, kc);  // chunk kc of the next row tile
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -107,8 +109,6 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
                 for (int nt = 0; nt < 4; ++nt)
                     if (nt * 16 + lg * 4 < CC1_PS) *(f32x4*)(Ps + hi * CC1_PS + nt * 16 + lg * 4) = acc[nt];
             }
-            cur = nxt;
-            nxt = src_of(i + 2);
         }
         __syncthreads();
 

@@ -9,9 +9,13 @@
 // A block of 8 waves walks 128-row tiles (persistent over gridDim.x); wave w
 // owns rows [16w, 16w+16) and keeps their C inputs in registers for the whole
 // tile. The hidden dimension is walked in chunks of 48: the chunk's fc1 rows
-// (48 x KP) and fc2 columns (NO x 48) are double-buffered in LDS, with the next
-// chunk's slices fetched into registers while this chunk computes (one barrier
-// per chunk). Both GEMMs use v_mfma_f32_16x16x4_f32 with weights as the A
+// (48 x KP) and fc2 columns (NO x 48) are double-buffered in LDS, the next
+// chunk's slices copied global -> LDS by the loads that write LDS directly
+// (global_load_lds_dwordx4, lane l of a wave's load filling 16 bytes at the
+// load's LDS base + 16 l) while this chunk computes, one barrier per chunk. The
+// slices sit unpadded in LDS with each row's float4 XOR-swizzled so the MFMA
+// operand reads of 16 consecutive rows hit 16 distinct bank groups: the lanes
+// choose which global float4 lands in their slot. Both GEMMs use v_mfma_f32_16x16x4_f32 with weights as the A
 // operand, so fc1's accumulators - lane (r, g) holds hidden units 4g..4g+3 of
 // each 16-unit tile for row r - are exactly the B operand fc2 needs for k =
 // 4g..4g+3: after bias + GELU they feed fc2 with no data movement. The fc2
@@ -27,27 +31,44 @@
 #define MLP_HC 48  // hidden units per chunk
 #define MLP_THREADS (MLP_WAVES * 64)
 
+// A zero float4 in global memory: the source of the LDS slots that lie past the
+// real weights (the padded C = 180 shape), since a direct-to-LDS load always
+// writes its slot.
+__device__ __attribute__((aligned(16))) float hat_mlp_zero4[4] = {0.f, 0.f, 0.f, 0.f};
+
+// Swizzle of float4 column c4 in LDS row `row` of a slice whose rows are R
+// float4 long: rows r..r+15 read at one c4 land in 16 distinct groups of four
+// banks (R = 36 or 12: rows 4 apart share a bank offset, the XOR separates
+// them; R = 48: all rows share one, the XOR spreads them over 16).
+template <int R>
+__device__ __forceinline__ int mlp_swz(int row)
+{
+    static_assert(R % 16 == 0 || R % 16 == 4 || R % 16 == 12, "slice row length");
+    return R % 16 == 0 ? (row & 15) : ((row >> 2) & 3);
+}
+
 // PAD: the real K, hidden and output widths are below KP, NH, NO (C = 180);
 // without it they are exactly KP, NH, NO and nothing is masked.
 template <int EPI, int KP, int NH, int NO, bool PAD>
 __device__ __forceinline__ void mlp_body(const MlpArgs& p)
 {
     constexpr int NCH = NH / MLP_HC;             // hidden chunks
-    constexpr int S1 = KP + 4;                   // LDS row stride of the fc1 slice [48][S1]
-    constexpr int S2 = MLP_HC + 4;               // LDS row stride of the fc2 slice [NO][S2]
-    constexpr int W1F4 = MLP_HC * KP / 4;        // float4 per fc1 slice
-    constexpr int F4 = W1F4 + NO * MLP_HC / 4;   // + the fc2 slice
-    constexpr int BUF = MLP_HC * S1 + NO * S2;
+    constexpr int R1 = KP / 4;                   // float4 per fc1 slice row [48][R1]
+    constexpr int R2 = MLP_HC / 4;               // float4 per fc2 slice row [NO][R2]
+    constexpr int W1F4 = MLP_HC * R1;            // float4 per fc1 slice
+    constexpr int F4 = W1F4 + NO * R2;           // + the fc2 slice
+    constexpr int BUF = F4 * 4;
     constexpr int PER = (F4 + MLP_THREADS - 1) / MLP_THREADS;
     static_assert(NCH % 2 == 0, "chunk parity must repeat across tiles");
     static_assert(KP % 16 == 0 && NO % 16 == 0 && NH % MLP_HC == 0, "tile multiples");
-    __shared__ float Wb[2 * BUF];
+    static_assert(W1F4 % 64 == 0 && F4 % 64 == 0, "a wave's load lies in one slice");
+    __shared__ __attribute__((aligned(16))) float Wb[2 * BUF];
     // The per-column constants, read in every chunk and every epilogue, from
     // LDS rather than through the cache hierarchy: b1, then b2, nw, nb.
     __shared__ __attribute__((aligned(16))) float Cs[NH + 3 * NO];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
     const int lane = tid & 63;
     const int lr = lane & 15;
     const int lg = lane >> 4;
@@ -57,69 +78,53 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     int tile = blockIdx.x;
     if (tile >= ntiles) return;  // whole block: no barrier has been passed yet
 
-    // This thread's share of a chunk, float4 i: fc1 slice entries (row = the
-    // hidden unit within the chunk, column k) then fc2 slice entries (row =
-    // output column, column = hidden unit within the chunk). A float4 outside
-    // the real weights (hidden >= H, fc2 column >= N) is zero.
-    // Without padding the per-thread offsets are kept in registers (relative
-    // to the chunk's uniform bases); with it they are recomputed, which leaves
-    // the registers to the wider tiles.
+    // This thread's LDS slots of a chunk, float4 idx = tid + 512 i: fc1 slice
+    // slots (row = the hidden unit within the chunk) then fc2 slice slots (row =
+    // output column); the lane fetches the global float4 whose swizzled column
+    // is the slot's. Without padding the global offsets (relative to the
+    // chunk's bases) are kept in registers; with it they are recomputed and
+    // slots past the real weights read hat_mlp_zero4.
     unsigned goff[PAD ? 1 : PER];
-    int loff[PAD ? 1 : PER];
     if constexpr (!PAD) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int idx = tid + i * MLP_THREADS;
             if (idx < W1F4) {
-                const int r = idx / (KP / 4), c4 = idx - r * (KP / 4);
+                const int r = idx / R1, c4 = (idx - r * R1) ^ mlp_swz<R1>(r);
                 goff[i] = r * p.ldw1 + c4 * 4;  // + chunk * 48 fc1 rows
-                loff[i] = r * S1 + c4 * 4;
             } else {
                 const int j = idx - W1F4;
-                const int r = j / (MLP_HC / 4), c4 = j - r * (MLP_HC / 4);
+                const int r = j / R2, c4 = (j - r * R2) ^ mlp_swz<R2>(r);
                 goff[i] = r * p.ldw2 + c4 * 4;  // + chunk * 48 fc2 columns
-                loff[i] = MLP_HC * S1 + r * S2 + c4 * 4;
             }
         }
     }
-    float4 stg[PER];
-    auto fetch = [&](int c) {
+    // Chunk c's slices into LDS buffer buf. The LDS side of each load is the
+    // wave's 64 consecutive slots; the writes land asynchronously, so a
+    // vmcnt(0) wait precedes the barrier that publishes them.
+    auto fetch = [&](int c, int buf) {
         const int h0 = c * MLP_HC;
         const float* w1c = p.w1 + (size_t)h0 * p.ldw1;  // uniform chunk bases
         const float* w2c = p.w2 + h0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + i * MLP_THREADS;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if constexpr (!PAD) {
-                if (idx < W1F4) v = *(const float4*)(w1c + goff[i]);
-                else if (idx < F4) v = *(const float4*)(w2c + goff[i]);
-            } else if (idx < W1F4) {
-                const int r = idx / (KP / 4), c4 = idx - r * (KP / 4);
-                if (h0 + r < H) v = *(const float4*)(p.w1 + (size_t)(h0 + r) * p.ldw1 + c4 * 4);
-            } else if (idx < F4) {
-                const int j = idx - W1F4;
-                const int r = j / (MLP_HC / 4), c4 = j - r * (MLP_HC / 4);
-                if (r < N && h0 + c4 * 4 < H) v = *(const float4*)(p.w2 + (size_t)r * p.ldw2 + h0 + c4 * 4);
-            }
-            stg[i] = v;
-        }
-    };
-    auto stash = [&](int buf) {
         float* B = Wb + buf * BUF;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int idx = tid + i * MLP_THREADS;
+            const int base = i * MLP_THREADS + wave * 64;  // wave-uniform
+            if (base >= F4) break;
+            const int idx = base + lane;
+            const float* src;
             if constexpr (!PAD) {
-                if (idx < F4) *(float4*)(B + loff[i]) = stg[i];
-            } else if (idx < W1F4) {
-                const int r = idx / (KP / 4), c4 = idx - r * (KP / 4);
-                *(float4*)(B + r * S1 + c4 * 4) = stg[i];
-            } else if (idx < F4) {
+                src = (base < W1F4 ? w1c : w2c) + goff[i];
+            } else if (base < W1F4) {
+                const int r = idx / R1, c4 = (idx - r * R1) ^ mlp_swz<R1>(r);
+                src = h0 + r < H ? p.w1 + (size_t)(h0 + r) * p.ldw1 + c4 * 4 : hat_mlp_zero4;
+            } else {
                 const int j = idx - W1F4;
-                const int r = j / (MLP_HC / 4), c4 = j - r * (MLP_HC / 4);
-                *(float4*)(B + MLP_HC * S1 + r * S2 + c4 * 4) = stg[i];
+                const int r = j / R2, c4 = (j - r * R2) ^ mlp_swz<R2>(r);
+                src = r < N && h0 + c4 * 4 < H ? p.w2 + (size_t)r * p.ldw2 + h0 + c4 * 4 : hat_mlp_zero4;
             }
+            __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(B + base * 4),
+                                             16, 0, 0);
         }
     };
     // The residual is loaded a chunk ahead of the epilogue where the registers
@@ -163,9 +168,13 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     g.ldo = N;
     g.eps = p.eps;
 
-    fetch(0);
-    stash(0);
+    // The lane's swizzled float4 column in the operand reads: rows nt*16 + lr
+    // and n2*16 + lr give (row >> 2) & 3 == (lr >> 2) & 3 and row & 15 == lr.
+    static_assert(R2 % 16 != 0, "the fc2 slice's swizzle is the 2-bit one");
+    const int sg = lg ^ mlp_swz<R1>(lr), sg2 = lg ^ mlp_swz<R2>(lr);
+    fetch(0, 0);
     load_a(tile);
+    __builtin_amdgcn_s_waitcnt(0);  // the LDS writes of fetch have landed
     __syncthreads();
 
     for (; tile < ntiles; tile += gridDim.x) {
@@ -178,7 +187,8 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
         for (int c = 0; c < NCH; ++c) {
             const float* B = Wb + (c & 1) * BUF;
             const bool more = c + 1 < NCH || !last_tile;  // block-uniform
-            if (more) fetch(c + 1 < NCH ? c + 1 : 0);
+            // the other buffer was last read in the previous chunk, before its barrier
+            if (more) fetch(c + 1 < NCH ? c + 1 : 0, (c + 1) & 1);
             // The residual rows for the epilogue, one chunk ahead of it.
             if constexpr (PRE) {
                 if (c == NCH - 1) {
@@ -201,7 +211,10 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             for (int kc = 0; kc < KP / 16; ++kc)
 #pragma unroll
                 for (int nt = 0; nt < MLP_HC / 16; ++nt) {
-                    const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * S1 + kc * 16 + lg * 4);
+                    // physical column: (kc*4 + lg) ^ swizzle, which for R1 % 16 != 0
+                    // (a 2-bit swizzle) is kc*4 + (lg ^ swizzle)
+                    const int pc = R1 % 16 == 0 ? ((kc * 4 + lg) ^ lr) : kc * 4 + sg;
+                    const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * KP + pc * 4);
 #pragma unroll
                     for (int s = 0; s < 4; ++s) h[nt] = mfma16(wv[s], xa[kc][s], h[nt]);
                 }
@@ -221,11 +234,11 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             for (int nt = 0; nt < MLP_HC / 16; ++nt)
 #pragma unroll
                 for (int n2 = 0; n2 < NO / 16; ++n2) {
-                    const f32x4 wv = *(const f32x4*)(B + MLP_HC * S1 + (n2 * 16 + lr) * S2 + nt * 16 + lg * 4);
+                    const f32x4 wv = *(const f32x4*)(B + W1F4 * 4 + (n2 * 16 + lr) * MLP_HC + nt * 16 + sg2 * 4);
 #pragma unroll
                     for (int s = 0; s < 4; ++s) acc2[0][n2] = mfma16(wv[s], h[nt][s], acc2[0][n2]);
                 }
-            if (more) stash((c + 1) & 1);
+            __builtin_amdgcn_s_waitcnt(0);  // the next chunk's LDS writes have landed
             __syncthreads();
         }
         if constexpr (PRE)
