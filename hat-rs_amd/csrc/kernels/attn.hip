@@ -140,12 +140,14 @@ __device__ __forceinline__ void attn_stash(float* Kl, float* Vt,
 
 // Bias table of a head, in log2 units. For OCA the table is stored rotated so
 // that the reference's negative-index wrap (plan.rs:397-416) becomes a plain
-// offset: Tb[j] = table[(j - 880) mod 1521].
+// offset: Tb[j] = table[(j - 880) mod 1521]. For SW it is stored reversed,
+// Tb[j] = table[960 - j], so that consecutive keys of a row read ascending
+// consecutive entries (straight into consecutive accumulator registers).
 template <int D, bool OCA>
 __device__ __forceinline__ void attn_table(const AttnArgs& p, float* Tb, int head)
 {
     for (int i = threadIdx.x; i < AttnShape<D, OCA>::TROWS; i += 512) {
-        int row = i;
+        int row = 960 - i;
         if (OCA) {
             row = i - 880;
             if (row < 0) row += 1521;
@@ -210,9 +212,10 @@ __device__ __forceinline__ void attn_compute(const AttnArgs& p, const float* lds
     const int q = wave * 32 + ql;
     const int qy = q >> 4, qx = q & 15;
 
-    // Bias addressing. SW: idx = (qy-ky+15)*31 + (qx-kx+15) = sw_base - (ky*31+kx).
+    // Bias addressing. SW: idx = (qy-ky+15)*31 + (qx-kx+15) = sw_base - (ky*31+kx),
+    // entry 960 - idx = sw_rbase + (ky*31+kx) of the reversed table.
     // OCA: idx = (ky*39+kx) - (qy*39+qx) + 600 on the rotated table.
-    const int sw_base = (qy + 15) * 31 + qx + 15 - 4 * h;
+    const int sw_rbase = 960 - ((qy + 15) * 31 + qx + 15 - 4 * h);
     const int oca_base = 600 - (qy * 39 + qx);
     // Mask addends (SW, shifted): a key differs in region from the query when
     // its half (bit 3 of y or x) differs, in the last window row / column.
@@ -258,7 +261,7 @@ __device__ __forceinline__ void attn_compute(const AttnArgs& p, const float* lds
                     b = Tb[oca_base + key + 15 * ky];
                 } else {
                     const int ky = key0 >> 4, kx = key0 & 15;
-                    b = Tb[sw_base - (ky * 31 + kx)];
+                    b = Tb[sw_rbase + (ky * 31 + kx)];
                     if (MASKED) b += madd[(ky >> 3) & 1][(kx >> 3) & 1];
                 }
                 a[i] = b;
