@@ -365,6 +365,14 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
         launch(s, wide, (unsigned)((W / 16) * (H / 16)), (unsigned)((C.CO + wbn - 1) / wbn), 1, 512, p);
         return;
     }
+    if (epi == CEPI_FINAL) {
+        if (crop_h > H || crop_w > W || crop_h < 1 || crop_w < 1) throw Error("conv: bad crop");
+        // conv_last 64 -> 3 by per-tap products, 16 x 32 output tiles
+        if (C.CO == 3 && C.CI == 64 && C.CIp == 64 && cin_stride >= 64) {
+            launch(s, "hat_conv_last3", (unsigned)(((W + 31) / 32) * ((H + 15) / 16)), 1, 1, 512, p);
+            return;
+        }
+    }
     launch(s, name, (unsigned)((W / 16) * (H / 8)), (unsigned)((C.CO + BN - 1) / BN), 1, 256, p);
 }
 

@@ -691,6 +691,15 @@ int gpu_selftest(std::string* err)
                 check_close(std::string(wide) + " " + cc.what, dout2.get(), want, 5e-5);
                 note(std::string(wide) + "  " + cc.what + "  32x48");
             }
+            // conv_last by per-tap products: 16 x 32 tiles, so W = 48 leaves a
+            // half tile whose pixels past W are zero halo and are not stored.
+            if (cc.epi == CEPI_FINAL) {
+                Dev dout3(out_n);
+                p.out = dout3.p;
+                launch(s, "hat_conv_last3", ((W + 31) / 32) * ((H + 15) / 16), 1, 1, 512, p);
+                check_close(std::string("hat_conv_last3 ") + cc.what, dout3.get(), want, 5e-5);
+                note(std::string("hat_conv_last3  ") + cc.what + "  32x48");
+            }
         }
 
         // ---- LayerNorm, input preparation, squeeze-excite.
