@@ -203,10 +203,11 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
                 }
             }
 
-            // fc1 for this chunk: h[16 rows][48] = a . w1[chunk]^T
+            // fc1 for this chunk: h[16 rows][48] = b1 + a . w1[chunk]^T, the
+            // accumulators starting from the bias (cpu.rs linear's order)
             f32x4 h[MLP_HC / 16];
 #pragma unroll
-            for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = *(const f32x4*)(Cs + c * MLP_HC + nt * 16 + lg * 4);
 #pragma unroll
             for (int kc = 0; kc < KP / 16; ++kc)
 #pragma unroll
@@ -222,13 +223,9 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             // tile's rows now, under this chunk's fc2 and the epilogue.
             if (c == NCH - 1 && !last_tile) load_a(tile + gridDim.x);
 #pragma unroll
-            for (int nt = 0; nt < MLP_HC / 16; ++nt) {
-                const float4 b4 = *(const float4*)(Cs + c * MLP_HC + nt * 16 + lg * 4);
-                h[nt][0] = gelu(h[nt][0] + b4.x);
-                h[nt][1] = gelu(h[nt][1] + b4.y);
-                h[nt][2] = gelu(h[nt][2] + b4.z);
-                h[nt][3] = gelu(h[nt][3] + b4.w);
-            }
+            for (int nt = 0; nt < MLP_HC / 16; ++nt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) h[nt][j] = gelu(h[nt][j]);
             // fc2 partial sums: out[16 rows][NO] += h . w2[:, chunk]^T
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt)
