@@ -54,7 +54,7 @@ __device__ __forceinline__ EpiConsts global_consts(const GemmArgs& p, int n0)
 // Epilogue shared by the GEMM kernels: lane (lr, lg) holds out[m][n .. n+3]
 // for m = mbase + 16*mt + lr and n = n0 + 16*nt + 4*lg. With pres, the
 // residual values were loaded ahead by the caller (same layout as acc).
-template <int MT, int NT, int EPI>
+template <int MT, int NT, int EPI, bool BIAS_IN_ACC = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts& k, f32x4 (&acc)[MT][NT],
                                               int mbase, int n0, int lr, int lg, const int* colmap,
                                               const f32x4 (*pres)[NT] = nullptr)
@@ -73,8 +73,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts
             const bool live = mlive && n < N;
             f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
             if (live) {
-                const float4 b4 = *(const float4*)(k.bias + (n - n0));
-                v = acc[mt][nt] + (f32x4){b4.x, b4.y, b4.z, b4.w};
+                // BIAS_IN_ACC: the accumulators started from the bias
+                if (BIAS_IN_ACC) {
+                    v = acc[mt][nt];
+                } else {
+                    const float4 b4 = *(const float4*)(k.bias + (n - n0));
+                    v = acc[mt][nt] + (f32x4){b4.x, b4.y, b4.z, b4.w};
+                }
                 if (EPI == EPI_GELU) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) v[j] = gelu(v[j]);
@@ -405,11 +410,15 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 }
             }
         }
+        // The accumulators start from the bias (cpu.rs linear's order: bias,
+        // then the products); Cs is zero past N.
         f32x4 acc[MT][NT];
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+        for (int j = 0; j < NT; ++j) {
+            const f32x4 b4 = *(const f32x4*)(Cs + j * 16 + lg * 4);
 #pragma unroll
-            for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < MT; ++i) acc[i][j] = b4;
+        }
 #pragma unroll 1
         for (int kg = 0; kg < NCH; kg += 3) {
 #pragma unroll
@@ -449,7 +458,7 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 }
             }
         }
-        gemm_epilogue<MT, NT, EPI>(p, kc, acc, mbase, n0, lr, lg, s_colmap, PRE ? rres : nullptr);
+        gemm_epilogue<MT, NT, EPI, true>(p, kc, acc, mbase, n0, lr, lg, s_colmap, PRE ? rres : nullptr);
     }
 }
 
