@@ -31,8 +31,9 @@
 // so D = 24 and D = 30 both need no padding in QK^T.
 //
 // Softmax is computed in base 2 (q pre-scaled by scale*log2(e), the bias table
-// by log2(e)) over key chunks with a running max, which equals the reference's
-// row max subtraction up to rounding.
+// by log2(e)) over key chunks with a running base that is raised only when a
+// score exceeds it by more than 2^8; after the division by the sum this equals
+// the reference's row max subtraction up to rounding.
 #include "common.h"
 
 using namespace hatk;
@@ -275,16 +276,23 @@ __device__ __forceinline__ void attn_compute(const AttnArgs& p, const float* lds
         for (int t = 0; t < CHT; ++t)
 #pragma unroll
             for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[t][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(mrun, mx);
-        const float corr = fast_exp2(mrun - mnew);
+        // Lazy rescaling: the exponent base mrun (shared by the two lane halves
+        // of a query) is raised only in the first chunk or when a score of the
+        // wave exceeds it by more than 8 (log2 units: probabilities stay below
+        // 2^8, sums below 2^16); the final division by the accumulated sum
+        // makes the result independent of the base.
+        if (ch == 0 || __any(mx > mrun + 8.0f)) {  // wave-uniform
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mnew = fmaxf(mrun, mx);
+            const float corr = fast_exp2(mrun - mnew);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i] *= corr;
-        mrun = mnew;
+            for (int i = 0; i < 16; ++i) o[i] *= corr;
+            mrun = mnew;
+        }
 #pragma unroll
         for (int t = 0; t < CHT; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[t][i] = fast_exp2(s[t][i] - mnew);
+            for (int i = 0; i < 16; ++i) s[t][i] = fast_exp2(s[t][i] - mrun);
         // O^T += V^T P^T
 #pragma unroll
         for (int t = 0; t < CHT; ++t) {
