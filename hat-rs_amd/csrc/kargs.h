@@ -61,7 +61,7 @@ struct GemmArgs {
 #define CAB_C 144
 #define CAB_CC 6             // compressed channels
 #define CAB_CS 8             // t1 channel stride (channels 6, 7 are zero)
-#define CAB_K2 80            // 9 taps x 8 channel slots, padded to 5 x 16
+#define CAB_K2 56            // 9 taps x 6 channels (k = tap*6 + ci), 2 zero: 3 x 16 + 8
 #define CAB_NSUM 5           // per-tile sums: whole tile, row 0, row H-1, col 0, col W-1
 
 struct CabConvArgs {
@@ -84,7 +84,7 @@ struct CabGateArgs {
     const float* wb;     // excite [144][sq]
     const float* bb;     // [144]
     const float* bproj;  // attention projection bias [144]
-    float* w2g;          // out: cscale * gate[c] * conv2 weight, [144][CAB_K2] (k = tap*8 + ci)
+    float* w2g;          // out: cscale * gate[c] * conv2 weight, [144][CAB_K2] (k = tap*6 + ci)
     float* bias2;        // out: bproj + cscale * gate * b2, [144]
     float* gate;         // out: the gate itself [144]
     float cscale;

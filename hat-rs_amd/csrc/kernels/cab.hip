@@ -11,9 +11,9 @@
 //     plus the corner counted twice. hat_cab_conv1 leaves per-tile sums of t1
 //     over the tile and over its pixels on the four border lines;
 //   * gate[c] * conv2(t1)[p][c] * cscale is a GEMM of the 3x3 neighbourhood of
-//     t1 at p (9 taps x 8 channel slots) with weights cscale * gate[c] * w2 -
-//     hat_cab_gate folds them, and the attention projection GEMM
-//     (hat_gemmws_cab_ln) runs them as 80 more K.
+//     t1 at p (9 taps x 6 channels, k = tap*6 + ci) with weights cscale *
+//     gate[c] * w2 - hat_cab_gate folds them, and the attention projection GEMM
+//     (hat_gemmws_cab_ln) runs them as 56 more K.
 // So conv2's T x 144 output is never written or read back.
 #include "common.h"
 
@@ -236,9 +236,9 @@ extern "C" __global__ __launch_bounds__(CG_WAVES * 64) void hat_cab_gate(CabGate
     __syncthreads();
     for (int i = tid; i < CAB_C * CAB_K2; i += CG_WAVES * 64) {
         const int c = i / CAB_K2, k = i - c * CAB_K2;
-        const int tap = k / CAB_CS, ci = k - tap * CAB_CS;
+        const int tap = k / CAB_CC, ci = k - tap * CAB_CC;
         float v = 0.0f;
-        if (tap < 9 && ci < CAB_CC) v = (p.cscale * s_gate[c]) * p.w2[(c * CAB_CC + ci) * 9 + tap];
+        if (tap < 9) v = (p.cscale * s_gate[c]) * p.w2[(c * CAB_CC + ci) * 9 + tap];
         p.w2g[i] = v;
     }
 }

@@ -296,8 +296,8 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
     static_assert(NCH % 3 == 0, "the K loop walks groups of three chunks");
     static_assert(!CAB || (KP == 144 && NT == 9), "the folded CAB is the C = 144 family's");
     constexpr int S2 = CAB_K2 + 4;         // LDS row stride of the conv2 slice
-    __shared__ float Wsm[BN * WS_KS];
-    __shared__ float W2s[CAB ? BN * S2 : 1];
+    __shared__ __attribute__((aligned(16))) float Wsm[BN * WS_KS];
+    __shared__ __attribute__((aligned(16))) float W2s[CAB ? BN * S2 : 1];
     __shared__ int s_colmap[EPI == EPI_QKV ? BN : 1];
     constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN;
     // bias (+ LayerNorm weight and bias) of the block's columns
@@ -374,23 +374,34 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         };
 #pragma unroll
         for (int s = 0; s < 3; ++s) load_a(s, s);
-        // CAB: the 3x3 neighbourhood of t1 at each row's pixel, k = tap*8 + ci;
-        // chunk kc2 holds taps 2*kc2 (lane groups 0, 1) and 2*kc2 + 1 (2, 3).
-        f32x4 xg[CAB ? MT : 1][CAB_K2 / 16];
+        // CAB: the 3x3 neighbourhood of t1 at each row's pixel, k = tap*6 + ci
+        // (54 values, 2 zero): three 16-k chunks, lane group g holding k =
+        // 16 kc2 + 4g .. +3 (two float2 of one or two taps), and an 8-k tail,
+        // g holding k = 48 + 2g, 49 + 2g (tap 8's channels 2g, 2g+1; zero for g = 3).
+        constexpr int K2F = CAB_K2 / 16;
+        f32x4 xg[CAB ? MT : 1][K2F];
+        float2 xh[CAB ? MT : 1];
         if (CAB) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const int m = mbase + mt * 16 + lr;
                 const int y = m / p.W, x = m - y * p.W;
-#pragma unroll
-                for (int kc2 = 0; kc2 < CAB_K2 / 16; ++kc2) {
-                    const int tap = 2 * kc2 + (lg >> 1), ci0 = (lg & 1) * 4;
+                // t1[neighbour at tap][ci, ci+1], zero outside the plane
+                auto pair = [&](int tap, int ci) -> float2 {
                     const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
-                    f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    float2 v = make_float2(0.f, 0.f);
                     if (alive[mt] && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W)
-                        v = *(const f32x4*)(p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci0);
-                    xg[mt][kc2] = v;
+                        v = *(const float2*)(p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci);
+                    return v;
+                };
+#pragma unroll
+                for (int kc2 = 0; kc2 < K2F; ++kc2) {
+                    const int k0 = kc2 * 16 + lg * 4, ta = k0 / CAB_CC, ca = k0 - ta * CAB_CC;  // ca: 0, 2 or 4
+                    const float2 lo = pair(ta, ca);
+                    const float2 hi = ca + 2 < CAB_CC ? pair(ta, ca + 2) : pair(ta + 1, 0);
+                    xg[mt][kc2] = (f32x4){lo.x, lo.y, hi.x, hi.y};
                 }
+                xh[mt] = pair(lg < 3 ? 8 : 9, 2 * lg);
             }
         }
         // The residual for the epilogue, loaded now so its latency hides under
@@ -442,19 +453,33 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         }
         if (CAB) {
 #pragma unroll
-            for (int kc2 = 0; kc2 < CAB_K2 / 16; ++kc2) {
+            for (int kc2 = 0; kc2 <= K2F; ++kc2) {
                 // keep each chunk's weight reads next to its MFMAs (hoisting
-                // all five chunks' reads costs more registers than there are)
+                // all of them costs more registers than there are)
                 __builtin_amdgcn_sched_barrier(0);
-                const float* wrow = W2s + lr * S2 + kc2 * 16 + lg * 4;
+                if (kc2 < K2F) {
+                    const float* wrow = W2s + lr * S2 + kc2 * 16 + lg * 4;
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    const f32x4 wv = *(const f32x4*)(wrow + nt * 16 * S2);
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const f32x4 wv = *(const f32x4*)(wrow + nt * 16 * S2);
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
+                        for (int s = 0; s < 4; ++s)
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt)
-                            acc[mt][nt] = mfma16(wv[s], xg[mt][kc2][s], acc[mt][nt]);
+                            for (int mt = 0; mt < MT; ++mt)
+                                acc[mt][nt] = mfma16(wv[s], xg[mt][kc2][s], acc[mt][nt]);
+                    }
+                } else {
+                    // the 8-k tail: two MFMAs, lane group g's k = 48 + 2g + s
+                    const float* wrow = W2s + lr * S2 + K2F * 16 + lg * 2;
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const float2 wv = *(const float2*)(wrow + nt * 16 * S2);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) {
+                            acc[mt][nt] = mfma16(wv.x, xh[mt].x, acc[mt][nt]);
+                            acc[mt][nt] = mfma16(wv.y, xh[mt].y, acc[mt][nt]);
+                        }
+                    }
                 }
             }
         }
@@ -496,7 +521,7 @@ GEMM_WS_INST(hat_gemmws12_gelu, EPI_GELU, 192, 12)
 GEMM_WS_INST(hat_gemmws12_resid_ln, EPI_RESID_LN, 192, 12)
 GEMM_WS_INST(hat_gemmws12_hab_ln, EPI_HAB_LN, 192, 12)
 
-// HAB attention projection with the CAB's conv2 folded in as 80 more K (the
+// HAB attention projection with the CAB's conv2 folded in as 56 more K (the
 // block input as residual, bias = proj bias + folded conv2 bias), then norm2.
 extern "C" __global__ __launch_bounds__(ws_waves(EPI_RESID_LN) * 64) void hat_gemmws_cab_ln(GemmArgs p)
 {

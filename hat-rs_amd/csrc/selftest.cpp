@@ -463,7 +463,7 @@ int gpu_selftest(std::string* err)
                 bias2[c] = bp[c] + cscale * gate[c] * b2[c];
                 for (int tap = 0; tap < 9; ++tap)
                     for (int ci = 0; ci < CC; ++ci)
-                        w2g[(size_t)c * CAB_K2 + tap * CAB_CS + ci] = cscale * gate[c] * w2[((size_t)c * CC + ci) * 9 + tap];
+                        w2g[(size_t)c * CAB_K2 + tap * CAB_CC + ci] = cscale * gate[c] * w2[((size_t)c * CC + ci) * 9 + tap];
             }
             std::vector<double> want((size_t)T * C), wxn((size_t)T * C);
             for (int m = 0; m < T; ++m) {
