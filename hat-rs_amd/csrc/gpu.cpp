@@ -305,8 +305,9 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
 {
     if (H % 8 != 0 || W % 16 != 0) throw Error("conv: plane must be a multiple of 8x16");
     if (cin_stride % 4 != 0 || cin_stride < C.CI) throw Error("conv: bad input channel stride");
-    // The wide-tile kernel (16x16 pixels, a whole 64- or 128-channel column
-    // block per block) for the head convs and the 60-channel CAB conv.
+    // The wide-tile kernel (16x16 pixels, a whole 64-, 96- or 128-channel
+    // column block per block) for the head convs, the 60-channel CAB conv and
+    // the C = 180 trunk convs.
     const char* wide = nullptr;
     int wbn = 0;
     if (H % 16 == 0 && W % 16 == 0 && C.CO % 4 == 0 && co_stride % 4 == 0) {
@@ -316,6 +317,9 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
         } else if (epi == CEPI_SHUFFLE) {
             wide = "hat_convw_n8_shuffle";
             wbn = 128;
+        } else if (epi == CEPI_RESID && C.CO > 144 && C.CO <= 192) {
+            wide = "hat_convw_n6_resid";  // C = 180 trunk convs, two 96-channel blocks
+            wbn = 96;
         }
     }
     const char* name = nullptr;

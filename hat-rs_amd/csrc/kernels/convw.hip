@@ -211,6 +211,9 @@ constexpr int convw_waves(int nt) { return nt > 9 ? 16 : 8; }
 CONVW_INST(hat_convw_n9_store_ln, 9, EPI_STORE_LN, -1)
 CONVW_INST(hat_convw_n9_resid_ln, 9, EPI_RESID_LN, -1)
 CONVW_INST(hat_convw_n9_resid, 9, EPI_RESID, -1)
+// C = 180 (two 96-channel column blocks): the RHAG conv and conv_after_body
+// with the residual (their LayerNorm, needing whole rows, runs separately).
+CONVW_INST(hat_convw_n6_resid, 6, EPI_RESID, -1)
 // Head: conv_before_upsample (-> 64, LeakyReLU) and the upsample convs
 // (64 -> 4*64 or 9*64 in 128-channel column blocks, + PixelShuffle).
 CONVW_INST(hat_convw_n4_store, 4, EPI_STORE, CEPI_STORE)

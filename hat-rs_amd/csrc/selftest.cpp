@@ -564,6 +564,7 @@ int gpu_selftest(std::string* err)
             {180, 60, CEPI_STORE, 1, 0, "cab conv1 180->60 + gelu"},
             {6, 144, CEPI_COLSUM, 0, 0, "cab conv2 6->144 + column sums"},
             {144, 144, CEPI_RESID, 0, 0, "rhag conv 144->144 + residual"},
+            {180, 180, CEPI_RESID, 0, 0, "rhag conv 180->180 + residual"},
             {3, 144, CEPI_STORE, 0, 0, "conv_first 3->144"},
             {144, 64, CEPI_STORE, 2, 0, "conv_before_upsample 144->64 + leaky"},
             {64, 256, CEPI_SHUFFLE, 0, 2, "upsample 64->256 + shuffle 2"},
@@ -682,9 +683,10 @@ int gpu_selftest(std::string* err)
             // The wide-tile kernel serves the same store / shuffle cases.
             const char* wide = cc.epi == CEPI_STORE && cc.CO > 16 && cc.CO <= 64 ? "hat_convw_n4_store"
                                : cc.epi == CEPI_SHUFFLE                           ? "hat_convw_n8_shuffle"
+                               : cc.epi == CEPI_RESID && cc.CO > 144              ? "hat_convw_n6_resid"
                                                                                   : nullptr;
             if (wide) {
-                const int wbn = cc.epi == CEPI_SHUFFLE ? 128 : 64;
+                const int wbn = cc.epi == CEPI_SHUFFLE ? 128 : cc.epi == CEPI_RESID ? 96 : 64;
                 Dev dout2(out_n);
                 p.out = dout2.p;
                 launch(s, wide, (W / 16) * (H / 16), (cc.CO + wbn - 1) / wbn, 1, 512, p);
