@@ -299,6 +299,18 @@ void run_se(hipStream_t s, const float* partial, int nblk, int C, float* red, fl
     launch(s, "hat_se_gate", 1, 1, 1, 256, se);
 }
 
+// The C = 180 CAB conv2 (CO in (144, 192]) and its column sums run on the
+// wide-tile kernel: one partial row per 16x16 tile; every other CEPI_COLSUM
+// conv leaves one per 8x16 tile.
+bool colsum_wide(int CO, int H, int W, int co_stride)
+{
+    return CO > 144 && CO <= 192 && H % 16 == 0 && W % 16 == 0 && CO % 4 == 0 && co_stride % 4 == 0;
+}
+int colsum_rows(int CO, int H, int W, int co_stride)
+{
+    return colsum_wide(CO, H, W, co_stride) ? (W / 16) * (H / 16) : (W / 16) * (H / 8);
+}
+
 void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, int H, int W,
               float* out, int co_stride, int epi, int act, const float* res, float* partial,
               int crop_h, int crop_w, float img_range, const float* mean)
@@ -319,6 +331,9 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
             wbn = 128;
         } else if (epi == CEPI_RESID && C.CO > 144 && C.CO <= 192) {
             wide = "hat_convw_n6_resid";  // C = 180 trunk convs, two 96-channel blocks
+            wbn = 96;
+        } else if (epi == CEPI_COLSUM && colsum_wide(C.CO, H, W, co_stride)) {
+            wide = "hat_convw_n6_colsum";  // C = 180 CAB conv2
             wbn = 96;
         }
     }
@@ -618,7 +633,7 @@ void GpuBackend::ensure_plan(int h, int w)
         return d;
     };
     t1_stride_ = (wt_.compressed + 3) / 4 * 4;
-    nblk_conv2_ = (p.wp / 16) * (p.hp / 8);
+    nblk_conv2_ = colsum_rows((int)C, p.hp, p.wp, (int)C);
     x0_ = A(T * 4);
     body_ = A(T * C);
     xa_ = A(T * C);

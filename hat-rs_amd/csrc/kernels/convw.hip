@@ -22,9 +22,10 @@
 #define CW_P (CW_T + 2)                // halo side
 #define CW_PX (CW_P * CW_P)            // 324 halo pixels
 
-// HEAD selects a head epilogue instead of a GEMM one: CEPI_SHUFFLE (store
-// into the PixelShuffle'd plane, channels pre-permuted at upload) or
-// CEPI_STORE (bias + activation); -1 = none (EPI applies).
+// HEAD selects a direct epilogue instead of a GEMM one: CEPI_SHUFFLE (store
+// into the PixelShuffle'd plane, channels pre-permuted at upload), CEPI_STORE
+// (bias + activation) or CEPI_COLSUM (bias, store, per-tile column sums);
+// -1 = none (EPI applies).
 template <int NT, int EPI, int HEAD, int WAVES>
 __device__ __forceinline__ void convw_body(const ConvArgs& p)
 {
@@ -144,8 +145,11 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
         }
     }
 
-    if (HEAD == CEPI_SHUFFLE || HEAD == CEPI_STORE) {
+    if (HEAD == CEPI_SHUFFLE || HEAD == CEPI_STORE || HEAD == CEPI_COLSUM) {
         // Lane (lr, lg) holds channels co .. co+3 of pixel (y, x), x = tx0 + lr.
+        f32x4 colsum[HEAD == CEPI_COLSUM ? NT : 1];
+#pragma unroll
+        for (int nt = 0; nt < (HEAD == CEPI_COLSUM ? NT : 1); ++nt) colsum[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const int y = ty0 + wave * MT + mt, x = tx0 + lr;
@@ -155,7 +159,10 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
                 if (co >= p.CO) continue;
                 const float4 b4 = *(const float4*)(Cs + j0);
                 f32x4 v = acc[mt][nt] + (f32x4){b4.x, b4.y, b4.z, b4.w};
-                if (HEAD == CEPI_STORE) {
+                if (HEAD == CEPI_COLSUM) {
+                    colsum[nt] += v;
+                    *(float4*)(p.out + ((size_t)y * W + x) * p.co_stride + co) = make_float4(v[0], v[1], v[2], v[3]);
+                } else if (HEAD == CEPI_STORE) {
                     if (p.act == 2) {
 #pragma unroll
                         for (int j = 0; j < 4; ++j) v[j] = v[j] < 0.0f ? v[j] * 0.01f : v[j];
@@ -171,6 +178,39 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
                     const int i = sub / r, jj = sub - i * r;
                     *(float4*)(p.out + ((size_t)(y * r + i) * (W * r) + x * r + jj) * p.co_stride + c) =
                         make_float4(v[0], v[1], v[2], v[3]);
+                }
+            }
+        }
+        if (HEAD == CEPI_COLSUM) {
+            // Column sums of the block's 256 pixels (lg_channel_mean's first
+            // stage, cuda.rs:259-272): over the 16 pixels of a tile row (the
+            // lanes with equal lg), then over the waves through LDS (the patch
+            // buffer, free once every wave is past its last chunk), in a fixed
+            // order; one partial row per tile, [tile][co_stride].
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float v = colsum[nt][j];
+                    v += __shfl_xor(v, 1, 64);
+                    v += __shfl_xor(v, 2, 64);
+                    v += __shfl_xor(v, 4, 64);
+                    v += __shfl_xor(v, 8, 64);
+                    colsum[nt][j] = v;
+                }
+            static_assert(WAVES * BN <= CW_PX * 16, "the column partials fit the patch buffer");
+            __syncthreads();
+            if (lr == 0) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) *(f32x4*)(Ps + wave * BN + nt * 16 + lg * 4) = colsum[nt];
+            }
+            __syncthreads();
+            for (int c = tid; c < BN; c += CW_THREADS) {
+                const int co = co0 + c;
+                if (co < p.CO) {
+                    float v = 0.0f;
+                    for (int w = 0; w < WAVES; ++w) v += Ps[w * BN + c];
+                    p.partial[(size_t)blockIdx.x * p.co_stride + co] = v;
                 }
             }
         }
@@ -214,6 +254,8 @@ CONVW_INST(hat_convw_n9_resid, 9, EPI_RESID, -1)
 // C = 180 (two 96-channel column blocks): the RHAG conv and conv_after_body
 // with the residual (their LayerNorm, needing whole rows, runs separately).
 CONVW_INST(hat_convw_n6_resid, 6, EPI_RESID, -1)
+// C = 180 CAB conv2 (60 -> 180) + per-tile column sums for the channel mean.
+CONVW_INST(hat_convw_n6_colsum, 6, EPI_STORE, CEPI_COLSUM)
 // Head: conv_before_upsample (-> 64, LeakyReLU) and the upsample convs
 // (64 -> 4*64 or 9*64 in 128-channel column blocks, + PixelShuffle).
 CONVW_INST(hat_convw_n4_store, 4, EPI_STORE, CEPI_STORE)

@@ -563,6 +563,7 @@ int gpu_selftest(std::string* err)
             {144, 6, CEPI_STORE, 1, 0, "cab conv1 144->6 + gelu"},
             {180, 60, CEPI_STORE, 1, 0, "cab conv1 180->60 + gelu"},
             {6, 144, CEPI_COLSUM, 0, 0, "cab conv2 6->144 + column sums"},
+            {60, 180, CEPI_COLSUM, 0, 0, "cab conv2 60->180 + column sums"},
             {144, 144, CEPI_RESID, 0, 0, "rhag conv 144->144 + residual"},
             {180, 180, CEPI_RESID, 0, 0, "rhag conv 180->180 + residual"},
             {3, 144, CEPI_STORE, 0, 0, "conv_first 3->144"},
@@ -684,13 +685,25 @@ int gpu_selftest(std::string* err)
             const char* wide = cc.epi == CEPI_STORE && cc.CO > 16 && cc.CO <= 64 ? "hat_convw_n4_store"
                                : cc.epi == CEPI_SHUFFLE                           ? "hat_convw_n8_shuffle"
                                : cc.epi == CEPI_RESID && cc.CO > 144              ? "hat_convw_n6_resid"
+                               : cc.epi == CEPI_COLSUM && cc.CO > 144             ? "hat_convw_n6_colsum"
                                                                                   : nullptr;
             if (wide) {
-                const int wbn = cc.epi == CEPI_SHUFFLE ? 128 : cc.epi == CEPI_RESID ? 96 : 64;
-                Dev dout2(out_n);
+                const int wbn = cc.epi == CEPI_SHUFFLE ? 128 : (cc.epi == CEPI_RESID || cc.epi == CEPI_COLSUM) ? 96 : 64;
+                Dev dout2(out_n), dpart2((size_t)(W / 16) * (H / 16) * cc.CO);
                 p.out = dout2.p;
+                p.partial = dpart2.p;
                 launch(s, wide, (W / 16) * (H / 16), (cc.CO + wbn - 1) / wbn, 1, 512, p);
                 check_close(std::string(wide) + " " + cc.what, dout2.get(), want, 5e-5);
+                if (cc.epi == CEPI_COLSUM) {
+                    // one partial row per 16x16 tile
+                    std::vector<double> ps((size_t)(W / 16) * (H / 16) * cc.CO, 0.0);
+                    for (int y = 0; y < H; ++y)
+                        for (int x = 0; x < W; ++x) {
+                            const int blk = (y / 16) * (W / 16) + x / 16;
+                            for (int o = 0; o < cc.CO; ++o) ps[(size_t)blk * cc.CO + o] += full[((size_t)y * W + x) * cc.CO + o];
+                        }
+                    check_close(std::string(wide) + " partial sums", dpart2.get(), ps, 5e-4);
+                }
                 note(std::string(wide) + "  " + cc.what + "  32x48");
             }
             // conv_last by per-tap products: 16 x 32 tiles, so W = 48 leaves a
