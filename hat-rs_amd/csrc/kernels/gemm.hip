@@ -144,6 +144,17 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts
                         make_float4(v[0], v[1], v[2], v[3]);
                     continue;
                 }
+                // With hdim even, column pairs (n, n+1), (n+2, n+3) are one
+                // head's dims d, d+1 with d even (n and d share parity): two
+                // aligned 8-byte stores.
+                if ((p.hdim & 1) == 0) {
+#pragma unroll
+                    for (int j = 0; j < 4; j += 2) {
+                        const int cm = colmap[n - n0 + j];
+                        *(float2*)(p.out + ((size_t)(cm >> 8) * M + m) * p.hdim + (cm & 255)) = make_float2(v[j], v[j + 1]);
+                    }
+                    continue;
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int cm = colmap[n - n0 + j];
