@@ -313,6 +313,11 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
     constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN;
     // bias (+ LayerNorm weight and bias) of the block's columns
     __shared__ __attribute__((aligned(16))) float Cs[(LNOUT ? 3 : 1) * BN];
+    // q/k/v staging of the 144-column, head_dim 24 shape: per wave 16 rows x 48
+    // columns (two heads), row stride QS_S.
+    constexpr bool QSTAGE = EPI == EPI_QKV && BN == 144 && MT == 1;
+    constexpr int QS_S = 52;
+    __shared__ __attribute__((aligned(16))) float Qs[QSTAGE ? WAVES * 16 * QS_S : 1];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -493,6 +498,31 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                     }
                 }
             }
+        }
+        if (QSTAGE && p.hdim == 24 && p.heads * 24 == BN) {
+            // A slice is one of q, k, v (6 heads x 24). Two heads at a time go
+            // through the wave's LDS region and leave as 16 consecutive rows of
+            // each head: 1536 contiguous bytes per head, every lane storing
+            // 16 bytes of one run, instead of 16-byte pieces 96 bytes apart.
+            float* Q = Qs + wave * 16 * QS_S;
+            const int mrows = M - mbase;  // rows of this wave that exist (may exceed 16)
+#pragma unroll
+            for (int ph = 0; ph < 3; ++ph) {
+#pragma unroll
+                for (int t = 0; t < 3; ++t) *(f32x4*)(Q + lr * QS_S + t * 16 + lg * 4) = acc[0][3 * ph + t];
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+#pragma unroll
+                for (int i = 0; i < 3; ++i) {
+                    const int f = lane + 64 * i, hh = f / 96, r = (f - hh * 96) / 6, d4 = f - hh * 96 - r * 6;
+                    const f32x4 v = *(const f32x4*)(Q + r * QS_S + hh * 24 + d4 * 4);
+                    if (r < mrows) {
+                        const int head = 2 * ph + hh;
+                        *(f32x4*)(p.out + ((size_t)(slice * p.heads + head) * M + mbase + r) * 24 + d4 * 4) = v;
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next phase's writes
+            }
+            continue;
         }
         gemm_epilogue<MT, NT, EPI, true>(p, kc, acc, mbase, n0, lr, lg, s_colmap, PRE ? rres : nullptr);
     }
