@@ -54,11 +54,46 @@ __device__ __forceinline__ EpiConsts global_consts(const GemmArgs& p, int n0)
 // Epilogue shared by the GEMM kernels: lane (lr, lg) holds out[m][n .. n+3]
 // for m = mbase + 16*mt + lr and n = n0 + 16*nt + 4*lg. With pres, the
 // residual values were loaded ahead by the caller (same layout as acc).
-template <int MT, int NT, int EPI, bool BIAS_IN_ACC = false>
+// Stores 16 consecutive whole rows of NT*16 floats (lane (lr, lg) holding
+// columns 16 nt + 4 lg .. +3 of row mbase + lr) through the wave's LDS region
+// `stage` (8 rows of NT*16 + 4 floats): 8 rows at a time go to LDS and leave as
+// one contiguous run, every lane storing whole 16-byte pieces of it, instead of
+// 64-byte pieces one row apart. Rows from M on are not stored.
+template <int NT>
+__device__ __forceinline__ void stage_store_rows(float* stage, const f32x4 (&v)[NT], int mbase, int M, float* dst,
+                                                 int lr, int lg)
+{
+    constexpr int BN = 16 * NT, SS = BN + 4, NF4 = 8 * BN / 4;
+    const int lane = lg * 16 + lr;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        if ((lr >> 3) == half) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) *(f32x4*)(stage + (lr & 7) * SS + nt * 16 + lg * 4) = v[nt];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
+#pragma unroll
+        for (int i = 0; i < (NF4 + 63) / 64; ++i) {
+            const int f = lane + 64 * i;
+            if (f < NF4) {
+                const int row = f / (BN / 4), c4 = f - row * (BN / 4);
+                const int m = mbase + half * 8 + row;
+                const f32x4 x = *(const f32x4*)(stage + row * SS + c4 * 4);
+                if (m < M) *(f32x4*)(dst + (size_t)m * BN + c4 * 4) = x;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // the reads are done before the region is rewritten
+    }
+}
+
+// STAGE: MT = 1, whole contiguous rows (n0 = 0, N = ldo = 16*NT), and `stage`
+// is the wave's LDS region for stage_store_rows.
+template <int MT, int NT, int EPI, bool BIAS_IN_ACC = false, bool STAGE = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts& k, f32x4 (&acc)[MT][NT],
                                               int mbase, int n0, int lr, int lg, const int* colmap,
-                                              const f32x4 (*pres)[NT] = nullptr)
+                                              const f32x4 (*pres)[NT] = nullptr, float* stage = nullptr)
 {
+    static_assert(!STAGE || (MT == 1 && EPI != EPI_QKV), "staged stores are for whole rows of one row tile");
     const int M = p.M, N = p.N;
     constexpr bool LNOUT = EPI == EPI_RESID_LN || EPI == EPI_HAB_LN || EPI == EPI_STORE_LN;
 #pragma unroll
@@ -127,6 +162,22 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts
             q += __shfl_xor(q, 16, 64);
             q += __shfl_xor(q, 32, 64);
             rstd = 1.0f / sqrtf(q / (float)N + p.eps);
+        }
+        if constexpr (STAGE) {
+            stage_store_rows<NT>(stage, acc[0], mbase, M, p.out, lr, lg);
+            if (LNOUT) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int j = nt * 16 + lg * 4;
+                    const float4 w4 = *(const float4*)(k.nw + j);
+                    const float4 b4 = *(const float4*)(k.nb + j);
+                    const f32x4 v = acc[0][nt];
+                    acc[0][nt] = (f32x4){(v[0] - mean) * rstd * w4.x + b4.x, (v[1] - mean) * rstd * w4.y + b4.y,
+                                         (v[2] - mean) * rstd * w4.z + b4.z, (v[3] - mean) * rstd * w4.w + b4.w};
+                }
+                stage_store_rows<NT>(stage, acc[0], mbase, M, p.xn, lr, lg);
+            }
+            continue;
         }
         if (!mlive) continue;
 #pragma unroll
@@ -318,6 +369,9 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
     constexpr bool QSTAGE = EPI == EPI_QKV && BN == 144 && MT == 1;
     constexpr int QS_S = 52;
     __shared__ __attribute__((aligned(16))) float Qs[QSTAGE ? WAVES * 16 * QS_S : 1];
+    // row staging of the whole-row epilogues (N = 144 in one column block)
+    constexpr bool RSTAGE = (EPI == EPI_RESID || EPI == EPI_RESID_LN || EPI == EPI_HAB_LN) && BN == 144 && MT == 1;
+    __shared__ __attribute__((aligned(16))) float Rs[RSTAGE ? WAVES * 8 * (BN + 4) : 1];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -523,6 +577,13 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next phase's writes
             }
             continue;
+        }
+        if constexpr (RSTAGE) {
+            if (N == BN && p.ldo == BN) {
+                gemm_epilogue<MT, NT, EPI, true, true>(p, kc, acc, mbase, n0, lr, lg, s_colmap, PRE ? rres : nullptr,
+                                                       Rs + wave * 8 * (BN + 4));
+                continue;
+            }
         }
         gemm_epilogue<MT, NT, EPI, true>(p, kc, acc, mbase, n0, lr, lg, s_colmap, PRE ? rres : nullptr);
     }
