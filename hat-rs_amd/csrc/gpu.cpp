@@ -190,7 +190,7 @@ void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const fl
         p.N = fc2.N;
         p.ldw1 = fc1.Kp;
         p.ldw2 = fc2.Kp;
-        // One block per CU (120 or 159 KB of LDS), persistent over the 128-row tiles.
+        // One block per CU (113 or 151 KB of LDS), persistent over the 128-row tiles.
         static const int cus = std::max(1, Runtime::get().cu_count());
         const long ntiles = (M + MLP_ROWS - 1) / MLP_ROWS;
         const long rounds = (ntiles + cus - 1) / cus;
