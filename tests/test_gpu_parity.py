@@ -167,6 +167,27 @@ def test_plan_cache_and_determinism(hl, weights_dir):
     assert np.isfinite(ya1).all() and np.isfinite(yb).all()
 
 
+@pytest.mark.parametrize("variant,scale", [("hat-s", 4), ("hat", 3), ("hat-s", 2)])
+def test_tiny_and_ragged_inputs_match_oracle(hl, weights_dir, variant, scale):
+    """Inputs far below and just past one window (1x1, 3x5, 17x33: edge-replicated
+    to 16x16, 16x16 and 32x48, Pre::adjust backend.rs:71-89, and cropped back), on
+    one backend whose plan changes between them, against the oracle."""
+    import oracle
+    wp = make_weights(weights_dir, variant, scale, 9, [2, 2])
+    be = hl.Backend(hl.Weights(wp))
+    om = oracle.OracleModel(wp)
+    rng = np.random.default_rng(9)
+    for h, w in [(1, 1), (3, 5), (17, 33)]:
+        img = rng.random((3, h, w), dtype=np.float32)
+        _say(f"forward {variant} x{scale} {h}x{w}")
+        got = be.forward(h, w, img)
+        assert got.shape == (3, h * scale, w * scale)
+        worst = np.abs(got - om.forward(h, w, img)).max()
+        _say(f"  worst |diff| vs oracle {worst:.3e}")
+        assert worst < FWD_TOL
+    be.close()
+
+
 def test_cfg1_hat_s_64_matches_oracle(hl, weights_dir):
     """Benchmark config 1: the full HAT-S x4 (6 stages x 6 HABs) at 64x64, the
     CPU path's own case, against the oracle."""
