@@ -275,6 +275,50 @@ void run_proj_cab(hipStream_t s, const DevLinear& L, const float* a, long M, flo
     launch(s, "hat_gemmws_cab_ln", (unsigned)g, 1, 1, ws_waves(EPI_RESID_LN) * 64, p);
 }
 
+// The second half of a HAB with the folded CAB, one kernel (C = 144):
+// x' = res + a . proj^T + conv2-segment + bias2; out = x' + MLP(norm2(x'));
+// xn = norm_next(out). out may alias res; a, t1 and xn must not overlap out.
+void run_hab_tail(hipStream_t s, const DevLinear& proj, const DevLinear& fc1, const DevLinear& fc2,
+                  const float* a, const float* res, float* out, float* xn, const float* t1, const float* w2g,
+                  const float* bias2, const float* n2w, const float* n2b, const float* nw, const float* nb,
+                  int H, int W)
+{
+    if (proj.K != CAB_C || proj.Kp != CAB_C || proj.N != CAB_C) throw Error("HAB tail: needs the 144 x 144 projection");
+    if (fc1.K != CAB_C || fc1.Kp != CAB_C || fc1.N != 2 * CAB_C || fc2.K != 2 * CAB_C || fc2.N != CAB_C)
+        throw Error("HAB tail: needs the 144 -> 288 -> 144 MLP");
+    const long M = (long)H * W;
+    if (M > 0x7fffffffL) throw Error("HAB tail: too many rows");
+    HabTailArgs p{};
+    p.a = a;
+    p.res = res;
+    p.out = out;
+    p.xn = xn;
+    p.wp = proj.w;
+    p.w2g = w2g;
+    p.bias2 = bias2;
+    p.t1 = t1;
+    p.n2w = n2w;
+    p.n2b = n2b;
+    p.w1 = fc1.w;
+    p.b1 = fc1.b;
+    p.w2 = fc2.w;
+    p.b2 = fc2.b;
+    p.nw = nw;
+    p.nb = nb;
+    p.M = (int)M;
+    p.H = H;
+    p.W = W;
+    p.eps = 1e-5f;
+    p.ldw1 = fc1.Kp;
+    p.ldw2 = fc2.Kp;
+    // One block per CU (113 KB of LDS), persistent over the 128-row tiles.
+    static const int cus = std::max(1, Runtime::get().cu_count());
+    const long ntiles = (M + MLP_ROWS - 1) / MLP_ROWS;
+    const long rounds = (ntiles + cus - 1) / cus;
+    const long g = std::max(1L, (ntiles + rounds - 1) / rounds);
+    launch(s, "hat_hab_tail", (unsigned)g, 1, 1, MLP_WAVES * 64, p);
+}
+
 // The channel-attention gate from the CAB conv's per-tile column sums:
 // reduce in fixed row blocks, then squeeze-excite.
 void run_se(hipStream_t s, const float* partial, int nblk, int C, float* red, float count,
@@ -734,9 +778,9 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
                 w2g_, bias2_, gate_);
         gemm(lin_.at(p + ".attn.qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
         attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0);
-        run_proj_cab(stream_, proj, ao_, T, x_out, x_in, xn_, raw_.at(p + ".norm2.weight"),
-                     raw_.at(p + ".norm2.bias"), bias2_, t1_, w2g_, H, W);
-        mlp(p + ".mlp", x_out, EPI_RESID_LN, next_norm);
+        run_hab_tail(stream_, proj, lin_.at(p + ".mlp.fc1"), lin_.at(p + ".mlp.fc2"), ao_, x_in, x_out, xn_, t1_,
+                     w2g_, bias2_, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
+                     raw_.at(next_norm + ".weight"), raw_.at(next_norm + ".bias"), H, W);
         return;
     }
     // CAB: conv3x3 -> GELU -> conv3x3 (+ per-tile channel sums) -> gate.

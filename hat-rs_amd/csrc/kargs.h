@@ -160,6 +160,31 @@ struct MlpArgs {
     int ldw1, ldw2;      // packed weight row strides
 };
 
+// The second half of a HAB, C = 144 with the folded CAB (hat_hab_tail):
+//   x' = res + a . wp^T + nb(t1) . w2g^T + bias2,  out = x' + fc2(gelu(fc1(LN2(x')))),
+//   xn = LN_next(out).
+struct HabTailArgs {
+    const float* a;      // [M][144] attention output
+    const float* res;    // [M][144] block input
+    float* out;          // [M][144] (may alias res)
+    float* xn;           // [M][144] LN_next(out)
+    const float* wp;     // [144][144] attention projection (packed, Kp = 144)
+    const float* w2g;    // [144][CAB_K2] gate-scaled conv2 weights
+    const float* bias2;  // [144] projection bias + gated conv2 bias
+    const float* t1;     // [H*W][CAB_CS] CAB conv1 output
+    const float* n2w;    // norm2
+    const float* n2b;
+    const float* w1;     // [288][ldw1]
+    const float* b1;
+    const float* w2;     // [144][ldw2]
+    const float* b2;
+    const float* nw;     // the next block's norm1
+    const float* nb;
+    int M, H, W;         // rows = the H x W plane
+    float eps;
+    int ldw1, ldw2;
+};
+
 struct LnArgs {
     const float* x;
     float* y;

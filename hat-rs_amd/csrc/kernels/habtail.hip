@@ -1,0 +1,301 @@
+// The second half of a HAB in one kernel, C = 144 with the folded CAB
+// (hat_arch.py HAB.forward; cpu.rs hab, 1090-1166; the reference's GPU path
+// runs it as the attention projection, the CAB's conv2 / channel scale, three
+// adds, norm2, the two MLP linears with GELU and the next block's norm1,
+// src/gpu.rs:469-520):
+//
+//   x'  = x + ao . Wp^T + nb(t1) . W2g^T + bias2     (proj, gated conv2, shortcut)
+//   out = x' + fc2(gelu(fc1(LN2(x'))))
+//   xn  = LN_next(out)
+//
+// ao is the attention output, nb(t1) the 3x3 neighbourhood of the CAB's conv1
+// output at the row's pixel (k = tap*6 + ci) and W2g / bias2 the gate-scaled
+// conv2 weights and combined bias (hat_cab_gate). x' and LN2(x') never leave
+// the registers: the projection's accumulators have the layout of the MLP's
+// input (lane (r, g) holds columns 16 kc + 4g .. +3 of row r), so LN2 turns
+// them into fc1's operand in place, and x' is the MLP's residual.
+//
+// A block of 8 waves walks 128-row tiles (wave w owns rows 16w .. 16w+15). Per
+// tile ten weight chunks pass through the double-buffered LDS of the fused
+// MLP (global_load_lds_dwordx4, swizzled unpadded rows, one barrier per
+// chunk): the projection in three chunks of 48 K (144 x 12 float4), the gated
+// conv2 (144 x 16 float4: 56 K, 8 zero), then the six 48-unit hidden chunks.
+// The attention rows of the next tile are loaded under the last chunk's fc2,
+// the residual rows and the t1 neighbourhood at the start of each tile, ahead
+// of the chunks that use them.
+//
+// Included after gemm.hip and mlp.hip in the one translation unit.
+
+#define HT_C 144
+#define HT_NPC 4                                // projection chunks per tile
+#define HT_NCT (HT_NPC + 288 / MLP_HC)          // chunks per tile
+
+__device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
+{
+    constexpr int C = HT_C, NT = C / 16, NH = 2 * C, NCH = NH / MLP_HC;
+    static_assert(HT_NCT % 2 == 0, "the buffer parity repeats per tile");
+    constexpr int R1 = C / 4, R2 = MLP_HC / 4;  // MLP slices: fc1 [48][36], fc2 [144][12] float4
+    constexpr int W1F4 = MLP_HC * R1, F4 = W1F4 + C * R2;
+    constexpr int RP = 12, RC = 16;             // projection chunk [144][12], conv2 chunk [144][16] float4
+    constexpr int PF4 = C * RP, CF4 = C * RC;
+    constexpr int BUF = F4 * 4;
+    constexpr int PER = (F4 + MLP_THREADS - 1) / MLP_THREADS;
+    static_assert(PF4 <= F4 && CF4 <= F4 && PF4 % 64 == 0 && CF4 % 64 == 0 && F4 % 64 == 0, "chunk sizes");
+    static_assert(CAB_K2 == 56 && CAB_C == C, "the conv2 chunk holds 56 K");
+    __shared__ __attribute__((aligned(16))) float Wb[2 * BUF];
+    // b1 [288], b2, next-norm w, b [144 each], bias2, norm2 w, b [144 each]
+    __shared__ __attribute__((aligned(16))) float Cs[NH + 6 * C];
+    float* const b1s = Cs;
+    float* const b2s = Cs + NH;
+    float* const bias2s = Cs + NH + 3 * C;
+    float* const n2ws = Cs + NH + 4 * C;
+    float* const n2bs = Cs + NH + 5 * C;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int M = p.M;
+    const int ntiles = (M + MLP_ROWS - 1) / MLP_ROWS;
+    int tile = blockIdx.x;
+    if (tile >= ntiles) return;  // whole block: no barrier has been passed yet
+
+    for (int i = tid; i < NH + 6 * C; i += MLP_THREADS) {
+        float v;
+        if (i < NH) v = p.b1[i];
+        else if (i < NH + C) v = p.b2[i - NH];
+        else if (i < NH + 2 * C) v = p.nw[i - NH - C];
+        else if (i < NH + 3 * C) v = p.nb[i - NH - 2 * C];
+        else if (i < NH + 4 * C) v = p.bias2[i - NH - 3 * C];
+        else if (i < NH + 5 * C) v = p.n2w[i - NH - 4 * C];
+        else v = p.n2b[i - NH - 5 * C];
+        Cs[i] = v;
+    }
+
+    // The MLP chunks' global offsets (relative to the chunk bases), as in mlp_body.
+    unsigned goff[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int idx = tid + i * MLP_THREADS;
+        if (idx < W1F4) {
+            const int r = idx / R1, c4 = (idx - r * R1) ^ mlp_swz<R1>(r);
+            goff[i] = r * p.ldw1 + c4 * 4;
+        } else {
+            const int j = idx - W1F4;
+            const int r = j / R2, c4 = (j - r * R2) ^ mlp_swz<R2>(r);
+            goff[i] = r * p.ldw2 + c4 * 4;
+        }
+    }
+    // Chunk cj of a tile into LDS buffer buf (cj < 3: projection k 48cj ..;
+    // cj = 3: gated conv2; else hidden chunk cj - 4).
+    auto fetch = [&](int cj, int buf) {
+        float* B = Wb + buf * BUF;
+        const int nf4 = cj < 3 ? PF4 : (cj == 3 ? CF4 : F4);
+        const int h0 = (cj - HT_NPC) * MLP_HC;
+        const float* w1c = p.w1 + (size_t)(h0 > 0 ? h0 : 0) * p.ldw1;
+        const float* w2c = p.w2 + (h0 > 0 ? h0 : 0);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int base = i * MLP_THREADS + wave * 64;  // wave-uniform
+            if (base >= nf4) break;
+            const int idx = base + lane;
+            const float* src;
+            if (cj < 3) {
+                const int r = idx / RP, c4 = (idx - r * RP) ^ mlp_swz<RP>(r);
+                src = p.wp + (size_t)r * C + cj * 48 + c4 * 4;
+            } else if (cj == 3) {
+                const int r = idx / RC, c4 = (idx - r * RC) ^ mlp_swz<RC>(r);
+                src = c4 < CAB_K2 / 4 ? p.w2g + (size_t)r * CAB_K2 + c4 * 4 : hat_mlp_zero4;
+            } else {
+                src = (base < W1F4 ? w1c : w2c) + goff[i];
+            }
+            __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(B + base * 4),
+                                             16, 0, 0);
+        }
+    };
+
+    // Registers: xa = the attention rows (projection phase), then LN2(x') (MLP
+    // phase); xr = the residual rows x, then x'.
+    f32x4 xa[NT], xr[NT];
+    auto load_rows = [&](f32x4 (&dst)[NT], const float* src, int t) {
+        const int m = t * MLP_ROWS + wave * 16 + lr;
+        const float* row = src + (size_t)(m < M ? m : 0) * C + lg * 4;
+#pragma unroll
+        for (int kc = 0; kc < NT; ++kc) {
+            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+            if (m < M) v = *(const f32x4*)(row + kc * 16);
+            dst[kc] = v;
+        }
+    };
+
+    GemmArgs g{};
+    g.out = p.out;
+    g.xn = p.xn;
+    g.M = M;
+    g.N = C;
+    g.ldo = C;
+    g.eps = p.eps;
+    const EpiConsts kc_out{b2s, Cs + NH + C, Cs + NH + 2 * C};
+
+    // Swizzled operand columns (rows nt*16 + lr: (row >> 2) & 3 == (lr >> 2) & 3,
+    // row & 15 == lr).
+    const int sg = lg ^ mlp_swz<R1>(lr), sg2 = lg ^ mlp_swz<R2>(lr), sgp = lg ^ mlp_swz<RP>(lr);
+    fetch(0, 0);
+    load_rows(xa, p.a, tile);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    for (; tile < ntiles; tile += gridDim.x) {
+        const bool last_tile = tile + (int)gridDim.x >= ntiles;
+        const int mbase = tile * MLP_ROWS + wave * 16;
+        // The residual rows and the t1 neighbourhood, loaded while projection
+        // chunk 1 computes (first used after chunk 3 / in chunk 3).
+        f32x4 xg[CAB_K2 / 16];
+        float2 xh;
+        auto load_tail_inputs = [&]() {
+            load_rows(xr, p.res, tile);
+            const int m = mbase + lr;
+            const bool alive = m < M;
+            const int y = m / p.W, x = m - y * p.W;
+            auto pair = [&](int tap, int ci) -> float2 {
+                const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
+                float2 v = make_float2(0.f, 0.f);
+                if (alive && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W)
+                    v = *(const float2*)(p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci);
+                return v;
+            };
+#pragma unroll
+            for (int kc2 = 0; kc2 < CAB_K2 / 16; ++kc2) {
+                const int k0 = kc2 * 16 + lg * 4, ta = k0 / CAB_CC, ca = k0 - ta * CAB_CC;
+                const float2 lo = pair(ta, ca);
+                const float2 hi = ca + 2 < CAB_CC ? pair(ta, ca + 2) : pair(ta + 1, 0);
+                xg[kc2] = (f32x4){lo.x, lo.y, hi.x, hi.y};
+            }
+            xh = pair(lg < 3 ? 8 : 9, 2 * lg);
+        };
+
+        // ---- projection + gated conv2, accumulators starting from bias2
+        f32x4 acc[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[nt] = *(const f32x4*)(bias2s + nt * 16 + lg * 4);
+#pragma unroll
+        for (int cj = 0; cj < HT_NPC; ++cj) {
+            const float* B = Wb + (cj & 1) * BUF;
+            fetch(cj + 1, (cj + 1) & 1);  // the next chunk is always of this tile
+            if (cj == 1) load_tail_inputs();
+            if (cj < 3) {
+#pragma unroll
+                for (int k3 = 0; k3 < 3; ++k3) {
+                    // A operand: the attention rows' 16-k chunk 3 cj + k3; each
+                    // k3's weight reads stay next to their MFMAs
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * 48 + (k3 * 4 + sgp) * 4);
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) acc[nt] = mfma16(wv[s], xa[3 * cj + k3][s], acc[nt]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int k3 = 0; k3 < 3; ++k3) {
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const int pc = (k3 * 4 + lg) ^ lr;  // 4-bit swizzle of the 16-float4 rows
+                        const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * 64 + pc * 4);
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) acc[nt] = mfma16(wv[s], xg[k3][s], acc[nt]);
+                    }
+                }
+                // the 8-k tail: lane group g's k = 48 + 2g + s, float4 12 + g/2
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int pc = (12 + (lg >> 1)) ^ lr;
+                    const float2 wv = *(const float2*)(B + (nt * 16 + lr) * 64 + pc * 4 + (lg & 1) * 2);
+                    acc[nt] = mfma16(wv.x, xh.x, acc[nt]);
+                    acc[nt] = mfma16(wv.y, xh.y, acc[nt]);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+
+        // ---- x' = x + acc (rows past M are zero); xa = LN2(x') (two-pass, biased
+        // variance, cpu.rs:563-581), the four lanes of a row reducing with shuffles.
+        float s = 0.0f;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            xr[nt] = xr[nt] + acc[nt];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s += xr[nt][j];
+        }
+        s += __shfl_xor(s, 16, 64);
+        s += __shfl_xor(s, 32, 64);
+        const float mean = s / (float)C;
+        float q = 0.0f;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float d = xr[nt][j] - mean;
+                q += d * d;
+            }
+        q += __shfl_xor(q, 16, 64);
+        q += __shfl_xor(q, 32, 64);
+        const float rstd = 1.0f / sqrtf(q / (float)C + p.eps);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const f32x4 w4 = *(const f32x4*)(n2ws + nt * 16 + lg * 4);
+            const f32x4 b4 = *(const f32x4*)(n2bs + nt * 16 + lg * 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xa[nt][j] = (xr[nt][j] - mean) * rstd * w4[j] + b4[j];
+        }
+
+        // ---- the MLP (mlp_body's chunk loop), residual x'
+        f32x4 acc2[1][NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc2[0][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int c = 0; c < NCH; ++c) {
+            const int cj = HT_NPC + c;
+            const float* B = Wb + (cj & 1) * BUF;
+            const bool more = c + 1 < NCH || !last_tile;  // block-uniform
+            if (more) fetch(c + 1 < NCH ? cj + 1 : 0, (cj + 1) & 1);
+            f32x4 h[MLP_HC / 16];
+#pragma unroll
+            for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = *(const f32x4*)(b1s + c * MLP_HC + nt * 16 + lg * 4);
+#pragma unroll
+            for (int kc = 0; kc < NT; ++kc)
+#pragma unroll
+                for (int nt = 0; nt < MLP_HC / 16; ++nt) {
+                    const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * C + (kc * 4 + sg) * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) h[nt] = mfma16(wv[s], xa[kc][s], h[nt]);
+                }
+            // the MLP input is dead after the last chunk's fc1: the next tile's
+            // attention rows load under this chunk's fc2 and the epilogue
+            if (c == NCH - 1 && !last_tile) load_rows(xa, p.a, tile + gridDim.x);
+#pragma unroll
+            for (int nt = 0; nt < MLP_HC / 16; ++nt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) h[nt][j] = gelu(h[nt][j]);
+#pragma unroll
+            for (int nt = 0; nt < MLP_HC / 16; ++nt)
+#pragma unroll
+                for (int n2 = 0; n2 < NT; ++n2) {
+                    const f32x4 wv = *(const f32x4*)(B + W1F4 * 4 + (n2 * 16 + lr) * MLP_HC + nt * 16 + sg2 * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) acc2[0][n2] = mfma16(wv[s], h[nt][s], acc2[0][n2]);
+                }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+        // the residual x' straight from xr (one row tile: pres[0][nt] = xr[nt])
+        gemm_epilogue<1, NT, EPI_RESID_LN>(g, kc_out, acc2, mbase, 0, lr, lg, nullptr,
+                                           (const f32x4(*)[NT])xr);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(MLP_THREADS) void hat_hab_tail(HabTailArgs p) { hab_tail_body(p); }

@@ -5,6 +5,7 @@
 #include "conv.hip"
 #include "gemm.hip"
 #include "mlp.hip"
+#include "habtail.hip"
 #include "cab.hip"
 #include "convw.hip"
 #include "misc.hip"

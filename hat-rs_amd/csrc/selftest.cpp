@@ -488,6 +488,67 @@ int gpu_selftest(std::string* err)
             check_close("hat_gemmws_cab_ln", dout.get(), want, 5e-5);
             check_close("hat_gemmws_cab_ln layernorm", dxo.get(), wxn, 5e-5);
             note("hat_gemmws_cab_ln proj + folded conv2 + norm2");
+
+            // The fused HAB tail against hat_gemmws_cab_ln followed by the fused
+            // MLP (both checked above against double precision) on the same
+            // inputs: out = x' + MLP(norm2(x')), xn = norm_next(out).
+            {
+                const int Hd = 2 * C;
+                std::vector<float> f1 = rng.vec((size_t)Hd * C, 0.05f), fb1 = rng.vec(Hd, 0.1f),
+                                   f2 = rng.vec((size_t)C * Hd, 0.05f), fb2 = rng.vec(C, 0.1f),
+                                   mw = rng.vec(C, 1.0f), mb = rng.vec(C, 0.1f);
+                int K1 = 0, K2 = 0;
+                std::vector<float> f1p = pack_linear(f1.data(), Hd, C, &K1), f2p = pack_linear(f2.data(), C, Hd, &K2);
+                Dev df1(f1p), dfb1(fb1), df2(f2p), dfb2(fb2), dmw(mw), dmb(mb), dxn_ref((size_t)T * C),
+                    dout_t(res), dxn_t((size_t)T * C);
+                MlpArgs mp{};
+                mp.a = dxo.p;  // norm2(x') from hat_gemmws_cab_ln
+                mp.w1 = df1.p;
+                mp.b1 = dfb1.p;
+                mp.w2 = df2.p;
+                mp.b2 = dfb2.p;
+                mp.res = dout.p;  // x', updated in place
+                mp.out = dout.p;
+                mp.xn = dxn_ref.p;
+                mp.nw = dmw.p;
+                mp.nb = dmb.p;
+                mp.M = T;
+                mp.eps = 1e-5f;
+                mp.K = C;
+                mp.H = Hd;
+                mp.N = C;
+                mp.ldw1 = K1;
+                mp.ldw2 = K2;
+                launch(s, "hat_mlp_resid_ln", 2, 1, 1, MLP_WAVES * 64, mp);
+                HabTailArgs tp{};
+                tp.a = dao.p;
+                tp.res = dout_t.p;  // in place over the block input, as in the forward
+                tp.out = dout_t.p;
+                tp.xn = dxn_t.p;
+                tp.wp = dwp.p;
+                tp.w2g = dw2g.p;
+                tp.bias2 = dbias2.p;
+                tp.t1 = dt1.p;
+                tp.n2w = dnw.p;
+                tp.n2b = dnb.p;
+                tp.w1 = df1.p;
+                tp.b1 = dfb1.p;
+                tp.w2 = df2.p;
+                tp.b2 = dfb2.p;
+                tp.nw = dmw.p;
+                tp.nb = dmb.p;
+                tp.M = T;
+                tp.H = H;
+                tp.W = W;
+                tp.eps = 1e-5f;
+                tp.ldw1 = K1;
+                tp.ldw2 = K2;
+                launch(s, "hat_hab_tail", 5, 1, 1, MLP_WAVES * 64, tp);  // 12 tiles: blocks walk 2 or 3
+                const std::vector<float> ro = dout.get(), rx = dxn_ref.get();
+                check_close("hat_hab_tail", dout_t.get(), std::vector<double>(ro.begin(), ro.end()), 2e-5);
+                check_close("hat_hab_tail next norm", dxn_t.get(), std::vector<double>(rx.begin(), rx.end()), 2e-5);
+                note("hat_hab_tail (proj + folded conv2 + norm2 + MLP + norm) vs the two-kernel path");
+            }
         }
 
         // ---- trunk convs with every output channel in a block (C -> 144):
