@@ -87,6 +87,23 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             goff[i] = r * p.ldw2 + c4 * 4;
         }
     }
+    // The projection chunks' offsets (chunk cj adds 48 cj) and the conv2
+    // chunk's (-1: a zero slot), per LDS slot of this thread.
+    constexpr int PPER = (PF4 + MLP_THREADS - 1) / MLP_THREADS, CPER = (CF4 + MLP_THREADS - 1) / MLP_THREADS;
+    unsigned poff[PPER];
+    int coff[CPER];
+#pragma unroll
+    for (int i = 0; i < PPER; ++i) {
+        const int idx = tid + i * MLP_THREADS;
+        const int r = idx / RP, c4 = (idx - r * RP) ^ mlp_swz<RP>(r);
+        poff[i] = r * C + c4 * 4;
+    }
+#pragma unroll
+    for (int i = 0; i < CPER; ++i) {
+        const int idx = tid + i * MLP_THREADS;
+        const int r = idx / RC, c4 = (idx - r * RC) ^ mlp_swz<RC>(r);
+        coff[i] = c4 < CAB_K2 / 4 ? r * CAB_K2 + c4 * 4 : -1;
+    }
     // Chunk cj of a tile into LDS buffer buf (cj < 3: projection k 48cj ..;
     // cj = 3: gated conv2; else hidden chunk cj - 4).
     auto fetch = [&](int cj, int buf) {
@@ -102,11 +119,10 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             const int idx = base + lane;
             const float* src;
             if (cj < 3) {
-                const int r = idx / RP, c4 = (idx - r * RP) ^ mlp_swz<RP>(r);
-                src = p.wp + (size_t)r * C + cj * 48 + c4 * 4;
+                src = p.wp + cj * 48 + poff[i < PPER ? i : 0];
             } else if (cj == 3) {
-                const int r = idx / RC, c4 = (idx - r * RC) ^ mlp_swz<RC>(r);
-                src = c4 < CAB_K2 / 4 ? p.w2g + (size_t)r * CAB_K2 + c4 * 4 : hat_mlp_zero4;
+                const int o = coff[i < CPER ? i : 0];
+                src = o >= 0 ? p.w2g + o : hat_mlp_zero4;
             } else {
                 src = (base < W1F4 ? w1c : w2c) + goff[i];
             }
