@@ -278,14 +278,22 @@ void run_proj_cab(hipStream_t s, const DevLinear& L, const float* a, long M, flo
 // The second half of a HAB with the folded CAB, one kernel (C = 144):
 // x' = res + a . proj^T + conv2-segment + bias2; out = x' + MLP(norm2(x'));
 // xn = norm_next(out). out may alias res; a, t1 and xn must not overlap out.
+// Without t1 (the OCAB): x' = res + a . proj^T + bias2 (the projection bias),
+// out = x' + MLP(norm2(x')), no xn.
+bool hab_tail_fits(const DevLinear& proj, const DevLinear& fc1, const DevLinear& fc2)
+{
+    return proj.K == HT_C && proj.Kp == HT_C && proj.N == HT_C && fc1.K == HT_C && fc1.Kp == HT_C &&
+           fc1.N == 2 * HT_C && fc2.K == 2 * HT_C && fc2.N == HT_C;
+}
+
 void run_hab_tail(hipStream_t s, const DevLinear& proj, const DevLinear& fc1, const DevLinear& fc2,
                   const float* a, const float* res, float* out, float* xn, const float* t1, const float* w2g,
                   const float* bias2, const float* n2w, const float* n2b, const float* nw, const float* nb,
                   int H, int W)
 {
-    if (proj.K != CAB_C || proj.Kp != CAB_C || proj.N != CAB_C) throw Error("HAB tail: needs the 144 x 144 projection");
-    if (fc1.K != CAB_C || fc1.Kp != CAB_C || fc1.N != 2 * CAB_C || fc2.K != 2 * CAB_C || fc2.N != CAB_C)
-        throw Error("HAB tail: needs the 144 -> 288 -> 144 MLP");
+    const bool cab = t1 != nullptr;
+    if (cab && (!w2g || !xn || !nw || !nb)) throw Error("HAB tail: the CAB form needs w2g and the next norm");
+    if (!hab_tail_fits(proj, fc1, fc2)) throw Error("HAB tail: needs the 144 x 144 projection and 144 -> 288 -> 144 MLP");
     const long M = (long)H * W;
     if (M > 0x7fffffffL) throw Error("HAB tail: too many rows");
     HabTailArgs p{};
@@ -316,7 +324,7 @@ void run_hab_tail(hipStream_t s, const DevLinear& proj, const DevLinear& fc1, co
     const long ntiles = (M + MLP_ROWS - 1) / MLP_ROWS;
     const long rounds = (ntiles + cus - 1) / cus;
     const long g = std::max(1L, (ntiles + rounds - 1) / rounds);
-    launch(s, "hat_hab_tail", (unsigned)g, 1, 1, MLP_WAVES * 64, p);
+    launch(s, cab ? "hat_hab_tail" : "hat_ocab_tail", (unsigned)g, 1, 1, MLP_WAVES * 64, p);
 }
 
 // The channel-attention gate from the CAB conv's per-tile column sums:
@@ -810,8 +818,16 @@ void GpuBackend::ocab(int stage, float* x)
     const int C = wt_.embed;
     gemm(lin_.at(p + ".qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
     attention(p + ".relative_position_bias_table", true, 0);
-    gemm(lin_.at(p + ".proj"), ao_, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, xn_,
-         p + ".norm2");
+    const DevLinear& proj = lin_.at(p + ".proj");
+    const DevLinear &fc1 = lin_.at(p + ".mlp.fc1"), &fc2 = lin_.at(p + ".mlp.fc2");
+    if (hab_tail_fits(proj, fc1, fc2)) {
+        // projection + shortcut + norm2 + MLP + residual in one kernel
+        run_hab_tail(stream_, proj, fc1, fc2, ao_, x, x, nullptr, nullptr,
+                     nullptr, proj.b, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"), nullptr, nullptr,
+                     plan_.hp, plan_.wp);
+        return;
+    }
+    gemm(proj, ao_, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, xn_, p + ".norm2");
     mlp(p + ".mlp", x, EPI_RESID, "");
 }
 

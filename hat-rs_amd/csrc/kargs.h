@@ -160,6 +160,9 @@ struct MlpArgs {
     int ldw1, ldw2;      // packed weight row strides
 };
 
+// The fused block tails' width.
+#define HT_C 144
+
 // The second half of a HAB, C = 144 with the folded CAB (hat_hab_tail):
 //   x' = res + a . wp^T + nb(t1) . w2g^T + bias2,  out = x' + fc2(gelu(fc1(LN2(x')))),
 //   xn = LN_next(out).

@@ -15,8 +15,11 @@
 // input (lane (r, g) holds columns 16 kc + 4g .. +3 of row r), so LN2 turns
 // them into fc1's operand in place, and x' is the MLP's residual.
 //
+// hat_ocab_tail is the same without the conv2 chunk and the next norm (the
+// OCAB: x' = x + ao . Wp^T + bp, out = x' + MLP(norm2(x'))).
+//
 // A block of 8 waves walks 128-row tiles (wave w owns rows 16w .. 16w+15). Per
-// tile ten weight chunks pass through the double-buffered LDS of the fused
+// tile ten (OCAB: nine) weight chunks pass through the double-buffered LDS of the fused
 // MLP (global_load_lds_dwordx4, swizzled unpadded rows, one barrier per
 // chunk): the projection in three chunks of 48 K (144 x 12 float4), the gated
 // conv2 (144 x 16 float4: 56 K, 8 zero), then the six 48-unit hidden chunks.
@@ -26,14 +29,15 @@
 //
 // Included after gemm.hip and mlp.hip in the one translation unit.
 
-#define HT_C 144
-#define HT_NPC 4                                // projection chunks per tile
-#define HT_NCT (HT_NPC + 288 / MLP_HC)          // chunks per tile
-
+// CAB: the HAB's tail (the gated conv2 chunk; EPI_RESID_LN writes the next
+// norm1). Without it, the OCAB's (hat_arch.py OCAB.forward, cpu.rs ocab
+// 983-1055): x' = x + a . Wp^T + bp, out = x' + MLP(norm2(x')), EPI_RESID.
+template <bool CAB, int EPI>
 __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
 {
     constexpr int C = HT_C, NT = C / 16, NH = 2 * C, NCH = NH / MLP_HC;
-    static_assert(HT_NCT % 2 == 0, "the buffer parity repeats per tile");
+    constexpr int HT_NPC = CAB ? 4 : 3;         // projection chunks per tile
+    constexpr int HT_NCT = HT_NPC + NCH;        // chunks per tile
     constexpr int R1 = C / 4, R2 = MLP_HC / 4;  // MLP slices: fc1 [48][36], fc2 [144][12] float4
     constexpr int W1F4 = MLP_HC * R1, F4 = W1F4 + C * R2;
     constexpr int RP = 12, RC = 16;             // projection chunk [144][12], conv2 chunk [144][16] float4
@@ -65,8 +69,8 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
         float v;
         if (i < NH) v = p.b1[i];
         else if (i < NH + C) v = p.b2[i - NH];
-        else if (i < NH + 2 * C) v = p.nw[i - NH - C];
-        else if (i < NH + 3 * C) v = p.nb[i - NH - 2 * C];
+        else if (i < NH + 2 * C) v = EPI == EPI_RESID_LN ? p.nw[i - NH - C] : 0.0f;
+        else if (i < NH + 3 * C) v = EPI == EPI_RESID_LN ? p.nb[i - NH - 2 * C] : 0.0f;
         else if (i < NH + 4 * C) v = p.bias2[i - NH - 3 * C];
         else if (i < NH + 5 * C) v = p.n2w[i - NH - 4 * C];
         else v = p.n2b[i - NH - 5 * C];
@@ -91,7 +95,7 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
     // chunk's (-1: a zero slot), per LDS slot of this thread.
     constexpr int PPER = (PF4 + MLP_THREADS - 1) / MLP_THREADS, CPER = (CF4 + MLP_THREADS - 1) / MLP_THREADS;
     unsigned poff[PPER];
-    int coff[CPER];
+    int coff[CAB ? CPER : 1];
 #pragma unroll
     for (int i = 0; i < PPER; ++i) {
         const int idx = tid + i * MLP_THREADS;
@@ -99,16 +103,16 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
         poff[i] = r * C + c4 * 4;
     }
 #pragma unroll
-    for (int i = 0; i < CPER; ++i) {
+    for (int i = 0; i < (CAB ? CPER : 0); ++i) {
         const int idx = tid + i * MLP_THREADS;
         const int r = idx / RC, c4 = (idx - r * RC) ^ mlp_swz<RC>(r);
         coff[i] = c4 < CAB_K2 / 4 ? r * CAB_K2 + c4 * 4 : -1;
     }
     // Chunk cj of a tile into LDS buffer buf (cj < 3: projection k 48cj ..;
-    // cj = 3: gated conv2; else hidden chunk cj - 4).
+    // cj = 3 with the CAB: gated conv2; else hidden chunk cj - HT_NPC).
     auto fetch = [&](int cj, int buf) {
         float* B = Wb + buf * BUF;
-        const int nf4 = cj < 3 ? PF4 : (cj == 3 ? CF4 : F4);
+        const int nf4 = cj < 3 ? PF4 : (CAB && cj == 3 ? CF4 : F4);
         const int h0 = (cj - HT_NPC) * MLP_HC;
         const float* w1c = p.w1 + (size_t)(h0 > 0 ? h0 : 0) * p.ldw1;
         const float* w2c = p.w2 + (h0 > 0 ? h0 : 0);
@@ -120,8 +124,8 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             const float* src;
             if (cj < 3) {
                 src = p.wp + cj * 48 + poff[i < PPER ? i : 0];
-            } else if (cj == 3) {
-                const int o = coff[i < CPER ? i : 0];
+            } else if (CAB && cj == 3) {
+                const int o = coff[i < CPER && CAB ? i : 0];
                 src = o >= 0 ? p.w2g + o : hat_mlp_zero4;
             } else {
                 src = (base < W1F4 ? w1c : w2c) + goff[i];
@@ -162,15 +166,19 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    for (; tile < ntiles; tile += gridDim.x) {
+    // gc: the block's chunk count so far; chunk gc sits in buffer gc & 1
+    int gc = 0;
+    for (; tile < ntiles; tile += gridDim.x, gc += HT_NCT) {
         const bool last_tile = tile + (int)gridDim.x >= ntiles;
         const int mbase = tile * MLP_ROWS + wave * 16;
-        // The residual rows and the t1 neighbourhood, loaded while projection
-        // chunk 1 computes (first used after chunk 3 / in chunk 3).
+        // The residual rows and (CAB) the t1 neighbourhood, loaded while
+        // projection chunk 1 computes (first used after the projection / in
+        // the conv2 chunk).
         f32x4 xg[CAB_K2 / 16];
         float2 xh;
         auto load_tail_inputs = [&]() {
             load_rows(xr, p.res, tile);
+            if (!CAB) return;
             const int m = mbase + lr;
             const bool alive = m < M;
             const int y = m / p.W, x = m - y * p.W;
@@ -191,14 +199,14 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             xh = pair(lg < 3 ? 8 : 9, 2 * lg);
         };
 
-        // ---- projection + gated conv2, accumulators starting from bias2
+        // ---- projection (+ gated conv2), accumulators starting from bias2
         f32x4 acc[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[nt] = *(const f32x4*)(bias2s + nt * 16 + lg * 4);
 #pragma unroll
         for (int cj = 0; cj < HT_NPC; ++cj) {
-            const float* B = Wb + (cj & 1) * BUF;
-            fetch(cj + 1, (cj + 1) & 1);  // the next chunk is always of this tile
+            const float* B = Wb + ((gc + cj) & 1) * BUF;
+            fetch(cj + 1, (gc + cj + 1) & 1);  // the next chunk is always of this tile
             if (cj == 1) load_tail_inputs();
             if (cj < 3) {
 #pragma unroll
@@ -213,7 +221,7 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
                         for (int s = 0; s < 4; ++s) acc[nt] = mfma16(wv[s], xa[3 * cj + k3][s], acc[nt]);
                     }
                 }
-            } else {
+            } else if (CAB) {
 #pragma unroll
                 for (int k3 = 0; k3 < 3; ++k3) {
                     __builtin_amdgcn_sched_barrier(0);
@@ -276,9 +284,9 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
 #pragma unroll 1
         for (int c = 0; c < NCH; ++c) {
             const int cj = HT_NPC + c;
-            const float* B = Wb + (cj & 1) * BUF;
+            const float* B = Wb + ((gc + cj) & 1) * BUF;
             const bool more = c + 1 < NCH || !last_tile;  // block-uniform
-            if (more) fetch(c + 1 < NCH ? cj + 1 : 0, (cj + 1) & 1);
+            if (more) fetch(c + 1 < NCH ? cj + 1 : 0, (gc + cj + 1) & 1);
             f32x4 h[MLP_HC / 16];
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = *(const f32x4*)(b1s + c * MLP_HC + nt * 16 + lg * 4);
@@ -309,9 +317,16 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             __syncthreads();
         }
         // the residual x' straight from xr (one row tile: pres[0][nt] = xr[nt])
-        gemm_epilogue<1, NT, EPI_RESID_LN>(g, kc_out, acc2, mbase, 0, lr, lg, nullptr,
+        gemm_epilogue<1, NT, EPI>(g, kc_out, acc2, mbase, 0, lr, lg, nullptr,
                                            (const f32x4(*)[NT])xr);
     }
 }
 
-extern "C" __global__ __launch_bounds__(MLP_THREADS) void hat_hab_tail(HabTailArgs p) { hab_tail_body(p); }
+extern "C" __global__ __launch_bounds__(MLP_THREADS) void hat_hab_tail(HabTailArgs p)
+{
+    hab_tail_body<true, EPI_RESID_LN>(p);
+}
+extern "C" __global__ __launch_bounds__(MLP_THREADS) void hat_ocab_tail(HabTailArgs p)
+{
+    hab_tail_body<false, EPI_RESID>(p);
+}

@@ -548,6 +548,46 @@ int gpu_selftest(std::string* err)
                 check_close("hat_hab_tail", dout_t.get(), std::vector<double>(ro.begin(), ro.end()), 2e-5);
                 check_close("hat_hab_tail next norm", dxn_t.get(), std::vector<double>(rx.begin(), rx.end()), 2e-5);
                 note("hat_hab_tail (proj + folded conv2 + norm2 + MLP + norm) vs the two-kernel path");
+
+                // The OCAB's tail: hat_gemmws_resid_ln (proj + bias + shortcut +
+                // norm2) then hat_mlp_resid, against hat_ocab_tail.
+                Dev dref2(res), dxn2((size_t)T * C), dout_o(res);
+                GemmArgs op{};
+                op.a = dao.p;
+                op.w = dwp.p;
+                op.bias = dbp.p;
+                op.out = dref2.p;
+                op.res = dref2.p;
+                op.xn = dxn2.p;
+                op.nw = dnw.p;
+                op.nb = dnb.p;
+                op.M = T;
+                op.N = C;
+                op.K = C;
+                op.Kp = Kp;
+                op.lda = C;
+                op.ldo = C;
+                op.eps = 1e-5f;
+                launch(s, "hat_gemmws_resid_ln", 3, 1, 1, ws_waves(EPI_RESID_LN) * 64, op);
+                MlpArgs mo = mp;
+                mo.a = dxn2.p;
+                mo.res = dref2.p;
+                mo.out = dref2.p;
+                mo.xn = nullptr;
+                launch(s, "hat_mlp_resid", 2, 1, 1, MLP_WAVES * 64, mo);
+                HabTailArgs to = tp;
+                to.res = dout_o.p;
+                to.out = dout_o.p;
+                to.xn = nullptr;
+                to.t1 = nullptr;
+                to.w2g = nullptr;
+                to.bias2 = dbp.p;
+                to.nw = nullptr;
+                to.nb = nullptr;
+                launch(s, "hat_ocab_tail", 5, 1, 1, MLP_WAVES * 64, to);
+                const std::vector<float> r2 = dref2.get();
+                check_close("hat_ocab_tail", dout_o.get(), std::vector<double>(r2.begin(), r2.end()), 2e-5);
+                note("hat_ocab_tail (proj + norm2 + MLP) vs the two-kernel path");
             }
         }
 
