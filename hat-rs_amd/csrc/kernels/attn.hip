@@ -199,7 +199,7 @@ __device__ __forceinline__ void attn_compute(const AttnArgs& p, const float* lds
     using S = AttnShape<D, OCA>;
     constexpr int HALF = S::HALF, HP = S::HP, RSK = S::RSK, NK = S::NK, RSV = S::RSV;
     constexpr int NKT = NK / 32;                // 32-key tiles
-    constexpr int CHT = OCA ? 3 : 2;            // tiles per softmax chunk
+    constexpr int CHT = OCA ? 3 : 1;            // tiles per softmax chunk
     constexpr int NCH = NKT / CHT;
     static_assert(NKT % CHT == 0, "chunking");
 
