@@ -208,9 +208,11 @@ void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const fl
 
 // Folded CAB, first half: t1 = gelu(conv1(xn)) with its per-tile sums, then
 // the gate and the gate-scaled conv2 weights (w2g) and combined bias (bias2 =
-// bproj + cscale * gate * b2) for the projection GEMM.
+// bproj + cscale * gate * b2) for the projection GEMM. With `defer`, the gate
+// is not launched: its arguments go to *defer, for the attention launch to run.
 void run_cab(hipStream_t s, const DevCab& cb, const float* xn, int H, int W, const float* bproj,
-             float cscale, int sq, float* t1, float* partial, float* w2g, float* bias2, float* gate)
+             float cscale, int sq, float* t1, float* partial, float* w2g, float* bias2, float* gate,
+             CabGateArgs* defer = nullptr)
 {
     if (H % 16 != 0 || W % 16 != 0 || H < 16 || W < 16) throw Error("CAB: plane must be 16-aligned");
     if (sq < 1 || sq > 64) throw Error("CAB: squeeze width must be 1..64");
@@ -237,6 +239,10 @@ void run_cab(hipStream_t s, const DevCab& cb, const float* xn, int H, int W, con
     g.gate = gate;
     g.cscale = cscale;
     g.sq = sq;
+    if (defer) {
+        *defer = g;
+        return;
+    }
     launch(s, "hat_cab_gate", 1, 1, 1, 1024, g);
 }
 
@@ -485,8 +491,9 @@ void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride,
 }
 
 void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, const Plan& pl,
-              int heads, int D, bool oca, int shift)
+              int heads, int D, bool oca, int shift, const CabGateArgs* gate = nullptr)
 {
+    if (gate && (oca || attn_persistent(D, oca))) throw Error("attention: the CAB gate rides on SW launches only");
     if (pl.win != 16 || pl.owin != 24)
         throw Error("attention: the gfx950 kernels are built for window 16 / overlap window 24");
     const char* name = nullptr;
@@ -509,6 +516,10 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
     p.opad = pl.opad();
     p.T = (int)pl.tokens();
     p.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+    if (gate) {
+        p.with_gate = 1;
+        p.gate = *gate;
+    }
     if (attn_persistent(D, oca)) {
         static const int cus = std::max(1, Runtime::get().cu_count());
         const long items = (long)pl.nw() * heads;
@@ -764,9 +775,9 @@ void GpuBackend::conv(const DevConv& C, const float* in, int cin_stride, int H, 
              crop_w, wt_.img_range, wt_.mean);
 }
 
-void GpuBackend::attention(const std::string& table, bool oca, int shift)
+void GpuBackend::attention(const std::string& table, bool oca, int shift, const CabGateArgs* gate)
 {
-    run_attn(stream_, qkv_, raw_.at(table), ao_, plan_, wt_.heads, wt_.head_dim, oca, shift);
+    run_attn(stream_, qkv_, raw_.at(table), ao_, plan_, wt_.heads, wt_.head_dim, oca, shift, gate);
 }
 
 // HAB.forward (hat_arch.py:266-309; cpu.rs:1090-1166):
@@ -780,12 +791,14 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
     const long T = plan_.tokens();
     const int C = wt_.embed, H = plan_.hp, W = plan_.wp;
     if (cab_fold_) {
-        // CAB, folded: conv1 + GELU and the gate here; conv2 runs inside proj.
+        // CAB, folded: conv1 + GELU here, the gate inside the attention
+        // launch (its first block), conv2 inside the tail's projection.
         const DevLinear& proj = lin_.at(p + ".attn.proj");
+        CabGateArgs gate{};
         run_cab(stream_, cab_.at(p), xn_, H, W, proj.b, wt_.conv_scale, wt_.squeezed, t1_, cab_part_,
-                w2g_, bias2_, gate_);
+                w2g_, bias2_, gate_, &gate);
         gemm(lin_.at(p + ".attn.qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
-        attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0);
+        attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, &gate);
         run_hab_tail(stream_, proj, lin_.at(p + ".mlp.fc1"), lin_.at(p + ".mlp.fc2"), ao_, x_in, x_out, xn_, t1_,
                      w2g_, bias2_, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
                      raw_.at(next_norm + ".weight"), raw_.at(next_norm + ".bias"), H, W);

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "hip_rt.h"
+#include "kargs.h"
 #include "plan.h"
 #include "weights.h"
 
@@ -106,7 +107,7 @@ private:
     void conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
               int co_stride, int epi, int act, const float* res = nullptr, float* partial = nullptr,
               int crop_h = 0, int crop_w = 0);
-    void attention(const std::string& table, bool oca, int shift);
+    void attention(const std::string& table, bool oca, int shift, const hatk::CabGateArgs* gate = nullptr);
     void mlp(const std::string& prefix, float* x, int epi, const std::string& norm);
     void hab(int stage, int block, float* x_in, float* x_out, const std::string& next_norm);
     void ocab(int stage, float* x);

@@ -136,6 +136,10 @@ struct AttnArgs {
     int owin, opad;      // OCA: unfold window and padding
     int T;
     float qscale;        // head_dim^-0.5 * log2(e)
+    // with_gate: block (0, 0) of the item grid first computes the folded CAB's
+    // gate (hat_cab_gate's work), which the HAB tail after this launch needs
+    int with_gate;
+    CabGateArgs gate;
 };
 
 // Fused MLP (C = 144, hidden 288; C = 180, hidden 360):

@@ -339,6 +339,13 @@ __device__ __forceinline__ void attn_item_kernel(const AttnArgs& p, float* lds)
     using S = AttnShape<D, OCA>;
     float* Vt = lds + S::NK * S::RSK;
     const int wi = blockIdx.x, head = blockIdx.y;
+    if (!OCA && p.with_gate && wi == 0 && head == 0) {  // block-uniform
+        // The CAB gate rides in this launch's first block: one block of work
+        // that would otherwise hold the whole GPU for a launch of its own.
+        static_assert(CAB_GATE_LDS <= S::LDS, "the gate's scratch fits the item LDS");
+        cab_gate_body<8>(p.gate, lds);
+        __syncthreads();  // the LDS is the item's next
+    }
     {
         typename S::vec ks[S::NE], vs[S::NE];
         attn_fetch<D, OCA>(p, wi, head, ks, vs);

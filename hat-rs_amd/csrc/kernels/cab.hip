@@ -171,19 +171,22 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
 // result does not depend on timing.
 #define CG_WAVES 16
 
-extern "C" __global__ __launch_bounds__(CG_WAVES * 64) void hat_cab_gate(CabGateArgs p)
+// The gate computation for a block of WAVES waves; lds: CAB_GATE_LDS floats.
+#define CAB_GATE_LDS (CAB_NSUM * CAB_CS + 9 * CAB_CC + CAB_C + 64 + CAB_C)
+template <int WAVES>
+__device__ __forceinline__ void cab_gate_body(const CabGateArgs& p, float* lds)
 {
     constexpr int NV = CAB_NSUM * CAB_CS;  // 40 sums per tile
-    __shared__ float s_sum[NV];
-    __shared__ float s_S[9 * CAB_CC];
-    __shared__ float s_mean[CAB_C];
-    __shared__ float s_z[64];
-    __shared__ float s_gate[CAB_C];
+    float* s_sum = lds;
+    float* s_S = s_sum + NV;
+    float* s_mean = s_S + 9 * CAB_CC;
+    float* s_z = s_mean + CAB_C;
+    float* s_gate = s_z + 64;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
 
     // Tile sums: partial is value-major, so a wave reads 64 tiles per load.
-    for (int v = wave; v < NV; v += CG_WAVES) {
+    for (int v = wave; v < NV; v += WAVES) {
         const float* src = p.partial + (size_t)v * p.tiles;
         float acc = 0.0f;
 #pragma unroll 8
@@ -207,8 +210,7 @@ extern "C" __global__ __launch_bounds__(CG_WAVES * 64) void hat_cab_gate(CabGate
     }
     __syncthreads();
     const float inv = 1.0f / ((float)H * (float)W);
-    if (tid < CAB_C) {
-        const int c = tid;
+    for (int c = tid; c < CAB_C; c += WAVES * 64) {
         float acc = 0.0f;
 #pragma unroll
         for (int ci = 0; ci < CAB_CC; ++ci)
@@ -217,15 +219,14 @@ extern "C" __global__ __launch_bounds__(CG_WAVES * 64) void hat_cab_gate(CabGate
         s_mean[c] = p.b2[c] + acc * inv;
     }
     __syncthreads();
-    for (int j = wave; j < p.sq; j += CG_WAVES) {
+    for (int j = wave; j < p.sq; j += WAVES) {
         float acc = 0.0f;
         for (int c = lane; c < CAB_C; c += 64) acc += s_mean[c] * p.wa[j * CAB_C + c];
         acc = wave_sum(acc) + p.ba[j];
         if (lane == 0) s_z[j] = acc < 0.0f ? 0.0f : acc;
     }
     __syncthreads();
-    if (tid < CAB_C) {
-        const int c = tid;
+    for (int c = tid; c < CAB_C; c += WAVES * 64) {
         float acc = p.bb[c];
         for (int j = 0; j < p.sq; ++j) acc += s_z[j] * p.wb[c * p.sq + j];
         const float g = 1.0f / (1.0f + __expf(-acc));
@@ -234,11 +235,17 @@ extern "C" __global__ __launch_bounds__(CG_WAVES * 64) void hat_cab_gate(CabGate
         p.bias2[c] = p.bproj[c] + (p.cscale * g) * p.b2[c];
     }
     __syncthreads();
-    for (int i = tid; i < CAB_C * CAB_K2; i += CG_WAVES * 64) {
+    for (int i = tid; i < CAB_C * CAB_K2; i += WAVES * 64) {
         const int c = i / CAB_K2, k = i - c * CAB_K2;
         const int tap = k / CAB_CC, ci = k - tap * CAB_CC;
         float v = 0.0f;
         if (tap < 9) v = (p.cscale * s_gate[c]) * p.w2[(c * CAB_CC + ci) * 9 + tap];
         p.w2g[i] = v;
     }
+}
+
+extern "C" __global__ __launch_bounds__(CG_WAVES * 64) void hat_cab_gate(CabGateArgs p)
+{
+    __shared__ float lds[CAB_GATE_LDS];
+    cab_gate_body<CG_WAVES>(p, lds);
 }

@@ -1,11 +1,11 @@
 // The single gfx950 code object of the library: every kernel the runtime
 // launches, built with
 //   hipcc --offload-arch=gfx950 --offload-device-only --no-gpu-bundle-output
+#include "cab.hip"
 #include "attn.hip"
 #include "conv.hip"
 #include "gemm.hip"
 #include "mlp.hip"
 #include "habtail.hip"
-#include "cab.hip"
 #include "convw.hip"
 #include "misc.hip"
