@@ -335,9 +335,30 @@ void run_hab_tail(hipStream_t s, const DevLinear& proj, const DevLinear& fc1, co
 
 // The channel-attention gate from the CAB conv's per-tile column sums:
 // reduce in fixed row blocks, then squeeze-excite.
+// With `defer` (C <= 192, sq <= 64), nothing is launched: *defer gets the
+// arguments for the attention launch's first block, which adds the nblk
+// partial rows itself.
 void run_se(hipStream_t s, const float* partial, int nblk, int C, float* red, float count,
-            const float* w1, const float* b1, const float* w2, const float* b2, int sq, float* gate)
+            const float* w1, const float* b1, const float* w2, const float* b2, int sq, float* gate,
+            SeArgs* defer = nullptr)
 {
+    if (defer && C <= 192 && sq >= 1 && sq <= 64) {
+        SeArgs se{};
+        se.partial = partial;
+        se.nblk = nblk;
+        se.co_stride = C;
+        se.count = count;
+        se.w1 = w1;
+        se.b1 = b1;
+        se.w2 = w2;
+        se.b2 = b2;
+        se.gate = gate;
+        se.C = C;
+        se.sq = sq;
+        *defer = se;
+        return;
+    }
+    if (defer) defer->gate = nullptr;  // not deferred: launched here
     const int rows_per = 32;
     const int nred = (nblk + rows_per - 1) / rows_per;
     ReduceArgs r{partial, red, nblk, C, C, rows_per};
@@ -491,8 +512,10 @@ void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride,
 }
 
 void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, const Plan& pl,
-              int heads, int D, bool oca, int shift, const CabGateArgs* gate = nullptr)
+              int heads, int D, bool oca, int shift, const CabGateArgs* gate = nullptr,
+              const SeArgs* se = nullptr)
 {
+    if (se && (oca || attn_persistent(D, oca))) throw Error("attention: the SE gate rides on SW launches only");
     if (gate && (oca || attn_persistent(D, oca))) throw Error("attention: the CAB gate rides on SW launches only");
     if (pl.win != 16 || pl.owin != 24)
         throw Error("attention: the gfx950 kernels are built for window 16 / overlap window 24");
@@ -519,6 +542,10 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
     if (gate) {
         p.with_gate = 1;
         p.gate = *gate;
+    }
+    if (se && se->gate) {
+        p.with_se = 1;
+        p.se = *se;
     }
     if (attn_persistent(D, oca)) {
         static const int cus = std::max(1, Runtime::get().cu_count());
@@ -775,9 +802,10 @@ void GpuBackend::conv(const DevConv& C, const float* in, int cin_stride, int H, 
              crop_w, wt_.img_range, wt_.mean);
 }
 
-void GpuBackend::attention(const std::string& table, bool oca, int shift, const CabGateArgs* gate)
+void GpuBackend::attention(const std::string& table, bool oca, int shift, const CabGateArgs* gate,
+                           const SeArgs* se)
 {
-    run_attn(stream_, qkv_, raw_.at(table), ao_, plan_, wt_.heads, wt_.head_dim, oca, shift, gate);
+    run_attn(stream_, qkv_, raw_.at(table), ao_, plan_, wt_.heads, wt_.head_dim, oca, shift, gate, se);
 }
 
 // HAB.forward (hat_arch.py:266-309; cpu.rs:1090-1166):
@@ -808,15 +836,17 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
     conv(conv_.at(p + ".conv_block.cab.0"), xn_, C, H, W, t1_, t1_stride_, CEPI_STORE, 1);
     conv(conv_.at(p + ".conv_block.cab.2"), t1_, t1_stride_, H, W, t2_, C, CEPI_COLSUM, 0, nullptr,
          partial_);
+    // The gate: computed by the attention launch's first block where it fits.
+    SeArgs se{};
     run_se(stream_, partial_, nblk_conv2_, C, red_, (float)T,
            raw_.at(p + ".conv_block.cab.3.attention.1.weight"),
            raw_.at(p + ".conv_block.cab.3.attention.1.bias"),
            raw_.at(p + ".conv_block.cab.3.attention.3.weight"),
-           raw_.at(p + ".conv_block.cab.3.attention.3.bias"), wt_.squeezed, gate_);
+           raw_.at(p + ".conv_block.cab.3.attention.3.bias"), wt_.squeezed, gate_, &se);
     // Window attention, the roll and the partition folded into its addressing;
     // proj's epilogue adds the shortcut and the gated conv branch, then norm2.
     gemm(lin_.at(p + ".attn.qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
-    attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0);
+    attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, nullptr, &se);
     gemm(lin_.at(p + ".attn.proj"), ao_, C, T, x_out, C, EPI_HAB_LN, x_in, t2_, gate_, xn_,
          p + ".norm2");
     mlp(p + ".mlp", x_out, EPI_RESID_LN, next_norm);

@@ -107,7 +107,8 @@ private:
     void conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
               int co_stride, int epi, int act, const float* res = nullptr, float* partial = nullptr,
               int crop_h = 0, int crop_w = 0);
-    void attention(const std::string& table, bool oca, int shift, const hatk::CabGateArgs* gate = nullptr);
+    void attention(const std::string& table, bool oca, int shift, const hatk::CabGateArgs* gate = nullptr,
+                   const hatk::SeArgs* se = nullptr);
     void mlp(const std::string& prefix, float* x, int epi, const std::string& norm);
     void hab(int stage, int block, float* x_in, float* x_out, const std::string& next_norm);
     void ocab(int stage, float* x);

@@ -122,6 +122,19 @@ struct ConvArgs {
     float eps;
 };
 
+// Squeeze-excite gate: gate[c] = sigmoid(b2 + W2 relu(b1 + W1 mean)).
+struct SeArgs {
+    const float* partial; // [nblk][co_stride]
+    int nblk, co_stride;
+    float count;          // pixel count (mean = sum / count)
+    const float* w1;      // [sq][C]
+    const float* b1;      // [sq]
+    const float* w2;      // [C][sq]
+    const float* b2;      // [C]
+    float* gate;          // [C]
+    int C, sq;
+};
+
 // Fused window attention: one block per (window, head) (grid nw x heads), or,
 // for OCA with head_dim 24, persistent blocks walking the (window, head) items
 // head-major (grid: at most one block per CU, gridDim.y = 1).
@@ -140,6 +153,9 @@ struct AttnArgs {
     // gate (hat_cab_gate's work), which the HAB tail after this launch needs
     int with_gate;
     CabGateArgs gate;
+    // with_se: the same for the unfolded CAB's squeeze-excite gate (C = 180)
+    int with_se;
+    SeArgs se;
 };
 
 // Fused MLP (C = 144, hidden 288; C = 180, hidden 360):
@@ -221,19 +237,6 @@ struct ReduceArgs {
     const float* in;
     float* out;
     int nrows, C, stride, rows_per;
-};
-
-// Squeeze-excite gate: gate[c] = sigmoid(b2 + W2 relu(b1 + W1 mean)).
-struct SeArgs {
-    const float* partial; // [nblk][co_stride]
-    int nblk, co_stride;
-    float count;          // pixel count (mean = sum / count)
-    const float* w1;      // [sq][C]
-    const float* b1;      // [sq]
-    const float* w2;      // [C][sq]
-    const float* b2;      // [C]
-    float* gate;          // [C]
-    int C, sq;
 };
 
 }  // namespace hatk

@@ -346,6 +346,11 @@ __device__ __forceinline__ void attn_item_kernel(const AttnArgs& p, float* lds)
         cab_gate_body<8>(p.gate, lds);
         __syncthreads();  // the LDS is the item's next
     }
+    if (!OCA && p.with_se && wi == 0 && head == 0) {  // block-uniform; the unfolded CAB's gate
+        static_assert(SE_GATE_LDS <= S::LDS, "the gate's scratch fits the item LDS");
+        se_gate_body<8>(p.se, lds);
+        __syncthreads();
+    }
     {
         typename S::vec ks[S::NE], vs[S::NE];
         attn_fetch<D, OCA>(p, wi, head, ks, vs);

@@ -244,6 +244,53 @@ __device__ __forceinline__ void cab_gate_body(const CabGateArgs& p, float* lds)
     }
 }
 
+// The unfolded CAB's gate (the C = 180 family; hat_arch.py:40-55, cpu.rs:
+// 940-955) for a block of WAVES waves, straight from the conv2 partial column
+// sums: wave w adds rows w, w + WAVES, ... (its lanes over the columns), the
+// waves' sums are added in wave order through LDS, then mean, squeeze + ReLU,
+// excite + sigmoid. lds: SE_GATE_LDS floats.
+#define SE_GATE_LDS (8 * 192 + 192 + 64)
+template <int WAVES>
+__device__ __forceinline__ void se_gate_body(const SeArgs& p, float* lds)
+{
+    static_assert(WAVES <= 8, "the LDS holds eight waves' sums");
+    float* s_part = lds;              // [WAVES][192]
+    float* s_mean = s_part + 8 * 192;  // [192]
+    float* s_sq = s_mean + 192;        // [64]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    for (int c0 = 0; c0 < p.C; c0 += 64) {
+        const int c = c0 + lane;
+        float a0 = 0.0f, a1 = 0.0f;
+        if (c < p.C) {
+            int b = wave;
+            for (; b + WAVES < p.nblk; b += 2 * WAVES) {
+                a0 += p.partial[(size_t)b * p.co_stride + c];
+                a1 += p.partial[(size_t)(b + WAVES) * p.co_stride + c];
+            }
+            if (b < p.nblk) a0 += p.partial[(size_t)b * p.co_stride + c];
+            s_part[wave * 192 + c] = a0 + a1;
+        }
+    }
+    __syncthreads();
+    for (int c = tid; c < p.C; c += WAVES * 64) {
+        float acc = 0.0f;
+        for (int w = 0; w < WAVES; ++w) acc += s_part[w * 192 + c];
+        s_mean[c] = acc / p.count;
+    }
+    __syncthreads();
+    for (int j = tid; j < p.sq; j += WAVES * 64) {
+        float acc = p.b1[j];
+        for (int c = 0; c < p.C; ++c) acc += s_mean[c] * p.w1[(size_t)j * p.C + c];
+        s_sq[j] = acc < 0.0f ? 0.0f : acc;
+    }
+    __syncthreads();
+    for (int c = tid; c < p.C; c += WAVES * 64) {
+        float acc = p.b2[c];
+        for (int j = 0; j < p.sq; ++j) acc += s_sq[j] * p.w2[(size_t)c * p.sq + j];
+        p.gate[c] = 1.0f / (1.0f + __expf(-acc));
+    }
+}
+
 extern "C" __global__ __launch_bounds__(CG_WAVES * 64) void hat_cab_gate(CabGateArgs p)
 {
     __shared__ float lds[CAB_GATE_LDS];
