@@ -23,6 +23,11 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c)
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// A compile-time int carried by a value, for generic lambdas: decltype(x)::value.
+template <int V> struct CInt {
+    static constexpr int value = V;
+};
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // GELU(v) = v Phi(v) = max(v, 0) - |v|/2 erfc(a), a = |v|/sqrt2, with erfc(a) =

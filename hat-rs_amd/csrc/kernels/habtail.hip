@@ -46,7 +46,12 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
     constexpr int PER = (F4 + MLP_THREADS - 1) / MLP_THREADS;
     static_assert(PF4 <= F4 && CF4 <= F4 && PF4 % 64 == 0 && CF4 % 64 == 0 && F4 % 64 == 0, "chunk sizes");
     static_assert(CAB_K2 == 56 && CAB_C == C, "the conv2 chunk holds 56 K");
-    __shared__ __attribute__((aligned(16))) float Wb[2 * BUF];
+    // The two chunk buffers are separate objects, and every access below names
+    // one of them at compile time (the chunk parity is static): the compiler
+    // then knows that reading one buffer does not depend on the DMA still
+    // filling the other, and does not wait for that DMA before the read.
+    __shared__ __attribute__((aligned(16))) float Wb0[BUF];
+    __shared__ __attribute__((aligned(16))) float Wb1[BUF];
     // b1 [288], b2, next-norm w, b [144 each], bias2, norm2 w, b [144 each]
     __shared__ __attribute__((aligned(16))) float Cs[NH + 6 * C];
     float* const b1s = Cs;
@@ -91,27 +96,11 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             goff[i] = r * p.ldw2 + c4 * 4;
         }
     }
-    // The projection chunks' offsets (chunk cj adds 48 cj) and the conv2
-    // chunk's (-1: a zero slot), per LDS slot of this thread.
-    constexpr int PPER = (PF4 + MLP_THREADS - 1) / MLP_THREADS, CPER = (CF4 + MLP_THREADS - 1) / MLP_THREADS;
-    unsigned poff[PPER];
-    int coff[CAB ? CPER : 1];
-#pragma unroll
-    for (int i = 0; i < PPER; ++i) {
-        const int idx = tid + i * MLP_THREADS;
-        const int r = idx / RP, c4 = (idx - r * RP) ^ mlp_swz<RP>(r);
-        poff[i] = r * C + c4 * 4;
-    }
-#pragma unroll
-    for (int i = 0; i < (CAB ? CPER : 0); ++i) {
-        const int idx = tid + i * MLP_THREADS;
-        const int r = idx / RC, c4 = (idx - r * RC) ^ mlp_swz<RC>(r);
-        coff[i] = c4 < CAB_K2 / 4 ? r * CAB_K2 + c4 * 4 : -1;
-    }
-    // Chunk cj of a tile into LDS buffer buf (cj < 3: projection k 48cj ..;
-    // cj = 3 with the CAB: gated conv2; else hidden chunk cj - HT_NPC).
-    auto fetch = [&](int cj, int buf) {
-        float* B = Wb + buf * BUF;
+    // Chunk cj of a tile into LDS buffer bufc (a CInt: 0 or 1) (cj < 3:
+    // projection k 48cj ..; cj = 3 with the CAB: gated conv2; else hidden
+    // chunk cj - HT_NPC).
+    auto fetch = [&](int cj, auto bufc) {
+        float* B = decltype(bufc)::value ? Wb1 : Wb0;
         const int nf4 = cj < 3 ? PF4 : (CAB && cj == 3 ? CF4 : F4);
         const int h0 = (cj - HT_NPC) * MLP_HC;
         const float* w1c = p.w1 + (size_t)(h0 > 0 ? h0 : 0) * p.ldw1;
@@ -122,11 +111,18 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             if (base >= nf4) break;
             const int idx = base + lane;
             const float* src;
+            // the projection's and the conv2 chunk's offsets are computed here,
+            // a few VALU ops per slot, from an index the compiler cannot see
+            // through: otherwise it hoists every (chunk, slot) address out of
+            // the tile loop, 64 bits each, and spills them
+            int id = idx;
+            asm volatile("" : "+v"(id));
             if (cj < 3) {
-                src = p.wp + cj * 48 + poff[i < PPER ? i : 0];
+                const int r = id / RP, c4 = (id - r * RP) ^ mlp_swz<RP>(r);
+                src = p.wp + cj * 48 + r * C + c4 * 4;
             } else if (CAB && cj == 3) {
-                const int o = coff[i < CPER && CAB ? i : 0];
-                src = o >= 0 ? p.w2g + o : hat_mlp_zero4;
+                const int r = id / RC, c4 = (id - r * RC) ^ mlp_swz<RC>(r);
+                src = c4 < CAB_K2 / 4 ? p.w2g + r * CAB_K2 + c4 * 4 : hat_mlp_zero4;  // k 56..63: zero
             } else {
                 src = (base < W1F4 ? w1c : w2c) + goff[i];
             }
@@ -161,14 +157,15 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
     // Swizzled operand columns (rows nt*16 + lr: (row >> 2) & 3 == (lr >> 2) & 3,
     // row & 15 == lr).
     const int sg = lg ^ mlp_swz<R1>(lr), sg2 = lg ^ mlp_swz<R2>(lr), sgp = lg ^ mlp_swz<RP>(lr);
-    fetch(0, 0);
+    fetch(0, CInt<0>{});
     load_rows(xa, p.a, tile);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    // gc: the block's chunk count so far; chunk gc sits in buffer gc & 1
-    int gc = 0;
-    for (; tile < ntiles; tile += gridDim.x, gc += HT_NCT) {
+    // One tile whose chunk 0 sits in buffer P; chunk cj then in buffer
+    // (P + cj) & 1, and the next tile's chunk 0 in (P + HT_NCT) & 1.
+    auto tile_body = [&](auto parity) {
+        constexpr int P = decltype(parity)::value;
         const bool last_tile = tile + (int)gridDim.x >= ntiles;
         const int mbase = tile * MLP_ROWS + wave * 16;
         // The residual rows and (CAB) the t1 neighbourhood, loaded while
@@ -182,18 +179,21 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             const int m = mbase + lr;
             const bool alive = m < M;
             const int y = m / p.W, x = m - y * p.W;
+            // branch-free: every lane loads (pixel 0 when the tap is outside the
+            // image) and selects zero, so no wait is needed for a lane's
+            // destination registers between two paths
             auto pair = [&](int tap, int ci) -> float2 {
                 const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
-                float2 v = make_float2(0.f, 0.f);
-                if (alive && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W)
-                    v = *(const float2*)(p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci);
-                return v;
+                const bool ok = alive && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W;
+                const float2 v = *(const float2*)(p.t1 + (ok ? ((size_t)yy * p.W + xx) * CAB_CS + ci : 0));
+                return ok ? v : make_float2(0.f, 0.f);
             };
 #pragma unroll
             for (int kc2 = 0; kc2 < CAB_K2 / 16; ++kc2) {
                 const int k0 = kc2 * 16 + lg * 4, ta = k0 / CAB_CC, ca = k0 - ta * CAB_CC;
                 const float2 lo = pair(ta, ca);
-                const float2 hi = ca + 2 < CAB_CC ? pair(ta, ca + 2) : pair(ta + 1, 0);
+                const bool same = ca + 2 < CAB_CC;
+                const float2 hi = pair(same ? ta : ta + 1, same ? ca + 2 : 0);
                 xg[kc2] = (f32x4){lo.x, lo.y, hi.x, hi.y};
             }
             xh = pair(lg < 3 ? 8 : 9, 2 * lg);
@@ -205,8 +205,10 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
         for (int nt = 0; nt < NT; ++nt) acc[nt] = *(const f32x4*)(bias2s + nt * 16 + lg * 4);
 #pragma unroll
         for (int cj = 0; cj < HT_NPC; ++cj) {
-            const float* B = Wb + ((gc + cj) & 1) * BUF;
-            fetch(cj + 1, (gc + cj + 1) & 1);  // the next chunk is always of this tile
+            const float* B = ((P + cj) & 1) ? Wb1 : Wb0;
+            // the next chunk is always of this tile
+            if ((P + cj) & 1) fetch(cj + 1, CInt<0>{});
+            else fetch(cj + 1, CInt<1>{});
             if (cj == 1) load_tail_inputs();
             if (cj < 3) {
 #pragma unroll
@@ -281,12 +283,14 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
         f32x4 acc2[1][NT];
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc2[0][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-        for (int c = 0; c < NCH; ++c) {
+        // hidden chunk c (cj = HT_NPC + c) from buffer bufc, fetching the next
+        // chunk (or the next tile's chunk 0) into the other one
+        auto mlp_chunk = [&](int c, auto bufc) {
+            constexpr int Q = decltype(bufc)::value;
+            const float* B = Q ? Wb1 : Wb0;
             const int cj = HT_NPC + c;
-            const float* B = Wb + ((gc + cj) & 1) * BUF;
             const bool more = c + 1 < NCH || !last_tile;  // block-uniform
-            if (more) fetch(c + 1 < NCH ? cj + 1 : 0, (gc + cj + 1) & 1);
+            if (more) fetch(c + 1 < NCH ? cj + 1 : 0, CInt<Q ^ 1>{});
             f32x4 h[MLP_HC / 16];
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = *(const f32x4*)(b1s + c * MLP_HC + nt * 16 + lg * 4);
@@ -315,10 +319,32 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
                 }
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
+        };
+        static_assert(NCH % 2 == 0, "hidden chunks go in pairs, one per buffer");
+        constexpr int Q0 = (P + HT_NPC) & 1;
+#pragma unroll 1
+        for (int c = 0; c < NCH; c += 2) {
+            mlp_chunk(c, CInt<Q0>{});
+            mlp_chunk(c + 1, CInt<Q0 ^ 1>{});
         }
         // the residual x' straight from xr (one row tile: pres[0][nt] = xr[nt])
         gemm_epilogue<1, NT, EPI>(g, kc_out, acc2, mbase, 0, lr, lg, nullptr,
                                            (const f32x4(*)[NT])xr);
+    };
+
+    // With an even chunk count per tile every tile starts in buffer 0; with
+    // an odd one the tiles alternate, and go in pairs.
+    if constexpr (HT_NCT % 2 == 0) {
+        for (; tile < ntiles; tile += gridDim.x) tile_body(CInt<0>{});
+    } else {
+        for (;;) {
+            tile_body(CInt<0>{});
+            tile += gridDim.x;
+            if (tile >= ntiles) break;
+            tile_body(CInt<1>{});
+            tile += gridDim.x;
+            if (tile >= ntiles) break;
+        }
     }
 }
 
