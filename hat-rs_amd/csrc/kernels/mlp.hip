@@ -62,7 +62,12 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     static_assert(NCH % 2 == 0, "chunk parity must repeat across tiles");
     static_assert(KP % 16 == 0 && NO % 16 == 0 && NH % MLP_HC == 0, "tile multiples");
     static_assert(W1F4 % 64 == 0 && F4 % 64 == 0, "a wave's load lies in one slice");
-    __shared__ __attribute__((aligned(16))) float Wb[2 * BUF];
+    // The two chunk buffers are separate objects and every access names one at
+    // compile time (chunk c uses buffer c & 1): the compiler then knows that a
+    // read of one does not depend on the DMA filling the other, and does not
+    // wait for it.
+    __shared__ __attribute__((aligned(16))) float Wb0[BUF];
+    __shared__ __attribute__((aligned(16))) float Wb1[BUF];
     // The per-column constants, read in every chunk and every epilogue, from
     // LDS rather than through the cache hierarchy: b1, then b2, nw, nb.
     __shared__ __attribute__((aligned(16))) float Cs[NH + 3 * NO];
@@ -102,16 +107,20 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     // Chunk c's slices into LDS buffer buf. The LDS side of each load is the
     // wave's 64 consecutive slots; the writes land asynchronously, so a
     // vmcnt(0) wait precedes the barrier that publishes them.
-    auto fetch = [&](int c, int buf) {
+    auto fetch = [&](int c, auto bufc) {
         const int h0 = c * MLP_HC;
         const float* w1c = p.w1 + (size_t)h0 * p.ldw1;  // uniform chunk bases
         const float* w2c = p.w2 + h0;
-        float* B = Wb + buf * BUF;
+        float* B = decltype(bufc)::value ? Wb1 : Wb0;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int base = i * MLP_THREADS + wave * 64;  // wave-uniform
             if (base >= F4) break;
-            const int idx = base + lane;
+            int idx = base + lane;
+            // (with padding) an index the compiler cannot see through, so the
+            // per-slot addresses are recomputed here instead of hoisted out of
+            // the loops and kept, 64 bits each
+            if constexpr (PAD) asm volatile("" : "+v"(idx));
             const float* src;
             if constexpr (!PAD) {
                 src = (base < W1F4 ? w1c : w2c) + goff[i];
@@ -172,7 +181,7 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     // and n2*16 + lr give (row >> 2) & 3 == (lr >> 2) & 3 and row & 15 == lr.
     static_assert(R2 % 16 != 0, "the fc2 slice's swizzle is the 2-bit one");
     const int sg = lg ^ mlp_swz<R1>(lr), sg2 = lg ^ mlp_swz<R2>(lr);
-    fetch(0, 0);
+    fetch(0, CInt<0>{});
     load_a(tile);
     __builtin_amdgcn_s_waitcnt(0);  // the LDS writes of fetch have landed
     __syncthreads();
@@ -183,12 +192,12 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
         f32x4 rres[1][RN];
 #pragma unroll
         for (int j = 0; j < NO / 16; ++j) acc2[0][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-        for (int c = 0; c < NCH; ++c) {
-            const float* B = Wb + (c & 1) * BUF;
+        auto chunk = [&](int c, auto bufc) {
+            constexpr int Q = decltype(bufc)::value;  // c & 1
+            const float* B = Q ? Wb1 : Wb0;
             const bool more = c + 1 < NCH || !last_tile;  // block-uniform
             // the other buffer was last read in the previous chunk, before its barrier
-            if (more) fetch(c + 1 < NCH ? c + 1 : 0, (c + 1) & 1);
+            if (more) fetch(c + 1 < NCH ? c + 1 : 0, CInt<Q ^ 1>{});
             // The residual rows for the epilogue, one chunk ahead of it.
             if constexpr (PRE) {
                 if (c == NCH - 1) {
@@ -237,6 +246,11 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
                 }
             __builtin_amdgcn_s_waitcnt(0);  // the next chunk's LDS writes have landed
             __syncthreads();
+        };
+#pragma unroll 1
+        for (int c = 0; c < NCH; c += 2) {
+            chunk(c, CInt<0>{});
+            chunk(c + 1, CInt<1>{});
         }
         if constexpr (PRE)
             gemm_epilogue<1, NO / 16, EPI>(g, kc, acc2, tile * MLP_ROWS + wave * 16, 0, lr, lg, nullptr, rres);
