@@ -49,6 +49,21 @@ __device__ __forceinline__ float gelu(float v)
     return __builtin_fmaf(-av, (q * t) * e, fmaxf(v, 0.0f));
 }
 
+// 1 KB of zeros in global memory, never written (and not const, so the
+// compiler cannot fold loads from it). Loads that fall outside an operand -
+// rows past M, padding channels, taps outside the plane, padding slots of the
+// weight chunks - read here. The alternatives cost more: a branch around the
+// load makes the number of loads in flight path-dependent, so the compiler's
+// later waits drain every load; zeroing the value after the load makes it wait
+// for that load at once.
+__device__ __attribute__((aligned(16))) float hat_zero_row[256] = {};
+
+// A float4 from p, or zeros (from hat_zero_row) where ok is false.
+__device__ __forceinline__ f32x4 load_or_zero(const float* p, bool ok)
+{
+    return *(const f32x4*)(ok ? p : hat_zero_row);
+}
+
 __device__ __forceinline__ float wave_sum(float v)
 {
 #pragma unroll

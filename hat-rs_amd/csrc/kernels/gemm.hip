@@ -263,9 +263,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p)
             const int idx = tid + j * 256;
             const int r = idx >> 2, c4 = (idx & 3) * 4;
             const int m = m0 + r, k = k0 + c4;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m < M && k < K) v = *(const float4*)(p.a + (size_t)m * p.lda + k);
-            ra[j] = v;
+            const bool ok = m < M && k < K;
+            const f32x4 v = load_or_zero(p.a + (size_t)m * p.lda + k, ok);
+            ra[j] = make_float4(v.x, v.y, v.z, v.w);
         }
 #pragma unroll
         for (int j = 0; j < WV; ++j) {
@@ -408,6 +408,39 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 
     const int ntiles = (M + ROWS - 1) / ROWS;
     const long units = (long)ntiles * ((N + BN - 1) / BN);
+
+    // The A rows of unit u's row tile, clamped to row 0 past M.
+    auto rows_of = [&](long u, const float* (&ar)[MT], bool (&al)[MT]) {
+        const int tile = (int)(u % ntiles);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int m = tile * ROWS + wave * 16 * MT + mt * 16 + lr;
+            al[mt] = m < M;
+            ar[mt] = al[mt] ? p.a + (size_t)m * p.lda + lg * 4 : hat_zero_row;  // + kc*16 stays in it
+        }
+    };
+    // A operands in three register slots, streamed three chunks ahead of the
+    // MFMAs that use them (the chunk loop is rolled over groups of 3 so the
+    // slots are fixed registers). The stream runs across units: the last three
+    // chunks of a unit load the first three of the block's next unit (or
+    // reload its own after its last unit), so every step issues exactly one
+    // load per slot and the compiler's waits name the oldest one only.
+    f32x4 xa[3][MT];
+    // k beyond K (K = 180 in 192) reads as zero: past it lies the next row
+    const bool kin_last = (NCH - 1) * 16 + lg * 4 < p.K;
+    auto load_a = [&](int slot, int kc, const float* const (&ar)[MT]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const bool kin = KP == 144 || kc < NCH - 1 || kin_last;
+            xa[slot][mt] = load_or_zero(ar[mt] + kc * 16, kin);
+        }
+    };
+    const float* arow[MT];
+    bool alive[MT];
+    rows_of(blockIdx.x, arow, alive);
+#pragma unroll
+    for (int s = 0; s < 3; ++s) load_a(s, s, arow);
+
     int slice = -1;
     for (long u = blockIdx.x; u < units; u += gridDim.x) {
         const int us = (int)(u / ntiles), tile = (int)(u - (long)us * ntiles);
@@ -419,31 +452,9 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
         }
         const int n0 = slice * BN;
         const int mbase = tile * ROWS + wave * 16 * MT;
-        const float* arow[MT];
-        bool alive[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const int m = mbase + mt * 16 + lr;
-            alive[mt] = m < M;
-            arow[mt] = p.a + (size_t)(alive[mt] ? m : 0) * p.lda + lg * 4;
-        }
-        // A operands in three register slots, streamed three chunks ahead of
-        // the MFMAs that use them (the chunk loop is rolled over groups of 3 so
-        // the slots are fixed registers).
-        f32x4 xa[3][MT];
-        // k beyond K (K = 180 in 192) reads as zero: past it lies the next row
-        const bool kin_last = (NCH - 1) * 16 + lg * 4 < p.K;
-        auto load_a = [&](int slot, int kc) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-                if (alive[mt] && (KP == 144 || kc < NCH - 1 || kin_last))
-                    v = *(const f32x4*)(arow[mt] + kc * 16);
-                xa[slot][mt] = v;
-            }
-        };
-#pragma unroll
-        for (int s = 0; s < 3; ++s) load_a(s, s);
+        const float* arow_n[MT];
+        bool alive_n[MT];
+        rows_of(u + gridDim.x < units ? u + gridDim.x : u, arow_n, alive_n);
         // CAB: the 3x3 neighbourhood of t1 at each row's pixel, k = tap*6 + ci
         // (54 values, 2 zero): three 16-k chunks, lane group g holding k =
         // 16 kc2 + 4g .. +3 (two float2 of one or two taps), and an 8-k tail,
@@ -457,18 +468,18 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 const int m = mbase + mt * 16 + lr;
                 const int y = m / p.W, x = m - y * p.W;
                 // t1[neighbour at tap][ci, ci+1], zero outside the plane
+                // out-of-plane taps read zeros
                 auto pair = [&](int tap, int ci) -> float2 {
                     const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
-                    float2 v = make_float2(0.f, 0.f);
-                    if (alive[mt] && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W)
-                        v = *(const float2*)(p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci);
-                    return v;
+                    const bool ok = alive[mt] && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W;
+                    return *(const float2*)(ok ? p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci : hat_zero_row);
                 };
 #pragma unroll
                 for (int kc2 = 0; kc2 < K2F; ++kc2) {
                     const int k0 = kc2 * 16 + lg * 4, ta = k0 / CAB_CC, ca = k0 - ta * CAB_CC;  // ca: 0, 2 or 4
                     const float2 lo = pair(ta, ca);
-                    const float2 hi = ca + 2 < CAB_CC ? pair(ta, ca + 2) : pair(ta + 1, 0);
+                    const bool same = ca + 2 < CAB_CC;
+                    const float2 hi = pair(same ? ta : ta + 1, same ? ca + 2 : 0);
                     xg[mt][kc2] = (f32x4){lo.x, lo.y, hi.x, hi.y};
                 }
                 xh[mt] = pair(lg < 3 ? 8 : 9, 2 * lg);
@@ -485,9 +496,8 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     const int n = n0 + nt * 16 + lg * 4;
-                    f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-                    if (alive[mt] && n < N) v = *(const f32x4*)(p.res + (size_t)m * p.ldo + n);
-                    rres[mt][nt] = v;
+                    const bool ok = alive[mt] && n < N;
+                    rres[mt][nt] = load_or_zero(p.res + (size_t)m * p.ldo + n, ok);
                 }
             }
         }
@@ -500,7 +510,7 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
 #pragma unroll
             for (int i = 0; i < MT; ++i) acc[i][j] = b4;
         }
-#pragma unroll 1
+#pragma unroll
         for (int kg = 0; kg < NCH; kg += 3) {
 #pragma unroll
             for (int slot = 0; slot < 3; ++slot) {
@@ -508,7 +518,11 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                 f32x4 cur[MT];
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) cur[mt] = xa[slot][mt];
-                if (kc + 3 < NCH) load_a(slot, kc + 3);
+                if (kc + 3 < NCH) load_a(slot, kc + 3, arow);  // compile-time choice
+                else load_a(slot, kc + 3 - NCH, arow_n);
+                // the load stays here, three chunks ahead of its MFMAs (the
+                // scheduler would otherwise sink it next to them)
+                __builtin_amdgcn_sched_barrier(0);
                 const float* wrow = Wsm + lr * WS_KS + kc * 16 + lg * 4;
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
@@ -520,6 +534,12 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                             acc[mt][nt] = mfma16(wv[s], cur[mt][s], acc[mt][nt]);
                 }
             }
+        }
+        // the slots now hold the next unit's first chunks
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            arow[mt] = arow_n[mt];
+            alive[mt] = alive_n[mt];
         }
         if (CAB) {
 #pragma unroll

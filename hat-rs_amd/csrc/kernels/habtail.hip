@@ -122,7 +122,7 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
                 src = p.wp + cj * 48 + r * C + c4 * 4;
             } else if (CAB && cj == 3) {
                 const int r = id / RC, c4 = (id - r * RC) ^ mlp_swz<RC>(r);
-                src = c4 < CAB_K2 / 4 ? p.w2g + r * CAB_K2 + c4 * 4 : hat_mlp_zero4;  // k 56..63: zero
+                src = c4 < CAB_K2 / 4 ? p.w2g + r * CAB_K2 + c4 * 4 : hat_zero_row;  // k 56..63: zero
             } else {
                 src = (base < W1F4 ? w1c : w2c) + goff[i];
             }
@@ -136,12 +136,10 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
     f32x4 xa[NT], xr[NT];
     auto load_rows = [&](f32x4 (&dst)[NT], const float* src, int t) {
         const int m = t * MLP_ROWS + wave * 16 + lr;
-        const float* row = src + (size_t)(m < M ? m : 0) * C + lg * 4;
+        const float* row = m < M ? src + (size_t)m * C + lg * 4 : hat_zero_row;  // + kc*16 stays in it
 #pragma unroll
         for (int kc = 0; kc < NT; ++kc) {
-            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-            if (m < M) v = *(const f32x4*)(row + kc * 16);
-            dst[kc] = v;
+            dst[kc] = *(const f32x4*)(row + kc * 16);
         }
     };
 
@@ -179,14 +177,11 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             const int m = mbase + lr;
             const bool alive = m < M;
             const int y = m / p.W, x = m - y * p.W;
-            // branch-free: every lane loads (pixel 0 when the tap is outside the
-            // image) and selects zero, so no wait is needed for a lane's
-            // destination registers between two paths
+            // taps outside the plane read zeros
             auto pair = [&](int tap, int ci) -> float2 {
                 const int yy = y + tap / 3 - 1, xx = x + tap % 3 - 1;
                 const bool ok = alive && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W;
-                const float2 v = *(const float2*)(p.t1 + (ok ? ((size_t)yy * p.W + xx) * CAB_CS + ci : 0));
-                return ok ? v : make_float2(0.f, 0.f);
+                return *(const float2*)(ok ? p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci : hat_zero_row);
             };
 #pragma unroll
             for (int kc2 = 0; kc2 < CAB_K2 / 16; ++kc2) {

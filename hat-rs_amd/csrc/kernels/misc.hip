@@ -7,9 +7,12 @@ using namespace hatk;
 // cpu.rs:563-581): two-pass mean then biased variance, y = (x - mean) * rstd *
 // w + b; y may alias x. For C % 4 == 0, C <= 192 (the models' 144 and 180): a
 // row per 16 lanes, four rows per wave, each lane holding up to three float4 of
-// its row, the sums reduced within the 16 lanes; x and y move with
-// non-temporal loads and stores (a streaming pass: on MI355X this measured
-// 5.7 TB/s against 5.4 TB/s with ordinary ones). Otherwise one wave per row.
+// its row, the sums reduced within the 16 lanes. y goes out with non-temporal
+// stores (a streaming pass); x comes in with ordinary loads: in the forward it
+// was written by the kernel just before, and the part of it still held in
+// MI355X's 256 MB last-level cache (MALL) is read from there (measured in the
+// HAT-S 512 forward: 51 us against 56 us with non-temporal loads, which are
+// faster only on data that is cold). Otherwise one wave per row.
 extern "C" __global__ __launch_bounds__(256) void hat_layernorm(LnArgs p)
 {
     const int lane = threadIdx.x & 63;
@@ -25,7 +28,7 @@ extern "C" __global__ __launch_bounds__(256) void hat_layernorm(LnArgs p)
 #pragma unroll
         for (int t = 0; t < 3; ++t) {
             const int k = g + 16 * t;
-            v[t] = k < n4 ? __builtin_nontemporal_load(x + k) : (f32x4){0.f, 0.f, 0.f, 0.f};
+            v[t] = k < n4 ? x[k] : (f32x4){0.f, 0.f, 0.f, 0.f};
             s += (v[t].x + v[t].y) + (v[t].z + v[t].w);
         }
 #pragma unroll

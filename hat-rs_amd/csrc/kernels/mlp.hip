@@ -31,10 +31,8 @@
 #define MLP_HC 48  // hidden units per chunk
 #define MLP_THREADS (MLP_WAVES * 64)
 
-// A zero float4 in global memory: the source of the LDS slots that lie past the
-// real weights (the padded C = 180 shape), since a direct-to-LDS load always
-// writes its slot.
-__device__ __attribute__((aligned(16))) float hat_mlp_zero4[4] = {0.f, 0.f, 0.f, 0.f};
+// The LDS slots that lie past the real weights (the padded C = 180 shape) load
+// from hat_zero_row, since a direct-to-LDS load always writes its slot.
 
 // Swizzle of float4 column c4 in LDS row `row` of a slice whose rows are R
 // float4 long: rows r..r+15 read at one c4 land in 16 distinct groups of four
@@ -88,7 +86,7 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     // output column); the lane fetches the global float4 whose swizzled column
     // is the slot's. Without padding the global offsets (relative to the
     // chunk's bases) are kept in registers; with it they are recomputed and
-    // slots past the real weights read hat_mlp_zero4.
+    // slots past the real weights read hat_zero_row.
     unsigned goff[PAD ? 1 : PER];
     if constexpr (!PAD) {
 #pragma unroll
@@ -126,11 +124,11 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
                 src = (base < W1F4 ? w1c : w2c) + goff[i];
             } else if (base < W1F4) {
                 const int r = idx / R1, c4 = (idx - r * R1) ^ mlp_swz<R1>(r);
-                src = h0 + r < H ? p.w1 + (size_t)(h0 + r) * p.ldw1 + c4 * 4 : hat_mlp_zero4;
+                src = h0 + r < H ? p.w1 + (size_t)(h0 + r) * p.ldw1 + c4 * 4 : hat_zero_row;
             } else {
                 const int j = idx - W1F4;
                 const int r = j / R2, c4 = (j - r * R2) ^ mlp_swz<R2>(r);
-                src = r < N && h0 + c4 * 4 < H ? p.w2 + (size_t)r * p.ldw2 + h0 + c4 * 4 : hat_mlp_zero4;
+                src = r < N && h0 + c4 * 4 < H ? p.w2 + (size_t)r * p.ldw2 + h0 + c4 * 4 : hat_zero_row;
             }
             __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(B + base * 4),
                                              16, 0, 0);
@@ -144,13 +142,11 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
     f32x4 xa[KP / 16];
     auto load_a = [&](int t) {
         const int m = t * MLP_ROWS + wave * 16 + lr;
-        const float* arow = p.a + (size_t)(m < M ? m : 0) * K + lg * 4;
+        const float* arow = m < M ? p.a + (size_t)m * K + lg * 4 : hat_zero_row;  // + kc*16 stays in it
 #pragma unroll
         for (int kc = 0; kc < KP / 16; ++kc) {
-            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
             // k beyond K (180 in 192) reads as zero: past it lies the next row
-            if (m < M && (!PAD || kc * 16 + lg * 4 < K)) v = *(const f32x4*)(arow + kc * 16);
-            xa[kc] = v;
+            xa[kc] = load_or_zero(arow + kc * 16, !PAD || kc * 16 + lg * 4 < K);
         }
     };
 
@@ -202,12 +198,10 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             if constexpr (PRE) {
                 if (c == NCH - 1) {
                     const int m = tile * MLP_ROWS + wave * 16 + lr;
-                    const float* rrow = p.res + (size_t)(m < M ? m : 0) * N + lg * 4;
+                    const float* rrow = m < M ? p.res + (size_t)m * N + lg * 4 : hat_zero_row;
 #pragma unroll
                     for (int n2 = 0; n2 < RN; ++n2) {
-                        f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-                        if (m < M && n2 * 16 + lg * 4 < N) v = *(const f32x4*)(rrow + n2 * 16);
-                        rres[0][n2] = v;
+                        rres[0][n2] = load_or_zero(rrow + n2 * 16, n2 * 16 + lg * 4 < N);
                     }
                 }
             }
