@@ -157,8 +157,10 @@ __device__ __forceinline__ void attn_table(const AttnArgs& p, float* Tb, int hea
     }
 }
 
-// This lane's query of item (wi, head): its pixel and its half of q, scaled
-// by head_dim^-0.5 * log2(e).
+// This lane's query of item (wi, head): its pixel and its half of q, as
+// stored (the caller scales it by head_dim^-0.5 * log2(e) where it is used:
+// scaling here would make the persistent kernel wait for the loads, and with
+// them for the next item's K and V, before the current item's work).
 template <int D>
 __device__ __forceinline__ int attn_query(const AttnArgs& p, int wi, int head, float (&qv)[D / 2], bool oca)
 {
@@ -177,14 +179,14 @@ __device__ __forceinline__ int attn_query(const AttnArgs& p, int wi, int head, f
 #pragma unroll
         for (int s4 = 0; s4 < HALF; s4 += 4) {
             const float4 v = *(const float4*)(Qg + s4);
-            qv[s4] = v.x * p.qscale;
-            qv[s4 + 1] = v.y * p.qscale;
-            qv[s4 + 2] = v.z * p.qscale;
-            qv[s4 + 3] = v.w * p.qscale;
+            qv[s4] = v.x;
+            qv[s4 + 1] = v.y;
+            qv[s4 + 2] = v.z;
+            qv[s4 + 3] = v.w;
         }
     } else {
 #pragma unroll
-        for (int s = 0; s < HALF; ++s) qv[s] = Qg[s] * p.qscale;
+        for (int s = 0; s < HALF; ++s) qv[s] = Qg[s];
     }
     return qpix;
 }
@@ -366,6 +368,8 @@ __device__ __forceinline__ void attn_item_kernel(const AttnArgs& p, float* lds)
     attn_table<D, OCA>(p, Vt + 32 * S::RSV, head);
     float qv[D / 2];
     const int qpix = attn_query<D>(p, wi, head, qv, OCA);
+#pragma unroll
+    for (int s = 0; s < D / 2; ++s) qv[s] *= p.qscale;
     __syncthreads();
     if (!OCA && p.shift > 0 && (wi / p.nx == p.ny - 1 || wi % p.nx == p.nx - 1))
         attn_compute<D, OCA, true>(p, lds, wi, head, qv, qpix);
@@ -409,7 +413,7 @@ __device__ __forceinline__ void attn_persistent_kernel(const AttnArgs& p, float*
         }
         float qv[D / 2];
 #pragma unroll
-        for (int s = 0; s < D / 2; ++s) qv[s] = qn[s];
+        for (int s = 0; s < D / 2; ++s) qv[s] = qn[s] * p.qscale;
         const int qpix = qpix_n;
         __syncthreads();
         const int next = item + gridDim.x;

@@ -119,14 +119,23 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    const int nchunks = p.CIp / 16;
-    fetch(0);
-#pragma unroll 1
-    for (int cc = 0; cc < nchunks; ++cc) {
-        __syncthreads();  // every read of the previous chunk is done
-        stash();
-        __syncthreads();
-        if (cc + 1 < nchunks) fetch(cc + 1);
+    // The residual of the GEMM epilogues, loaded under the last chunk's MFMAs
+    // (loaded in the epilogue, each row's loads would wait in turn).
+    constexpr bool PRE = HEAD < 0 && (EPI == EPI_RESID || EPI == EPI_RESID_LN);
+    f32x4 rres[PRE ? MT : 1][NT];
+    auto load_res = [&]() {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const size_t m = (size_t)(ty0 + wave * MT + mt) * W + tx0 + lr;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int co = co0 + nt * 16 + lg * 4;
+                rres[mt][nt] = load_or_zero(p.res + m * p.co_stride + co, co < p.CO);
+            }
+        }
+    };
+
+    auto chunk_mfma = [&]() {
 #pragma unroll
         for (int tap = 0; tap < 9; ++tap) {
             const int dy = tap / 3, dx = tap - dy * 3;
@@ -141,6 +150,53 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
                 for (int s = 0; s < 4; ++s)
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16(wv[s], xv[mt][s], acc[mt][nt]);
+            }
+        }
+    };
+
+    const int nchunks = p.CIp / 16;
+    fetch(0);
+    if constexpr (PRE) {
+        // The last chunk is peeled: it loads the residual where the others
+        // load the next chunk (in the loop, the residual's registers would be
+        // held across it, beside the staging registers).
+#pragma unroll 1
+        for (int cc = 0; cc + 1 < nchunks; ++cc) {
+            __syncthreads();  // every read of the previous chunk is done
+            stash();
+            __syncthreads();
+            fetch(cc + 1);
+            chunk_mfma();
+        }
+        __syncthreads();
+        stash();
+        __syncthreads();
+        load_res();
+        chunk_mfma();
+    } else {
+        // (the MFMAs written out here rather than through chunk_mfma: through
+        // the lambda the compiler copies accumulators around in this loop)
+#pragma unroll 1
+        for (int cc = 0; cc < nchunks; ++cc) {
+            __syncthreads();  // every read of the previous chunk is done
+            stash();
+            __syncthreads();
+            if (cc + 1 < nchunks) fetch(cc + 1);
+#pragma unroll
+            for (int tap = 0; tap < 9; ++tap) {
+                const int dy = tap / 3, dx = tap - dy * 3;
+                f32x4 xv[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    xv[mt] = *(const f32x4*)(Ps + ((wave * MT + mt + dy) * CW_P + lr + dx) * 16 + lg * 4);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const f32x4 wv = *(const f32x4*)(Ws + (tap * BN + nt * 16 + lr) * 16 + lg * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16(wv[s], xv[mt][s], acc[mt][nt]);
+                }
             }
         }
     }
@@ -233,7 +289,8 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) a1[0][nt] = acc[mt][nt];
         const int y = ty0 + wave * MT + mt;
-        gemm_epilogue<1, NT, EPI>(g, kc, a1, y * W + tx0, co0, lr, lg, nullptr);
+        gemm_epilogue<1, NT, EPI>(g, kc, a1, y * W + tx0, co0, lr, lg, nullptr,
+                                  PRE ? (const f32x4(*)[NT]) & rres[PRE ? mt : 0] : nullptr);
     }
 }
 
