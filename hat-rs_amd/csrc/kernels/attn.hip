@@ -157,6 +157,38 @@ __device__ __forceinline__ void attn_table(const AttnArgs& p, float* Tb, int hea
     }
 }
 
+// attn_table in two steps, so that its loads can be in flight together with
+// the item's other loads: this thread's entries into registers, then into LDS.
+template <int D, bool OCA>
+struct AttnTableRegs {
+    static constexpr int N = (AttnShape<D, OCA>::TROWS + 511) / 512;
+    float v[N];
+};
+template <int D, bool OCA>
+__device__ __forceinline__ void attn_table_load(const AttnArgs& p, int head, AttnTableRegs<D, OCA>& t)
+{
+#pragma unroll
+    for (int j = 0; j < AttnTableRegs<D, OCA>::N; ++j) {
+        const int i = threadIdx.x + 512 * j;
+        int row = 960 - i;
+        if (OCA) {
+            row = i - 880;
+            if (row < 0) row += 1521;
+        }
+        const bool ok = i < AttnShape<D, OCA>::TROWS;
+        t.v[j] = p.table[(size_t)(ok ? row : 0) * p.heads + head];
+    }
+}
+template <int D, bool OCA>
+__device__ __forceinline__ void attn_table_store(float* Tb, const AttnTableRegs<D, OCA>& t)
+{
+#pragma unroll
+    for (int j = 0; j < AttnTableRegs<D, OCA>::N; ++j) {
+        const int i = threadIdx.x + 512 * j;
+        if (i < AttnShape<D, OCA>::TROWS) Tb[i] = t.v[j] * HAT_LOG2E;
+    }
+}
+
 // This lane's query of item (wi, head): its pixel and its half of q, as
 // stored (the caller scales it by head_dim^-0.5 * log2(e) where it is used:
 // scaling here would make the persistent kernel wait for the loads, and with
@@ -353,10 +385,18 @@ __device__ __forceinline__ void attn_item_kernel(const AttnArgs& p, float* lds)
         se_gate_body<8>(p.se, lds);
         __syncthreads();
     }
+    // Every load of the item (K, V, the bias table, q) is issued before any
+    // of them is waited for.
+    float qv[D / 2];
+    int qpix;
     {
         typename S::vec ks[S::NE], vs[S::NE];
         attn_fetch<D, OCA>(p, wi, head, ks, vs);
+        AttnTableRegs<D, OCA> tr;
+        attn_table_load<D, OCA>(p, head, tr);
+        qpix = attn_query<D>(p, wi, head, qv, OCA);
         attn_stash<D, OCA>(lds, Vt, ks, vs);
+        attn_table_store<D, OCA>(Vt + 32 * S::RSV, tr);
     }
     if (OCA) {
         // V^T rows past D: row D all ones (it sums the probabilities), the rest zero.
@@ -365,9 +405,6 @@ __device__ __forceinline__ void attn_item_kernel(const AttnArgs& p, float* lds)
             Vt[r * S::RSV + k] = r == D ? 1.0f : 0.0f;
         }
     }
-    attn_table<D, OCA>(p, Vt + 32 * S::RSV, head);
-    float qv[D / 2];
-    const int qpix = attn_query<D>(p, wi, head, qv, OCA);
 #pragma unroll
     for (int s = 0; s < D / 2; ++s) qv[s] *= p.qscale;
     __syncthreads();
