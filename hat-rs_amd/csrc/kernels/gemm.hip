@@ -578,6 +578,8 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
             // through the wave's LDS region and leave as 16 consecutive rows of
             // each head: 1536 contiguous bytes per head, every lane storing
             // 16 bytes of one run, instead of 16-byte pieces 96 bytes apart.
+            // The stores are non-temporal (measured faster, for this kernel
+            // and for the attention that reads q, k, v next).
             float* Q = Qs + wave * 16 * QS_S;
             const int mrows = M - mbase;  // rows of this wave that exist (may exceed 16)
 #pragma unroll
@@ -591,7 +593,7 @@ __device__ __forceinline__ void gemm_ws_body(const GemmArgs& p)
                     const f32x4 v = *(const f32x4*)(Q + r * QS_S + hh * 24 + d4 * 4);
                     if (r < mrows) {
                         const int head = 2 * ph + hh;
-                        *(f32x4*)(p.out + ((size_t)(slice * p.heads + head) * M + mbase + r) * 24 + d4 * 4) = v;
+                        __builtin_nontemporal_store(v, (f32x4*)(p.out + ((size_t)(slice * p.heads + head) * M + mbase + r) * 24 + d4 * 4));
                     }
                 }
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next phase's writes
