@@ -289,14 +289,19 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             f32x4 h[MLP_HC / 16];
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = *(const f32x4*)(b1s + c * MLP_HC + nt * 16 + lg * 4);
+            // fc1, per 16-k step: the three weight reads, then their 12 MFMAs
 #pragma unroll
-            for (int kc = 0; kc < NT; ++kc)
+            for (int kc = 0; kc < NT; ++kc) {
+                __builtin_amdgcn_sched_barrier(0);
+                f32x4 wv[MLP_HC / 16];
 #pragma unroll
-                for (int nt = 0; nt < MLP_HC / 16; ++nt) {
-                    const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * C + (kc * 4 + sg) * 4);
+                for (int nt = 0; nt < MLP_HC / 16; ++nt)
+                    wv[nt] = *(const f32x4*)(B + (nt * 16 + lr) * C + (kc * 4 + sg) * 4);
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) h[nt] = mfma16(wv[s], xa[kc][s], h[nt]);
-                }
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = mfma16(wv[nt][s], xa[kc][s], h[nt]);
+            }
             // the MLP input is dead after the last chunk's fc1: the next tile's
             // attention rows load under this chunk's fc2 and the epilogue
             if (c == NCH - 1 && !last_tile) load_rows(xa, p.a, tile + gridDim.x);
@@ -304,13 +309,22 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             for (int nt = 0; nt < MLP_HC / 16; ++nt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) h[nt][j] = gelu(h[nt][j]);
+            // fc2, per 16-unit step of the hidden chunk and three output
+            // column tiles: the three weight reads, then their 12 MFMAs (the
+            // reads in flight together, not one read's latency per four MFMAs)
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt)
 #pragma unroll
-                for (int n2 = 0; n2 < NT; ++n2) {
-                    const f32x4 wv = *(const f32x4*)(B + W1F4 * 4 + (n2 * 16 + lr) * MLP_HC + nt * 16 + sg2 * 4);
+                for (int g3 = 0; g3 < NT; g3 += 3) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    f32x4 wv[3];
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) acc2[0][n2] = mfma16(wv[s], h[nt][s], acc2[0][n2]);
+                    for (int j = 0; j < 3; ++j)
+                        wv[j] = *(const f32x4*)(B + W1F4 * 4 + ((g3 + j) * 16 + lr) * MLP_HC + nt * 16 + sg2 * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int j = 0; j < 3; ++j) acc2[0][g3 + j] = mfma16(wv[j][s], h[nt][s], acc2[0][g3 + j]);
                 }
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
