@@ -211,17 +211,21 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             f32x4 h[MLP_HC / 16];
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = *(const f32x4*)(Cs + c * MLP_HC + nt * 16 + lg * 4);
+            // per 16-k step: the three weight reads, then their 12 MFMAs
 #pragma unroll
-            for (int kc = 0; kc < KP / 16; ++kc)
+            for (int kc = 0; kc < KP / 16; ++kc) {
+                __builtin_amdgcn_sched_barrier(0);
+                // physical column: (kc*4 + lg) ^ swizzle, which for R1 % 16 != 0
+                // (a 2-bit swizzle) is kc*4 + (lg ^ swizzle)
+                const int pc = R1 % 16 == 0 ? ((kc * 4 + lg) ^ lr) : kc * 4 + sg;
+                f32x4 wv[MLP_HC / 16];
 #pragma unroll
-                for (int nt = 0; nt < MLP_HC / 16; ++nt) {
-                    // physical column: (kc*4 + lg) ^ swizzle, which for R1 % 16 != 0
-                    // (a 2-bit swizzle) is kc*4 + (lg ^ swizzle)
-                    const int pc = R1 % 16 == 0 ? ((kc * 4 + lg) ^ lr) : kc * 4 + sg;
-                    const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * KP + pc * 4);
+                for (int nt = 0; nt < MLP_HC / 16; ++nt) wv[nt] = *(const f32x4*)(B + (nt * 16 + lr) * KP + pc * 4);
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) h[nt] = mfma16(wv[s], xa[kc][s], h[nt]);
-                }
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int nt = 0; nt < MLP_HC / 16; ++nt) h[nt] = mfma16(wv[nt][s], xa[kc][s], h[nt]);
+            }
             // The inputs are dead after the last chunk's fc1: fetch the next
             // tile's rows now, under this chunk's fc2 and the epilogue.
             if (c == NCH - 1 && !last_tile) load_a(tile + gridDim.x);
@@ -229,14 +233,22 @@ __device__ __forceinline__ void mlp_body(const MlpArgs& p)
             for (int nt = 0; nt < MLP_HC / 16; ++nt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) h[nt][j] = gelu(h[nt][j]);
-            // fc2 partial sums: out[16 rows][NO] += h . w2[:, chunk]^T
+            // fc2 partial sums: out[16 rows][NO] += h . w2[:, chunk]^T, three
+            // output column tiles at a time: their reads, then 12 MFMAs
+            static_assert((NO / 16) % 3 == 0, "output column tiles go in threes");
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt)
 #pragma unroll
-                for (int n2 = 0; n2 < NO / 16; ++n2) {
-                    const f32x4 wv = *(const f32x4*)(B + W1F4 * 4 + (n2 * 16 + lr) * MLP_HC + nt * 16 + sg2 * 4);
+                for (int g3 = 0; g3 < NO / 16; g3 += 3) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    f32x4 wv[3];
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) acc2[0][n2] = mfma16(wv[s], h[nt][s], acc2[0][n2]);
+                    for (int j = 0; j < 3; ++j)
+                        wv[j] = *(const f32x4*)(B + W1F4 * 4 + ((g3 + j) * 16 + lr) * MLP_HC + nt * 16 + sg2 * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int j = 0; j < 3; ++j) acc2[0][g3 + j] = mfma16(wv[j][s], h[nt][s], acc2[0][g3 + j]);
                 }
             __builtin_amdgcn_s_waitcnt(0);  // the next chunk's LDS writes have landed
             __syncthreads();
