@@ -100,6 +100,17 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts
     for (int mt = 0; mt < MT; ++mt) {
         const int m = mbase + mt * 16 + lr;
         const bool mlive = m < M;
+        // Without a preloaded residual, the row's residual loads are all issued
+        // here, before any is used (one at a time, each would wait in turn).
+        constexpr bool RES = EPI == EPI_RESID || EPI == EPI_RESID_LN || EPI == EPI_HAB || EPI == EPI_HAB_LN;
+        f32x4 rl[RES ? NT : 1];
+        if (RES && !pres) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int n = n0 + nt * 16 + lg * 4;
+                rl[nt] = load_or_zero(p.res + (size_t)m * p.ldo + n, mlive && n < N);
+            }
+        }
         // Values (bias + residual combine) in place. N is a multiple of 4, so a
         // lane's four columns are all live or all padding: whole float4 accesses.
 #pragma unroll
@@ -120,12 +131,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts
                     for (int j = 0; j < 4; ++j) v[j] = gelu(v[j]);
                 }
                 if (EPI == EPI_RESID || EPI == EPI_RESID_LN || EPI == EPI_HAB || EPI == EPI_HAB_LN) {
-                    if (pres) {
-                        v = pres[mt][nt] + v;
-                    } else {
-                        const float4 r4 = *(const float4*)(p.res + (size_t)m * p.ldo + n);
-                        v = (f32x4){r4.x, r4.y, r4.z, r4.w} + v;
-                    }
+                    v = (pres ? pres[mt][nt] : rl[RES ? nt : 0]) + v;
                 }
                 if (EPI == EPI_HAB || EPI == EPI_HAB_LN) {
                     const float4 a4 = *(const float4*)(p.aux + (size_t)m * p.ldo + n);
