@@ -216,11 +216,17 @@ void run_cab(hipStream_t s, const DevCab& cb, const float* xn, int H, int W, con
 {
     if (H % 16 != 0 || W % 16 != 0 || H < 16 || W < 16) throw Error("CAB: plane must be 16-aligned");
     if (sq < 1 || sq > 64) throw Error("CAB: squeeze width must be 1..64");
-    const int tiles = (H / 16) * (W / 16);
     static const int cus = std::max(1, Runtime::get().cu_count());
     CabConvArgs a{xn, cb.w1, cb.b1, t1, partial, H, W};
-    // Two blocks per CU (73 KB of LDS each), persistent over the 16 x 16 tiles.
-    launch(s, "hat_cab_conv1", (unsigned)std::min(tiles, 2 * cus), 1, 1, 256, a);
+    // Persistent over the output tiles: 16 wide x 32 tall with one block of 8
+    // waves per CU (137 KB of LDS) when the height allows, else 16 x 16 with
+    // two blocks of 4 waves per CU (73 KB each).
+    const bool t32 = H % 32 == 0;
+    const int tiles = (H / (t32 ? 32 : 16)) * (W / 16);
+    if (t32)
+        launch(s, "hat_cab_conv1_t32", (unsigned)std::min(tiles, cus), 1, 1, 512, a);
+    else
+        launch(s, "hat_cab_conv1", (unsigned)std::min(tiles, 2 * cus), 1, 1, 256, a);
     CabGateArgs g{};
     g.partial = partial;
     g.t1 = t1;

@@ -20,23 +20,41 @@
 using namespace hatk;
 
 // ---------------------------------------------------------------------------
-// conv1 (144 -> 6, 3x3, zero padding) + GELU, one 16 x 16 output tile at a time.
+// conv1 (144 -> 6, 3x3, zero padding) + GELU, one 16-wide, TY-tall output tile
+// at a time.
 //
-// Per-tap products: for each pixel q of the tile's 18 x 18 halo, P[q][tap*6+co]
-// = sum_ci xn[q][ci] * w[co][ci][tap] is a 144-deep product with 54 (padded to
-// 64) outputs - one MFMA row tile of 16 halo pixels x 4 column tiles. The conv
-// output at p is then sum over the 9 taps of P[p + d(tap)][tap*6 + co], read
-// from LDS. The weights (64 x 144) stay in registers for the whole kernel, so a
-// block streams its tiles with no weight traffic; two blocks share a CU.
-#define CC1_HS 18                       // halo side
-#define CC1_HP (CC1_HS * CC1_HS)        // 324 halo pixels
-#define CC1_RT ((CC1_HP + 15) / 16)     // 21 row tiles of 16 pixels
-#define CC1_PS 56                       // LDS row stride of P (54 used)
+// Per-tap products: for each pixel q of the tile's 18 x (TY+2) halo,
+// P[q][tap*6+co] = sum_ci xn[q][ci] * w[co][ci][tap] is a 144-deep product with
+// 54 (padded to 64) outputs - one MFMA row tile of 16 halo pixels x 4 column
+// tiles. The conv output at p is then sum over the 9 taps of
+// P[p + d(tap)][tap*6 + co], read from LDS. The weights (64 x 144) stay in
+// registers for the whole kernel, so a block streams its tiles with no weight
+// traffic.
+//   TY = 16: 4 waves, two blocks per CU (73 KB of LDS each); the halo is 21 row
+//            tiles (one wave has six, the others five).
+//   TY = 32: 8 waves, one block per CU (137 KB); the halo is 39 row tiles (five
+//            per wave, one wave four) for twice the pixels: fewer halo pixels
+//            per output pixel and a better balance across the waves.
+#define CC1_HS 18   // halo width
+#define CC1_PS 56   // LDS row stride of P (54 used)
 
-extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p)
+template <int TY>
+struct Cc1Shape {
+    static constexpr int WAVES = TY == 32 ? 8 : 4;
+    static constexpr int THREADS = WAVES * 64;
+    static constexpr int HY = TY + 2;            // halo height
+    static constexpr int HP = CC1_HS * HY;       // halo pixels
+    static constexpr int RT = (HP + 15) / 16;    // row tiles of 16 pixels
+    static_assert(16 * TY == THREADS, "one output pixel per thread");
+};
+
+template <int TY>
+__device__ __forceinline__ void cab_conv1_body(const CabConvArgs& p)
 {
-    __shared__ float Ps[CC1_HP * CC1_PS];
-    __shared__ float red[4][CAB_NSUM * CAB_CC];
+    using S = Cc1Shape<TY>;
+    constexpr int WAVES = S::WAVES;
+    __shared__ float Ps[S::HP * CC1_PS];
+    __shared__ float red[WAVES][CAB_NSUM * CAB_CC];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -45,7 +63,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
     const int lg = lane >> 4;
     const int H = p.H, W = p.W;
     const int ntx = W / 16;
-    const int ntiles = ntx * (H / 16);
+    const int ntiles = ntx * (H / TY);
 
     f32x4 wreg[4][CAB_C / 16];
 #pragma unroll
@@ -57,19 +75,20 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
 #pragma unroll
     for (int co = 0; co < CAB_CC; ++co) bias[co] = p.bias[co];
 
-    // This wave's halo row tiles rt = wave, wave + 4, ... of the block's tiles
-    // are walked as one stream of 16-channel chunks (9 per row tile), the input
-    // rows held in nine register slots: chunk kc of the next row tile (of this
-    // tile, or the first of the block's next tile) is loaded as soon as chunk kc
-    // of this one has gone to its MFMAs, a whole row tile (144 MFMAs) ahead.
-    const int nrt = (CC1_RT - wave + 3) / 4;
+    // This wave's halo row tiles rt = wave, wave + WAVES, ... of the block's
+    // tiles are walked as one stream of 16-channel chunks (9 per row tile), the
+    // input rows held in nine register slots: chunk kc of the next row tile (of
+    // this tile, or the first of the block's next tile) is loaded as soon as
+    // chunk kc of this one has gone to its MFMAs, a whole row tile (144 MFMAs)
+    // ahead.
+    const int nrt = (S::RT - wave + WAVES - 1) / WAVES;
     auto src_of = [&](int tl, int i) -> const float* {  // lane's input row of row tile i of tile tl, or null
         if (tl >= ntiles) return nullptr;
         const int ty = tl / ntx, tx = tl - ty * ntx;
-        const int hi = (wave + 4 * i) * 16 + lr;
+        const int hi = (wave + WAVES * i) * 16 + lr;
         const int hy = hi / CC1_HS, hx = hi - hy * CC1_HS;
-        const int gy = ty * 16 - 1 + hy, gx = tx * 16 - 1 + hx;
-        const bool valid = hi < CC1_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
+        const int gy = ty * TY - 1 + hy, gx = tx * 16 - 1 + hx;
+        const bool valid = hi < S::HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
         return valid ? p.xn + (size_t)(gy * W + gx) * CAB_C + lg * 4 : nullptr;
     };
     f32x4 xa[CAB_C / 16];
@@ -86,7 +105,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
 
     for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int ty = tile / ntx, tx = tile - ty * ntx;
-        const int y0 = ty * 16, x0 = tx * 16;
+        const int y0 = ty * TY, x0 = tx * 16;
 #pragma unroll 1
         for (int i = 0; i < nrt; ++i) {
             const float* nxt = i + 1 < nrt ? src_of(tile, i + 1) : src_of(tile + gridDim.x, 0);
@@ -103,8 +122,8 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
                     for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16(wreg[nt][kc][s], a[s], acc[nt]);
             }
             // lane (lr, lg) holds P[hi][16nt + 4lg .. +3]; columns 56.. are not stored
-            const int hi = (wave + 4 * i) * 16 + lr;
-            if (hi < CC1_HP) {
+            const int hi = (wave + WAVES * i) * 16 + lr;
+            if (hi < S::HP) {
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt)
                     if (nt * 16 + lg * 4 < CC1_PS) *(f32x4*)(Ps + hi * CC1_PS + nt * 16 + lg * 4) = acc[nt];
@@ -138,7 +157,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
 
         // Per-tile sums: the tile, and its pixels on row 0, row H-1, col 0,
         // col W-1 - only tiles on the plane's border have any of the latter.
-        const bool border = y0 == 0 || y0 + 16 == H || x0 == 0 || x0 + 16 == W;  // tile-uniform
+        const bool border = y0 == 0 || y0 + TY == H || x0 == 0 || x0 + 16 == W;  // tile-uniform
         const bool line[CAB_NSUM] = {true, gy == 0, gy == H - 1, gx == 0, gx == W - 1};
 #pragma unroll
         for (int l = 0; l < CAB_NSUM; ++l) {
@@ -155,7 +174,8 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
             float s = 0.0f;
             if (co < CAB_CC && (l == 0 || border)) {
                 const int i = l * CAB_CC + co;
-                s = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) s += red[w][i];  // waves in order
             }
             p.partial[(size_t)tid * ntiles + tile] = s;  // value-major: [40][tiles]
         }
@@ -163,6 +183,15 @@ extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p
         // and red above precedes it.
         __syncthreads();
     }
+}
+
+extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p)
+{
+    cab_conv1_body<16>(p);
+}
+extern "C" __global__ __launch_bounds__(512, 1) void hat_cab_conv1_t32(CabConvArgs p)
+{
+    cab_conv1_body<32>(p);
 }
 
 // ---------------------------------------------------------------------------

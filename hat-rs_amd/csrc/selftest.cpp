@@ -485,6 +485,26 @@ int gpu_selftest(std::string* err)
             check_close("hat_cab_gate bias2", dbias2.get(), bias2, 2e-6);
             check_close("hat_cab_gate w2g", dw2g.get(), w2g, 1e-7);
             note("hat_cab_gate (mean by linearity) vs conv2 in full");
+            // The 16 x 32 tile form (3 tiles over 2 blocks) and the gate from its
+            // per-tile sums.
+            {
+                const int tiles32 = (H / 32) * (W / 16);
+                Dev dt1b((size_t)T * CAB_CS), dpartb((size_t)tiles32 * CAB_NSUM * CAB_CS), dw2gb((size_t)C * CAB_K2),
+                    dbias2b(C), dgateb(C);
+                CabConvArgs cb2{dxn.p, dw1.p, db1.p, dt1b.p, dpartb.p, H, W};
+                launch(s, "hat_cab_conv1_t32", 2, 1, 1, 512, cb2);
+                CabGateArgs gb = ga;
+                gb.partial = dpartb.p;
+                gb.t1 = dt1b.p;
+                gb.tiles = tiles32;
+                gb.w2g = dw2gb.p;
+                gb.bias2 = dbias2b.p;
+                gb.gate = dgateb.p;
+                launch(s, "hat_cab_gate", 1, 1, 1, 1024, gb);
+                check_close("hat_cab_conv1_t32 t1", dt1b.get(), t1, 2e-5);
+                check_close("hat_cab_gate gate (16x32 tiles)", dgateb.get(), gate, 2e-6);
+                note("hat_cab_conv1_t32 144->6 + gelu, 32x48, and its tile sums");
+            }
             check_close("hat_gemmws_cab_ln", dout.get(), want, 5e-5);
             check_close("hat_gemmws_cab_ln layernorm", dxo.get(), wxn, 5e-5);
             note("hat_gemmws_cab_ln proj + folded conv2 + norm2");
