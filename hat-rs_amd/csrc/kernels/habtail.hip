@@ -311,12 +311,13 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
                 for (int j = 0; j < 4; ++j) h[nt][j] = gelu(h[nt][j]);
             // fc2, per 16-unit step of the hidden chunk and three output
             // column tiles: the three weight reads, then their 12 MFMAs (the
-            // reads in flight together, not one read's latency per four MFMAs)
+            // reads in flight together, not one read's latency per four MFMAs;
+            // the scheduler is free within a step)
 #pragma unroll
             for (int nt = 0; nt < MLP_HC / 16; ++nt)
 #pragma unroll
                 for (int g3 = 0; g3 < NT; g3 += 3) {
-                    __builtin_amdgcn_sched_barrier(0);
+                    if (g3 == 0) __builtin_amdgcn_sched_barrier(0);
                     f32x4 wv[3];
 #pragma unroll
                     for (int j = 0; j < 3; ++j)
