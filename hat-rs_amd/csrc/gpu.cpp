@@ -406,20 +406,24 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
     // column block per block) for the head convs, the 60-channel CAB conv and
     // the C = 180 trunk convs.
     const char* wide = nullptr;
-    int wbn = 0;
+    int wbn = 0, wwaves = 0;
     if (H % 16 == 0 && W % 16 == 0 && C.CO % 4 == 0 && co_stride % 4 == 0) {
         if (epi == CEPI_STORE && C.CO > 16 && C.CO <= 64) {
             wide = "hat_convw_n4_store";
             wbn = 64;
+            wwaves = CONVW_WAVES_N4_STORE;
         } else if (epi == CEPI_SHUFFLE) {
             wide = "hat_convw_n8_shuffle";
             wbn = 128;
+            wwaves = CONVW_WAVES_N8_SHUFFLE;
         } else if (epi == CEPI_RESID && C.CO > 144 && C.CO <= 192) {
             wide = "hat_convw_n6_resid";  // C = 180 trunk convs, two 96-channel blocks
             wbn = 96;
+            wwaves = CONVW_WAVES_N6_RESID;
         } else if (epi == CEPI_COLSUM && colsum_wide(C.CO, H, W, co_stride)) {
             wide = "hat_convw_n6_colsum";  // C = 180 CAB conv2
             wbn = 96;
+            wwaves = CONVW_WAVES_N6_COLSUM;
         }
     }
     const char* name = nullptr;
@@ -466,7 +470,8 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
         p.mean2 = mean[2];
     }
     if (wide) {
-        launch(s, wide, (unsigned)((W / 16) * (H / 16)), (unsigned)((C.CO + wbn - 1) / wbn), 1, 512, p);
+        launch(s, wide, (unsigned)((W / 16) * (H / 16)), (unsigned)((C.CO + wbn - 1) / wbn), 1,
+               (unsigned)(wwaves * 64), p);
         return;
     }
     if (epi == CEPI_FINAL) {
@@ -496,6 +501,9 @@ void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride,
                        : epi == EPI_RESID    ? "hat_convw_n9_resid"
                                              : nullptr;
     if (!name) throw Error("convw: bad epilogue");
+    const int waves = epi == EPI_STORE_LN   ? CONVW_WAVES_N9_STORE_LN
+                      : epi == EPI_RESID_LN ? CONVW_WAVES_N9_RESID_LN
+                                            : CONVW_WAVES_N9_RESID;
     ConvArgs p{};
     p.in = in;
     p.w = C.w;
@@ -514,7 +522,7 @@ void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride,
     p.nw = nw;
     p.nb = nb;
     p.eps = 1e-5f;
-    launch(s, name, (unsigned)((W / 16) * (H / 16)), 1, 1, 512, p);
+    launch(s, name, (unsigned)((W / 16) * (H / 16)), 1, 1, (unsigned)(waves * 64), p);
 }
 
 void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, const Plan& pl,

@@ -31,6 +31,17 @@ constexpr int ws_mt(int /*epi*/) { return 1; }
 constexpr int ws_waves(int epi) { return epi == EPI_RESID_LN || epi == EPI_HAB_LN ? 8 : 16; }
 constexpr int ws_rows(int epi) { return ws_waves(epi) * 16 * ws_mt(epi); }
 
+// Waves per block of the wide-tile 3x3 conv instances (convw.hip): 8 own two
+// 16-pixel tile rows each (2 waves per SIMD), 16 own one (4 per SIMD, where
+// the registers allow it; measured faster for these three).
+#define CONVW_WAVES_N9_STORE_LN 16
+#define CONVW_WAVES_N9_RESID_LN 8
+#define CONVW_WAVES_N9_RESID 8
+#define CONVW_WAVES_N6_RESID 8
+#define CONVW_WAVES_N6_COLSUM 8
+#define CONVW_WAVES_N4_STORE 16
+#define CONVW_WAVES_N8_SHUFFLE 16
+
 struct GemmArgs {
     const float* a;      // [M][lda]
     const float* w;      // [N][Kp] row-major, K contiguous, zero-padded to Kp

@@ -294,26 +294,23 @@ __device__ __forceinline__ void convw_body(const ConvArgs& p)
     }
 }
 
-// Waves per block: 8, two tile rows each (the instances here have at most
-// 144 channels; wider blocks would need one row per wave).
-constexpr int convw_waves(int nt) { return nt > 9 ? 16 : 8; }
-
-#define CONVW_INST(NAME, NT, EPI, HEAD)                                                      \
-    extern "C" __global__ __launch_bounds__(convw_waves(NT) * 64) void NAME(ConvArgs p)      \
+// Waves per block: CONVW_WAVES_* (kargs.h), 8 (two tile rows each) or 16 (one).
+#define CONVW_INST(NAME, NT, EPI, HEAD, WAVES)                                               \
+    extern "C" __global__ __launch_bounds__(WAVES * 64) void NAME(ConvArgs p)                \
     {                                                                                        \
-        convw_body<NT, EPI, HEAD, convw_waves(NT)>(p);                                       \
+        convw_body<NT, EPI, HEAD, WAVES>(p);                                                 \
     }
 
 // C = 144 (NT = 9) trunk convs.
-CONVW_INST(hat_convw_n9_store_ln, 9, EPI_STORE_LN, -1)
-CONVW_INST(hat_convw_n9_resid_ln, 9, EPI_RESID_LN, -1)
-CONVW_INST(hat_convw_n9_resid, 9, EPI_RESID, -1)
+CONVW_INST(hat_convw_n9_store_ln, 9, EPI_STORE_LN, -1, CONVW_WAVES_N9_STORE_LN)
+CONVW_INST(hat_convw_n9_resid_ln, 9, EPI_RESID_LN, -1, CONVW_WAVES_N9_RESID_LN)
+CONVW_INST(hat_convw_n9_resid, 9, EPI_RESID, -1, CONVW_WAVES_N9_RESID)
 // C = 180 (two 96-channel column blocks): the RHAG conv and conv_after_body
 // with the residual (their LayerNorm, needing whole rows, runs separately).
-CONVW_INST(hat_convw_n6_resid, 6, EPI_RESID, -1)
+CONVW_INST(hat_convw_n6_resid, 6, EPI_RESID, -1, CONVW_WAVES_N6_RESID)
 // C = 180 CAB conv2 (60 -> 180) + per-tile column sums for the channel mean.
-CONVW_INST(hat_convw_n6_colsum, 6, EPI_STORE, CEPI_COLSUM)
+CONVW_INST(hat_convw_n6_colsum, 6, EPI_STORE, CEPI_COLSUM, CONVW_WAVES_N6_COLSUM)
 // Head: conv_before_upsample (-> 64, LeakyReLU) and the upsample convs
 // (64 -> 4*64 or 9*64 in 128-channel column blocks, + PixelShuffle).
-CONVW_INST(hat_convw_n4_store, 4, EPI_STORE, CEPI_STORE)
-CONVW_INST(hat_convw_n8_shuffle, 8, EPI_STORE, CEPI_SHUFFLE)
+CONVW_INST(hat_convw_n4_store, 4, EPI_STORE, CEPI_STORE, CONVW_WAVES_N4_STORE)
+CONVW_INST(hat_convw_n8_shuffle, 8, EPI_STORE, CEPI_SHUFFLE, CONVW_WAVES_N8_SHUFFLE)

@@ -615,10 +615,10 @@ int gpu_selftest(std::string* err)
         // residual (in place) + LayerNorm, conv_first's 3-channel input +
         // LayerNorm, and a plain residual; 32 x 48 plane = 6 tiles.
         {
-            struct WCase { int CI, cin_stride, CO, epi; const char* k; };
-            const WCase wc[] = {{144, 144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln"},
-                                {3, 4, 144, EPI_STORE_LN, "hat_convw_n9_store_ln"},
-                                {144, 144, 144, EPI_RESID, "hat_convw_n9_resid"}};
+            struct WCase { int CI, cin_stride, CO, epi; const char* k; int waves; };
+            const WCase wc[] = {{144, 144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln", CONVW_WAVES_N9_RESID_LN},
+                                {3, 4, 144, EPI_STORE_LN, "hat_convw_n9_store_ln", CONVW_WAVES_N9_STORE_LN},
+                                {144, 144, 144, EPI_RESID, "hat_convw_n9_resid", CONVW_WAVES_N9_RESID}};
             for (const WCase& c : wc) {
                 const int H = 32, W = 48, HW = H * W, CO = c.CO;
                 std::vector<float> in((size_t)HW * c.cin_stride, 0.0f);
@@ -649,7 +649,7 @@ int gpu_selftest(std::string* err)
                 p.nw = dnw.p;
                 p.nb = dnb.p;
                 p.eps = 1e-5f;
-                launch(s, c.k, (W / 16) * (H / 16), 1, 1, 512, p);
+                launch(s, c.k, (W / 16) * (H / 16), 1, 1, c.waves * 64, p);
                 std::vector<double> want((size_t)HW * CO), wxn((size_t)HW * CO);
                 for (int y = 0; y < H; ++y)
                     for (int x = 0; x < W; ++x) {
@@ -810,10 +810,14 @@ int gpu_selftest(std::string* err)
                                                                                   : nullptr;
             if (wide) {
                 const int wbn = cc.epi == CEPI_SHUFFLE ? 128 : (cc.epi == CEPI_RESID || cc.epi == CEPI_COLSUM) ? 96 : 64;
+                const int wwaves = cc.epi == CEPI_SHUFFLE  ? CONVW_WAVES_N8_SHUFFLE
+                                   : cc.epi == CEPI_RESID  ? CONVW_WAVES_N6_RESID
+                                   : cc.epi == CEPI_COLSUM ? CONVW_WAVES_N6_COLSUM
+                                                           : CONVW_WAVES_N4_STORE;
                 Dev dout2(out_n), dpart2((size_t)(W / 16) * (H / 16) * cc.CO);
                 p.out = dout2.p;
                 p.partial = dpart2.p;
-                launch(s, wide, (W / 16) * (H / 16), (cc.CO + wbn - 1) / wbn, 1, 512, p);
+                launch(s, wide, (W / 16) * (H / 16), (cc.CO + wbn - 1) / wbn, 1, wwaves * 64, p);
                 check_close(std::string(wide) + " " + cc.what, dout2.get(), want, 5e-5);
                 if (cc.epi == CEPI_COLSUM) {
                     // one partial row per 16x16 tile
