@@ -252,42 +252,6 @@ void run_cab(hipStream_t s, const DevCab& cb, const float* xn, int H, int W, con
     launch(s, "hat_cab_gate", 1, 1, 1, 1024, g);
 }
 
-// Folded CAB, second half: out = res + a . proj^T + conv2-segment + bias2,
-// xn = LayerNorm(out) (norm2).
-void run_proj_cab(hipStream_t s, const DevLinear& L, const float* a, long M, float* out,
-                  const float* res, float* xn, const float* nw, const float* nb, const float* bias2,
-                  const float* t1, const float* w2g, int H, int W)
-{
-    if (L.K != CAB_C || L.Kp != CAB_C || L.N != CAB_C) throw Error("CAB projection: needs 144 x 144");
-    if ((long)H * W != M) throw Error("CAB projection: rows must be the H x W plane");
-    GemmArgs p{};
-    p.a = a;
-    p.w = L.w;
-    p.bias = bias2;
-    p.out = out;
-    p.res = res;
-    p.xn = xn;
-    p.nw = nw;
-    p.nb = nb;
-    p.M = (int)M;
-    p.N = L.N;
-    p.K = L.K;
-    p.Kp = L.Kp;
-    p.lda = CAB_C;
-    p.ldo = CAB_C;
-    p.eps = 1e-5f;
-    p.t1 = t1;
-    p.w2g = w2g;
-    p.H = H;
-    p.W = W;
-    static const int cus = std::max(1, Runtime::get().cu_count());
-    const long ntiles = (M + ws_rows(EPI_RESID_LN) - 1) / ws_rows(EPI_RESID_LN);
-    const long rounds = (ntiles + cus - 1) / cus;
-    const long g = std::max(1L, (ntiles + rounds - 1) / rounds);
-    launch(s, "hat_gemmws_cab_ln", (unsigned)g, 1, 1, ws_waves(EPI_RESID_LN) * 64, p);
-}
-
-// The second half of a HAB with the folded CAB, one kernel (C = 144):
 // x' = res + a . proj^T + conv2-segment + bias2; out = x' + MLP(norm2(x'));
 // xn = norm_next(out). out may alias res; a, t1 and xn must not overlap out.
 // Without t1 (the OCAB): x' = res + a . proj^T + bias2 (the projection bias),
