@@ -19,13 +19,14 @@
 // OCAB: x' = x + ao . Wp^T + bp, out = x' + MLP(norm2(x'))).
 //
 // A block of 8 waves walks 128-row tiles (wave w owns rows 16w .. 16w+15). Per
-// tile ten (OCAB: nine) weight chunks pass through the double-buffered LDS of the fused
+// tile eight weight chunks pass through the double-buffered LDS of the fused
 // MLP (global_load_lds_dwordx4, swizzled unpadded rows, one barrier per
-// chunk): the projection in three chunks of 48 K (144 x 12 float4), the gated
-// conv2 (144 x 16 float4: 56 K, 8 zero), then the six 48-unit hidden chunks.
-// The attention rows of the next tile are loaded under the last chunk's fc2,
-// the residual rows and the t1 neighbourhood at the start of each tile, ahead
-// of the chunks that use them.
+// chunk): the projection in two, k 0..79 (144 x 20 float4) and k 80..143
+// (144 x 16 float4), then the six 48-unit hidden chunks. The gated conv2's
+// weights (144 x 16 float4: 56 K, 8 zero) stay in LDS for the whole launch
+// and run in the second projection chunk. The attention rows of the next
+// tile are loaded under the last chunk's fc2, the residual rows and the t1
+// neighbourhood at the start of each tile, ahead of the chunks that use them.
 //
 // Included after gemm.hip and mlp.hip in the one translation unit.
 
@@ -36,22 +37,28 @@ template <bool CAB, int EPI>
 __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
 {
     constexpr int C = HT_C, NT = C / 16, NH = 2 * C, NCH = NH / MLP_HC;
-    constexpr int HT_NPC = CAB ? 4 : 3;         // projection chunks per tile
-    constexpr int HT_NCT = HT_NPC + NCH;        // chunks per tile
+    constexpr int HT_NPC = 2;                   // projection chunks per tile
+    constexpr int HT_NCT = HT_NPC + NCH;        // chunks per tile (8: every tile starts in buffer 0)
     constexpr int R1 = C / 4, R2 = MLP_HC / 4;  // MLP slices: fc1 [48][36], fc2 [144][12] float4
     constexpr int W1F4 = MLP_HC * R1, F4 = W1F4 + C * R2;
-    constexpr int RP = 12, RC = 16;             // projection chunk [144][12], conv2 chunk [144][16] float4
-    constexpr int PF4 = C * RP, CF4 = C * RC;
+    // projection chunks [144][20] (k 0..79) and [144][16] (k 80..143), the
+    // resident conv2 slice [144][16] float4
+    constexpr int RA = 20, RB = 16, RC = 16, KA = 4 * RA;
+    constexpr int AF4 = C * RA, BF4 = C * RB, CF4 = C * RC;
     constexpr int BUF = F4 * 4;
     constexpr int PER = (F4 + MLP_THREADS - 1) / MLP_THREADS;
-    static_assert(PF4 <= F4 && CF4 <= F4 && PF4 % 64 == 0 && CF4 % 64 == 0 && F4 % 64 == 0, "chunk sizes");
-    static_assert(CAB_K2 == 56 && CAB_C == C, "the conv2 chunk holds 56 K");
+    static_assert(HT_NCT % 2 == 0, "an even chunk count keeps the buffer parity static");
+    static_assert(KA + 4 * RB == C, "the two projection chunks cover K");
+    static_assert(AF4 <= F4 && BF4 <= F4 && AF4 % 64 == 0 && BF4 % 64 == 0 && CF4 % 64 == 0 && F4 % 64 == 0,
+                  "chunk sizes");
+    static_assert(CAB_K2 == 56 && CAB_C == C, "the conv2 slice holds 56 K");
     // The two chunk buffers are separate objects, and every access below names
     // one of them at compile time (the chunk parity is static): the compiler
     // then knows that reading one buffer does not depend on the DMA still
     // filling the other, and does not wait for that DMA before the read.
     __shared__ __attribute__((aligned(16))) float Wb0[BUF];
     __shared__ __attribute__((aligned(16))) float Wb1[BUF];
+    __shared__ __attribute__((aligned(16))) float W2s[CAB ? CF4 * 4 : 4];
     // b1 [288], b2, next-norm w, b [144 each], bias2, norm2 w, b [144 each]
     __shared__ __attribute__((aligned(16))) float Cs[NH + 6 * C];
     float* const b1s = Cs;
@@ -96,12 +103,11 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             goff[i] = r * p.ldw2 + c4 * 4;
         }
     }
-    // Chunk cj of a tile into LDS buffer bufc (a CInt: 0 or 1) (cj < 3:
-    // projection k 48cj ..; cj = 3 with the CAB: gated conv2; else hidden
-    // chunk cj - HT_NPC).
+    // Chunk cj of a tile into LDS buffer bufc (a CInt: 0 or 1): cj = 0, 1 the
+    // projection's k 0..79 and 80..143, else hidden chunk cj - HT_NPC.
     auto fetch = [&](int cj, auto bufc) {
         float* B = decltype(bufc)::value ? Wb1 : Wb0;
-        const int nf4 = cj < 3 ? PF4 : (CAB && cj == 3 ? CF4 : F4);
+        const int nf4 = cj == 0 ? AF4 : (cj == 1 ? BF4 : F4);
         const int h0 = (cj - HT_NPC) * MLP_HC;
         const float* w1c = p.w1 + (size_t)(h0 > 0 ? h0 : 0) * p.ldw1;
         const float* w2c = p.w2 + (h0 > 0 ? h0 : 0);
@@ -111,18 +117,18 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             if (base >= nf4) break;
             const int idx = base + lane;
             const float* src;
-            // the projection's and the conv2 chunk's offsets are computed here,
-            // a few VALU ops per slot, from an index the compiler cannot see
-            // through: otherwise it hoists every (chunk, slot) address out of
-            // the tile loop, 64 bits each, and spills them
+            // the projection chunks' offsets are computed here, a few VALU ops
+            // per slot, from an index the compiler cannot see through:
+            // otherwise it hoists every (chunk, slot) address out of the tile
+            // loop, 64 bits each, and spills them
             int id = idx;
             asm volatile("" : "+v"(id));
-            if (cj < 3) {
-                const int r = id / RP, c4 = (id - r * RP) ^ mlp_swz<RP>(r);
-                src = p.wp + cj * 48 + r * C + c4 * 4;
-            } else if (CAB && cj == 3) {
-                const int r = id / RC, c4 = (id - r * RC) ^ mlp_swz<RC>(r);
-                src = c4 < CAB_K2 / 4 ? p.w2g + r * CAB_K2 + c4 * 4 : hat_zero_row;  // k 56..63: zero
+            if (cj == 0) {
+                const int r = id / RA, c4 = (id - r * RA) ^ mlp_swz<RA>(r);
+                src = p.wp + r * C + c4 * 4;
+            } else if (cj == 1) {
+                const int r = id / RB, c4 = (id - r * RB) ^ mlp_swz<RB>(r);
+                src = p.wp + r * C + KA + c4 * 4;
             } else {
                 src = (base < W1F4 ? w1c : w2c) + goff[i];
             }
@@ -154,21 +160,32 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
 
     // Swizzled operand columns (rows nt*16 + lr: (row >> 2) & 3 == (lr >> 2) & 3,
     // row & 15 == lr).
-    const int sg = lg ^ mlp_swz<R1>(lr), sg2 = lg ^ mlp_swz<R2>(lr), sgp = lg ^ mlp_swz<RP>(lr);
+    const int sg = lg ^ mlp_swz<R1>(lr), sg2 = lg ^ mlp_swz<R2>(lr), sga = lg ^ mlp_swz<RA>(lr);
     fetch(0, CInt<0>{});
+    if (CAB) {
+        // the gated conv2 slice, once per launch: k 56..63 of a row are zero
+#pragma unroll
+        for (int i = 0; i < (CF4 + MLP_THREADS - 1) / MLP_THREADS; ++i) {
+            const int base = i * MLP_THREADS + wave * 64;  // wave-uniform
+            if (base >= CF4) break;
+            const int idx = base + lane;
+            const int r = idx / RC, c4 = (idx - r * RC) ^ mlp_swz<RC>(r);
+            const float* src = c4 < CAB_K2 / 4 ? p.w2g + r * CAB_K2 + c4 * 4 : hat_zero_row;
+            __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(W2s + base * 4),
+                                             16, 0, 0);
+        }
+    }
     load_rows(xa, p.a, tile);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    // One tile whose chunk 0 sits in buffer P; chunk cj then in buffer
-    // (P + cj) & 1, and the next tile's chunk 0 in (P + HT_NCT) & 1.
-    auto tile_body = [&](auto parity) {
-        constexpr int P = decltype(parity)::value;
+    // One tile: chunk cj in buffer cj & 1 (the chunk count per tile is even).
+    for (; tile < ntiles; tile += gridDim.x) {
         const bool last_tile = tile + (int)gridDim.x >= ntiles;
         const int mbase = tile * MLP_ROWS + wave * 16;
         // The residual rows and (CAB) the t1 neighbourhood, loaded while
-        // projection chunk 1 computes (first used after the projection / in
-        // the conv2 chunk).
+        // projection chunk 0 computes (first used after the projection / by
+        // the conv2 MFMAs in chunk 1).
         f32x4 xg[CAB_K2 / 16];
         float2 xh;
         auto load_tail_inputs = [&]() {
@@ -198,50 +215,60 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
         f32x4 acc[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[nt] = *(const f32x4*)(bias2s + nt * 16 + lg * 4);
+        // chunk 0 (buffer 0): k 0..79, five 16-k steps
+        fetch(1, CInt<1>{});
+        load_tail_inputs();
 #pragma unroll
-        for (int cj = 0; cj < HT_NPC; ++cj) {
-            const float* B = ((P + cj) & 1) ? Wb1 : Wb0;
-            // the next chunk is always of this tile
-            if ((P + cj) & 1) fetch(cj + 1, CInt<0>{});
-            else fetch(cj + 1, CInt<1>{});
-            if (cj == 1) load_tail_inputs();
-            if (cj < 3) {
+        for (int k3 = 0; k3 < KA / 16; ++k3) {
+            // A operand: the attention rows' 16-k chunk k3; each step's weight
+            // reads stay next to their MFMAs
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int k3 = 0; k3 < 3; ++k3) {
-                    // A operand: the attention rows' 16-k chunk 3 cj + k3; each
-                    // k3's weight reads stay next to their MFMAs
-                    __builtin_amdgcn_sched_barrier(0);
+            for (int nt = 0; nt < NT; ++nt) {
+                const f32x4 wv = *(const f32x4*)(Wb0 + (nt * 16 + lr) * (4 * RA) + (k3 * 4 + sga) * 4);
 #pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) {
-                        const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * 48 + (k3 * 4 + sgp) * 4);
+                for (int s = 0; s < 4; ++s) acc[nt] = mfma16(wv[s], xa[k3][s], acc[nt]);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        // chunk 1 (buffer 1): k 80..143, four 16-k steps, then the gated conv2
+        // from its resident slice
+        fetch(HT_NPC, CInt<0>{});
 #pragma unroll
-                        for (int s = 0; s < 4; ++s) acc[nt] = mfma16(wv[s], xa[3 * cj + k3][s], acc[nt]);
-                    }
-                }
-            } else if (CAB) {
+        for (int k3 = 0; k3 < RB / 4; ++k3) {
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int k3 = 0; k3 < 3; ++k3) {
-                    __builtin_amdgcn_sched_barrier(0);
+            for (int nt = 0; nt < NT; ++nt) {
+                const int pc = (k3 * 4 + lg) ^ lr;  // 4-bit swizzle of the 16-float4 rows
+                const f32x4 wv = *(const f32x4*)(Wb1 + (nt * 16 + lr) * (4 * RB) + pc * 4);
 #pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) {
-                        const int pc = (k3 * 4 + lg) ^ lr;  // 4-bit swizzle of the 16-float4 rows
-                        const f32x4 wv = *(const f32x4*)(B + (nt * 16 + lr) * 64 + pc * 4);
+                for (int s = 0; s < 4; ++s) acc[nt] = mfma16(wv[s], xa[KA / 16 + k3][s], acc[nt]);
+            }
+        }
+        if (CAB) {
 #pragma unroll
-                        for (int s = 0; s < 4; ++s) acc[nt] = mfma16(wv[s], xg[k3][s], acc[nt]);
-                    }
-                }
-                // the 8-k tail: lane group g's k = 48 + 2g + s, float4 12 + g/2
+            for (int k3 = 0; k3 < 3; ++k3) {
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
-                    const int pc = (12 + (lg >> 1)) ^ lr;
-                    const float2 wv = *(const float2*)(B + (nt * 16 + lr) * 64 + pc * 4 + (lg & 1) * 2);
-                    acc[nt] = mfma16(wv.x, xh.x, acc[nt]);
-                    acc[nt] = mfma16(wv.y, xh.y, acc[nt]);
+                    const int pc = (k3 * 4 + lg) ^ lr;
+                    const f32x4 wv = *(const f32x4*)(W2s + (nt * 16 + lr) * (4 * RC) + pc * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) acc[nt] = mfma16(wv[s], xg[k3][s], acc[nt]);
                 }
             }
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+            // the 8-k tail: lane group g's k = 48 + 2g + s, float4 12 + g/2
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int pc = (12 + (lg >> 1)) ^ lr;
+                const float2 wv = *(const float2*)(W2s + (nt * 16 + lr) * (4 * RC) + pc * 4 + (lg & 1) * 2);
+                acc[nt] = mfma16(wv.x, xh.x, acc[nt]);
+                acc[nt] = mfma16(wv.y, xh.y, acc[nt]);
+            }
         }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
 
         // ---- x' = x + acc (rows past M are zero); xa = LN2(x') (two-pass, biased
         // variance, cpu.rs:563-581), the four lanes of a row reducing with shuffles.
@@ -331,30 +358,15 @@ __device__ __forceinline__ void hab_tail_body(const HabTailArgs& p)
             __syncthreads();
         };
         static_assert(NCH % 2 == 0, "hidden chunks go in pairs, one per buffer");
-        constexpr int Q0 = (P + HT_NPC) & 1;
+        static_assert(HT_NPC % 2 == 0, "hidden chunk c sits in buffer c & 1");
 #pragma unroll 1
         for (int c = 0; c < NCH; c += 2) {
-            mlp_chunk(c, CInt<Q0>{});
-            mlp_chunk(c + 1, CInt<Q0 ^ 1>{});
+            mlp_chunk(c, CInt<0>{});
+            mlp_chunk(c + 1, CInt<1>{});
         }
         // the residual x' straight from xr (one row tile: pres[0][nt] = xr[nt])
         gemm_epilogue<1, NT, EPI>(g, kc_out, acc2, mbase, 0, lr, lg, nullptr,
                                            (const f32x4(*)[NT])xr);
-    };
-
-    // With an even chunk count per tile every tile starts in buffer 0; with
-    // an odd one the tiles alternate, and go in pairs.
-    if constexpr (HT_NCT % 2 == 0) {
-        for (; tile < ntiles; tile += gridDim.x) tile_body(CInt<0>{});
-    } else {
-        for (;;) {
-            tile_body(CInt<0>{});
-            tile += gridDim.x;
-            if (tile >= ntiles) break;
-            tile_body(CInt<1>{});
-            tile += gridDim.x;
-            if (tile >= ntiles) break;
-        }
     }
 }
 
