@@ -87,8 +87,9 @@ __device__ __forceinline__ void stage_store_rows(float* stage, const f32x4 (&v)[
 }
 
 // STAGE: MT = 1, whole contiguous rows (n0 = 0, N = ldo = 16*NT), and `stage`
-// is the wave's LDS region for stage_store_rows.
-template <int MT, int NT, int EPI, bool BIAS_IN_ACC = false, bool STAGE = false>
+// is the wave's LDS region for stage_store_rows. NTSTORE: `out` (not xn) goes
+// out with non-temporal stores.
+template <int MT, int NT, int EPI, bool BIAS_IN_ACC = false, bool STAGE = false, bool NTSTORE = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts& k, f32x4 (&acc)[MT][NT],
                                               int mbase, int n0, int lr, int lg, const int* colmap,
                                               const f32x4 (*pres)[NT] = nullptr, float* stage = nullptr)
@@ -219,7 +220,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const EpiConsts
                 }
                 continue;
             }
-            *(float4*)(p.out + (size_t)m * p.ldo + n) = make_float4(v[0], v[1], v[2], v[3]);
+            if (NTSTORE)
+                __builtin_nontemporal_store(v, (f32x4*)(p.out + (size_t)m * p.ldo + n));
+            else
+                *(float4*)(p.out + (size_t)m * p.ldo + n) = make_float4(v[0], v[1], v[2], v[3]);
             if (LNOUT) {
                 const float4 w4 = *(const float4*)(k.nw + (n - n0));
                 const float4 b4 = *(const float4*)(k.nb + (n - n0));
