@@ -99,8 +99,21 @@ __device__ __forceinline__ void attn_fetch(const AttnArgs& p, int wi, int head,
             const int k = e / PER_KEY, d = (e - k * PER_KEY) * S::U;
             const int pix = attn_key_pixel<OCA>(p, wi, k);
             if (pix >= 0) {
-                kv = *(const vec*)(Kg + (size_t)pix * D + d);
-                vv = *(const vec*)(Vg + (size_t)pix * D + d);
+                if (OCA) {
+                    kv = *(const vec*)(Kg + (size_t)pix * D + d);
+                    vv = *(const vec*)(Vg + (size_t)pix * D + d);
+                } else if constexpr (S::U == 4) {
+                    // SW: this item is the only reader of these keys and values;
+                    // non-temporal loads leave the last-level cache to the
+                    // attention output and residual the next kernel reads
+                    const f32x4 a = __builtin_nontemporal_load((const f32x4*)(Kg + (size_t)pix * D + d));
+                    const f32x4 b = __builtin_nontemporal_load((const f32x4*)(Vg + (size_t)pix * D + d));
+                    kv = make_float4(a[0], a[1], a[2], a[3]);
+                    vv = make_float4(b[0], b[1], b[2], b[3]);
+                } else {
+                    kv = *(const vec*)(Kg + (size_t)pix * D + d);
+                    vv = *(const vec*)(Vg + (size_t)pix * D + d);
+                }
             }
         }
         ks[i] = kv;
