@@ -240,7 +240,10 @@ extern "C" __global__ __launch_bounds__(CL_WAVES * 64) void hat_conv_last3(ConvA
     const int lg = lane >> 4;
     const int H = p.H, W = p.W;
     const int ntx = (W + CL_TW - 1) / CL_TW;
-    const int ty = blockIdx.x / ntx, tx = blockIdx.x - ty * ntx;
+    // Tiles are taken bottom row first: the conv before this one wrote its
+    // bottom rows last, so those are the ones still in the last-level cache.
+    const int bt = (int)gridDim.x - 1 - (int)blockIdx.x;
+    const int ty = bt / ntx, tx = bt - ty * ntx;
     const int y0 = ty * CL_TH, x0 = tx * CL_TW;
 
     // A operand: row n = tap*3 + co of the per-tap products (rows 27.. zero).
