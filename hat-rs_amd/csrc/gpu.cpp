@@ -53,6 +53,31 @@ std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int
     return out;
 }
 
+// [CO][CI][3][3] -> the Winograd F(2x2, 3x3) weights U[xi] = G g G^T for the
+// 144 -> 144 convs (hat_convwino_*), G = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2;
+// 0 0 1], formed in double and arranged [kc][xi][nt][lane][4]: lane r + 16 g
+// of (kc, xi, nt) holds U[xi][16 nt + r][16 kc + 4 g .. 16 kc + 4 g + 3].
+std::vector<float> pack_wino(const float* w, int CO, int CI)
+{
+    if (CO != 144 || CI != 144) throw Error("pack_wino: 144 -> 144 convs only");
+    static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    std::vector<float> out((size_t)16 * CO * CI);
+    for (int co = 0; co < CO; ++co)
+        for (int ci = 0; ci < CI; ++ci) {
+            const float* g = w + ((size_t)co * CI + ci) * 9;
+            for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 4; ++j) {
+                    double u = 0.0;
+                    for (int a = 0; a < 3; ++a)
+                        for (int b = 0; b < 3; ++b) u += G[i][a] * (double)g[a * 3 + b] * G[j][b];
+                    const int xi = 4 * i + j, kc = ci / 16, c16 = ci % 16, nt = co / 16, r = co % 16;
+                    const int lane = r + 16 * (c16 / 4);
+                    out[((((size_t)kc * 16 + xi) * 9 + nt) * 64 + lane) * 4 + c16 % 4] = (float)u;
+                }
+        }
+    return out;
+}
+
 std::vector<float> pack_cab_conv1(const float* w)
 {
     std::vector<float> out((size_t)64 * CAB_C, 0.0f);
@@ -486,6 +511,16 @@ void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride,
     p.nw = nw;
     p.nb = nb;
     p.eps = 1e-5f;
+    p.wu = C.wu;
+    // The 144 -> 144 residual convs by Winograd F(2x2, 3x3): 8 x 16 output
+    // tiles, 32-bit element offsets into the input plane.
+    if (C.wu && C.CI == 144 && (epi == EPI_RESID_LN || epi == EPI_RESID) && H % 8 == 0 &&
+        (size_t)H * W * cin_stride < ((size_t)1 << 31)) {
+        if (in == out) throw Error("convw: the output must not overlap the input");
+        launch(s, epi == EPI_RESID_LN ? "hat_convwino_resid_ln" : "hat_convwino_resid",
+               (unsigned)((W / 16) * (H / 8)), 1, 1, 512, p);
+        return;
+    }
     launch(s, name, (unsigned)((W / 16) * (H / 16)), 1, 1, (unsigned)(waves * 64), p);
 }
 
@@ -588,6 +623,10 @@ void GpuBackend::upload_conv(const std::string& name, int r)
                                       &bias, &C.CIp, &C.COp);
     C.w = upload(pk.data(), pk.size());
     C.b = upload(bias.data(), bias.size());
+    if (r == 0 && C.CO == 144 && C.CI == 144) {
+        std::vector<float> wu = pack_wino(wt_.t(name + ".weight"), C.CO, C.CI);
+        C.wu = upload(wu.data(), wu.size());
+    }
     conv_[name] = C;
 }
 

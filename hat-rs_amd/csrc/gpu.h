@@ -49,11 +49,13 @@ std::vector<float> pack_cab_conv1(const float* w);
 struct DevConv {
     float* w = nullptr;  // [CIp/16][9][COp][16]
     float* b = nullptr;  // [COp]
+    float* wu = nullptr; // 144 -> 144 convs: Winograd weights (pack_wino)
     int CI = 0, CIp = 0, CO = 0, COp = 0, r = 0;
 };
 
 // Host-side repacking (also used by the selftest and the op entry points).
 std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
+std::vector<float> pack_wino(const float* w, int CO, int CI);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);
 

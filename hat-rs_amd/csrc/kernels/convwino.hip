@@ -1,0 +1,265 @@
+// 3x3 convolution C -> C (C = 144, stride 1, zero padding 1, NHWC) by
+// Winograd's minimal filtering F(2x2, 3x3) (Lavin & Gray, "Fast Algorithms
+// for Convolutional Neural Networks", 2016), with the bias, the residual and
+// (RESID_LN) the LayerNorm of the result in the epilogue. The reference runs
+// the RHAG conv and conv_after_body as lg_conv3x3_winograd (gpu.rs:605, 742)
+// followed by lg_add and lg_channel_layer_norm (cuda.rs:227-248, 185-191).
+//
+// For each 2x2 output tile with the 4x4 input patch d (rows y-1 .. y+2):
+//   Y = A^T [ U (.) V ] A,   U = G g G^T (per co, ci),   V = B^T d B (per ci)
+// so each of the 16 transform points xi = 4i + j is an independent GEMM
+// M[xi] (co x tile) = U[xi] (co x ci) . V[xi] (ci x tile): 16 * 144 * 144
+// MACs per tile against 4 * 9 * 144 * 144 for the direct form (2.25x fewer).
+//
+// A block owns an 8 x 16 output tile (32 Winograd tiles, two 16-wide MFMA
+// column tiles), all 144 output channels. Wave w computes the two transform
+// points xi = 2w, 2w + 1 (B^T row i = w / 2, columns j = 2 (w % 2) + {0, 1}),
+// accumulating M[xi] (co 144 x tile 32) in 144 registers per lane. Input
+// channels go in 9 chunks of 16: the chunk's 10 x 18 halo patch is staged
+// in LDS (global_load_lds, double-buffered, channel-quad-major); each lane
+// forms V for its
+// (tile, four channels) from the patch and feeds it to the MFMAs as the B
+// operand. U (pre-transformed on the host, 1.33 MB, L2-resident) streams
+// from global memory as the A operand, two steps ahead of its MFMAs.
+//
+// Epilogue, per 16-channel slice: the waves write their M slices to LDS, then
+// each thread forms the 2x2 outputs of one (tile, channel) from the 16 points.
+// A thread ends with 4 pixels x 9 channels; the 16 lanes of a tile hold a
+// pixel's 144 channels, reducing the LayerNorm statistics with shuffles.
+//
+// Included after gemm.hip in the one translation unit.
+
+#define WG_TH 8                            // output tile rows
+#define WG_TW 16                           // output tile columns
+#define WG_PH (WG_TH + 2)                  // 10 halo rows
+#define WG_PW (WG_TW + 2)                  // 18 halo columns
+#define WG_PPX (WG_PH * WG_PW)             // 180 halo pixels
+#define WG_SLOTS 768                       // float4 slots per patch buffer (720 used)
+#define WG_MS 20                           // LDS row stride of an M slice entry (16 used)
+
+template <int EPI>
+__device__ __forceinline__ void convwino_body(const ConvArgs& p)
+{
+    constexpr int C = 144, NT = C / 16, NKC = C / 16;
+    constexpr bool LN = EPI == EPI_RESID_LN;
+    static_assert(EPI == EPI_RESID || EPI == EPI_RESID_LN, "residual epilogues only");
+    __shared__ __attribute__((aligned(16))) float Pb0[WG_SLOTS * 4];
+    __shared__ __attribute__((aligned(16))) float Pb1[WG_SLOTS * 4];
+    __shared__ __attribute__((aligned(16))) float Ms0[16 * 32 * WG_MS];
+    __shared__ __attribute__((aligned(16))) float Ms1[16 * 32 * WG_MS];
+    __shared__ __attribute__((aligned(16))) float Cs[3 * C];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int H = p.H, W = p.W;
+    const int tiles_x = W / WG_TW;
+    const int y0 = (blockIdx.x / tiles_x) * WG_TH;
+    const int x0 = (blockIdx.x % tiles_x) * WG_TW;
+
+    for (int i = tid; i < (LN ? 3 : 1) * C; i += 512) {
+        const float* src = i < C ? p.bias : (i < 2 * C ? p.nw : p.nb);
+        Cs[i] = src[i % C];
+    }
+
+    // The patch is channel-quad-major: float4 slot q * 180 + pix holds
+    // channels 4q .. 4q+3 of halo pixel pix, so a lane's reads sit at one
+    // lane offset plus wave-uniform ones. The two slots this thread stages per
+    // chunk (the second for waves 0..3 only): element offsets of the quad in
+    // chunk 0, or -1 for slots outside the plane or past the 720 used.
+    int soff[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int s = r * 512 + tid;
+        const int q = s / WG_PPX, pix = s - q * WG_PPX;
+        const int hy = pix / WG_PW, hx = pix - hy * WG_PW;
+        const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
+        const bool ok = s < WG_PPX * 4 && gy >= 0 && gy < H && gx >= 0 && gx < W;
+        soff[r] = ok ? (gy * W + gx) * p.cin_stride + q * 4 : -1;
+    }
+    auto fetch = [&](int kc, auto bufc) {
+        float* B = decltype(bufc)::value ? Pb1 : Pb0;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            if (r == 1 && wave >= 4) break;  // wave-uniform
+            const float* src = soff[r] >= 0 ? p.in + soff[r] + kc * 16 : hat_zero_row;
+            __builtin_amdgcn_global_load_lds((const void*)src,
+                                             (__attribute__((address_space(3))) void*)(B + (r * 512 + wave * 64) * 4),
+                                             16, 0, 0);
+        }
+    };
+
+    // U, pre-arranged as [kc][xi][nt][lane] float4: lane (r, g) of step (e, nt)
+    // holds U[2w + e][16 nt + r][16 kc + 4 g .. +3], the MFMA A operand.
+    const float* ubase = p.wu + (size_t)(2 * wave) * NT * 256 + lane * 4;
+    auto ldu = [&](int kc, int t) -> f32x4 {
+        return *(const f32x4*)(ubase + ((size_t)kc * 16 * NT + t) * 256);
+    };
+
+    // The lane's B^T row / column pattern: R(col) = d[ra][col] + sr d[rb][col],
+    // V[2w] = R(cA) - R(cB), V[2w+1] = R(cC) + sc R(cD).
+    const int bi = wave >> 1, jp = wave & 1;
+    const int ra = bi == 0 ? 0 : (bi == 2 ? 2 : 1);
+    const int rb = bi == 0 ? 2 : (bi == 1 ? 2 : (bi == 2 ? 1 : 3));
+    const float sr = bi == 1 ? 1.0f : -1.0f;
+    const int cA = jp ? 2 : 0, cB = jp ? 1 : 2, cC = 1, cD = jp ? 3 : 2;
+    const float sc = jp ? -1.0f : 1.0f;
+    // LDS float offsets: the lane's tile origin (tile 16 nt2 + lr, quad lg)
+    // and the wave's rows / columns
+    int pbase[2];
+#pragma unroll
+    for (int nt2 = 0; nt2 < 2; ++nt2) {
+        const int n = nt2 * 16 + lr, ty = n >> 3, tx = n & 7;
+        pbase[nt2] = (lg * WG_PPX + 2 * ty * WG_PW + 2 * tx) * 4;
+    }
+    const int cols[4] = {cA, cB, cC, cD};
+    int uoff[4][2];  // [column A..D][row a / b]
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uoff[c][0] = (ra * WG_PW + cols[c]) * 4;
+        uoff[c][1] = (rb * WG_PW + cols[c]) * 4;
+    }
+
+    f32x4 acc[2][NT][2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    f32x4 ur[3];
+    fetch(0, CInt<0>{});
+    ur[0] = ldu(0, 0);
+    ur[1] = ldu(0, 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // Chunk kc from patch buffer Q; U steps t = e * 9 + nt, the load of step
+    // t + 2 (the next chunk's first two at the end) issued ahead of step t.
+    auto chunk = [&](int kc, auto bufc, auto lastc) {
+        constexpr int Q = decltype(bufc)::value;
+        constexpr bool LAST = decltype(lastc)::value;
+        const float* B = Q ? Pb1 : Pb0;
+        f32x4 v[2][2];
+#pragma unroll
+        for (int nt2 = 0; nt2 < 2; ++nt2) {
+            f32x4 R[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f32x4 da = *(const f32x4*)(B + pbase[nt2] + uoff[c][0]);
+                const f32x4 db = *(const f32x4*)(B + pbase[nt2] + uoff[c][1]);
+                R[c] = da + sr * db;
+            }
+            v[0][nt2] = R[0] - R[1];
+            v[1][nt2] = R[2] + sc * R[3];
+        }
+        const int kn = LAST ? kc : kc + 1;
+#pragma unroll
+        for (int t = 0; t < 2 * NT; ++t) {
+            ur[(t + 2) % 3] = t + 2 < 2 * NT ? ldu(kc, t + 2) : ldu(kn, t + 2 - 2 * NT);
+            if (!LAST && t == 0) fetch(kc + 1, CInt<Q ^ 1>{});
+            __builtin_amdgcn_sched_barrier(0);
+            const int e = t / NT, nt = t - e * NT;
+            const f32x4 u = ur[t % 3];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = mfma16(u[s], v[e][nt2][s], acc[e][nt][nt2]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    };
+#pragma unroll 1
+    for (int kc = 0; kc < NKC - 1; kc += 2) {
+        chunk(kc, CInt<0>{}, CInt<0>{});
+        chunk(kc + 1, CInt<1>{}, CInt<0>{});
+    }
+    static_assert(NKC % 2 == 1, "the last chunk sits in buffer 0");
+    chunk(NKC - 1, CInt<0>{}, CInt<1>{});
+
+    // ---- epilogue. Thread (tile = tid / 16, c = tid % 16): outputs of tile
+    // (ty, tx) for channels 16 nt + c.
+    const int et = tid >> 4, ec = tid & 15;
+    const int ety = et >> 3, etx = et & 7;
+    const int py = y0 + 2 * ety, px = x0 + 2 * etx;
+    // element offsets of the thread's four pixels (the plane is below 2^31
+    // elements: checked at launch)
+    const int pix0 = ((py * W) + px) * C, prow = W * C;
+    float y[NT][4];
+    auto out_slice = [&](int nt, auto bufc) {
+        float* Ms = decltype(bufc)::value ? Ms1 : Ms0;
+        // the slice's residual, loaded under the barrier and the transforms
+#pragma unroll
+        for (int q = 0; q < 4; ++q) y[nt][q] = p.res[pix0 + (q >> 1) * prow + (q & 1) * C + nt * 16 + ec];
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int nt2 = 0; nt2 < 2; ++nt2)
+                *(f32x4*)(Ms + ((2 * wave + e) * 32 + nt2 * 16 + lr) * WG_MS + 4 * lg) = acc[e][nt][nt2];
+        __syncthreads();
+        float m[16];
+#pragma unroll
+        for (int x = 0; x < 16; ++x) m[x] = Ms[(x * 32 + et) * WG_MS + ec];
+        float t0[4], t1[4];  // T[i][0], T[i][1] = M[i] A
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            t0[i] = m[4 * i] + m[4 * i + 1] + m[4 * i + 2];
+            t1[i] = m[4 * i + 1] - m[4 * i + 2] - m[4 * i + 3];
+        }
+        const float bias = Cs[nt * 16 + ec];
+        y[nt][0] += (t0[0] + t0[1] + t0[2]) + bias;
+        y[nt][1] += (t1[0] + t1[1] + t1[2]) + bias;
+        y[nt][2] += (t0[1] - t0[2] - t0[3]) + bias;
+        y[nt][3] += (t1[1] - t1[2] - t1[3]) + bias;
+    };
+#pragma unroll
+    for (int nt = 0; nt < NT - 1; nt += 2) {
+        out_slice(nt, CInt<0>{});
+        out_slice(nt + 1, CInt<1>{});
+    }
+    out_slice(NT - 1, CInt<0>{});
+
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p.out[pix0 + (q >> 1) * prow + (q & 1) * C + nt * 16 + ec] = y[nt][q];
+    if (LN) {
+        // two-pass mean then biased variance over the 144 channels of each
+        // pixel (the 16 lanes of the tile), as cpu.rs:563-581
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float s = 0.0f;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) s += y[nt][q];
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o, 64);
+            const float mean = s / (float)C;
+            float v = 0.0f;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const float d = y[nt][q] - mean;
+                v += d * d;
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+            const float rstd = 1.0f / sqrtf(v / (float)C + p.eps);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int co = nt * 16 + ec;
+                p.xn[pix0 + (q >> 1) * prow + (q & 1) * C + co] = (y[nt][q] - mean) * rstd * Cs[C + co] + Cs[2 * C + co];
+            }
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid_ln(ConvArgs p)
+{
+    convwino_body<EPI_RESID_LN>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid(ConvArgs p)
+{
+    convwino_body<EPI_RESID>(p);
+}

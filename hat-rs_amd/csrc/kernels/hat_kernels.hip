@@ -8,4 +8,5 @@
 #include "mlp.hip"
 #include "habtail.hip"
 #include "convw.hip"
+#include "convwino.hip"
 #include "misc.hip"

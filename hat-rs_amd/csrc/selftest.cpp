@@ -615,10 +615,13 @@ int gpu_selftest(std::string* err)
         // residual (in place) + LayerNorm, conv_first's 3-channel input +
         // LayerNorm, and a plain residual; 32 x 48 plane = 6 tiles.
         {
-            struct WCase { int CI, cin_stride, CO, epi; const char* k; int waves; };
-            const WCase wc[] = {{144, 144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln", CONVW_WAVES_N9_RESID_LN},
-                                {3, 4, 144, EPI_STORE_LN, "hat_convw_n9_store_ln", CONVW_WAVES_N9_STORE_LN},
-                                {144, 144, 144, EPI_RESID, "hat_convw_n9_resid", CONVW_WAVES_N9_RESID}};
+            // wino: the Winograd F(2x2, 3x3) kernels (8 x 16 tiles, 512 threads)
+            struct WCase { int CI, cin_stride, CO, epi; const char* k; int waves; bool wino; };
+            const WCase wc[] = {{144, 144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln", CONVW_WAVES_N9_RESID_LN, false},
+                                {3, 4, 144, EPI_STORE_LN, "hat_convw_n9_store_ln", CONVW_WAVES_N9_STORE_LN, false},
+                                {144, 144, 144, EPI_RESID, "hat_convw_n9_resid", CONVW_WAVES_N9_RESID, false},
+                                {144, 144, 144, EPI_RESID_LN, "hat_convwino_resid_ln", 8, true},
+                                {144, 144, 144, EPI_RESID, "hat_convwino_resid", 8, true}};
             for (const WCase& c : wc) {
                 const int H = 32, W = 48, HW = H * W, CO = c.CO;
                 std::vector<float> in((size_t)HW * c.cin_stride, 0.0f);
@@ -631,6 +634,7 @@ int gpu_selftest(std::string* err)
                 int CIp = 0, COp = 0;
                 std::vector<float> pk = pack_conv(w.data(), b.data(), CO, c.CI, 0, &bias, &CIp, &COp);
                 Dev din(in), dw(pk), db(bias), dres(res), dnw(nw), dnb(nb), dxn((size_t)HW * CO);
+                Dev dwu(c.wino ? pack_wino(w.data(), CO, c.CI) : std::vector<float>(4, 0.0f));
                 ConvArgs p{};
                 p.in = din.p;
                 p.w = dw.p;
@@ -649,7 +653,9 @@ int gpu_selftest(std::string* err)
                 p.nw = dnw.p;
                 p.nb = dnb.p;
                 p.eps = 1e-5f;
-                launch(s, c.k, (W / 16) * (H / 16), 1, 1, c.waves * 64, p);
+                p.wu = dwu.p;
+                if (c.wino) launch(s, c.k, (W / 16) * (H / 8), 1, 1, 512, p);
+                else launch(s, c.k, (W / 16) * (H / 16), 1, 1, c.waves * 64, p);
                 std::vector<double> want((size_t)HW * CO), wxn((size_t)HW * CO);
                 for (int y = 0; y < H; ++y)
                     for (int x = 0; x < W; ++x) {
