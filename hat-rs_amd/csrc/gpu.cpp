@@ -53,29 +53,44 @@ std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int
     return out;
 }
 
-// [CO][CI][3][3] -> the Winograd F(2x2, 3x3) weights U[xi] = G g G^T for the
-// 144 -> 144 convs (hat_convwino_*), G = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2;
-// 0 0 1], formed in double and arranged [kc][xi][nt][lane][4]: lane r + 16 g
-// of (kc, xi, nt) holds U[xi][16 nt + r][16 kc + 4 g .. 16 kc + 4 g + 3].
-std::vector<float> pack_wino(const float* w, int CO, int CI)
+// [CO][CI][3][3] -> the Winograd F(2x2, 3x3) weights U[xi] = G g G^T of the
+// hat_convwino_* kernels, G = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2; 0 0 1],
+// formed in double and arranged [kc][xi][nt][lane][4]: lane r + 16 g of
+// (kc, xi, nt) holds U[xi][16 nt + r][16 kc + 4 g .. 16 kc + 4 g + 3]. With
+// r > 0 the output channels are permuted as pack_conv permutes them.
+std::vector<float> pack_wino(const float* w, int CO, int CI, int r)
 {
-    if (CO != 144 || CI != 144) throw Error("pack_wino: 144 -> 144 convs only");
+    if (CO % 16 != 0 || CI % 16 != 0) throw Error("pack_wino: channel counts must be multiples of 16");
     static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    const int NTT = CO / 16, Cf = r > 0 ? CO / (r * r) : 0;
     std::vector<float> out((size_t)16 * CO * CI);
-    for (int co = 0; co < CO; ++co)
+    for (int o2 = 0; o2 < CO; ++o2) {
+        int o = o2;
+        if (r > 0) {
+            const int sub = o2 / Cf, c = o2 % Cf;
+            o = c * r * r + (sub / r) * r + sub % r;
+        }
         for (int ci = 0; ci < CI; ++ci) {
-            const float* g = w + ((size_t)co * CI + ci) * 9;
+            const float* g = w + ((size_t)o * CI + ci) * 9;
             for (int i = 0; i < 4; ++i)
                 for (int j = 0; j < 4; ++j) {
                     double u = 0.0;
                     for (int a = 0; a < 3; ++a)
                         for (int b = 0; b < 3; ++b) u += G[i][a] * (double)g[a * 3 + b] * G[j][b];
-                    const int xi = 4 * i + j, kc = ci / 16, c16 = ci % 16, nt = co / 16, r = co % 16;
-                    const int lane = r + 16 * (c16 / 4);
-                    out[((((size_t)kc * 16 + xi) * 9 + nt) * 64 + lane) * 4 + c16 % 4] = (float)u;
+                    const int xi = 4 * i + j, kc = ci / 16, c16 = ci % 16, nt = o2 / 16, rr = o2 % 16;
+                    const int lane = rr + 16 * (c16 / 4);
+                    out[((((size_t)kc * 16 + xi) * NTT + nt) * 64 + lane) * 4 + c16 % 4] = (float)u;
                 }
         }
+    }
     return out;
+}
+
+// Which convs have a Winograd kernel (hat_convwino_*): the 144 -> 144 trunk
+// convs, conv_before_upsample 144 -> 64 and the x2 upsample convs 64 -> 256.
+static bool wino_conv(int CO, int CI, int r)
+{
+    return (r == 0 && CI == 144 && (CO == 144 || CO == 64)) || (r == 2 && CI == 64 && CO == 256);
 }
 
 std::vector<float> pack_cab_conv1(const float* w)
@@ -458,6 +473,22 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
         p.mean1 = mean[1];
         p.mean2 = mean[2];
     }
+    // conv_before_upsample and the x2 upsample convs by Winograd F(2x2, 3x3):
+    // 8 x 16 output tiles, 32-bit element offsets into both planes
+    p.wu = C.wu;
+    const size_t rr = C.r > 0 ? (size_t)C.r * C.r : 1;
+    if (C.wu && H % 16 == 0 && W % 16 == 0 && cin_stride % 4 == 0 && cin_stride >= C.CI &&
+        (size_t)H * W * cin_stride < ((size_t)1 << 31) && (size_t)H * W * rr * co_stride < ((size_t)1 << 31)) {
+        const unsigned tiles = (unsigned)((W / 16) * (H / 8));
+        if (epi == CEPI_STORE && act == 2 && C.CO == 64 && C.CI == 144 && co_stride >= 64) {
+            launch(s, "hat_convwino_n4_store", tiles, 1, 1, 512, p);
+            return;
+        }
+        if (epi == CEPI_SHUFFLE && C.r == 2 && C.CO == 256 && C.CI == 64 && co_stride >= 64) {
+            launch(s, "hat_convwino_n8_shuffle", tiles, 2, 1, 512, p);
+            return;
+        }
+    }
     if (wide) {
         launch(s, wide, (unsigned)((W / 16) * (H / 16)), (unsigned)((C.CO + wbn - 1) / wbn), 1,
                (unsigned)(wwaves * 64), p);
@@ -623,8 +654,8 @@ void GpuBackend::upload_conv(const std::string& name, int r)
                                       &bias, &C.CIp, &C.COp);
     C.w = upload(pk.data(), pk.size());
     C.b = upload(bias.data(), bias.size());
-    if (r == 0 && C.CO == 144 && C.CI == 144) {
-        std::vector<float> wu = pack_wino(wt_.t(name + ".weight"), C.CO, C.CI);
+    if (wino_conv(C.CO, C.CI, r)) {
+        std::vector<float> wu = pack_wino(wt_.t(name + ".weight"), C.CO, C.CI, r);
         C.wu = upload(wu.data(), wu.size());
     }
     conv_[name] = C;

@@ -55,7 +55,7 @@ struct DevConv {
 
 // Host-side repacking (also used by the selftest and the op entry points).
 std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
-std::vector<float> pack_wino(const float* w, int CO, int CI);
+std::vector<float> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);
 

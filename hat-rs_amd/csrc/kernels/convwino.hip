@@ -1,9 +1,14 @@
-// 3x3 convolution C -> C (C = 144, stride 1, zero padding 1, NHWC) by
-// Winograd's minimal filtering F(2x2, 3x3) (Lavin & Gray, "Fast Algorithms
-// for Convolutional Neural Networks", 2016), with the bias, the residual and
-// (RESID_LN) the LayerNorm of the result in the epilogue. The reference runs
-// the RHAG conv and conv_after_body as lg_conv3x3_winograd (gpu.rs:605, 742)
-// followed by lg_add and lg_channel_layer_norm (cuda.rs:227-248, 185-191).
+// 3x3 convolution (stride 1, zero padding 1, NHWC) by Winograd's minimal
+// filtering F(2x2, 3x3) (Lavin & Gray, "Fast Algorithms for Convolutional
+// Neural Networks", 2016), for the convs whose input channels come in 16s
+// and output channels in blocks of 16 NT:
+//   - the 144 -> 144 trunk convs with the bias, the residual and (RESID_LN)
+//     the LayerNorm of the result in the epilogue: the reference's RHAG conv
+//     and conv_after_body, lg_conv3x3_winograd (gpu.rs:605, 742) then lg_add
+//     and lg_channel_layer_norm (cuda.rs:227-248, 185-191);
+//   - the head's conv_before_upsample (144 -> 64, LeakyReLU) and upsample
+//     convs (64 -> 256 into the PixelShuffle'd plane, two 128-channel column
+//     blocks), gpu.rs:622-653.
 //
 // For each 2x2 output tile with the 4x4 input patch d (rows y-1 .. y+2):
 //   Y = A^T [ U (.) V ] A,   U = G g G^T (per co, ci),   V = B^T d B (per ci)
@@ -12,19 +17,20 @@
 // MACs per tile against 4 * 9 * 144 * 144 for the direct form (2.25x fewer).
 //
 // A block owns an 8 x 16 output tile (32 Winograd tiles, two 16-wide MFMA
-// column tiles), all 144 output channels. Wave w computes the two transform
+// column tiles) and 16 NT output channels. Wave w computes the two transform
 // points xi = 2w, 2w + 1 (B^T row i = w / 2, columns j = 2 (w % 2) + {0, 1}),
-// accumulating M[xi] (co 144 x tile 32) in 144 registers per lane. Input
-// channels go in 9 chunks of 16: the chunk's 10 x 18 halo patch is staged
+// accumulating M[xi] (co 16 NT x tile 32) in 16 NT registers per lane (144
+// for the trunk convs). Input channels go in chunks of 16: the chunk's
+// 10 x 18 halo patch is staged
 // in LDS (global_load_lds, double-buffered, channel-quad-major); each lane
 // forms V for its
 // (tile, four channels) from the patch and feeds it to the MFMAs as the B
-// operand. U (pre-transformed on the host, 1.33 MB, L2-resident) streams
+// operand. U (pre-transformed on the host, 1.33 MB at 144 -> 144, L2-resident) streams
 // from global memory as the A operand, two steps ahead of its MFMAs.
 //
 // Epilogue, per 16-channel slice: the waves write their M slices to LDS, then
 // each thread forms the 2x2 outputs of one (tile, channel) from the 16 points.
-// A thread ends with 4 pixels x 9 channels; the 16 lanes of a tile hold a
+// A thread ends with 4 pixels x NT channels; the 16 lanes of a tile hold a
 // pixel's 144 channels, reducing the LayerNorm statistics with shuffles.
 //
 // Included after gemm.hip in the one translation unit.
@@ -37,12 +43,19 @@
 #define WG_SLOTS 768                       // float4 slots per patch buffer (720 used)
 #define WG_MS 20                           // LDS row stride of an M slice entry (16 used)
 
-template <int EPI>
+// NT: output channel tiles per block (column block blockIdx.y), NTT: all of
+// them (the U layout), NKC: 16-channel input chunks. EPI selects a residual
+// epilogue (EPI_RESID, EPI_RESID_LN; NT = NTT = 9) when HEAD is -1, else
+// HEAD = CEPI_STORE (LeakyReLU 0.01) or CEPI_SHUFFLE (into the shuffled plane,
+// channels pre-permuted as for the direct convs).
+template <int NT, int NTT, int NKC, int EPI, int HEAD>
 __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 {
-    constexpr int C = 144, NT = C / 16, NKC = C / 16;
-    constexpr bool LN = EPI == EPI_RESID_LN;
-    static_assert(EPI == EPI_RESID || EPI == EPI_RESID_LN, "residual epilogues only");
+    constexpr int C = 144;  // the residual epilogues' row width
+    constexpr bool LN = HEAD < 0 && EPI == EPI_RESID_LN;
+    static_assert(HEAD == CEPI_STORE || HEAD == CEPI_SHUFFLE || EPI == EPI_RESID || EPI == EPI_RESID_LN,
+                  "residual, store or shuffle epilogues");
+    static_assert(HEAD >= 0 || (NT == 9 && NTT == 9), "the residual epilogues cover 144 channels");
     __shared__ __attribute__((aligned(16))) float Pb0[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Pb1[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Ms0[16 * 32 * WG_MS];
@@ -59,9 +72,10 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     const int y0 = (blockIdx.x / tiles_x) * WG_TH;
     const int x0 = (blockIdx.x % tiles_x) * WG_TW;
 
-    for (int i = tid; i < (LN ? 3 : 1) * C; i += 512) {
-        const float* src = i < C ? p.bias : (i < 2 * C ? p.nw : p.nb);
-        Cs[i] = src[i % C];
+    const int cb = blockIdx.y;  // column block: channels 16 NT cb ..
+    for (int i = tid; i < (LN ? 3 : 1) * 16 * NT; i += 512) {
+        const float* src = i < 16 * NT ? p.bias + 16 * NT * cb : (i < 32 * NT ? p.nw : p.nb);
+        Cs[i] = src[i % (16 * NT)];
     }
 
     // The patch is channel-quad-major: float4 slot q * 180 + pix holds
@@ -93,9 +107,10 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 
     // U, pre-arranged as [kc][xi][nt][lane] float4: lane (r, g) of step (e, nt)
     // holds U[2w + e][16 nt + r][16 kc + 4 g .. +3], the MFMA A operand.
-    const float* ubase = p.wu + (size_t)(2 * wave) * NT * 256 + lane * 4;
+    const float* ubase = p.wu + ((size_t)(2 * wave) * NTT + NT * cb) * 256 + lane * 4;
     auto ldu = [&](int kc, int t) -> f32x4 {
-        return *(const f32x4*)(ubase + ((size_t)kc * 16 * NT + t) * 256);
+        const int e = t / NT, nt = t - e * NT;
+        return *(const f32x4*)(ubase + ((size_t)(kc * 16 + e) * NTT + nt) * 256);
     };
 
     // The lane's B^T row / column pattern: R(col) = d[ra][col] + sr d[rb][col],
@@ -130,14 +145,14 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 #pragma unroll
             for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    f32x4 ur[3];
+    f32x4 ur[2];
     fetch(0, CInt<0>{});
     ur[0] = ldu(0, 0);
     ur[1] = ldu(0, 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    // Chunk kc from patch buffer Q; U steps t = e * 9 + nt, the load of step
+    // Chunk kc from patch buffer Q; U steps t = e * NT + nt, the load of step
     // t + 2 (the next chunk's first two at the end) issued ahead of step t.
     auto chunk = [&](int kc, auto bufc, auto lastc) {
         constexpr int Q = decltype(bufc)::value;
@@ -159,11 +174,13 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         const int kn = LAST ? kc : kc + 1;
 #pragma unroll
         for (int t = 0; t < 2 * NT; ++t) {
-            ur[(t + 2) % 3] = t + 2 < 2 * NT ? ldu(kc, t + 2) : ldu(kn, t + 2 - 2 * NT);
+            // step t's operand out of its slot, step t + 2's load into it (the
+            // step count per chunk is even, so slot t % 2 lines up across chunks)
+            const f32x4 u = ur[t % 2];
+            ur[t % 2] = t + 2 < 2 * NT ? ldu(kc, t + 2) : ldu(kn, t + 2 - 2 * NT);
             if (!LAST && t == 0) fetch(kc + 1, CInt<Q ^ 1>{});
             __builtin_amdgcn_sched_barrier(0);
             const int e = t / NT, nt = t - e * NT;
-            const f32x4 u = ur[t % 3];
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -173,12 +190,16 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         __syncthreads();
     };
 #pragma unroll 1
-    for (int kc = 0; kc < NKC - 1; kc += 2) {
+    for (int kc = 0; kc + 2 < NKC; kc += 2) {
         chunk(kc, CInt<0>{}, CInt<0>{});
         chunk(kc + 1, CInt<1>{}, CInt<0>{});
     }
-    static_assert(NKC % 2 == 1, "the last chunk sits in buffer 0");
-    chunk(NKC - 1, CInt<0>{}, CInt<1>{});
+    if constexpr (NKC % 2 == 1) {
+        chunk(NKC - 1, CInt<0>{}, CInt<1>{});
+    } else {
+        chunk(NKC - 2, CInt<0>{}, CInt<0>{});
+        chunk(NKC - 1, CInt<1>{}, CInt<1>{});
+    }
 
     // ---- epilogue. Thread (tile = tid / 16, c = tid % 16): outputs of tile
     // (ty, tx) for channels 16 nt + c.
@@ -193,7 +214,8 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         float* Ms = decltype(bufc)::value ? Ms1 : Ms0;
         // the slice's residual, loaded under the barrier and the transforms
 #pragma unroll
-        for (int q = 0; q < 4; ++q) y[nt][q] = p.res[pix0 + (q >> 1) * prow + (q & 1) * C + nt * 16 + ec];
+        for (int q = 0; q < 4; ++q)
+            y[nt][q] = HEAD < 0 ? p.res[pix0 + (q >> 1) * prow + (q & 1) * C + nt * 16 + ec] : 0.0f;
 #pragma unroll
         for (int e = 0; e < 2; ++e)
 #pragma unroll
@@ -216,11 +238,35 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         y[nt][3] += (t1[1] - t1[2] - t1[3]) + bias;
     };
 #pragma unroll
-    for (int nt = 0; nt < NT - 1; nt += 2) {
+    for (int nt = 0; nt + 1 < NT; nt += 2) {
         out_slice(nt, CInt<0>{});
         out_slice(nt + 1, CInt<1>{});
     }
-    out_slice(NT - 1, CInt<0>{});
+    if constexpr (NT % 2 == 1) out_slice(NT - 1, CInt<0>{});
+
+    if constexpr (HEAD >= 0) {
+        // Channel o = 16 NT cb + 16 nt + c of pixel (y, x): CEPI_STORE writes it
+        // there (LeakyReLU 0.01); CEPI_SHUFFLE writes o = (i r + jj) Cf + c' to
+        // pixel (y r + i, x r + jj), channel c' of the r-times larger plane.
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int o = 16 * NT * cb + 16 * nt + ec;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int yy = py + (q >> 1), xx = px + (q & 1);
+                float v = y[nt][q];
+                if (HEAD == CEPI_STORE) {
+                    v = v < 0.0f ? v * 0.01f : v;
+                    p.out[(yy * W + xx) * p.co_stride + o] = v;
+                } else {
+                    const int r = p.r, Cf = p.CO / (r * r);
+                    const int sub = o / Cf, c = o - sub * Cf, i = sub / r, jj = sub - i * r;
+                    p.out[((yy * r + i) * (W * r) + xx * r + jj) * p.co_stride + c] = v;
+                }
+            }
+        }
+        return;
+    }
 
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -257,9 +303,19 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid_ln(ConvArgs p)
 {
-    convwino_body<EPI_RESID_LN>(p);
+    convwino_body<9, 9, 9, EPI_RESID_LN, -1>(p);
 }
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid(ConvArgs p)
 {
-    convwino_body<EPI_RESID>(p);
+    convwino_body<9, 9, 9, EPI_RESID, -1>(p);
+}
+// conv_before_upsample: 144 -> 64, LeakyReLU
+extern "C" __global__ __launch_bounds__(512) void hat_convwino_n4_store(ConvArgs p)
+{
+    convwino_body<4, 4, 9, EPI_STORE, CEPI_STORE>(p);
+}
+// upsample convs: 64 -> 256 in two 128-channel column blocks, PixelShuffle(2)
+extern "C" __global__ __launch_bounds__(512) void hat_convwino_n8_shuffle(ConvArgs p)
+{
+    convwino_body<8, 16, 4, EPI_STORE, CEPI_SHUFFLE>(p);
 }

@@ -634,7 +634,7 @@ int gpu_selftest(std::string* err)
                 int CIp = 0, COp = 0;
                 std::vector<float> pk = pack_conv(w.data(), b.data(), CO, c.CI, 0, &bias, &CIp, &COp);
                 Dev din(in), dw(pk), db(bias), dres(res), dnw(nw), dnb(nb), dxn((size_t)HW * CO);
-                Dev dwu(c.wino ? pack_wino(w.data(), CO, c.CI) : std::vector<float>(4, 0.0f));
+                Dev dwu(c.wino ? pack_wino(w.data(), CO, c.CI, 0) : std::vector<float>(4, 0.0f));
                 ConvArgs p{};
                 p.in = din.p;
                 p.w = dw.p;
@@ -836,6 +836,21 @@ int gpu_selftest(std::string* err)
                     check_close(std::string(wide) + " partial sums", dpart2.get(), ps, 5e-4);
                 }
                 note(std::string(wide) + "  " + cc.what + "  32x48");
+            }
+            // The Winograd kernels serve conv_before_upsample and the x2 upsample
+            // convs (8 x 16 tiles; the shuffle in two 128-channel column blocks).
+            const char* wino = cc.epi == CEPI_STORE && cc.act == 2 && cc.CI == 144 && cc.CO == 64
+                                   ? "hat_convwino_n4_store"
+                               : cc.epi == CEPI_SHUFFLE && cc.r == 2 && cc.CI == 64 && cc.CO == 256
+                                   ? "hat_convwino_n8_shuffle"
+                                   : nullptr;
+            if (wino) {
+                Dev dwu(pack_wino(w.data(), cc.CO, cc.CI, cc.r)), dout4(out_n);
+                p.out = dout4.p;
+                p.wu = dwu.p;
+                launch(s, wino, (W / 16) * (H / 8), cc.CO / 128 > 1 ? cc.CO / 128 : 1, 1, 512, p);
+                check_close(std::string(wino) + " " + cc.what, dout4.get(), want, 5e-5);
+                note(std::string(wino) + "  " + cc.what + "  32x48");
             }
             // conv_last by per-tap products: 16 x 32 tiles, so W = 48 leaves a
             // half tile whose pixels past W are zero halo and are not stored.
