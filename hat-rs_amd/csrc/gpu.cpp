@@ -510,6 +510,8 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
 // xn = LN(out)) or EPI_RESID. out may alias res; in, out and xn must not overlap.
 bool convw_fits(const DevConv& C) { return C.r == 0 && C.CO == 144 && C.COp == 144; }
 
+void run_ln(hipStream_t s, const float* x, float* y, const float* w, const float* b, long rows, int C);
+
 void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride, int H, int W,
                float* out, int epi, const float* res, float* xn, const float* nw, const float* nb)
 {
@@ -544,12 +546,13 @@ void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride,
     p.eps = 1e-5f;
     p.wu = C.wu;
     // The 144 -> 144 residual convs by Winograd F(2x2, 3x3): 8 x 16 output
-    // tiles, 32-bit element offsets into the input plane.
+    // tiles, 32-bit element offsets into the input plane. The RHAG conv's
+    // LayerNorm follows as its own HBM-bound pass over the just-written rows.
     if (C.wu && C.CI == 144 && (epi == EPI_RESID_LN || epi == EPI_RESID) && H % 8 == 0 &&
         (size_t)H * W * cin_stride < ((size_t)1 << 31)) {
         if (in == out) throw Error("convw: the output must not overlap the input");
-        launch(s, epi == EPI_RESID_LN ? "hat_convwino_resid_ln" : "hat_convwino_resid",
-               (unsigned)((W / 16) * (H / 8)), 1, 1, 512, p);
+        launch(s, "hat_convwino_resid", (unsigned)((W / 16) * (H / 8)), 1, 1, 512, p);
+        if (epi == EPI_RESID_LN) run_ln(s, out, xn, nw, nb, (long)H * W, C.CO);
         return;
     }
     launch(s, name, (unsigned)((W / 16) * (H / 16)), 1, 1, (unsigned)(waves * 64), p);

@@ -2,10 +2,13 @@
 // filtering F(2x2, 3x3) (Lavin & Gray, "Fast Algorithms for Convolutional
 // Neural Networks", 2016), for the convs whose input channels come in 16s
 // and output channels in blocks of 16 NT:
-//   - the 144 -> 144 trunk convs with the bias, the residual and (RESID_LN)
-//     the LayerNorm of the result in the epilogue: the reference's RHAG conv
-//     and conv_after_body, lg_conv3x3_winograd (gpu.rs:605, 742) then lg_add
-//     and lg_channel_layer_norm (cuda.rs:227-248, 185-191);
+//   - the 144 -> 144 trunk convs with the bias and the residual in the
+//     epilogue: the reference's RHAG conv and conv_after_body,
+//     lg_conv3x3_winograd (gpu.rs:605, 742) then lg_add (cuda.rs:227-248).
+//     The RHAG conv's LayerNorm (lg_channel_layer_norm, cuda.rs:185-191)
+//     follows as hat_layernorm: in this kernel it would run where no MFMA
+//     work overlaps it (one block per CU) and cost more than the separate,
+//     HBM-bound pass over rows still in the last-level cache;
 //   - the head's conv_before_upsample (144 -> 64, LeakyReLU) and upsample
 //     convs (64 -> 256 into the PixelShuffle'd plane, two 128-channel column
 //     blocks), gpu.rs:622-653.
@@ -30,8 +33,7 @@
 //
 // Epilogue, per 16-channel slice: the waves write their M slices to LDS, then
 // each thread forms the 2x2 outputs of one (tile, channel) from the 16 points.
-// A thread ends with 4 pixels x NT channels; the 16 lanes of a tile hold a
-// pixel's 144 channels, reducing the LayerNorm statistics with shuffles.
+// A thread ends with 4 pixels x NT channels.
 //
 // Included after gemm.hip in the one translation unit.
 
@@ -44,23 +46,22 @@
 #define WG_MS 20                           // LDS row stride of an M slice entry (16 used)
 
 // NT: output channel tiles per block (column block blockIdx.y), NTT: all of
-// them (the U layout), NKC: 16-channel input chunks. EPI selects a residual
-// epilogue (EPI_RESID, EPI_RESID_LN; NT = NTT = 9) when HEAD is -1, else
+// them (the U layout), NKC: 16-channel input chunks. EPI_RESID (NT = NTT = 9)
+// adds the bias and the residual when HEAD is -1, else
 // HEAD = CEPI_STORE (LeakyReLU 0.01) or CEPI_SHUFFLE (into the shuffled plane,
 // channels pre-permuted as for the direct convs).
 template <int NT, int NTT, int NKC, int EPI, int HEAD>
 __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 {
-    constexpr int C = 144;  // the residual epilogues' row width
-    constexpr bool LN = HEAD < 0 && EPI == EPI_RESID_LN;
-    static_assert(HEAD == CEPI_STORE || HEAD == CEPI_SHUFFLE || EPI == EPI_RESID || EPI == EPI_RESID_LN,
+    constexpr int C = 144;  // the residual epilogue's row width
+    static_assert(HEAD == CEPI_STORE || HEAD == CEPI_SHUFFLE || EPI == EPI_RESID,
                   "residual, store or shuffle epilogues");
-    static_assert(HEAD >= 0 || (NT == 9 && NTT == 9), "the residual epilogues cover 144 channels");
+    static_assert(HEAD >= 0 || (NT == 9 && NTT == 9), "the residual epilogue covers 144 channels");
     __shared__ __attribute__((aligned(16))) float Pb0[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Pb1[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Ms0[16 * 32 * WG_MS];
     __shared__ __attribute__((aligned(16))) float Ms1[16 * 32 * WG_MS];
-    __shared__ __attribute__((aligned(16))) float Cs[3 * C];
+    __shared__ __attribute__((aligned(16))) float Cs[16 * NT];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -73,10 +74,7 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     const int x0 = (blockIdx.x % tiles_x) * WG_TW;
 
     const int cb = blockIdx.y;  // column block: channels 16 NT cb ..
-    for (int i = tid; i < (LN ? 3 : 1) * 16 * NT; i += 512) {
-        const float* src = i < 16 * NT ? p.bias + 16 * NT * cb : (i < 32 * NT ? p.nw : p.nb);
-        Cs[i] = src[i % (16 * NT)];
-    }
+    for (int i = tid; i < 16 * NT; i += 512) Cs[i] = p.bias[16 * NT * cb + i];
 
     // The patch is channel-quad-major: float4 slot q * 180 + pix holds
     // channels 4q .. 4q+3 of halo pixel pix, so a lane's reads sit at one
@@ -272,39 +270,8 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int q = 0; q < 4; ++q) p.out[pix0 + (q >> 1) * prow + (q & 1) * C + nt * 16 + ec] = y[nt][q];
-    if (LN) {
-        // two-pass mean then biased variance over the 144 channels of each
-        // pixel (the 16 lanes of the tile), as cpu.rs:563-581
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            float s = 0.0f;
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) s += y[nt][q];
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o, 64);
-            const float mean = s / (float)C;
-            float v = 0.0f;
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const float d = y[nt][q] - mean;
-                v += d * d;
-            }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
-            const float rstd = 1.0f / sqrtf(v / (float)C + p.eps);
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const int co = nt * 16 + ec;
-                p.xn[pix0 + (q >> 1) * prow + (q & 1) * C + co] = (y[nt][q] - mean) * rstd * Cs[C + co] + Cs[2 * C + co];
-            }
-        }
-    }
 }
 
-extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid_ln(ConvArgs p)
-{
-    convwino_body<9, 9, 9, EPI_RESID_LN, -1>(p);
-}
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid(ConvArgs p)
 {
     convwino_body<9, 9, 9, EPI_RESID, -1>(p);

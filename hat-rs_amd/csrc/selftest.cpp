@@ -620,7 +620,6 @@ int gpu_selftest(std::string* err)
             const WCase wc[] = {{144, 144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln", CONVW_WAVES_N9_RESID_LN, false},
                                 {3, 4, 144, EPI_STORE_LN, "hat_convw_n9_store_ln", CONVW_WAVES_N9_STORE_LN, false},
                                 {144, 144, 144, EPI_RESID, "hat_convw_n9_resid", CONVW_WAVES_N9_RESID, false},
-                                {144, 144, 144, EPI_RESID_LN, "hat_convwino_resid_ln", 8, true},
                                 {144, 144, 144, EPI_RESID, "hat_convwino_resid", 8, true}};
             for (const WCase& c : wc) {
                 const int H = 32, W = 48, HW = H * W, CO = c.CO;
