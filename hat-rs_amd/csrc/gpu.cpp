@@ -485,7 +485,7 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
             return;
         }
         if (epi == CEPI_SHUFFLE && C.r == 2 && C.CO == 256 && C.CI == 64 && co_stride >= 64) {
-            launch(s, "hat_convwino_n8_shuffle", tiles, 2, 1, 512, p);
+            launch(s, "hat_convwino_n8_shuffle", 2 * tiles, 1, 1, 512, p);
             return;
         }
     }

@@ -45,7 +45,7 @@
 #define WG_SLOTS 768                       // float4 slots per patch buffer (720 used)
 #define WG_MS 20                           // LDS row stride of an M slice entry (16 used)
 
-// NT: output channel tiles per block (column block blockIdx.y), NTT: all of
+// NT: output channel tiles per block (column block cb), NTT: all of
 // them (the U layout), NKC: 16-channel input chunks. EPI_RESID (NT = NTT = 9)
 // adds the bias and the residual when HEAD is -1, else
 // HEAD = CEPI_STORE (LeakyReLU 0.01) or CEPI_SHUFFLE (into the shuffled plane,
@@ -70,10 +70,13 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     const int lg = lane >> 4;
     const int H = p.H, W = p.W;
     const int tiles_x = W / WG_TW;
-    const int y0 = (blockIdx.x / tiles_x) * WG_TH;
-    const int x0 = (blockIdx.x % tiles_x) * WG_TW;
+    // a tile's column blocks are consecutive blocks, so they read its patch
+    // from L2 at about the same time
+    constexpr int NCB = NTT / NT;
+    const int tile = (int)blockIdx.x / NCB, cb = (int)blockIdx.x - tile * NCB;
+    const int y0 = (tile / tiles_x) * WG_TH;
+    const int x0 = (tile % tiles_x) * WG_TW;
 
-    const int cb = blockIdx.y;  // column block: channels 16 NT cb ..
     for (int i = tid; i < 16 * NT; i += 512) Cs[i] = p.bias[16 * NT * cb + i];
 
     // The patch is channel-quad-major: float4 slot q * 180 + pix holds

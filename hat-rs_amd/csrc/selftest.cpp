@@ -847,7 +847,7 @@ int gpu_selftest(std::string* err)
                 Dev dwu(pack_wino(w.data(), cc.CO, cc.CI, cc.r)), dout4(out_n);
                 p.out = dout4.p;
                 p.wu = dwu.p;
-                launch(s, wino, (W / 16) * (H / 8), cc.CO / 128 > 1 ? cc.CO / 128 : 1, 1, 512, p);
+                launch(s, wino, (W / 16) * (H / 8) * (cc.CO / 128 > 1 ? cc.CO / 128 : 1), 1, 1, 512, p);
                 check_close(std::string(wino) + " " + cc.what, dout4.get(), want, 5e-5);
                 note(std::string(wino) + "  " + cc.what + "  32x48");
             }
