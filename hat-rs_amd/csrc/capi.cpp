@@ -187,6 +187,17 @@ int hat_backend_synchronize(hat_backend* b)
     });
 }
 
+int hat_backend_hab(hat_backend* b, int stage, int block, size_t hp, size_t wp, const float* x, float* out,
+                    int iters, float* ms)
+{
+    return guard([&] {
+        if (!b || !x || !out) throw hat::Error("null argument");
+        if (hp > 65536 || wp > 65536) throw hat::Error("hab: plane too large");
+        b->b->op_hab(stage, block, (int)hp, (int)wp, x, out, iters, ms);
+        return 0;
+    });
+}
+
 size_t hat_backend_acts_bytes(const hat_backend* b) { return b ? b->b->acts_bytes() : 0; }
 size_t hat_backend_weight_bytes(const hat_backend* b) { return b ? b->b->weight_bytes() : 0; }
 void hat_backend_free(hat_backend* b) { delete b; }
@@ -214,6 +225,13 @@ int hat_verify(const hat_weights* w, const char* device, const char* fixture_pat
                        flags = u32(28);
         if (version != 1) throw hat::Error("fixture version " + std::to_string(version) + ", this engine reads 1");
         if (flags != 0) throw hat::Error("fixture flags are not zero");
+        // The backend takes and returns 3-channel planes: a fixture of any
+        // other width cannot be run, and sizing the buffers by it would read
+        // and write past them.
+        if (c != 3)
+            throw hat::Error(std::string(fixture_path) + ": a " + std::to_string(c) +
+                             "-channel fixture; the model takes 3-channel RGB input");
+        if (h == 0 || wd == 0 || scale == 0) throw hat::Error(std::string(fixture_path) + ": empty fixture");
         const size_t need = 36 + 4 * ((size_t)h * wd * c + (size_t)h * scale * wd * scale * c);
         if (b.size() != need)
             throw hat::Error(std::string(fixture_path) + ": " + std::to_string(need) + " bytes expected, " +
@@ -339,6 +357,16 @@ int hat_device_synchronize(void)
 {
     return guard([&] {
         hat::Runtime::get().sync();
+        return 0;
+    });
+}
+
+int hat_device_mem_info(size_t* free_bytes, size_t* total_bytes)
+{
+    return guard([&] {
+        if (!free_bytes || !total_bytes) throw hat::Error("null argument");
+        hat::Runtime& rt = hat::Runtime::get();
+        rt.check(rt.api().MemGetInfo(free_bytes, total_bytes), "hipMemGetInfo");
         return 0;
     });
 }

@@ -203,14 +203,24 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
 // The MLP of one block: x_out = res + fc2(gelu(fc1(a))), for EPI_RESID_LN also
 // xn = LayerNorm(x_out). One fused kernel for C = 144 (hidden 288) and
 // C = 180 (hidden 360), else fc1 and fc2 as two GEMMs through the hidden buffer.
+// The fused MLP kernels: C = 144 (hidden 288) and C = 180 (hidden 360). Other
+// shapes run fc1 and fc2 as two GEMMs through a T x hidden buffer.
+bool mlp_c144(const DevLinear& fc1, const DevLinear& fc2)
+{
+    return fc1.K == 144 && fc1.Kp == 144 && fc1.N == 288 && fc2.K == 288 && fc2.N == 144;
+}
+bool mlp_c180(const DevLinear& fc1, const DevLinear& fc2)
+{
+    return fc1.K == 180 && fc1.Kp == 192 && fc1.N == 360 && fc2.K == 360 && fc2.N == 180;
+}
+bool mlp_fused(const DevLinear& fc1, const DevLinear& fc2) { return mlp_c144(fc1, fc2) || mlp_c180(fc1, fc2); }
+
 void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const float* a, long M,
              const float* res, float* out, int epi, const GemmEpilogue& ln, float* hidden)
 {
     if (epi != EPI_RESID && epi != EPI_RESID_LN) throw Error("MLP: bad epilogue");
-    // the fused kernels: C = 144 (hidden 288) and C = 180 (hidden 360)
-    const bool c144 = fc1.K == 144 && fc1.Kp == 144 && fc1.N == 288 && fc2.K == 288 && fc2.N == 144;
-    const bool c180 = fc1.K == 180 && fc1.Kp == 192 && fc1.N == 360 && fc2.K == 360 && fc2.N == 180;
-    if (c144 || c180) {
+    const bool c144 = mlp_c144(fc1, fc2);
+    if (mlp_fused(fc1, fc2)) {
         if (M > 0x7fffffffL) throw Error("MLP: too many rows");
         MlpArgs p{};
         p.a = a;
@@ -240,6 +250,7 @@ void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const fl
         launch(s, name, (unsigned)g, 1, 1, MLP_WAVES * 64, p);
         return;
     }
+    if (!hidden) throw Error("MLP: the unfused form needs a hidden buffer");
     GemmEpilogue e = ln;
     e.res = res;
     run_gemm(s, fc1, a, fc1.K, M, hidden, fc1.N, EPI_GELU, GemmEpilogue{}, 0, 0, 0.f);
@@ -566,6 +577,12 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
     if (gate && (oca || attn_persistent(D, oca))) throw Error("attention: the CAB gate rides on SW launches only");
     if (pl.win != 16 || pl.owin != 24)
         throw Error("attention: the gfx950 kernels are built for window 16 / overlap window 24");
+    // The kernels wrap a rolled coordinate once, upward, and build the SW-MSA
+    // mask from bit 3 of the unrolled position: only the plan's half-window
+    // shift (or none) is meaningful, and the OCAB has no shift.
+    if (!(shift == 0 || (!oca && shift == pl.shift)))
+        throw Error("attention: shift " + std::to_string(shift) + " is not supported (0" +
+                    (oca ? "" : " or " + std::to_string(pl.shift)) + ")");
     const char* name = nullptr;
     if (D == 24) name = oca ? "hat_attn_oca_d24" : "hat_attn_sw_d24";
     else if (D == 30) name = oca ? "hat_attn_oca_d30" : "hat_attn_sw_d30";
@@ -793,7 +810,11 @@ void GpuBackend::ensure_plan(int h, int w)
     gate_ = A(C);
     qkv_ = A(3 * T * C);
     ao_ = A(T * C);
-    hidden_ = A(T * C * wt_.mlp_ratio);
+    // The T x hidden buffer only for MLP shapes without a fused kernel (every
+    // block of a network shares one shape).
+    const std::string b0 = "layers.0.residual_group.blocks.0.mlp.";
+    const bool fused_mlp = mlp_fused(lin_.at(b0 + "fc1"), lin_.at(b0 + "fc2"));
+    hidden_ = fused_mlp ? nullptr : A(T * C * wt_.mlp_ratio);
     // Head ping-pong: the plane at each resolution goes to alternate buffers.
     size_t need[2] = {T * (size_t)wt_.head_feat, 0};
     size_t res = 1;
@@ -997,6 +1018,49 @@ void GpuBackend::forward_device(int h, int w, const float* d_in, float* d_out)
          h * wt_.scale, w * wt_.scale);
 }
 
+void GpuBackend::op_hab(int stage, int block, int hp, int wp, const float* x, float* out, int iters,
+                        float* ms)
+{
+    if (!x || !out) throw Error("hab: null argument");
+    if (stage < 0 || stage >= (int)wt_.depths.size())
+        throw Error("hab: stage " + std::to_string(stage) + " of " + std::to_string(wt_.depths.size()));
+    if (block < 0 || block >= wt_.depths[stage])
+        throw Error("hab: block " + std::to_string(block) + " of " + std::to_string(wt_.depths[stage]) +
+                    " in stage " + std::to_string(stage));
+    if (hp <= 0 || wp <= 0 || hp % wt_.window || wp % wt_.window)
+        throw Error("hab: the plane must be a non-empty window multiple");
+    ensure_plan(hp, wp);
+    Runtime& rt = Runtime::get();
+    const HipApi& api = rt.api();
+    const long T = plan_.tokens();
+    const size_t bytes = (size_t)T * wt_.embed * sizeof(float);
+    const std::string p = "layers." + std::to_string(stage) + ".residual_group.blocks." + std::to_string(block);
+    rt.h2d(xa_, x, bytes);
+    // norm1 into xn_, then the block from xa_ into xb_. The block also writes
+    // the next norm's output into xn_; its own norm1 stands in for it.
+    auto run = [&]() {
+        layernorm(xa_, xn_, p + ".norm1", T);
+        hab(stage, block, xa_, xb_, p + ".norm1");
+    };
+    run();
+    rt.check(api.StreamSynchronize(stream_), "hab");
+    rt.d2h(out, xb_, bytes);
+    if (iters > 0 && ms) {
+        hipEvent_t a = nullptr, b = nullptr;
+        rt.check(api.EventCreate(&a), "hipEventCreate");
+        rt.check(api.EventCreate(&b), "hipEventCreate");
+        api.EventRecord(a, stream_);
+        for (int i = 0; i < iters; ++i) run();
+        api.EventRecord(b, stream_);
+        rt.check(api.EventSynchronize(b), "hab timing");
+        float e = 0.f;
+        api.EventElapsedTime(&e, a, b);
+        *ms = e / iters;
+        api.EventDestroy(a);
+        api.EventDestroy(b);
+    }
+}
+
 // Backend::forward: host [3][h][w] in, host [3][h*s][w*s] out.
 void GpuBackend::forward(int h, int w, const float* in, float* out)
 {
@@ -1063,12 +1127,19 @@ void op_swmsa(const float* x, float* out, int hp, int wp, int c, int heads, int 
               const float* qkv_w, const float* qkv_b, const float* proj_w, const float* proj_b,
               const float* table, int iters, float* ms, float* attn_ms)
 {
-    Runtime& rt = Runtime::get();
-    const HipApi& api = rt.api();
+    // Arguments are checked before the runtime is touched.
+    if (!x || !out || !qkv_w || !qkv_b || !proj_w || !proj_b || !table) throw Error("swmsa: null argument");
+    if (hp <= 0 || wp <= 0 || c <= 0 || heads <= 0) throw Error("swmsa: empty plane or no channels");
     if (c % heads) throw Error("swmsa: c must be divisible by heads");
     const int D = c / heads;
+    if (D != 24 && D != 30) throw Error("swmsa: head_dim " + std::to_string(D) + " has no kernel (24, 30)");
     Plan pl = Plan::make(hp, wp, 16, c);
     if (pl.hp != hp || pl.wp != wp) throw Error("swmsa: the plane must be a window multiple");
+    if (shift != 0 && shift != pl.shift)
+        throw Error("swmsa: shift " + std::to_string(shift) + " is not supported (0 or " +
+                    std::to_string(pl.shift) + ")");
+    Runtime& rt = Runtime::get();
+    const HipApi& api = rt.api();
     const size_t T = (size_t)hp * wp;
     hipStream_t s = nullptr;
     rt.check(api.StreamCreate(&s), "hipStreamCreate");
@@ -1109,12 +1180,17 @@ void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int m
              const float* n2b, const float* fc1_w, const float* fc1_b, const float* fc2_w,
              const float* fc2_b, int iters, float* ms, float* attn_ms)
 {
-    Runtime& rt = Runtime::get();
-    const HipApi& api = rt.api();
+    if (!x || !out || !n1w || !n1b || !qkv_w || !qkv_b || !proj_w || !proj_b || !table || !n2w || !n2b ||
+        !fc1_w || !fc1_b || !fc2_w || !fc2_b)
+        throw Error("ocab: null argument");
+    if (hp <= 0 || wp <= 0 || c <= 0 || heads <= 0 || mlp_ratio <= 0) throw Error("ocab: empty plane or no channels");
     if (c % heads) throw Error("ocab: c must be divisible by heads");
     const int D = c / heads;
+    if (D != 24 && D != 30) throw Error("ocab: head_dim " + std::to_string(D) + " has no kernel (24, 30)");
     Plan pl = Plan::make(hp, wp, 16, c);
     if (pl.hp != hp || pl.wp != wp) throw Error("ocab: the plane must be a window multiple");
+    Runtime& rt = Runtime::get();
+    const HipApi& api = rt.api();
     const size_t T = (size_t)hp * wp, hid = (size_t)c * mlp_ratio;
     hipStream_t s = nullptr;
     rt.check(api.StreamCreate(&s), "hipStreamCreate");

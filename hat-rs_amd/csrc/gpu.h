@@ -67,6 +67,11 @@ public:
     void forward(int h, int w, const float* in, float* out) override;
     // Device-resident variant: d_in [3][h][w], d_out [3][h*s][w*s].
     void forward_device(int h, int w, const float* d_in, float* d_out);
+    // HAB.forward of one block (gpu.rs:469-520 `hab`) on a window-multiple
+    // hp x wp plane: host x, out token-major [hp*wp][embed]; with the block's
+    // shift and mask when it is odd. iters > 0: *ms = mean device time of the
+    // block (its norm1 included) over that many further runs.
+    void op_hab(int stage, int block, int hp, int wp, const float* x, float* out, int iters, float* ms);
     size_t acts_bytes() const { return acts_bytes_; }
     size_t weight_bytes() const { return weight_bytes_; }
     hipStream_t stream() const { return stream_; }

@@ -411,6 +411,30 @@ void Weights::validate(const std::string& path) const
                         ", expected " + join_dims(kv.second) + " for " + variant + " at embed " +
                         std::to_string(embed));
     }
+    // The attention kernels index the bias tables by closed forms. The
+    // reference instead reads the checkpoint's index buffers, folded into the
+    // table with rem_euclid (gpu.rs:59-62), and its tests hold those buffers to
+    // its own construction (tests/parity.rs:114-149). A checkpoint whose
+    // buffers, folded the same way, differ from the closed forms describes a
+    // different network: refuse it rather than run it with other semantics.
+    const int64_t rows_sa = (2 * (int64_t)win - 1) * (2 * (int64_t)win - 1);
+    const int64_t rows_oca = ((int64_t)win + ow - 1) * ((int64_t)win + ow - 1);
+    auto fold = [](int64_t v, int64_t rows) { return ((v % rows) + rows) % rows; };
+    auto check_index = [&](const char* name, const std::vector<int64_t>& want, int64_t rows) {
+        const std::vector<int64_t> got = i64(name);
+        if (got.size() != want.size())
+            throw Error(path + ": `" + name + "` has " + std::to_string(got.size()) + " entries, expected " +
+                        std::to_string(want.size()));
+        for (size_t i = 0; i < got.size(); ++i)
+            if (fold(got[i], rows) != fold(want[i], rows))
+                throw Error(path + ": `" + name + "`[" + std::to_string(i / (win * win)) + "][" +
+                            std::to_string(i % (win * win)) + "] = " + std::to_string(got[i]) +
+                            " but the window geometry gives " + std::to_string(want[i]) + " (mod " +
+                            std::to_string(rows) + "): the checkpoint's relative-position index is not "
+                            "the one this network's attention uses");
+    };
+    check_index("relative_position_index_SA", rpi_sa_raw((int)win), rows_sa);
+    check_index("relative_position_index_OCA", rpi_oca_raw((int)win, (int)ow), rows_oca);
 }
 
 // ---------------------------------------------------------------------------

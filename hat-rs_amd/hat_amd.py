@@ -62,6 +62,8 @@ def lib():
         "hat_backend_forward_device": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
                                                  C.c_void_p]),
         "hat_backend_synchronize": (C.c_int, [C.c_void_p]),
+        "hat_backend_hab": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_size_t, C.c_size_t, _f32p, _f32p,
+                                      C.c_int, _f32p]),
         "hat_backend_acts_bytes": (C.c_size_t, [C.c_void_p]),
         "hat_backend_weight_bytes": (C.c_size_t, [C.c_void_p]),
         "hat_backend_free": (None, [C.c_void_p]),
@@ -77,6 +79,7 @@ def lib():
         "hat_memcpy_d2h": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
         "hat_device_copy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
         "hat_device_synchronize": (C.c_int, []),
+        "hat_device_mem_info": (C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
         "hat_device_name": (C.c_char_p, []),
         "hat_device_cu_count": (C.c_int, []),
         "hat_profile_begin": (C.c_int, []),
@@ -220,6 +223,16 @@ class Backend:
     def synchronize(self):
         _check(lib().hat_backend_synchronize(self.h), "synchronize")
 
+    def hab(self, stage, block, hp, wp, x, iters=0):
+        """One HAB (gpu.rs:469-520) on a token-major [hp*wp][embed] plane; returns
+        (out, mean ms over `iters` further runs)."""
+        x = f32(x).reshape(hp * wp, self.weights.embed)
+        out = np.empty_like(x)
+        ms = C.c_float(0)
+        _check(lib().hat_backend_hab(self.h, stage, block, hp, wp, _fp(x), _fp(out), iters,
+                                     C.cast(C.byref(ms), _f32p)), "hat_backend_hab")
+        return out, ms.value
+
     def acts_bytes(self):
         return lib().hat_backend_acts_bytes(self.h)
 
@@ -312,6 +325,13 @@ def device_copy(dst, src, nbytes):
     d = dst.ptr if isinstance(dst, DeviceBuffer) else dst
     s = src.ptr if isinstance(src, DeviceBuffer) else src
     _check(lib().hat_device_copy(d, s, nbytes), "device_copy")
+
+
+def device_mem_info():
+    """(free, total) device memory in bytes."""
+    fr, tot = C.c_size_t(0), C.c_size_t(0)
+    _check(lib().hat_device_mem_info(C.byref(fr), C.byref(tot)), "device_mem_info")
+    return fr.value, tot.value
 
 
 def device_name():

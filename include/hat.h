@@ -84,6 +84,14 @@ int hat_backend_forward(hat_backend *b, size_t h, size_t w, const float *in, flo
  * asynchronous on the backend's stream until hat_backend_synchronize. */
 int hat_backend_forward_device(hat_backend *b, size_t h, size_t w, const float *d_in, float *d_out);
 int hat_backend_synchronize(hat_backend *b);
+/* One HAB of the backend's network, `hab` (gpu.rs:469-520; HAB.forward,
+ * hat_arch.py:266-309): x' = x + W-MSA(norm1 x) + conv_scale * CAB(norm1 x),
+ * out = x' + MLP(norm2 x'), for layers.<stage>.residual_group.blocks.<block>,
+ * shifted and masked when the block is odd. x/out: host token-major
+ * [hp*wp][embed] on a plane whose sides are window multiples. iters > 0: *ms
+ * (if non-NULL) = mean device time of the block over that many further runs. */
+int hat_backend_hab(hat_backend *b, int stage, int block, size_t hp, size_t wp, const float *x,
+                    float *out, int iters, float *ms);
 /* Device bytes of the per-plan buffers and of the uploaded weights
  * (Acts/footprint, gpu.rs:78-290). */
 size_t hat_backend_acts_bytes(const hat_backend *b);
@@ -132,6 +140,10 @@ int hat_memcpy_d2h(void *dst, const void *src, size_t bytes);
  * also the HBM reference point the benchmark scales traffic counters by. */
 int hat_device_copy(void *dst, const void *src, size_t bytes);
 int hat_device_synchronize(void);
+/* Free and total device memory in bytes (hipMemGetInfo): the measured side
+ * of the working-set figures (the reference's free-VRAM delta,
+ * examples/bench.rs:110-184). */
+int hat_device_mem_info(size_t *free_bytes, size_t *total_bytes);
 /* Device name and compute-unit count; "" / 0 when no device. */
 const char *hat_device_name(void);
 int hat_device_cu_count(void);

@@ -9,8 +9,24 @@ import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(REPO, "tests", "golden")
+# Written by tests/golden/make_x3_checkpoint.py (generated, not committed).
+X3_CHECKPOINT = os.path.join(GOLDEN, "_gen", "hats_x3_seed5.safetensors")
 sys.path.insert(0, os.path.join(REPO, "hat-rs_amd"))
 sys.path.insert(0, os.path.join(REPO, "oracle"))
+
+
+# Parity bars.
+# CONTRACT_TOL is the reference's own `--verify` bound: worst |diff| on the [0,1]
+# image (src/main.rs:306-310). It is too loose to see a mistake deep in the
+# trunk at the seeded N(0, 0.02) weights (a zeroed bias table of one block moves
+# the HAT-S output by 3.4e-6), so the seeded whole-forward fixtures are held to
+# FWD_TOL on the worst difference and FWD_MEAN_TOL on the mean difference, which
+# tests/test_oracle_golden.py shows every planted single-block slip exceeds.
+# OP_TOL bounds the isolated ops on N(0,1) inputs.
+CONTRACT_TOL = 1e-4
+FWD_TOL = 2e-6
+FWD_MEAN_TOL = 1.5e-7
+OP_TOL = 2e-5
 
 
 def pytest_configure(config):

@@ -159,3 +159,58 @@ def test_verify_rejects_bad_fixtures(weights_dir):
     with pytest.raises(hat_amd.HatError) as e:
         hat_amd.verify(W, short)
     assert "bytes expected" in str(e.value)
+
+
+def test_verify_rejects_a_fixture_that_is_not_rgb(weights_dir):
+    """A HATF header with c != 3 is refused before anything is sized by it (the
+    backend takes 3-channel input and returns 3-channel output)."""
+    W = hat_amd.Weights(make_weights(weights_dir, "hat-s", 4, 2, [1]))
+    h, w, scale, c = 16, 16, 4, 1
+    one = str(weights_dir / "c1.hatf")
+    with open(one, "wb") as f:
+        f.write(struct.pack("<4sIIIIIIII", b"HATF", 1, h, w, c, scale, 16, 0, 0))
+        f.write(np.zeros(h * w * c + h * scale * w * scale * c, dtype="<f4").tobytes())
+    with pytest.raises(hat_amd.HatError) as e:
+        hat_amd.verify(W, one)
+    assert "3-channel" in str(e.value)
+
+
+@pytest.mark.parametrize("shift", [-8, 1, 4, 7, 9, 16, 32])
+def test_swmsa_refuses_a_shift_the_kernels_do_not_build(shift):
+    """The attention kernels roll by the plan's half window or not at all; any
+    other shift is an error raised before any device work."""
+    c, hh, ww = 144, 32, 32
+    x = np.zeros((hh * ww, c), dtype=np.float32)
+    w = [np.zeros(s, dtype=np.float32) for s in ((3 * c, c), (3 * c,), (c, c), (c,), (961, 6))]
+    with pytest.raises(hat_amd.HatError) as e:
+        hat_amd.op_swmsa(x, hh, ww, c, 6, shift, *w)
+    assert "shift" in str(e.value)
+
+
+def _tamper_i64(src, dst, name, index, value):
+    b = bytearray(open(src, "rb").read())
+    (n,) = struct.unpack("<Q", b[:8])
+    hdr = json.loads(b[8:8 + n])
+    begin = hdr[name]["data_offsets"][0]
+    struct.pack_into("<q", b, 8 + n + begin + 8 * index, value)
+    open(dst, "wb").write(bytes(b))
+
+
+@pytest.mark.parametrize("name,index,value,ok", [
+    ("relative_position_index_SA", 1000, 0, False),
+    ("relative_position_index_OCA", 5, 3, False),
+    # the same entry plus a whole table: PyTorch's indexing and the reference's
+    # rem_euclid fold (gpu.rs:59-62) read the same row, so this one is accepted
+    ("relative_position_index_OCA", 0, -280 + 1521, True),
+])
+def test_loader_checks_the_index_buffers(weights_dir, name, index, value, ok):
+    good = make_weights(weights_dir, "hat-s", 4, 2, [1])
+    assert hat_amd.Weights(good).i64("relative_position_index_OCA")[0] == -280
+    p = str(weights_dir / f"idx_{name}_{index}.safetensors")
+    _tamper_i64(good, p, name, index, value)
+    if ok:
+        hat_amd.Weights(p)
+        return
+    with pytest.raises(hat_amd.HatError) as e:
+        hat_amd.Weights(p)
+    assert name in str(e.value) and "relative-position index" in str(e.value)

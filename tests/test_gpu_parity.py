@@ -1,23 +1,30 @@
 """Parity of the MI355X path, through the C ABI, against the golden vectors of
 the upstream network and against the CPU oracle.
 
-Tolerances: whole-forward 1e-4 max |diff| on the [0,1] image (the reference's
-own bar, src/main.rs:310, README.md:29); isolated ops 2e-5 max |diff| on
-N(0,1) inputs (the reference's attention selftest uses 1e-5 against a twin in
-the kernel's own order, src/selftest.rs:49; these compare across different
-summation orders).
+Tolerances (tests/conftest.py): the seeded whole-forward fixtures are held to
+FWD_TOL (2e-6) on the worst and FWD_MEAN_TOL (1e-7) on the mean |diff| of the
+[0,1] image, bars tests/test_oracle_golden.py shows a single-block slip deep in
+the trunk exceeds; the reference's own 1e-4 (src/main.rs:310, README.md:29) is
+the `--verify` contract. Isolated ops: 2e-5 max |diff| on N(0,1) inputs (the
+reference's attention selftest uses 1e-5 against a twin in the kernel's own
+order, src/selftest.rs:49; these compare across different summation orders).
 """
 import os
 
 import numpy as np
 import pytest
 
-from conftest import GOLDEN, OCAB_NAMES, make_weights, op_input, read_hatf
+from conftest import (FWD_MEAN_TOL, FWD_TOL, GOLDEN, OCAB_NAMES, OP_TOL, X3_CHECKPOINT,
+                      make_weights, op_input, read_hatf)
 
 pytestmark = pytest.mark.gpu
 
-FWD_TOL = 1e-4
-OP_TOL = 2e-5
+
+def _fwd_ok(got, want, what):
+    d = np.abs(got - want)
+    _say(f"  {what}: worst |diff| {d.max():.3e}, mean {d.mean():.3e}")
+    assert d.max() < FWD_TOL, what
+    assert d.mean() < FWD_MEAN_TOL, what
 
 
 @pytest.fixture(scope="module")
@@ -130,12 +137,55 @@ def test_forward_matches_golden_and_oracle(hl, weights_dir, fx):
     _say(f"forward {fx['name']}")
     got = be.forward(h, w, inp)
     assert got.shape == exp.shape
-    worst = np.abs(got - exp).max()
     orc = oracle.OracleModel(wp).forward(h, w, inp)
-    worst_o = np.abs(got - orc).max()
-    _say(f"  worst |diff| vs upstream {worst:.3e}, vs oracle {worst_o:.3e}")
-    assert worst < FWD_TOL
-    assert worst_o < FWD_TOL
+    _fwd_ok(got, exp, "vs upstream")
+    _fwd_ok(got, orc, "vs oracle")
+    be.close()
+
+
+@pytest.mark.skipif(not os.path.exists(X3_CHECKPOINT),
+                    reason="the seed-5 HAT-S x3 checkpoint is generated, not committed: "
+                           "run tests/golden/make_x3_checkpoint.py in the build container")
+def test_reference_x3_fixture(hl):
+    """The reference's own whole-forward fixture, tests/data/hats_x3_48x48.bin
+    (HAT-S x3, the single-conv 3x shuffle head, a torch-seeded checkpoint rebuilt
+    from the recipe at tests/parity.rs:30-37 and converted to convert.py's
+    format), through `--verify` (hat_verify, the reference's 1e-4 contract) and
+    against the tight whole-forward bars."""
+    import oracle
+    path = os.path.join(GOLDEN, "hats_x3_48x48.bin")
+    W = hl.Weights(X3_CHECKPOINT)
+    assert W.scale == 3 and W.embed == 144
+    _say("verify hats_x3_48x48.bin (the reference's fixture)")
+    assert hl.verify(W, path) == 0
+    h, w, scale, inp, exp = read_hatf(path)
+    be = hl.Backend(W)
+    got = be.forward(h, w, inp)
+    _fwd_ok(got, exp, "vs the reference's fixture")
+    _fwd_ok(got, oracle.OracleModel(X3_CHECKPOINT).forward(h, w, inp), "vs oracle")
+    be.close()
+
+
+@pytest.mark.parametrize("variant", ["hat-s", "hat"])
+@pytest.mark.parametrize("block", [0, 1])
+def test_hab_matches_golden_and_oracle(hl, golden_manifest, weights_dir, variant, block):
+    """One whole HAB through the production path (hat-s: the folded CAB, its
+    gate in the attention launch, conv2 inside the projection's tail; hat: the
+    compress-to-60 CAB on the direct convs), unshifted (block 0) and shifted with
+    the mask (block 1), against the upstream HAB.forward and the oracle."""
+    import oracle
+    o = next(x for x in golden_manifest["ops"] if x["variant"] == variant)
+    wp = make_weights(weights_dir, o["variant"], 4, o["weight_seed"], o["depths"])
+    hh, ww, c = o["h"], o["w"], o["c"]
+    x = op_input(o["input_seed"], hh * ww, c)
+    be = hl.Backend(hl.Weights(wp))
+    _say(f"hab {variant} block {block} {hh}x{ww}")
+    got, _ = be.hab(0, block, hh, ww, x)
+    ref = np.load(os.path.join(GOLDEN, o["file"]))[f"hab{block}"]
+    orc = oracle.OracleModel(wp).hab(x, hh, ww, 0, block)
+    d_ref, d_orc = np.abs(got - ref).max(), np.abs(got - orc).max()
+    _say(f"  worst |diff| vs upstream {d_ref:.3e}, vs oracle {d_orc:.3e}")
+    assert d_ref < OP_TOL and d_orc < OP_TOL
     be.close()
 
 
@@ -182,9 +232,7 @@ def test_tiny_and_ragged_inputs_match_oracle(hl, weights_dir, variant, scale):
         _say(f"forward {variant} x{scale} {h}x{w}")
         got = be.forward(h, w, img)
         assert got.shape == (3, h * scale, w * scale)
-        worst = np.abs(got - om.forward(h, w, img)).max()
-        _say(f"  worst |diff| vs oracle {worst:.3e}")
-        assert worst < FWD_TOL
+        _fwd_ok(got, om.forward(h, w, img), "vs oracle")
     be.close()
 
 
@@ -199,73 +247,7 @@ def test_cfg1_hat_s_64_matches_oracle(hl, weights_dir):
     _say("forward HAT-S x4 64x64 (cfg1)")
     got = be.forward(64, 64, img)
     orc = oracle.OracleModel(wp).forward(64, 64, img)
-    worst = np.abs(got - orc).max()
-    _say(f"  worst |diff| vs oracle {worst:.3e}")
-    assert worst < FWD_TOL
-
-
-def test_hat_s_512_full_size(hl, weights_dir):
-    """The metric configuration itself: HAT-S x4 at 512x512, single pass. At this
-    size the oracle would take minutes, so it is checked through size-independent
-    properties: finite, bit-exact on a second run, the image mean preserved (the
-    network is a small residual on the mean-subtracted input at these weights)."""
-    wp = make_weights(weights_dir, "hat-s", 4, 1, None)
-    W = hl.Weights(wp)
-    be = hl.Backend(W)
-    rng = np.random.default_rng(512)
-    img = rng.random((3, 512, 512), dtype=np.float32)
-    _say("forward HAT-S x4 512x512")
-    y1 = be.forward(512, 512, img)
-    y2 = be.forward(512, 512, img)
-    assert y1.shape == (3, 2048, 2048)
-    assert np.isfinite(y1).all()
-    assert np.array_equal(y1, y2)
-    assert abs(float(y1.mean()) - float(img.mean())) < 0.2
-
-
-def test_cfg4_hat_full_depth(hl, weights_dir):
-    """Benchmark config 4's network, HAT x4 (C = 180, 6 stages x 6 HABs, the
-    compress-3 CAB on the unfolded path): the full depth against the oracle at
-    32x48, then the config's own size, 256x256, through the size-independent
-    properties of the 512x512 test."""
-    import oracle
-    wp = make_weights(weights_dir, "hat", 4, 4, None)
-    be = hl.Backend(hl.Weights(wp))
-    rng = np.random.default_rng(44)
-    small = rng.random((3, 32, 48), dtype=np.float32)
-    _say("forward HAT x4 32x48 (full depth) vs oracle")
-    got = be.forward(32, 48, small)
-    orc = oracle.OracleModel(wp).forward(32, 48, small)
-    worst = np.abs(got - orc).max()
-    _say(f"  worst |diff| vs oracle {worst:.3e}")
-    assert worst < FWD_TOL
-    img = rng.random((3, 256, 256), dtype=np.float32)
-    _say("forward HAT x4 256x256 (cfg4)")
-    y1 = be.forward(256, 256, img)
-    y2 = be.forward(256, 256, img)
-    assert y1.shape == (3, 1024, 1024)
-    assert np.isfinite(y1).all()
-    assert np.array_equal(y1, y2)
-    assert abs(float(y1.mean()) - float(img.mean())) < 0.2
-
-
-def test_cfg5_hat_l_512_single_pass(hl, weights_dir):
-    """Benchmark config 5: HAT-L x4 (12 stages) at 512x512 in a single pass.
-    Finite, bit-exact on a second run, the image mean preserved; the per-plan
-    working set is reported (the reference's buffers: 7.8 GiB, README.md:141)."""
-    wp = make_weights(weights_dir, "hat-l", 4, 5, None)
-    W = hl.Weights(wp)
-    be = hl.Backend(W)
-    img = np.random.default_rng(55).random((3, 512, 512), dtype=np.float32)
-    _say("forward HAT-L x4 512x512 (cfg5)")
-    y1 = be.forward(512, 512, img)
-    _say(f"  per-plan buffers {be.acts_bytes() / 2**30:.2f} GiB, weights {be.weight_bytes() / 2**20:.1f} MiB")
-    y2 = be.forward(512, 512, img)
-    assert y1.shape == (3, 2048, 2048)
-    assert np.isfinite(y1).all()
-    assert np.array_equal(y1, y2)
-    assert abs(float(y1.mean()) - float(img.mean())) < 0.2
-    assert be.acts_bytes() < 8 * 2**30
+    _fwd_ok(got, orc, "vs oracle")
 
 
 @pytest.mark.parametrize("n4", [1, 257, 4 * 256 * 16384 + 5, 9 * 256 * 16384 + 3])

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import GOLDEN, OCAB_NAMES, make_weights, op_input, read_hatf
+from conftest import (FWD_MEAN_TOL, FWD_TOL, GOLDEN, OCAB_NAMES, OP_TOL, X3_CHECKPOINT, make_weights,
+                      op_input, read_hatf)
 
 
 def _manifest():
@@ -25,7 +26,8 @@ def test_oracle_forward_matches_upstream(weights_dir, fx):
     h, w, scale, inp, exp = read_hatf(os.path.join(GOLDEN, fx["file"]))
     got = oracle.OracleModel(wp).forward(h, w, inp)
     assert got.shape == exp.shape
-    assert np.abs(got - exp).max() < 2e-6
+    d = np.abs(got - exp)
+    assert d.max() < FWD_TOL and d.mean() < FWD_MEAN_TOL
 
 
 @pytest.mark.parametrize("o", _manifest()["ops"], ids=lambda o: o["variant"])
@@ -58,3 +60,75 @@ def test_oracle_detects_a_planted_mistake(weights_dir):
     M = oracle.OracleModel(wp)
     M.arrays["layers.0.residual_group.blocks.1.attn.qkv.bias"][:] += 1e-3
     assert np.abs(M.forward(h, w, inp) - exp).max() > 1e-5
+
+
+# One deep block (stage 3, block 4) of the full-depth HAT-S fixture, slipped in
+# ways a wrong kernel could slip: each must move the output past the bars the
+# GPU's whole-forward tests use, or those tests could not see it.
+PLANTS = {
+    "zeroed SW bias table": ("layers.3.residual_group.blocks.4.attn.relative_position_bias_table",
+                             lambda a: a * 0),
+    "zeroed OCAB bias table": ("layers.3.residual_group.overlap_attn.relative_position_bias_table",
+                               lambda a: a * 0),
+    "dropped CAB conv2 weights": ("layers.3.residual_group.blocks.4.conv_block.cab.2.weight",
+                                  lambda a: a * 0),
+    "dropped CAB conv2 bias": ("layers.3.residual_group.blocks.4.conv_block.cab.2.bias", lambda a: a * 0),
+    "qkv bias +1e-3": ("layers.3.residual_group.blocks.4.attn.qkv.bias", lambda a: a + 1e-3),
+    "channel-attention gate shut": ("layers.3.residual_group.blocks.4.conv_block.cab.3.attention.3.bias",
+                                    lambda a: a - 50),
+}
+
+
+@pytest.mark.parametrize("plant", sorted(PLANTS))
+def test_forward_bars_see_a_slip_in_a_deep_block(weights_dir, plant):
+    fx = next(f for f in _manifest()["forward"] if f["name"] == "hats_x4_full_32x48")
+    wp = make_weights(weights_dir, fx["variant"], fx["scale"], fx["weight_seed"], fx["depths"])
+    h, w, scale, inp, exp = read_hatf(os.path.join(GOLDEN, fx["file"]))
+    M = oracle.OracleModel(wp)
+    name, edit = PLANTS[plant]
+    M.arrays[name][:] = edit(M.arrays[name])
+    d = np.abs(M.forward(h, w, inp) - exp)
+    print(f"{plant}: worst {d.max():.3e}, mean {d.mean():.3e}")
+    # the mean bar alone catches every one of them
+    assert d.mean() > FWD_MEAN_TOL
+
+
+HAB_PLANTS = {
+    "dropped CAB conv2 weights": ("conv_block.cab.2.weight", lambda a: a * 0),
+    "dropped CAB conv2 bias": ("conv_block.cab.2.bias", lambda a: a * 0),
+    "zeroed bias table": ("attn.relative_position_bias_table", lambda a: a * 0),
+    "channel-attention gate shut": ("conv_block.cab.3.attention.3.bias", lambda a: a - 50),
+}
+
+
+@pytest.mark.parametrize("o", _manifest()["ops"], ids=lambda o: o["variant"])
+@pytest.mark.parametrize("plant", sorted(HAB_PLANTS))
+def test_hab_bar_sees_a_slip(weights_dir, o, plant):
+    """The GPU's HAB op test compares whole blocks at OP_TOL: every slip in the
+    CAB branch (scaled by conv_scale = 0.01 in the block's output) or the bias
+    table moves that output by more than that, in both blocks."""
+    wp = make_weights(weights_dir, o["variant"], 4, o["weight_seed"], o["depths"])
+    hh, ww, c = o["h"], o["w"], o["c"]
+    x = op_input(o["input_seed"], hh * ww, c)
+    ref = np.load(os.path.join(GOLDEN, o["file"]))
+    for blk in (0, 1):
+        M = oracle.OracleModel(wp)
+        name, edit = HAB_PLANTS[plant]
+        k = f"layers.0.residual_group.blocks.{blk}." + name
+        M.arrays[k][:] = edit(M.arrays[k])
+        assert np.abs(M.hab(x, hh, ww, 0, blk) - ref[f"hab{blk}"]).max() > 5 * OP_TOL
+
+
+@pytest.mark.skipif(not os.path.exists(X3_CHECKPOINT),
+                    reason="the seed-5 HAT-S x3 checkpoint is generated, not committed: "
+                           "run tests/golden/make_x3_checkpoint.py in the build container")
+def test_oracle_matches_the_reference_x3_fixture():
+    """The reference's own whole-forward fixture (tests/data/hats_x3_48x48.bin,
+    made by its tools/make_fixture.py from a torch-seeded HAT-S x3, recipe at
+    tests/parity.rs:30-37), on the checkpoint rebuilt from that recipe."""
+    h, w, scale, inp, exp = read_hatf(os.path.join(GOLDEN, "hats_x3_48x48.bin"))
+    M = oracle.OracleModel(X3_CHECKPOINT)
+    assert (M.scale, h, w) == (3, 48, 48)
+    d = np.abs(M.forward(h, w, inp) - exp)
+    print(f"oracle vs the reference's x3 fixture: worst {d.max():.3e}, mean {d.mean():.3e}")
+    assert d.max() < FWD_TOL and d.mean() < FWD_MEAN_TOL
