@@ -177,6 +177,16 @@ int hat_backend_forward_device(hat_backend* b, size_t h, size_t w, const float* 
     });
 }
 
+int hat_backend_forward_noalloc(hat_backend* b, size_t h, size_t w, const float* d_in, float* d_out)
+{
+    return guard([&] {
+        if (!b || !d_in || !d_out) throw hat::Error("null argument");
+        if (h > 65536 || w > 65536) throw hat::Error("forward_noalloc: image too large");
+        b->b->forward_noalloc((int)h, (int)w, d_in, d_out);
+        return 0;
+    });
+}
+
 int hat_backend_synchronize(hat_backend* b)
 {
     return guard([&] {

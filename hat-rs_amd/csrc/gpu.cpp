@@ -771,50 +771,20 @@ void GpuBackend::free_plan()
     for (void* p : acts_) rt.free(p);
     acts_.clear();
     acts_bytes_ = 0;
+    a_ = Acts{};
     have_plan_ = false;
 }
 
-// Acts::new (gpu.rs:293-334): one allocation set per plan, reused by every
-// forward at that size.
-void GpuBackend::ensure_plan(int h, int w)
+// Acts::new (gpu.rs:293-334): the buffer set of one plan.
+std::vector<std::pair<float**, size_t>> GpuBackend::layout(const Plan& p, Acts& a, bool host_io) const
 {
-    Plan p = Plan::make(h, w, wt_.window, wt_.embed);
-    if (have_plan_ && p == plan_) return;
-    free_plan();
-    plan_ = p;
-    Runtime& rt = Runtime::get();
     const size_t T = (size_t)p.tokens(), C = wt_.embed;
-    auto A = [&](size_t floats) -> float* {
-        float* d = (float*)rt.alloc(floats * sizeof(float));
-        acts_.push_back(d);
-        acts_bytes_ += floats * sizeof(float);
-        return d;
-    };
-    t1_stride_ = (wt_.compressed + 3) / 4 * 4;
-    nblk_conv2_ = colsum_rows((int)C, p.hp, p.wp, (int)C);
-    x0_ = A(T * 4);
-    body_ = A(T * C);
-    xa_ = A(T * C);
-    xb_ = A(T * C);
-    xn_ = A(T * C);
-    t1_ = A(T * t1_stride_);
-    if (cab_fold_) {
-        cab_part_ = A((size_t)(p.hp / 16) * (p.wp / 16) * CAB_NSUM * CAB_CS);
-        w2g_ = A((size_t)C * CAB_K2);
-        bias2_ = A(C);
-    } else {
-        t2_ = A(T * C);
-        partial_ = A((size_t)nblk_conv2_ * C);
-        red_ = A((size_t)((nblk_conv2_ + 31) / 32) * C);
-    }
-    gate_ = A(C);
-    qkv_ = A(3 * T * C);
-    ao_ = A(T * C);
+    const size_t t1_stride = (size_t)(wt_.compressed + 3) / 4 * 4;
+    const size_t nblk = (size_t)colsum_rows((int)C, p.hp, p.wp, (int)C);
     // The T x hidden buffer only for MLP shapes without a fused kernel (every
     // block of a network shares one shape).
     const std::string b0 = "layers.0.residual_group.blocks.0.mlp.";
     const bool fused_mlp = mlp_fused(lin_.at(b0 + "fc1"), lin_.at(b0 + "fc2"));
-    hidden_ = fused_mlp ? nullptr : A(T * C * wt_.mlp_ratio);
     // Head ping-pong: the plane at each resolution goes to alternate buffers.
     size_t need[2] = {T * (size_t)wt_.head_feat, 0};
     size_t res = 1;
@@ -824,11 +794,49 @@ void GpuBackend::ensure_plan(int h, int w)
         which ^= 1;
         need[which] = std::max(need[which], T * res * (size_t)wt_.head_feat);
     }
-    head0_ = A(need[0]);
-    head1_ = A(std::max<size_t>(need[1], 4));
     const size_t s2 = (size_t)wt_.scale * wt_.scale;
-    din_ = A(3 * (size_t)h * w);
-    dout_ = A(3 * (size_t)h * w * s2);
+    return {
+        {&a.x0, T * 4},
+        {&a.body, T * C},
+        {&a.xa, T * C},
+        {&a.xb, T * C},
+        {&a.xn, T * C},
+        {&a.t1, T * t1_stride},
+        {&a.cab_part, cab_fold_ ? (size_t)(p.hp / 16) * (p.wp / 16) * CAB_NSUM * CAB_CS : 0},
+        {&a.w2g, cab_fold_ ? C * CAB_K2 : 0},
+        {&a.bias2, cab_fold_ ? C : 0},
+        {&a.t2, cab_fold_ ? 0 : T * C},
+        {&a.partial, cab_fold_ ? 0 : nblk * C},
+        {&a.red, cab_fold_ ? 0 : (nblk + 31) / 32 * C},
+        {&a.gate, C},
+        {&a.qkv, 3 * T * C},
+        {&a.ao, T * C},
+        {&a.hidden, fused_mlp ? 0 : T * C * wt_.mlp_ratio},
+        {&a.head0, need[0]},
+        {&a.head1, std::max<size_t>(need[1], 4)},
+        {&a.din, host_io ? 3 * (size_t)p.h * p.w : 0},
+        {&a.dout, host_io ? 3 * (size_t)p.h * p.w * s2 : 0},
+    };
+}
+
+// One allocation set per plan, reused by every forward at that size.
+void GpuBackend::ensure_plan(int h, int w)
+{
+    Plan p = Plan::make(h, w, wt_.window, wt_.embed);
+    if (have_plan_ && p == plan_) return;
+    free_plan();
+    plan_ = p;
+    Runtime& rt = Runtime::get();
+    t1_stride_ = (wt_.compressed + 3) / 4 * 4;
+    nblk_conv2_ = colsum_rows(wt_.embed, p.hp, p.wp, wt_.embed);
+    a_ = Acts{};
+    for (auto& b : layout(p, a_, true)) {
+        if (b.second == 0) continue;
+        float* d = (float*)rt.alloc(b.second * sizeof(float));
+        acts_.push_back(d);
+        acts_bytes_ += b.second * sizeof(float);
+        *b.first = d;
+    }
     have_plan_ = true;
 }
 
@@ -853,17 +861,17 @@ void GpuBackend::gemm(const DevLinear& L, const float* a, int lda, long M, float
     run_gemm(stream_, L, a, lda, M, out, ldo, epi, e, wt_.heads, wt_.head_dim, wt_.conv_scale);
 }
 
-// x = x + fc2(gelu(fc1(xn_))), in place; with a norm also xn_ = norm(x).
+// x = x + fc2(gelu(fc1(a_.xn))), in place; with a norm also a_.xn = norm(x).
 void GpuBackend::mlp(const std::string& prefix, float* x, int epi, const std::string& norm)
 {
     GemmEpilogue e;
     if (!norm.empty()) {
-        e.xn = xn_;
+        e.xn = a_.xn;
         e.nw = raw_.at(norm + ".weight");
         e.nb = raw_.at(norm + ".bias");
     }
-    run_mlp(stream_, lin_.at(prefix + ".fc1"), lin_.at(prefix + ".fc2"), xn_, plan_.tokens(), x, x, epi,
-            e, hidden_);
+    run_mlp(stream_, lin_.at(prefix + ".fc1"), lin_.at(prefix + ".fc2"), a_.xn, plan_.tokens(), x, x, epi,
+            e, a_.hidden);
 }
 
 void GpuBackend::conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
@@ -877,13 +885,13 @@ void GpuBackend::conv(const DevConv& C, const float* in, int cin_stride, int H, 
 void GpuBackend::attention(const std::string& table, bool oca, int shift, const CabGateArgs* gate,
                            const SeArgs* se)
 {
-    run_attn(stream_, qkv_, raw_.at(table), ao_, plan_, wt_.heads, wt_.head_dim, oca, shift, gate, se);
+    run_attn(stream_, a_.qkv, raw_.at(table), a_.ao, plan_, wt_.heads, wt_.head_dim, oca, shift, gate, se);
 }
 
 // HAB.forward (hat_arch.py:266-309; cpu.rs:1090-1166):
 //   x = shortcut + attn(norm1 x) + conv_x * conv_scale;  x = x + mlp(norm2 x)
-// On entry xn_ holds norm1(x_in); on exit x_out holds the block's result and
-// xn_ holds next_norm(x_out), the input of whatever block follows.
+// On entry a_.xn holds norm1(x_in); on exit x_out holds the block's result and
+// a_.xn holds next_norm(x_out), the input of whatever block follows.
 void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std::string& next_norm)
 {
     const std::string p = "layers." + std::to_string(stage) + ".residual_group.blocks." +
@@ -895,54 +903,54 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
         // launch (its first block), conv2 inside the tail's projection.
         const DevLinear& proj = lin_.at(p + ".attn.proj");
         CabGateArgs gate{};
-        run_cab(stream_, cab_.at(p), xn_, H, W, proj.b, wt_.conv_scale, wt_.squeezed, t1_, cab_part_,
-                w2g_, bias2_, gate_, &gate);
-        gemm(lin_.at(p + ".attn.qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
+        run_cab(stream_, cab_.at(p), a_.xn, H, W, proj.b, wt_.conv_scale, wt_.squeezed, a_.t1, a_.cab_part,
+                a_.w2g, a_.bias2, a_.gate, &gate);
+        gemm(lin_.at(p + ".attn.qkv"), a_.xn, C, T, a_.qkv, 0, EPI_QKV);
         attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, &gate);
-        run_hab_tail(stream_, proj, lin_.at(p + ".mlp.fc1"), lin_.at(p + ".mlp.fc2"), ao_, x_in, x_out, xn_, t1_,
-                     w2g_, bias2_, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
+        run_hab_tail(stream_, proj, lin_.at(p + ".mlp.fc1"), lin_.at(p + ".mlp.fc2"), a_.ao, x_in, x_out, a_.xn, a_.t1,
+                     a_.w2g, a_.bias2, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
                      raw_.at(next_norm + ".weight"), raw_.at(next_norm + ".bias"), H, W);
         return;
     }
     // CAB: conv3x3 -> GELU -> conv3x3 (+ per-tile channel sums) -> gate.
-    conv(conv_.at(p + ".conv_block.cab.0"), xn_, C, H, W, t1_, t1_stride_, CEPI_STORE, 1);
-    conv(conv_.at(p + ".conv_block.cab.2"), t1_, t1_stride_, H, W, t2_, C, CEPI_COLSUM, 0, nullptr,
-         partial_);
+    conv(conv_.at(p + ".conv_block.cab.0"), a_.xn, C, H, W, a_.t1, t1_stride_, CEPI_STORE, 1);
+    conv(conv_.at(p + ".conv_block.cab.2"), a_.t1, t1_stride_, H, W, a_.t2, C, CEPI_COLSUM, 0, nullptr,
+         a_.partial);
     // The gate: computed by the attention launch's first block where it fits.
     SeArgs se{};
-    run_se(stream_, partial_, nblk_conv2_, C, red_, (float)T,
+    run_se(stream_, a_.partial, nblk_conv2_, C, a_.red, (float)T,
            raw_.at(p + ".conv_block.cab.3.attention.1.weight"),
            raw_.at(p + ".conv_block.cab.3.attention.1.bias"),
            raw_.at(p + ".conv_block.cab.3.attention.3.weight"),
-           raw_.at(p + ".conv_block.cab.3.attention.3.bias"), wt_.squeezed, gate_, &se);
+           raw_.at(p + ".conv_block.cab.3.attention.3.bias"), wt_.squeezed, a_.gate, &se);
     // Window attention, the roll and the partition folded into its addressing;
     // proj's epilogue adds the shortcut and the gated conv branch, then norm2.
-    gemm(lin_.at(p + ".attn.qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
+    gemm(lin_.at(p + ".attn.qkv"), a_.xn, C, T, a_.qkv, 0, EPI_QKV);
     attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, nullptr, &se);
-    gemm(lin_.at(p + ".attn.proj"), ao_, C, T, x_out, C, EPI_HAB_LN, x_in, t2_, gate_, xn_,
+    gemm(lin_.at(p + ".attn.proj"), a_.ao, C, T, x_out, C, EPI_HAB_LN, x_in, a_.t2, a_.gate, a_.xn,
          p + ".norm2");
     mlp(p + ".mlp", x_out, EPI_RESID_LN, next_norm);
 }
 
 // OCAB.forward (hat_arch.py:392-438; cpu.rs:1170-1198): x = proj(attn) + x;
-// x = x + mlp(norm2 x). On entry xn_ holds norm1(x).
+// x = x + mlp(norm2 x). On entry a_.xn holds norm1(x).
 void GpuBackend::ocab(int stage, float* x)
 {
     const std::string p = "layers." + std::to_string(stage) + ".residual_group.overlap_attn";
     const long T = plan_.tokens();
     const int C = wt_.embed;
-    gemm(lin_.at(p + ".qkv"), xn_, C, T, qkv_, 0, EPI_QKV);
+    gemm(lin_.at(p + ".qkv"), a_.xn, C, T, a_.qkv, 0, EPI_QKV);
     attention(p + ".relative_position_bias_table", true, 0);
     const DevLinear& proj = lin_.at(p + ".proj");
     const DevLinear &fc1 = lin_.at(p + ".mlp.fc1"), &fc2 = lin_.at(p + ".mlp.fc2");
     if (hab_tail_fits(proj, fc1, fc2)) {
         // projection + shortcut + norm2 + MLP + residual in one kernel
-        run_hab_tail(stream_, proj, fc1, fc2, ao_, x, x, nullptr, nullptr,
+        run_hab_tail(stream_, proj, fc1, fc2, a_.ao, x, x, nullptr, nullptr,
                      nullptr, proj.b, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"), nullptr, nullptr,
                      plan_.hp, plan_.wp);
         return;
     }
-    gemm(proj, ao_, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, xn_, p + ".norm2");
+    gemm(proj, a_.ao, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, a_.xn, p + ".norm2");
     mlp(p + ".mlp", x, EPI_RESID, "");
 }
 
@@ -952,59 +960,121 @@ void GpuBackend::forward_device(int h, int w, const float* d_in, float* d_out)
 {
     if (h <= 0 || w <= 0) throw Error(std::to_string(h) + "x" + std::to_string(w) + " is empty");
     ensure_plan(h, w);
+    run_forward(h, w, d_in, d_out);
+}
+
+size_t GpuBackend::noalloc_bytes(int h, int w) const
+{
+    if (h <= 0 || w <= 0) throw Error(std::to_string(h) + "x" + std::to_string(w) + " is empty");
+    Acts a;
+    size_t off = 0;
+    for (auto& b : layout(Plan::make(h, w, wt_.window, wt_.embed), a, false))
+        if (b.second) off += (b.second * sizeof(float) + 255) / 256 * 256;
+    return off;
+}
+
+// forward_device with the per-plan buffers carved, 256-byte aligned, from the
+// scratch array the code object holds (hipModuleGetGlobal at start-up), in
+// place of the plan's own allocations, which are left as they are.
+void GpuBackend::forward_noalloc(int h, int w, const float* d_in, float* d_out)
+{
+    if (h <= 0 || w <= 0) throw Error(std::to_string(h) + "x" + std::to_string(w) + " is empty");
+    if (!d_in || !d_out) throw Error("null argument");
+    Runtime& rt = Runtime::get();
+    const Plan p = Plan::make(h, w, wt_.window, wt_.embed);
+    // 64 KiB of the array stay unused past the last buffer, so no buffer ends
+    // at the array's end.
+    const size_t need = noalloc_bytes(h, w), cap = rt.scratch_bytes() - (64u << 10);
+    if (need > cap) {
+        char m[192];
+        snprintf(m, sizeof m, "forward_noalloc: a %dx%d forward needs %.1f MiB of scratch; the library's "
+                 "fixed array holds %.1f MiB", h, w, need / 1048576.0, cap / 1048576.0);
+        throw Error(m);
+    }
+    Acts a;
+    char* base = (char*)rt.scratch();
+    size_t off = 0;
+    for (auto& b : layout(p, a, false)) {
+        if (b.second == 0) continue;
+        *b.first = (float*)(base + off);
+        off += (b.second * sizeof(float) + 255) / 256 * 256;
+    }
+    const Acts saved = a_;
+    const Plan saved_plan = plan_;
+    const int saved_nblk = nblk_conv2_;
+    a_ = a;
+    plan_ = p;
+    t1_stride_ = (wt_.compressed + 3) / 4 * 4;
+    nblk_conv2_ = colsum_rows(wt_.embed, p.hp, p.wp, wt_.embed);
+    try {
+        run_forward(h, w, d_in, d_out);
+    } catch (...) {
+        a_ = saved;
+        plan_ = saved_plan;
+        nblk_conv2_ = saved_nblk;
+        throw;
+    }
+    a_ = saved;
+    plan_ = saved_plan;
+    nblk_conv2_ = saved_nblk;
+}
+
+// The forward on the current plan's buffers (a_, plan_).
+void GpuBackend::run_forward(int h, int w, const float* d_in, float* d_out)
+{
     const long T = plan_.tokens();
     const int C = wt_.embed, H = plan_.hp, W = plan_.wp;
-    PreArgs pa{d_in, x0_, h, w, H, W, 4, wt_.mean[0], wt_.mean[1], wt_.mean[2], wt_.img_range};
+    PreArgs pa{d_in, a_.x0, h, w, H, W, 4, wt_.mean[0], wt_.mean[1], wt_.mean[2], wt_.img_range};
     launch(stream_, "hat_pre", (unsigned)((T + 255) / 256), 1, 1, 256, pa);
     const DevConv& cf = conv_.at("conv_first");
     // With 144 channels the trunk convs carry the LayerNorm that follows them.
     const bool fused = convw_fits(cf);
     if (fused) {
-        run_convw(stream_, cf, x0_, 4, H, W, body_, EPI_STORE_LN, nullptr, xa_,
+        run_convw(stream_, cf, a_.x0, 4, H, W, a_.body, EPI_STORE_LN, nullptr, a_.xa,
                   raw_.at("patch_embed.norm.weight"), raw_.at("patch_embed.norm.bias"));
     } else {
-        conv(cf, x0_, 4, H, W, body_, C, CEPI_STORE, 0);
-        layernorm(body_, xa_, "patch_embed.norm", T);
+        conv(cf, a_.x0, 4, H, W, a_.body, C, CEPI_STORE, 0);
+        layernorm(a_.body, a_.xa, "patch_embed.norm", T);
     }
     const size_t S = wt_.depths.size();
     for (size_t s = 0; s < S; ++s) {
         // RHAG (gpu.rs:592-610): conv3x3(blocks(x)) + x, with the stage input
-        // kept in xa_ and the blocks working in xb_. Each block's last GEMM
-        // leaves the next block's norm1 in xn_; the first block's comes from
+        // kept in a_.xa and the blocks working in a_.xb. Each block's last GEMM
+        // leaves the next block's norm1 in a_.xn; the first block's comes from
         // the previous stage's conv (or its own pass).
         const std::string L = "layers." + std::to_string(s) + ".residual_group.";
-        if (!fused || s == 0) layernorm(xa_, xn_, L + "blocks.0.norm1", T);
+        if (!fused || s == 0) layernorm(a_.xa, a_.xn, L + "blocks.0.norm1", T);
         for (int b = 0; b < wt_.depths[s]; ++b) {
             const std::string next = b + 1 < wt_.depths[s]
                                          ? L + "blocks." + std::to_string(b + 1) + ".norm1"
                                          : L + "overlap_attn.norm1";
-            hab((int)s, b, b == 0 ? xa_ : xb_, xb_, next);
+            hab((int)s, b, b == 0 ? a_.xa : a_.xb, a_.xb, next);
         }
-        ocab((int)s, xb_);
+        ocab((int)s, a_.xb);
         const DevConv& rc = conv_.at("layers." + std::to_string(s) + ".conv");
         if (fused) {
             // x = conv(blocks) + x, then the next stage's norm1 or the final
-            // norm into xn_ (xb_, the conv's input, is still being read).
+            // norm into a_.xn (a_.xb, the conv's input, is still being read).
             const std::string nn = s + 1 < S ? "layers." + std::to_string(s + 1) + ".residual_group.blocks.0.norm1"
                                              : std::string("norm");
-            run_convw(stream_, rc, xb_, C, H, W, xa_, EPI_RESID_LN, xa_, xn_, raw_.at(nn + ".weight"),
+            run_convw(stream_, rc, a_.xb, C, H, W, a_.xa, EPI_RESID_LN, a_.xa, a_.xn, raw_.at(nn + ".weight"),
                       raw_.at(nn + ".bias"));
         } else {
-            conv(rc, xb_, C, H, W, xa_, C, CEPI_RESID, 0, xa_);
+            conv(rc, a_.xb, C, H, W, a_.xa, C, CEPI_RESID, 0, a_.xa);
         }
     }
     if (fused) {
-        run_convw(stream_, conv_.at("conv_after_body"), xn_, C, H, W, xa_, EPI_RESID, body_, nullptr,
+        run_convw(stream_, conv_.at("conv_after_body"), a_.xn, C, H, W, a_.xa, EPI_RESID, a_.body, nullptr,
                   nullptr, nullptr);
     } else {
-        layernorm(xa_, xb_, "norm", T);
-        conv(conv_.at("conv_after_body"), xb_, C, H, W, xa_, C, CEPI_RESID, 0, body_);
+        layernorm(a_.xa, a_.xb, "norm", T);
+        conv(conv_.at("conv_after_body"), a_.xb, C, H, W, a_.xa, C, CEPI_RESID, 0, a_.body);
     }
     // Head (gpu.rs:622-653): conv + LeakyReLU, [conv + PixelShuffle] per block, conv_last.
     const int feat = wt_.head_feat;
-    conv(conv_.at("conv_before_upsample.0"), xa_, C, H, W, head0_, feat, CEPI_STORE, 2);
-    float* cur = head0_;
-    float* nxt = head1_;
+    conv(conv_.at("conv_before_upsample.0"), a_.xa, C, H, W, a_.head0, feat, CEPI_STORE, 2);
+    float* cur = a_.head0;
+    float* nxt = a_.head1;
     int hh = H, ww = W;
     const auto blocks = wt_.up_blocks();
     for (size_t b = 0; b < blocks.size(); ++b) {
@@ -1035,16 +1105,16 @@ void GpuBackend::op_hab(int stage, int block, int hp, int wp, const float* x, fl
     const long T = plan_.tokens();
     const size_t bytes = (size_t)T * wt_.embed * sizeof(float);
     const std::string p = "layers." + std::to_string(stage) + ".residual_group.blocks." + std::to_string(block);
-    rt.h2d(xa_, x, bytes);
-    // norm1 into xn_, then the block from xa_ into xb_. The block also writes
-    // the next norm's output into xn_; its own norm1 stands in for it.
+    rt.h2d(a_.xa, x, bytes);
+    // norm1 into a_.xn, then the block from a_.xa into a_.xb. The block also writes
+    // the next norm's output into a_.xn; its own norm1 stands in for it.
     auto run = [&]() {
-        layernorm(xa_, xn_, p + ".norm1", T);
-        hab(stage, block, xa_, xb_, p + ".norm1");
+        layernorm(a_.xa, a_.xn, p + ".norm1", T);
+        hab(stage, block, a_.xa, a_.xb, p + ".norm1");
     };
     run();
     rt.check(api.StreamSynchronize(stream_), "hab");
-    rt.d2h(out, xb_, bytes);
+    rt.d2h(out, a_.xb, bytes);
     if (iters > 0 && ms) {
         hipEvent_t a = nullptr, b = nullptr;
         rt.check(api.EventCreate(&a), "hipEventCreate");
@@ -1068,10 +1138,10 @@ void GpuBackend::forward(int h, int w, const float* in, float* out)
     ensure_plan(h, w);
     Runtime& rt = Runtime::get();
     const size_t s2 = (size_t)wt_.scale * wt_.scale;
-    rt.h2d(din_, in, 3 * (size_t)h * w * sizeof(float));
-    forward_device(h, w, din_, dout_);
+    rt.h2d(a_.din, in, 3 * (size_t)h * w * sizeof(float));
+    forward_device(h, w, a_.din, a_.dout);
     rt.check(rt.api().StreamSynchronize(stream_), "forward");
-    rt.d2h(out, dout_, 3 * (size_t)h * w * s2 * sizeof(float));
+    rt.d2h(out, a_.dout, 3 * (size_t)h * w * s2 * sizeof(float));
 }
 
 // ---------------------------------------------------------------------------

@@ -67,6 +67,12 @@ public:
     void forward(int h, int w, const float* in, float* out) override;
     // Device-resident variant: d_in [3][h][w], d_out [3][h*s][w*s].
     void forward_device(int h, int w, const float* d_in, float* d_out);
+    // The same pass with every per-plan buffer carved from the library's fixed
+    // scratch array: no device memory is allocated. Throws if the plan does not
+    // fit. Calls that overlap on one GPU share the array and race.
+    void forward_noalloc(int h, int w, const float* d_in, float* d_out);
+    // Bytes forward_noalloc needs at h x w.
+    size_t noalloc_bytes(int h, int w) const;
     // HAB.forward of one block (gpu.rs:469-520 `hab`) on a window-multiple
     // hp x wp plane: host x, out token-major [hp*wp][embed]; with the block's
     // shift and mask when it is odd. iters > 0: *ms = mean device time of the
@@ -87,17 +93,24 @@ private:
     std::vector<void*> owned_;
     size_t weight_bytes_ = 0;
 
-    // per-plan buffers
+    // The per-plan device buffers of one forward (Acts, gpu.rs:78-290). They
+    // come from hipMalloc, once per input size (ensure_plan), or, for
+    // forward_noalloc, from the library's fixed scratch array.
+    struct Acts {
+        float *x0 = nullptr, *body = nullptr, *xa = nullptr, *xb = nullptr, *xn = nullptr, *t1 = nullptr,
+              *t2 = nullptr, *partial = nullptr, *red = nullptr, *gate = nullptr, *qkv = nullptr, *ao = nullptr,
+              *hidden = nullptr, *head0 = nullptr, *head1 = nullptr, *din = nullptr, *dout = nullptr,
+              *cab_part = nullptr, *w2g = nullptr, *bias2 = nullptr;
+    };
+    // Each buffer of plan p and its size in floats (0: not used by this
+    // network); host_io adds the staging buffers of the host-memory forward.
+    std::vector<std::pair<float**, size_t>> layout(const Plan& p, Acts& a, bool host_io) const;
+
     Plan plan_;
     bool have_plan_ = false;
     std::vector<void*> acts_;
     size_t acts_bytes_ = 0;
-    float *x0_ = nullptr, *body_ = nullptr, *xa_ = nullptr, *xb_ = nullptr, *xn_ = nullptr,
-          *t1_ = nullptr, *t2_ = nullptr, *partial_ = nullptr, *red_ = nullptr, *gate_ = nullptr,
-          *qkv_ = nullptr,
-          *ao_ = nullptr, *hidden_ = nullptr, *head0_ = nullptr, *head1_ = nullptr,
-          *din_ = nullptr, *dout_ = nullptr;
-    float *cab_part_ = nullptr, *w2g_ = nullptr, *bias2_ = nullptr;
+    Acts a_;
     int t1_stride_ = 0, nblk_conv2_ = 0;
 
     float* upload(const float* src, size_t n);
@@ -106,6 +119,7 @@ private:
     void upload_conv(const std::string& name, int r = 0);
     void ensure_plan(int h, int w);
     void free_plan();
+    void run_forward(int h, int w, const float* d_in, float* d_out);
 
     void layernorm(const float* x, float* y, const std::string& prefix, long rows);
     void gemm(const DevLinear& L, const float* a, int lda, long M, float* out, int ldo, int epi,

@@ -1,4 +1,5 @@
 #include "hip_rt.h"
+#include "kargs.h"
 
 #include <dlfcn.h>
 
@@ -104,6 +105,7 @@ Runtime::Runtime()
     sym(l, api_.ModuleLoadData, "hipModuleLoadData");
     sym(l, api_.ModuleUnload, "hipModuleUnload");
     sym(l, api_.ModuleGetFunction, "hipModuleGetFunction");
+    sym(l, api_.ModuleGetGlobal, "hipModuleGetGlobal");
     sym(l, api_.ModuleLaunchKernel, "hipModuleLaunchKernel");
     sym(l, api_.Malloc, "hipMalloc");
     sym(l, api_.Free, "hipFree");
@@ -134,6 +136,17 @@ Runtime::Runtime()
         fns_[k] = f;
         names_.push_back(k);
     }
+    // The device address of the scratch array, resolved once with device 0
+    // current. The kernels live in a module loaded at run time, so host code
+    // has no symbol for the array at all: this pointer is the only handle.
+    hipDeviceptr_t sp = nullptr;
+    size_t sb = 0;
+    check(api_.ModuleGetGlobal(&sp, &sb, module_, "hat_scratch"), "hipModuleGetGlobal(hat_scratch)");
+    if (!sp || sb != (size_t)hatk::SCRATCH_BYTES)
+        throw Error("the code object's scratch array is " + std::to_string(sb) + " bytes, expected " +
+                    std::to_string((size_t)hatk::SCRATCH_BYTES));
+    scratch_ = sp;
+    scratch_bytes_ = sb;
 }
 
 void Runtime::check(hipError_t e, const char* what) const

@@ -35,6 +35,7 @@ struct HipApi {
     hipError_t (*ModuleLoadData)(hipModule_t*, const void*);
     hipError_t (*ModuleUnload)(hipModule_t);
     hipError_t (*ModuleGetFunction)(hipFunction_t*, hipModule_t, const char*);
+    hipError_t (*ModuleGetGlobal)(hipDeviceptr_t*, size_t*, hipModule_t, const char*);
     hipError_t (*ModuleLaunchKernel)(hipFunction_t, unsigned, unsigned, unsigned, unsigned,
                                      unsigned, unsigned, unsigned, hipStream_t, void**, void**);
     hipError_t (*Malloc)(void**, size_t);
@@ -70,6 +71,10 @@ public:
     void h2d(void* dst, const void* src, size_t bytes);
     void d2h(void* dst, const void* src, size_t bytes);
     void sync();
+    // The code object's fixed scratch array (hat_scratch) on this device, as
+    // hipModuleGetGlobal reports it at start-up; used only by forward_noalloc.
+    void* scratch() const { return scratch_; }
+    size_t scratch_bytes() const { return scratch_bytes_; }
 
 private:
     Runtime();
@@ -77,6 +82,8 @@ private:
     hipModule_t module_ = nullptr;
     std::unordered_map<std::string, hipFunction_t> fns_;
     std::vector<std::string> names_;
+    void* scratch_ = nullptr;
+    size_t scratch_bytes_ = 0;
 };
 
 // True if the HIP runtime library can be opened and reports a device. Never

@@ -7,6 +7,12 @@
 
 namespace hatk {
 
+// The fixed device array behind hat_backend_forward_noalloc (hat_scratch in
+// misc.hip): 256 MiB, enough for the per-plan buffers of a HAT-S or HAT x4
+// forward up to 128 x 128 input pixels. Every process that loads the library
+// holds it on the device until it exits.
+constexpr unsigned long long SCRATCH_BYTES = 256ull << 20;
+
 // Activation layout everywhere on the device: token-major NHWC, [pixel][channel],
 // pixels in image row-major order over the padded plane (hp x wp).
 

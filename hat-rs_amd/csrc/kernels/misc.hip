@@ -3,6 +3,12 @@
 
 using namespace hatk;
 
+// The device memory of hat_backend_forward_noalloc: the per-plan buffers of a
+// forward carved from one array of fixed size, for callers that cannot
+// allocate. The host resolves its address with hipModuleGetGlobal when the
+// module loads; no kernel names it, they receive pointers into it.
+__device__ __align__(256) unsigned char hat_scratch[SCRATCH_BYTES];
+
 // LayerNorm over C channels of each row (lg_channel_layer_norm, cuda.rs:185-191;
 // cpu.rs:563-581): two-pass mean then biased variance, y = (x - mean) * rstd *
 // w + b; y may alias x. For C % 4 == 0, C <= 192 (the models' 144 and 180): a

@@ -62,6 +62,8 @@ def lib():
         "hat_backend_forward_device": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
                                                  C.c_void_p]),
         "hat_backend_synchronize": (C.c_int, [C.c_void_p]),
+        "hat_backend_forward_noalloc": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
+                                                  C.c_void_p]),
         "hat_backend_hab": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_size_t, C.c_size_t, _f32p, _f32p,
                                       C.c_int, _f32p]),
         "hat_backend_acts_bytes": (C.c_size_t, [C.c_void_p]),
@@ -219,6 +221,9 @@ class Backend:
 
     def forward_device(self, h, w, d_in, d_out):
         _check(lib().hat_backend_forward_device(self.h, h, w, d_in, d_out), "forward_device")
+
+    def forward_noalloc(self, h, w, d_in, d_out):
+        _check(lib().hat_backend_forward_noalloc(self.h, h, w, d_in, d_out), "forward_noalloc")
 
     def synchronize(self):
         _check(lib().hat_backend_synchronize(self.h), "synchronize")

@@ -84,6 +84,16 @@ int hat_backend_forward(hat_backend *b, size_t h, size_t w, const float *in, flo
  * asynchronous on the backend's stream until hat_backend_synchronize. */
 int hat_backend_forward_device(hat_backend *b, size_t h, size_t w, const float *d_in, float *d_out);
 int hat_backend_synchronize(hat_backend *b);
+/* hat_backend_forward_device without allocating: no reference counterpart. It
+ * is for callers that cannot call hipMalloc (code under graph capture, serving
+ * loops that forbid allocation). Every per-plan buffer of the pass is carved
+ * from one fixed 256 MiB device array the library holds from load to process
+ * exit (enough for HAT-S or HAT x4 up to 128 x 128 input pixels); a larger
+ * plan is refused with an error and nothing runs. The caller passes device
+ * input and output as for hat_backend_forward_device; the pass is asynchronous
+ * on the backend's stream. All calls in a process share the one array: calls
+ * that overlap on the GPU (two backends, two streams, two threads) race. */
+int hat_backend_forward_noalloc(hat_backend *b, size_t h, size_t w, const float *d_in, float *d_out);
 /* One HAB of the backend's network, `hab` (gpu.rs:469-520; HAB.forward,
  * hat_arch.py:266-309): x' = x + W-MSA(norm1 x) + conv_scale * CAB(norm1 x),
  * out = x' + MLP(norm2 x'), for layers.<stage>.residual_group.blocks.<block>,
