@@ -12,6 +12,8 @@
 
 #include "gpu.h"
 #include "hip_rt.h"
+#include "image.h"
+#include "tile.h"
 #include "kargs.h"
 #include "weights.h"
 
@@ -85,6 +87,9 @@ int hat_weights_info(const hat_weights* w, hat_model_info* o)
         return 0;
     });
 }
+
+const char* hat_weights_variant(const hat_weights* w) { return w ? w->w->variant.c_str() : nullptr; }
+unsigned long long hat_weights_file_bytes(const hat_weights* w) { return w ? w->w->file_bytes : 0; }
 
 int hat_weights_count(const hat_weights* w) { return w ? (int)w->w->names.size() : -1; }
 
@@ -211,6 +216,108 @@ int hat_backend_hab(hat_backend* b, int stage, int block, size_t hp, size_t wp, 
 size_t hat_backend_acts_bytes(const hat_backend* b) { return b ? b->b->acts_bytes() : 0; }
 size_t hat_backend_weight_bytes(const hat_backend* b) { return b ? b->b->weight_bytes() : 0; }
 void hat_backend_free(hat_backend* b) { delete b; }
+
+int hat_backend_forward_batch(hat_backend* b, size_t n, size_t h, size_t w, const float* in, float* out)
+{
+    return guard([&] {
+        if (!b || !in || !out) throw hat::Error("null argument");
+        if (n > (1u << 20) || h > 65536 || w > 65536) throw hat::Error("forward_batch: too large");
+        b->b->forward_batch((int)n, (int)h, (int)w, in, out);
+        return 0;
+    });
+}
+
+int hat_tile_forward(hat_backend* b, size_t h, size_t w, const float* in, float* out, size_t tile,
+                     size_t margin, hat_tiling* info)
+{
+    return guard([&] {
+        if (!b || !in || !out) throw hat::Error("null argument");
+        if (h > 65536 || w > 65536) throw hat::Error("tile: image too large");
+        const hat::Weights& wt = b->b->weights();
+        hat::Tiling t = hat::tile_forward(*b->b, h, w, in, out, tile, margin, (size_t)wt.scale,
+                                          (size_t)wt.window);
+        if (info) {
+            info->tile = t.tile;
+            info->margin = t.margin;
+            info->scale = t.scale;
+            info->tiles = t.tiles;
+            info->largest_h = t.largest_h;
+            info->largest_w = t.largest_w;
+        }
+        return 0;
+    });
+}
+
+size_t hat_auto_tile(size_t h, size_t w, size_t win, unsigned long long budget_bytes,
+                     unsigned long long per_pixel_floats, unsigned long long constant_floats, size_t margin)
+{
+    if (win == 0) return 0;
+    return hat::auto_tile(h, w, win, budget_bytes, per_pixel_floats, constant_floats, margin);
+}
+
+int hat_gpu_plan(const hat_weights* w, size_t h, size_t wd, hat_mem_plan* out)
+{
+    return guard([&] {
+        if (!w || !out) throw hat::Error("null argument");
+        if (h == 0 || wd == 0 || h > 65536 || wd > 65536) throw hat::Error("gpu_plan: bad size");
+        hat::MemPlan p = hat::gpu_plan(*w->w, h, wd);
+        out->activations = p.activations;
+        out->weights = p.weights;
+        out->base = p.base;
+        out->need = p.need;
+        out->avail = p.avail;
+        out->have_avail = p.have_avail ? 1 : 0;
+        return 0;
+    });
+}
+
+long hat_gpu_auto_tile(const hat_weights* w, size_t h, size_t wd)
+{
+    long r = -1;
+    guard([&] {
+        if (!w) throw hat::Error("null argument");
+        if (h == 0 || wd == 0 || h > 65536 || wd > 65536) throw hat::Error("gpu_auto_tile: bad size");
+        r = (long)hat::gpu_auto_tile(*w->w, h, wd);
+        return 0;
+    });
+    return r;
+}
+
+int hat_png_load(const char* path, size_t* w, size_t* h, float* out, size_t cap)
+{
+    return guard([&] {
+        if (!path || !w || !h) throw hat::Error("null argument");
+        hat::Image img = hat::load_png(path);
+        *w = img.w;
+        *h = img.h;
+        if (out) {
+            if (cap < img.data.size())
+                throw hat::Error(std::string(path) + ": " + std::to_string(img.data.size()) +
+                                 " floats needed, room for " + std::to_string(cap));
+            memcpy(out, img.data.data(), img.data.size() * sizeof(float));
+        }
+        return 0;
+    });
+}
+
+int hat_png_save(const char* path, size_t w, size_t h, const float* planes)
+{
+    return guard([&] {
+        if (!path || !planes) throw hat::Error("null argument");
+        hat::save_png(path, w, h, planes);
+        return 0;
+    });
+}
+
+int hat_weights_shape(const hat_weights* w, const char* name, size_t* dims, int cap)
+{
+    return guard([&] {
+        if (!w || !name) throw hat::Error("null argument");
+        const hat::TensorInfo& ti = w->w->info(name);
+        for (int i = 0; i < (int)ti.shape.size() && i < cap && dims; ++i) dims[i] = ti.shape[i];
+        return (int)ti.shape.size();
+    });
+}
 
 // main.rs:312-326 with the fixture format of fixture.rs:44-107.
 int hat_verify(const hat_weights* w, const char* device, const char* fixture_path)

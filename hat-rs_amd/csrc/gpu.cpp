@@ -5,6 +5,7 @@
 #include <cstring>
 
 #include "kargs.h"
+#include "tile.h"
 
 namespace hat {
 
@@ -685,6 +686,7 @@ void GpuBackend::upload_conv(const std::string& name, int r)
 GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
 {
     Runtime& rt = Runtime::get();
+    check_gpu_weights(wt);
     if (wt.window != 16 || wt.owin != 24)
         throw Error("the gfx950 attention kernels are built for window 16 and overlap window 24");
     if (wt.head_dim != 24 && wt.head_dim != 30)
@@ -694,7 +696,7 @@ GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
     if (wt.head_feat % 4 != 0) throw Error("head width must be a multiple of 4");
     for (int d : wt.depths)
         if (d < 1) throw Error("every stage needs at least one HAB");
-    cab_fold_ = wt.embed == CAB_C && wt.compressed == CAB_CC;
+    cab_fold_ = cab_folded(wt);
     rt.check(rt.api().StreamCreate(&stream_), "hipStreamCreate");
     upload_conv("conv_first");
     upload_raw("patch_embed.norm.weight");
@@ -758,6 +760,7 @@ GpuBackend::~GpuBackend()
     try {
         Runtime& rt = Runtime::get();
         rt.api().StreamSynchronize(stream_);
+        free_batch();
         free_plan();
         for (void* p : owned_) rt.free(p);
         rt.api().StreamDestroy(stream_);
@@ -775,16 +778,28 @@ void GpuBackend::free_plan()
     have_plan_ = false;
 }
 
+// The compress-to-6 CAB at C = 144 (HAT-S) runs folded (cab.hip + habtail.hip).
+bool GpuBackend::cab_folded(const Weights& wt) { return wt.embed == CAB_C && wt.compressed == CAB_CC; }
+
+size_t GpuBackend::plan_bytes(const Weights& wt, int h, int w, bool host_io)
+{
+    Acts a;
+    size_t n = 0;
+    for (auto& b : layout(wt, Plan::make(h, w, wt.window, wt.embed), a, host_io)) n += b.second * sizeof(float);
+    return n;
+}
+
 // Acts::new (gpu.rs:293-334): the buffer set of one plan.
-std::vector<std::pair<float**, size_t>> GpuBackend::layout(const Plan& p, Acts& a, bool host_io) const
+std::vector<std::pair<float**, size_t>> GpuBackend::layout(const Weights& wt_, const Plan& p, Acts& a,
+                                                           bool host_io)
 {
     const size_t T = (size_t)p.tokens(), C = wt_.embed;
     const size_t t1_stride = (size_t)(wt_.compressed + 3) / 4 * 4;
     const size_t nblk = (size_t)colsum_rows((int)C, p.hp, p.wp, (int)C);
+    const bool cab_fold_ = cab_folded(wt_);
     // The T x hidden buffer only for MLP shapes without a fused kernel (every
-    // block of a network shares one shape).
-    const std::string b0 = "layers.0.residual_group.blocks.0.mlp.";
-    const bool fused_mlp = mlp_fused(lin_.at(b0 + "fc1"), lin_.at(b0 + "fc2"));
+    // block of a network shares one shape: fc1 C -> mlp_ratio * C).
+    const bool fused_mlp = wt_.mlp_ratio == 2 && (C == 144 || C == 180);
     // Head ping-pong: the plane at each resolution goes to alternate buffers.
     size_t need[2] = {T * (size_t)wt_.head_feat, 0};
     size_t res = 1;
@@ -819,18 +834,20 @@ std::vector<std::pair<float**, size_t>> GpuBackend::layout(const Plan& p, Acts& 
     };
 }
 
-// One allocation set per plan, reused by every forward at that size.
+// One allocation set per plan, reused by every forward at that size. A new
+// plan is admitted against the device's free memory first (gpu.rs:766-771).
 void GpuBackend::ensure_plan(int h, int w)
 {
     Plan p = Plan::make(h, w, wt_.window, wt_.embed);
     if (have_plan_ && p == plan_) return;
+    check_gpu(wt_, (size_t)h, (size_t)w);
     free_plan();
     plan_ = p;
     Runtime& rt = Runtime::get();
     t1_stride_ = (wt_.compressed + 3) / 4 * 4;
     nblk_conv2_ = colsum_rows(wt_.embed, p.hp, p.wp, wt_.embed);
     a_ = Acts{};
-    for (auto& b : layout(p, a_, true)) {
+    for (auto& b : layout(wt_, p, a_, true)) {
         if (b.second == 0) continue;
         float* d = (float*)rt.alloc(b.second * sizeof(float));
         acts_.push_back(d);
@@ -968,7 +985,7 @@ size_t GpuBackend::noalloc_bytes(int h, int w) const
     if (h <= 0 || w <= 0) throw Error(std::to_string(h) + "x" + std::to_string(w) + " is empty");
     Acts a;
     size_t off = 0;
-    for (auto& b : layout(Plan::make(h, w, wt_.window, wt_.embed), a, false))
+    for (auto& b : layout(wt_, Plan::make(h, w, wt_.window, wt_.embed), a, false))
         if (b.second) off += (b.second * sizeof(float) + 255) / 256 * 256;
     return off;
 }
@@ -994,7 +1011,7 @@ void GpuBackend::forward_noalloc(int h, int w, const float* d_in, float* d_out)
     Acts a;
     char* base = (char*)rt.scratch();
     size_t off = 0;
-    for (auto& b : layout(p, a, false)) {
+    for (auto& b : layout(wt_, p, a, false)) {
         if (b.second == 0) continue;
         *b.first = (float*)(base + off);
         off += (b.second * sizeof(float) + 255) / 256 * 256;
@@ -1128,6 +1145,101 @@ void GpuBackend::op_hab(int stage, int block, int hp, int wp, const float* x, fl
         *ms = e / iters;
         api.EventDestroy(a);
         api.EventDestroy(b);
+    }
+}
+
+void GpuBackend::free_batch()
+{
+    Runtime& rt = Runtime::get();
+    for (BatchSlot& sl : batch_) {
+        if (sl.s) {
+            rt.api().StreamSynchronize(sl.s);
+            rt.api().StreamDestroy(sl.s);
+        }
+        if (sl.hin) rt.api().HostFree(sl.hin);
+        if (sl.hout) rt.api().HostFree(sl.hout);
+    }
+    batch_.clear();
+    for (void* p : batch_dev_) rt.free(p);
+    batch_dev_.clear();
+}
+
+void GpuBackend::forward_batch(int n, int h, int w, const float* in, float* out)
+{
+    if (n <= 0 || h <= 0 || w <= 0) throw Error("forward_batch: empty batch or image");
+    if (!in || !out) throw Error("forward_batch: null argument");
+    Runtime& rt = Runtime::get();
+    const HipApi& api = rt.api();
+    const size_t s2 = (size_t)wt_.scale * wt_.scale;
+    const size_t isz = 3 * (size_t)h * w, osz = isz * s2;
+    const int slots = std::min(n, kBatchSlots);
+    const Plan p = Plan::make(h, w, wt_.window, wt_.embed);
+    if (!(batch_plan_ == p) || (int)batch_.size() < slots) {
+        free_batch();
+        // admission for all the slots' buffers at once (the weights are already up)
+        const MemPlan mp = gpu_plan(wt_, (size_t)h, (size_t)w);
+        const uint64_t need = (uint64_t)((double)mp.activations * kSlack) * slots + mp.base;
+        if (mp.have_avail && need > mp.avail)
+            throw Error("not enough video memory for a batch of " + std::to_string(slots) + " concurrent " +
+                        std::to_string(w) + "x" + std::to_string(h) + " passes: about " + fmt_bytes(need) +
+                        " needed, " + fmt_bytes(mp.avail) + " free");
+        batch_plan_ = p;
+        batch_.resize(slots);
+        for (BatchSlot& sl : batch_) {
+            rt.check(api.StreamCreate(&sl.s), "hipStreamCreate");
+            for (auto& b : layout(wt_, p, sl.a, true)) {
+                if (b.second == 0) continue;
+                float* d = (float*)rt.alloc(b.second * sizeof(float));
+                batch_dev_.push_back(d);
+                *b.first = d;
+            }
+            rt.check(api.HostMalloc((void**)&sl.hin, isz * sizeof(float), 0), "hipHostMalloc");
+            rt.check(api.HostMalloc((void**)&sl.hout, osz * sizeof(float), 0), "hipHostMalloc");
+        }
+    }
+    // Swap a slot's stream and buffers in for run_forward, which only enqueues.
+    const hipStream_t own_stream = stream_;
+    const Acts own_acts = a_;
+    const Plan own_plan = plan_;
+    const int own_nblk = nblk_conv2_;
+    auto restore = [&]() {
+        stream_ = own_stream;
+        a_ = own_acts;
+        plan_ = own_plan;
+        nblk_conv2_ = own_nblk;
+    };
+    auto drain = [&](BatchSlot& sl) {
+        if (sl.img < 0) return;
+        rt.check(api.StreamSynchronize(sl.s), "forward_batch");
+        memcpy(out + (size_t)sl.img * osz, sl.hout, osz * sizeof(float));
+        sl.img = -1;
+    };
+    try {
+        for (int i = 0; i < n; ++i) {
+            BatchSlot& sl = batch_[i % slots];
+            drain(sl);
+            memcpy(sl.hin, in + (size_t)i * isz, isz * sizeof(float));
+            rt.check(api.MemcpyAsync(sl.a.din, sl.hin, isz * sizeof(float), hipMemcpyHostToDevice, sl.s),
+                     "hipMemcpyAsync H2D");
+            stream_ = sl.s;
+            a_ = sl.a;
+            plan_ = p;
+            t1_stride_ = (wt_.compressed + 3) / 4 * 4;
+            nblk_conv2_ = colsum_rows(wt_.embed, p.hp, p.wp, wt_.embed);
+            run_forward(h, w, sl.a.din, sl.a.dout);
+            restore();
+            rt.check(api.MemcpyAsync(sl.hout, sl.a.dout, osz * sizeof(float), hipMemcpyDeviceToHost, sl.s),
+                     "hipMemcpyAsync D2H");
+            sl.img = i;
+        }
+        for (BatchSlot& sl : batch_) drain(sl);
+    } catch (...) {
+        restore();
+        for (BatchSlot& sl : batch_) {
+            api.StreamSynchronize(sl.s);
+            sl.img = -1;
+        }
+        throw;
     }
 }
 

@@ -71,8 +71,18 @@ public:
     // scratch array: no device memory is allocated. Throws if the plan does not
     // fit. Calls that overlap on one GPU share the array and race.
     void forward_noalloc(int h, int w, const float* d_in, float* d_out);
+    // n images of one size, host [n][3][h][w] in, host [n][3][h*s][w*s] out:
+    // up to kBatchSlots images in flight at once, each on its own stream with
+    // its own per-plan buffers and pinned staging, so the kernels of several
+    // small images fill the device together. Synchronous.
+    void forward_batch(int n, int h, int w, const float* in, float* out);
+    static constexpr int kBatchSlots = 4;
     // Bytes forward_noalloc needs at h x w.
     size_t noalloc_bytes(int h, int w) const;
+    // Device bytes of the per-plan buffers a backend over `wt` allocates for an
+    // h x w forward (gpu.rs:78-290 footprint_floats), computed without a device.
+    static size_t plan_bytes(const Weights& wt, int h, int w, bool host_io);
+    static bool cab_folded(const Weights& wt);
     // HAB.forward of one block (gpu.rs:469-520 `hab`) on a window-multiple
     // hp x wp plane: host x, out token-major [hp*wp][embed]; with the block's
     // shift and mask when it is odd. iters > 0: *ms = mean device time of the
@@ -81,6 +91,7 @@ public:
     size_t acts_bytes() const { return acts_bytes_; }
     size_t weight_bytes() const { return weight_bytes_; }
     hipStream_t stream() const { return stream_; }
+    const Weights& weights() const { return wt_; }
 
 private:
     const Weights& wt_;
@@ -104,7 +115,8 @@ private:
     };
     // Each buffer of plan p and its size in floats (0: not used by this
     // network); host_io adds the staging buffers of the host-memory forward.
-    std::vector<std::pair<float**, size_t>> layout(const Plan& p, Acts& a, bool host_io) const;
+    static std::vector<std::pair<float**, size_t>> layout(const Weights& wt, const Plan& p, Acts& a,
+                                                          bool host_io);
 
     Plan plan_;
     bool have_plan_ = false;
@@ -112,6 +124,19 @@ private:
     size_t acts_bytes_ = 0;
     Acts a_;
     int t1_stride_ = 0, nblk_conv2_ = 0;
+
+    // forward_batch's slots: a stream, a per-plan buffer set and pinned
+    // staging each, kept for the last batch size.
+    struct BatchSlot {
+        hipStream_t s = nullptr;
+        Acts a;
+        float *hin = nullptr, *hout = nullptr;
+        int img = -1;
+    };
+    std::vector<BatchSlot> batch_;
+    Plan batch_plan_;
+    std::vector<void*> batch_dev_;
+    void free_batch();
 
     float* upload(const float* src, size_t n);
     void upload_raw(const std::string& name);

@@ -112,6 +112,8 @@ Runtime::Runtime()
     sym(l, api_.Memcpy, "hipMemcpy");
     sym(l, api_.MemcpyAsync, "hipMemcpyAsync");
     sym(l, api_.MemGetInfo, "hipMemGetInfo");
+    sym(l, api_.HostMalloc, "hipHostMalloc");
+    sym(l, api_.HostFree, "hipHostFree");
     sym(l, api_.StreamCreate, "hipStreamCreate");
     sym(l, api_.StreamDestroy, "hipStreamDestroy");
     sym(l, api_.StreamSynchronize, "hipStreamSynchronize");

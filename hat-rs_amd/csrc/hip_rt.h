@@ -43,6 +43,8 @@ struct HipApi {
     hipError_t (*Memcpy)(void*, const void*, size_t, hipMemcpyKind);
     hipError_t (*MemcpyAsync)(void*, const void*, size_t, hipMemcpyKind, hipStream_t);
     hipError_t (*MemGetInfo)(size_t*, size_t*);
+    hipError_t (*HostMalloc)(void**, size_t, unsigned int);
+    hipError_t (*HostFree)(void*);
     hipError_t (*StreamCreate)(hipStream_t*);
     hipError_t (*StreamDestroy)(hipStream_t);
     hipError_t (*StreamSynchronize)(hipStream_t);

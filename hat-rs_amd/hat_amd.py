@@ -32,6 +32,15 @@ class ModelInfo(C.Structure):
                 ("img_range", C.c_float), ("mean", C.c_float * 3)]
 
 
+class Tiling(C.Structure):
+    _fields_ = [(n, C.c_size_t) for n in ("tile", "margin", "scale", "tiles", "largest_h", "largest_w")]
+
+
+class MemPlan(C.Structure):
+    _fields_ = [(n, C.c_ulonglong) for n in ("activations", "weights", "base", "need", "avail")] + \
+               [("have_avail", C.c_int)]
+
+
 _lib = None
 
 
@@ -55,6 +64,18 @@ def lib():
         "hat_weights_index_i64": (C.c_long, [C.c_void_p, C.c_char_p, C.POINTER(C.c_longlong), C.c_size_t]),
         "hat_weights_generate": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int, C.c_ulonglong,
                                            C.POINTER(C.c_int), C.c_int]),
+        "hat_weights_variant": (C.c_char_p, [C.c_void_p]),
+        "hat_weights_file_bytes": (C.c_ulonglong, [C.c_void_p]),
+        "hat_weights_shape": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_size_t), C.c_int]),
+        "hat_backend_forward_batch": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, _f32p, _f32p]),
+        "hat_tile_forward": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, _f32p, _f32p, C.c_size_t, C.c_size_t,
+                                       C.POINTER(Tiling)]),
+        "hat_auto_tile": (C.c_size_t, [C.c_size_t, C.c_size_t, C.c_size_t, C.c_ulonglong, C.c_ulonglong,
+                                       C.c_ulonglong, C.c_size_t]),
+        "hat_gpu_plan": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(MemPlan)]),
+        "hat_gpu_auto_tile": (C.c_long, [C.c_void_p, C.c_size_t, C.c_size_t]),
+        "hat_png_load": (C.c_int, [C.c_char_p, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t), _f32p, C.c_size_t]),
+        "hat_png_save": (C.c_int, [C.c_char_p, C.c_size_t, C.c_size_t, _f32p]),
         "hat_gpu_available": (C.c_int, []),
         "hat_backend_new": (C.c_void_p, [C.c_void_p, C.c_char_p]),
         "hat_backend_name": (C.c_char_p, [C.c_void_p]),
@@ -164,6 +185,22 @@ class Weights:
         self.img_range = info.img_range
         self.mean = [info.mean[i] for i in range(3)]
 
+    def variant(self):
+        return lib().hat_weights_variant(self.h).decode()
+
+    def file_bytes(self):
+        return lib().hat_weights_file_bytes(self.h)
+
+    def shape(self, name):
+        d = (C.c_size_t * 16)()
+        n = _check(lib().hat_weights_shape(self.h, name.encode(), d, 16), "hat_weights_shape")
+        return [d[i] for i in range(n)]
+
+    def gpu_plan(self, h, w):
+        p = MemPlan()
+        _check(lib().hat_gpu_plan(self.h, h, w, C.byref(p)), "hat_gpu_plan")
+        return {n: getattr(p, n) for n, _ in MemPlan._fields_}
+
     def names(self):
         L = lib()
         return [L.hat_weights_name(self.h, i).decode() for i in range(L.hat_weights_count(self.h))]
@@ -222,6 +259,22 @@ class Backend:
     def forward_device(self, h, w, d_in, d_out):
         _check(lib().hat_backend_forward_device(self.h, h, w, d_in, d_out), "forward_device")
 
+    def forward_batch(self, n, h, w, imgs):
+        imgs = f32(imgs).reshape(n, 3, h, w)
+        s = self.weights.scale
+        out = np.empty((n, 3, h * s, w * s), dtype=np.float32)
+        _check(lib().hat_backend_forward_batch(self.h, n, h, w, _fp(imgs), _fp(out)), "forward_batch")
+        return out
+
+    def tile_forward(self, h, w, img, tile, margin):
+        img = f32(img).reshape(3, h, w)
+        s = self.weights.scale
+        out = np.empty((3, h * s, w * s), dtype=np.float32)
+        t = Tiling()
+        _check(lib().hat_tile_forward(self.h, h, w, _fp(img), _fp(out), tile, margin, C.byref(t)),
+               "tile_forward")
+        return out, {n: getattr(t, n) for n, _ in Tiling._fields_}
+
     def forward_noalloc(self, h, w, d_in, d_out):
         _check(lib().hat_backend_forward_noalloc(self.h, h, w, d_in, d_out), "forward_noalloc")
 
@@ -261,6 +314,30 @@ def verify(weights, fixture_path, device="gpu"):
     if rc < 0:
         raise HatError(_err())
     return rc
+
+
+def auto_tile(h, w, win, budget_bytes, per_pixel_floats, constant_floats, margin):
+    """tile::auto_tile; None when not even one window fits."""
+    t = lib().hat_auto_tile(h, w, win, budget_bytes, per_pixel_floats, constant_floats, margin)
+    return t or None
+
+
+def png_load(path):
+    w, h = C.c_size_t(0), C.c_size_t(0)
+    _check(lib().hat_png_load(str(path).encode(), C.byref(w), C.byref(h), None, 0), "hat_png_load")
+    out = np.empty((3, h.value, w.value), dtype=np.float32)
+    _check(lib().hat_png_load(str(path).encode(), C.byref(w), C.byref(h), _fp(out), out.size), "hat_png_load")
+    return out
+
+
+def png_save(path, planes):
+    planes = f32(planes)
+    c, h, w = planes.shape
+    assert c == 3
+    _check(lib().hat_png_save(str(path).encode(), w, h, _fp(planes)), "hat_png_save")
+
+
+CLI_PATH = os.path.join(HERE, "build", "hat")
 
 
 def selftest():

@@ -45,6 +45,11 @@ typedef struct {
 } hat_model_info;
 int hat_weights_info(const hat_weights *w, hat_model_info *out);
 
+/* The checkpoint's `variant` metadata and its size in bytes (Weights.variant,
+ * Weights.bytes, weights.rs:28-57; main.rs:205-206 prints both). */
+const char *hat_weights_variant(const hat_weights *w);
+unsigned long long hat_weights_file_bytes(const hat_weights *w);
+
 /* Tensor listing and access (weights.rs:270-272 `t`, `--list-weights`). */
 int hat_weights_count(const hat_weights *w);
 const char *hat_weights_name(const hat_weights *w, int i);
@@ -107,6 +112,59 @@ int hat_backend_hab(hat_backend *b, int stage, int block, size_t hp, size_t wp, 
 size_t hat_backend_acts_bytes(const hat_backend *b);
 size_t hat_backend_weight_bytes(const hat_backend *b);
 void hat_backend_free(hat_backend *b);
+
+/* ---- Batching, tiling and memory admission (src/tile.rs, src/memguard.rs) */
+
+/* n images of one size through the backend: in = host [n][3][h][w], out =
+ * host [n][3][h*scale][w*scale]. Up to 4 images are in flight at once, each on
+ * its own stream with its own per-plan buffers, so the kernels of several
+ * small images fill the device together (the single-GPU part of multi-image
+ * batching). Synchronous; results identical to n calls of hat_backend_forward. */
+int hat_backend_forward_batch(hat_backend *b, size_t n, size_t h, size_t w, const float *in, float *out);
+
+/* tile::Tiling (tile.rs:34-45). */
+typedef struct {
+    size_t tile, margin, scale, tiles, largest_h, largest_w;
+} hat_tiling;
+/* tile::forward (tile.rs:50-107): the image in window-aligned cores of `tile`
+ * input pixels, each run with a halo of `margin` pixels (both rounded up to
+ * the window) on every side that is not the image's edge; only the cores are
+ * copied to out. info (may be NULL) reports what ran. */
+int hat_tile_forward(hat_backend *b, size_t h, size_t w, const float *in, float *out, size_t tile,
+                     size_t margin, hat_tiling *info);
+/* tile::auto_tile (tile.rs:140-184): the largest window-multiple core whose
+ * sub-image (core plus both margins) fits budget_bytes at per_pixel_floats per
+ * pixel plus constant_floats; 0 when not even one window fits (None). */
+size_t hat_auto_tile(size_t h, size_t w, size_t win, unsigned long long budget_bytes,
+                     unsigned long long per_pixel_floats, unsigned long long constant_floats, size_t margin);
+/* memguard::Plan (memguard.rs:46-58). */
+typedef struct {
+    unsigned long long activations, weights, base, need, avail;
+    int have_avail;
+} hat_mem_plan;
+/* memguard::gpu_plan (memguard.rs:147-160): the per-plan device buffers of an
+ * h x w pass, the checkpoint's bytes and 128 MiB of runtime, with 5% slack,
+ * against free device memory (have_avail = 0 when no device answers). The
+ * backend refuses a plan that does not fit, with the reference's message
+ * (memguard.rs:162-190), before allocating it. */
+int hat_gpu_plan(const hat_weights *w, size_t h, size_t wd, hat_mem_plan *out);
+/* main.rs:115-140 gpu_auto_tile: the tile a run without --tile/--mem uses,
+ * halved from the larger image side until hat_gpu_plan fits. */
+long hat_gpu_auto_tile(const hat_weights *w, size_t h, size_t wd);
+
+/* ---- PNG I/O (src/image.rs) ------------------------------------------- */
+
+/* image::load_rgb (image.rs:43-99): decode an 8- or 16-bit grey, grey+alpha,
+ * RGB or RGBA PNG into planar [3][h][w] floats in [0,1]. Sets *w and *h; with
+ * out non-NULL also writes the planes (cap >= 3*w*h floats). */
+int hat_png_load(const char *path, size_t *w, size_t *h, float *out, size_t cap);
+/* image::save_rgb of Image::to_rgb8 (image.rs:30-41,101-114): planar [3][h][w]
+ * floats, clamped to [0,1], scaled by 255, rounded half up, as 8-bit RGB. */
+int hat_png_save(const char *path, size_t w, size_t h, const float *planes);
+
+/* Weights::shape (weights.rs:275-280, `--list-weights`): writes up to cap
+ * dimensions of the named tensor; returns its rank. */
+int hat_weights_shape(const hat_weights *w, const char *name, size_t *dims, int cap);
 
 /* ---- Contracts (src/main.rs:312-326, src/selftest.rs:437-523) ----------- */
 
