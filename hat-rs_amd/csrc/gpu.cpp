@@ -585,8 +585,9 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
         throw Error("attention: shift " + std::to_string(shift) + " is not supported (0" +
                     (oca ? "" : " or " + std::to_string(pl.shift)) + ")");
     const char* name = nullptr;
-    if (D == 24) name = oca ? "hat_attn_oca_d24" : "hat_attn_sw_d24";
-    else if (D == 30) name = oca ? "hat_attn_oca_d30" : "hat_attn_sw_d30";
+    // SW: the split-bf16 kernels (attnx.hip); OCA: FP32 MFMA (attn.hip)
+    if (D == 24) name = oca ? "hat_attn_oca_d24" : "hat_attnx_sw_d24";
+    else if (D == 30) name = oca ? "hat_attn_oca_d30" : "hat_attnx_sw_d30";
     else throw Error("attention: head_dim " + std::to_string(D) + " has no kernel (24 and 30 do)");
     AttnArgs p{};
     p.qkv = qkv;

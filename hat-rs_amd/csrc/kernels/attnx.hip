@@ -1,0 +1,344 @@
+// Shifted-window attention on BF16 MFMA with fp32 accuracy: QK^T + relative-
+// position bias + shift mask + softmax + PV for one (window, head) per block.
+//
+// The same operator as attn.hip (cpu.rs:772-844; hat.cu:246-316) on gfx950's
+// BF16 matrix path, which runs at 13.7x the FP32 MFMA rate and, unlike FP32
+// MFMA, overlaps with VALU work on a SIMD (measured: a BF16 MFMA stream and an
+// independent FMA stream together take the time of the longer one). Every fp32
+// operand x enters as three bf16 parts, x = x0 + x1 + x2 + e with |e| <=
+// 2^-27 |x| (each part the round-to-nearest of what the earlier ones leave),
+// and a product as the six terms a_i b_j with i + j <= 2, accumulated in fp32
+// by v_mfma_f32_32x32x16_bf16; the terms dropped (i + j >= 3) are below
+// 2^-26 |ab|. Measured at K = 144 against a double reference: worst error
+// 1.25e-7 of sum|ab| against 1.42e-7 for FP32 MFMA.
+//
+// Layout (all per item, in LDS): K as three bf16 planes [256 keys][KS] and V^T
+// as three planes [D + 1][VS] whose key order is permuted within each 16 so
+// that a lane's eight keys of one MFMA step are contiguous; row D of V^T is
+// ones in the high plane and zeros in the others, so row D of O^T is the
+// softmax denominator. The bias table of the head is kept in log2 units. Wave
+// w owns queries [32w, 32w+32). Scores are computed transposed, S^T = K Q^T
+// (A = a 32-key tile of K, B = the wave's q, split in registers): lane l holds
+// 16 scores of query l%32, which after the softmax are split and used directly
+// as the B operand of O^T += V^T P^T. Bias, mask, online softmax in base 2 and
+// the output are those of attn.hip.
+#include "common.h"
+
+using namespace hatk;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// (a, b) rounded to nearest bf16, packed: a in the low half (element 0).
+__device__ __forceinline__ unsigned pk_bf16(float a, float b)
+{
+    return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+
+// The three-way split of a pair: (a, b) = p0 + p1 + p2 (+ below 2^-27 of
+// each), every part a packed pair of bf16, each the round-to-nearest of what
+// the earlier parts leave (x - its rounding is exact in fp32).
+__device__ __forceinline__ void split3_pk(float a, float b, unsigned& p0, unsigned& p1, unsigned& p2)
+{
+    p0 = pk_bf16(a, b);
+    a -= __uint_as_float(p0 << 16);
+    b -= __uint_as_float(p0 & 0xffff0000u);
+    p1 = pk_bf16(a, b);
+    a -= __uint_as_float(p1 << 16);
+    b -= __uint_as_float(p1 & 0xffff0000u);
+    p2 = pk_bf16(a, b);
+}
+
+// Eight consecutive fp32 values as three 8-wide bf16 parts.
+__device__ __forceinline__ void split3_x8(const float (&v)[8], u32x4 (&out)[3])
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        unsigned p0, p1, p2;
+        split3_pk(v[2 * j], v[2 * j + 1], p0, p1, p2);
+        out[0][j] = p0;
+        out[1][j] = p1;
+        out[2][j] = p2;
+    }
+}
+
+// The six products of a 3-part A and a 3-part B into c, smallest first.
+__device__ __forceinline__ f32x16 mfma6(const u32x4 (&a)[3], const u32x4 (&b)[3], f32x16 c)
+{
+    c = mfma_bf16(a[2], b[0], c);
+    c = mfma_bf16(a[1], b[1], c);
+    c = mfma_bf16(a[0], b[2], c);
+    c = mfma_bf16(a[1], b[0], c);
+    c = mfma_bf16(a[0], b[1], c);
+    return mfma_bf16(a[0], b[0], c);
+}
+
+template <int D>
+struct AttnXShape {
+    static constexpr int NK = 256;
+    // K row stride in bf16: 24 (48 B) and 40 (80 B) put the 16 rows a ds_read_b128
+    // phase touches on distinct banks.
+    static constexpr int KS = D == 24 ? 24 : 40;
+    static constexpr int VS = NK + 8;  // V^T row stride (528 B: rows 4 banks apart)
+    static constexpr int KPL = NK * KS, VPL = (D + 1) * VS;  // elements per plane
+    static constexpr int TROWS = 961;
+    static constexpr int LDS_BYTES = 2 * 3 * (KPL + VPL) + 4 * TROWS;
+};
+
+// Position of key k in the V^T planes: within each 16 keys, bits 2 and 3
+// swap, so that lane half h's eight keys of an MFMA step (16s + 8a + 4h + t,
+// a, t the slot's high bit and low two bits) are positions 16s + 8h .. +7.
+__device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+
+// Item staging: this thread's K and V units (attn_fetch's registers), split
+// into the LDS planes; row D of V^T: ones (high plane), zeros; K dims D .. 31
+// of D = 30 zeroed (the q operand is zero there; LDS that was never written
+// could hold a NaN).
+template <int D>
+__device__ __forceinline__ void attnx_stash(unsigned short* Kp, unsigned short* Vp,
+                                            const typename AttnShape<D, false>::vec (&ks)[AttnShape<D, false>::NE],
+                                            const typename AttnShape<D, false>::vec (&vs)[AttnShape<D, false>::NE])
+{
+    using S = AttnShape<D, false>;
+    using X = AttnXShape<D>;
+    constexpr int PER_KEY = D / S::U;
+#pragma unroll
+    for (int i = 0; i < S::NE; ++i) {
+        const int e = threadIdx.x + i * 512;
+        if (e < S::NK * PER_KEY) {
+            const int k = e / PER_KEY, d = (e - k * PER_KEY) * S::U;
+            float kv[4], vv[4];
+            if constexpr (S::U == 4) {
+                kv[0] = ks[i].x, kv[1] = ks[i].y, kv[2] = ks[i].z, kv[3] = ks[i].w;
+                vv[0] = vs[i].x, vv[1] = vs[i].y, vv[2] = vs[i].z, vv[3] = vs[i].w;
+            } else {
+                kv[0] = ks[i].x, kv[1] = ks[i].y, kv[2] = kv[3] = 0.f;
+                vv[0] = vs[i].x, vv[1] = vs[i].y, vv[2] = vv[3] = 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < S::U; j += 2) {
+                unsigned k0, k1, k2, v0, v1, v2;
+                split3_pk(kv[j], kv[j + 1], k0, k1, k2);
+                *(unsigned*)(Kp + 0 * X::KPL + k * X::KS + d + j) = k0;
+                *(unsigned*)(Kp + 1 * X::KPL + k * X::KS + d + j) = k1;
+                *(unsigned*)(Kp + 2 * X::KPL + k * X::KS + d + j) = k2;
+                split3_pk(vv[j], vv[j + 1], v0, v1, v2);
+                const int pos = vpos(k);
+                Vp[0 * X::VPL + (d + j) * X::VS + pos] = (unsigned short)v0;
+                Vp[0 * X::VPL + (d + j + 1) * X::VS + pos] = (unsigned short)(v0 >> 16);
+                Vp[1 * X::VPL + (d + j) * X::VS + pos] = (unsigned short)v1;
+                Vp[1 * X::VPL + (d + j + 1) * X::VS + pos] = (unsigned short)(v1 >> 16);
+                Vp[2 * X::VPL + (d + j) * X::VS + pos] = (unsigned short)v2;
+                Vp[2 * X::VPL + (d + j + 1) * X::VS + pos] = (unsigned short)(v2 >> 16);
+            }
+        }
+    }
+    for (int e = threadIdx.x; e < 3 * (S::NK / 2); e += 512) {
+        const int pl = e / (S::NK / 2), k2 = e - pl * (S::NK / 2);
+        *(unsigned*)(Vp + pl * X::VPL + D * X::VS + 2 * k2) = pl == 0 ? 0x3f803f80u : 0u;  // bf16 1.0 pairs
+    }
+    if (D == 30) {
+        for (int e = threadIdx.x; e < 3 * S::NK; e += 512) {
+            const int pl = e / S::NK, k = e - pl * S::NK;
+            *(unsigned*)(Kp + pl * X::KPL + k * X::KS + 30) = 0u;
+        }
+    }
+}
+
+// The lane's q, pre-scaled and split: qb[s][part] = dims 16s + 8h .. 16s + 8h
+// + 7 of its query (zeros past D).
+template <int D>
+__device__ __forceinline__ int attnx_query(const AttnArgs& p, int wi, int head, u32x4 (&qb)[2][3])
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ql = lane & 31, h = lane >> 5;
+    const int q = wave * 32 + ql, qy = q >> 4, qx = q & 15;
+    const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
+    int y = wy * 16 + qy + p.shift, x = wx * 16 + qx + p.shift;
+    if (y >= p.hp) y -= p.hp;
+    if (x >= p.wp) x -= p.wp;
+    const int qpix = y * p.wp + x;
+    const float* Qg = p.qkv + (size_t)head * p.T * D + (size_t)qpix * D;
+    float qv[2][8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int d0 = 16 * s + 8 * h;
+        if constexpr (D % 4 == 0) {
+            // D = 24: dims 24..31 (s = 1, h = 1) are zero
+            const bool live = d0 + 8 <= D;
+            const f32x4 a = load_or_zero(Qg + d0, live), b = load_or_zero(Qg + d0 + 4, live);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qv[s][j] = a[j], qv[s][4 + j] = b[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const bool live = d0 + j + 2 <= D;
+                const float2 v = *(const float2*)(live ? Qg + d0 + j : hat_zero_row);
+                qv[s][j] = v.x;
+                qv[s][j + 1] = v.y;
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qv[s][j] *= p.qscale;
+        split3_x8(qv[s], qb[s]);
+    }
+    return qpix;
+}
+
+template <int D, bool MASKED>
+__device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned char* lds, int wi, int head,
+                                              const u32x4 (&qb)[2][3], int qpix)
+{
+    using X = AttnXShape<D>;
+    constexpr int NKT = X::NK / 32;
+    const unsigned short* Kp = (const unsigned short*)lds;
+    const unsigned short* Vp = Kp + 3 * X::KPL;
+    const float* Tb = (const float*)(Vp + 3 * X::VPL);
+
+    const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ql = lane & 31, h = lane >> 5;
+    const int q = wave * 32 + ql;
+    const int qy = q >> 4, qx = q & 15;
+    const int sw_rbase = 960 - ((qy + 15) * 31 + qx + 15 - 4 * h);
+    const float NEG = -100.0f * HAT_LOG2E;
+    const bool mrow = MASKED && wy == p.ny - 1;
+    const bool mcol = MASKED && wx == p.nx - 1;
+    const bool r_lo = mrow && (qy & 8), r_hi = mrow && !(qy & 8);
+    const bool c_lo = mcol && (qx & 8), c_hi = mcol && !(qx & 8);
+    const float madd[2][2] = {{(r_lo || c_lo) ? NEG : 0.0f, (r_lo || c_hi) ? NEG : 0.0f},
+                              {(r_hi || c_lo) ? NEG : 0.0f, (r_hi || c_hi) ? NEG : 0.0f}};
+    static_assert(D < 32, "a spare V^T row is needed");
+    constexpr int RH = (D % 8) / 4, RR = (D / 8) * 4 + D % 4;
+
+    // The lane's V^T row (dims past D read row D: their outputs are not used)
+    // and K row. For D = 24 the second step's upper lane half reads the next
+    // key's first dims, multiplied by the zeros of its q operand.
+    const unsigned short* vrow = Vp + (ql < D ? ql : D) * X::VS + 8 * h;
+    const unsigned short* krow = Kp + ql * X::KS + 8 * h;
+
+    f32x16 o;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+    float mrun = -INFINITY;
+
+#pragma unroll 1
+    for (int kt = 0; kt < NKT; ++kt) {
+        // S^T = bias (+ mask) + K Q^T
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int key0 = kt * 32 + (i >> 2) * 8 + (i & 3);
+            const int ky = key0 >> 4, kx = key0 & 15;
+            float b = Tb[sw_rbase + (ky * 31 + kx)];
+            if (MASKED) b += madd[(ky >> 3) & 1][(kx >> 3) & 1];
+            s[i] = b;
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            u32x4 ka[3];
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) ka[pl] = *(const u32x4*)(krow + pl * X::KPL + kt * 32 * X::KS + 16 * st);
+            s = mfma6(ka, qb[st], s);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        if (kt == 0 || __any(mx > mrun + 8.0f)) {  // wave-uniform
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mnew = fmaxf(mrun, mx);
+            const float corr = fast_exp2(mrun - mnew);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[i] *= corr;
+            mrun = mnew;
+        }
+        // O^T += V^T P^T, P = exp2(S - base): the B operand of step st is
+        // registers 8st .. 8st+7, split.
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(s[8 * st + j] - mrun);
+            u32x4 pb[3], va[3];
+            split3_x8(pv, pb);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) va[pl] = *(const u32x4*)(vrow + pl * X::VPL + kt * 32 + 16 * st);
+            o = mfma6(va, pb, o);
+        }
+    }
+
+    const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
+    const float inv = 1.0f / ltot;
+    float* orow = p.out + (size_t)qpix * p.C + head * D;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+        const int d0 = 8 * i4 + 4 * h;
+        if (D % 4 == 0) {
+            if (d0 + 3 < D)
+                *(float4*)(orow + d0) = make_float4(o[i4 * 4] * inv, o[i4 * 4 + 1] * inv,
+                                                    o[i4 * 4 + 2] * inv, o[i4 * 4 + 3] * inv);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (d0 + j < D) orow[d0 + j] = o[i4 * 4 + j] * inv;
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void attnx_item_kernel(const AttnArgs& p, unsigned char* lds)
+{
+    using S = AttnShape<D, false>;
+    using X = AttnXShape<D>;
+    const int wi = blockIdx.x, head = blockIdx.y;
+    if (p.with_gate && wi == 0 && head == 0) {  // block-uniform
+        static_assert(4 * CAB_GATE_LDS <= X::LDS_BYTES, "the gate's scratch fits the item LDS");
+        cab_gate_body<8>(p.gate, (float*)lds);
+        __syncthreads();
+    }
+    if (p.with_se && wi == 0 && head == 0) {  // block-uniform
+        static_assert(4 * SE_GATE_LDS <= X::LDS_BYTES, "the gate's scratch fits the item LDS");
+        se_gate_body<8>(p.se, (float*)lds);
+        __syncthreads();
+    }
+    unsigned short* Kp = (unsigned short*)lds;
+    unsigned short* Vp = Kp + 3 * X::KPL;
+    float* Tb = (float*)(Vp + 3 * X::VPL);
+    u32x4 qb[2][3];
+    int qpix;
+    {
+        typename S::vec ks[S::NE], vs[S::NE];
+        attn_fetch<D, false>(p, wi, head, ks, vs);
+        AttnTableRegs<D, false> tr;
+        attn_table_load<D, false>(p, head, tr);
+        qpix = attnx_query<D>(p, wi, head, qb);
+        attnx_stash<D>(Kp, Vp, ks, vs);
+        attn_table_store<D, false>(Tb, tr);
+    }
+    __syncthreads();
+    if (p.shift > 0 && (wi / p.nx == p.ny - 1 || wi % p.nx == p.nx - 1))
+        attnx_compute<D, true>(p, lds, wi, head, qb, qpix);
+    else
+        attnx_compute<D, false>(p, lds, wi, head, qb, qpix);
+}
+
+#define ATTNX_INST(NAME, D, OCC)                                                             \
+    extern "C" __global__ __launch_bounds__(512, OCC) void NAME(AttnArgs p)                  \
+    {                                                                                        \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[AttnXShape<D>::LDS_BYTES]; \
+        attnx_item_kernel<D>(p, lds);                                                        \
+    }
+
+ATTNX_INST(hat_attnx_sw_d24, 24, 4)
+ATTNX_INST(hat_attnx_sw_d30, 30, 2)

@@ -3,6 +3,7 @@
 //   hipcc --offload-arch=gfx950 --offload-device-only --no-gpu-bundle-output
 #include "cab.hip"
 #include "attn.hip"
+#include "attnx.hip"
 #include "conv.hip"
 #include "gemm.hip"
 #include "mlp.hip"

@@ -194,16 +194,20 @@ int gpu_selftest(std::string* err)
                     p.opad = 4;
                     p.T = T;
                     p.qscale = (float)(1.0 / std::sqrt((double)D) * 1.4426950408889634);
-                    std::string k = std::string(oca ? "hat_attn_oca_d" : "hat_attn_sw_d") + std::to_string(D);
-                    if (attn_persistent(D, oca))  // 3 blocks, so a block walks several items
-                        launch(s, k.c_str(), 3, 1, 1, 512, p);
-                    else
-                        launch(s, k.c_str(), pl.nw(), heads, 1, 512, p);
                     std::vector<double> want = attn_twin(qkv, tab, hp, wp, heads, D, oca, shift);
-                    char nm[128];
-                    snprintf(nm, sizeof nm, "%s %dx%d shift %d", k.c_str(), hp, wp, shift);
-                    check_close(nm, dout.get(), want, 2e-5);
-                    note(nm);
+                    // SW: the FP32-MFMA kernel and the split-bf16 one
+                    for (const char* fam : {oca ? "hat_attn_oca_d" : "hat_attn_sw_d", oca ? "" : "hat_attnx_sw_d"}) {
+                        if (!*fam) continue;
+                        std::string k = std::string(fam) + std::to_string(D);
+                        if (attn_persistent(D, oca))  // 3 blocks, so a block walks several items
+                            launch(s, k.c_str(), 3, 1, 1, 512, p);
+                        else
+                            launch(s, k.c_str(), pl.nw(), heads, 1, 512, p);
+                        char nm[128];
+                        snprintf(nm, sizeof nm, "%s %dx%d shift %d", k.c_str(), hp, wp, shift);
+                        check_close(nm, dout.get(), want, 2e-5);
+                        note(nm);
+                    }
                 }
 
         // ---- GEMM epilogues (n9: the C = 144 family; n12: C = 180). The
