@@ -574,8 +574,8 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
               int heads, int D, bool oca, int shift, const CabGateArgs* gate = nullptr,
               const SeArgs* se = nullptr)
 {
-    if (se && (oca || attn_persistent(D, oca))) throw Error("attention: the SE gate rides on SW launches only");
-    if (gate && (oca || attn_persistent(D, oca))) throw Error("attention: the CAB gate rides on SW launches only");
+    if (se && oca) throw Error("attention: the SE gate rides on SW launches only");
+    if (gate && oca) throw Error("attention: the CAB gate rides on SW launches only");
     if (pl.win != 16 || pl.owin != 24)
         throw Error("attention: the gfx950 kernels are built for window 16 / overlap window 24");
     // The kernels wrap a rolled coordinate once, upward, and build the SW-MSA
@@ -585,10 +585,18 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
         throw Error("attention: shift " + std::to_string(shift) + " is not supported (0" +
                     (oca ? "" : " or " + std::to_string(pl.shift)) + ")");
     const char* name = nullptr;
-    // SW: the split-bf16 kernels (attnx.hip); OCA: FP32 MFMA (attn.hip)
-    if (D == 24) name = oca ? "hat_attn_oca_d24" : "hat_attnx_sw_d24";
-    else if (D == 30) name = oca ? "hat_attn_oca_d30" : "hat_attnx_sw_d30";
-    else throw Error("attention: head_dim " + std::to_string(D) + " has no kernel (24 and 30 do)");
+    // The split-bf16 kernels (attnx.hip), except OCA at head_dim 30, whose
+    // persistent split-bf16 form spills: there the FP32-MFMA item kernel (attn.hip).
+    bool persistent = false;
+    if (D == 24) {
+        name = oca ? "hat_attnx_oca_d24" : "hat_attnx_sw_d24";
+        persistent = attnx_persistent(oca);
+    } else if (D == 30) {
+        name = oca ? "hat_attn_oca_d30" : "hat_attnx_sw_d30";
+        persistent = oca ? attn_persistent(D, oca) : attnx_persistent(oca);
+    } else {
+        throw Error("attention: head_dim " + std::to_string(D) + " has no kernel (24 and 30 do)");
+    }
     AttnArgs p{};
     p.qkv = qkv;
     p.table = table;
@@ -613,7 +621,7 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
         p.with_se = 1;
         p.se = *se;
     }
-    if (attn_persistent(D, oca)) {
+    if (persistent) {
         static const int cus = std::max(1, Runtime::get().cu_count());
         const long items = (long)pl.nw() * heads;
         launch(s, name, (unsigned)std::min<long>(items, cus), 1, 1, 512, p);

@@ -333,6 +333,243 @@ __device__ __forceinline__ void attnx_item_kernel(const AttnArgs& p, unsigned ch
         attnx_compute<D, false>(p, lds, wi, head, qb, qpix);
 }
 
+// ---------------------------------------------------------------------------
+// OCA (overlapping cross-attention: 576 keys of the 24x24 unfold with padding
+// 4, zero outside the plane, biased and unmasked; hat_arch.py:373-427,
+// cpu.rs:852-900). The three-plane K and V^T of 576 keys would need 177 KB of
+// LDS, so an item runs as two halves of 288 keys (key rows 0-11, 12-23) that
+// share the online softmax. The kernel is persistent (one block per CU) over
+// the items, head-major: while one half computes, the next half's K and V
+// travel through registers, and go to LDS between two barriers; the bias
+// table is reloaded only when the head changes.
+
+template <int D>
+struct AttnXOcaShape {
+    static constexpr int NK = 288;                    // keys per half
+    static constexpr int KS = D == 24 ? 24 : 40;
+    static constexpr int VS = NK + 8;
+    static constexpr int KPL = NK * KS, VPL = (D + 1) * VS;
+    static constexpr int TROWS = 1521;
+    static constexpr int LDS_BYTES = 2 * 3 * (KPL + VPL) + 4 * TROWS;
+    static constexpr int U = D % 4 == 0 ? 4 : 2;       // floats per staging unit
+    static constexpr int NE = (NK * D / U + 511) / 512;
+    using vec = typename pick_t<U == 4, float4, float2>::type;
+};
+
+// This thread's share of half `half` of item (wi, head): K and V units.
+template <int D>
+__device__ __forceinline__ void attnx_oca_fetch(const AttnArgs& p, int wi, int head, int half,
+                                                typename AttnXOcaShape<D>::vec (&ks)[AttnXOcaShape<D>::NE],
+                                                typename AttnXOcaShape<D>::vec (&vs)[AttnXOcaShape<D>::NE])
+{
+    using X = AttnXOcaShape<D>;
+    using vec = typename X::vec;
+    constexpr int PER_KEY = D / X::U;
+    const float* Kg = p.qkv + (size_t)(p.heads + head) * p.T * D;
+    const float* Vg = p.qkv + (size_t)(2 * p.heads + head) * p.T * D;
+#pragma unroll
+    for (int i = 0; i < X::NE; ++i) {
+        const int e = threadIdx.x + i * 512;
+        vec kv{}, vv{};
+        if (e < X::NK * PER_KEY) {
+            const int kl = e / PER_KEY, d = (e - kl * PER_KEY) * X::U;
+            const int pix = attn_key_pixel<true>(p, wi, half * X::NK + kl);
+            if (pix >= 0) {
+                kv = *(const vec*)(Kg + (size_t)pix * D + d);
+                vv = *(const vec*)(Vg + (size_t)pix * D + d);
+            }
+        }
+        ks[i] = kv;
+        vs[i] = vv;
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void attnx_oca_stash(unsigned short* Kp, unsigned short* Vp,
+                                                const typename AttnXOcaShape<D>::vec (&ks)[AttnXOcaShape<D>::NE],
+                                                const typename AttnXOcaShape<D>::vec (&vs)[AttnXOcaShape<D>::NE])
+{
+    using X = AttnXOcaShape<D>;
+    constexpr int PER_KEY = D / X::U;
+#pragma unroll
+    for (int i = 0; i < X::NE; ++i) {
+        const int e = threadIdx.x + i * 512;
+        if (e < X::NK * PER_KEY) {
+            const int k = e / PER_KEY, d = (e - k * PER_KEY) * X::U;
+            float kv[4], vv[4];
+            if constexpr (X::U == 4) {
+                kv[0] = ks[i].x, kv[1] = ks[i].y, kv[2] = ks[i].z, kv[3] = ks[i].w;
+                vv[0] = vs[i].x, vv[1] = vs[i].y, vv[2] = vs[i].z, vv[3] = vs[i].w;
+            } else {
+                kv[0] = ks[i].x, kv[1] = ks[i].y, kv[2] = kv[3] = 0.f;
+                vv[0] = vs[i].x, vv[1] = vs[i].y, vv[2] = vv[3] = 0.f;
+            }
+            const int pos = vpos(k);
+#pragma unroll
+            for (int j = 0; j < X::U; j += 2) {
+                unsigned k0, k1, k2, v0, v1, v2;
+                split3_pk(kv[j], kv[j + 1], k0, k1, k2);
+                *(unsigned*)(Kp + 0 * X::KPL + k * X::KS + d + j) = k0;
+                *(unsigned*)(Kp + 1 * X::KPL + k * X::KS + d + j) = k1;
+                *(unsigned*)(Kp + 2 * X::KPL + k * X::KS + d + j) = k2;
+                split3_pk(vv[j], vv[j + 1], v0, v1, v2);
+                Vp[0 * X::VPL + (d + j) * X::VS + pos] = (unsigned short)v0;
+                Vp[0 * X::VPL + (d + j + 1) * X::VS + pos] = (unsigned short)(v0 >> 16);
+                Vp[1 * X::VPL + (d + j) * X::VS + pos] = (unsigned short)v1;
+                Vp[1 * X::VPL + (d + j + 1) * X::VS + pos] = (unsigned short)(v1 >> 16);
+                Vp[2 * X::VPL + (d + j) * X::VS + pos] = (unsigned short)v2;
+                Vp[2 * X::VPL + (d + j + 1) * X::VS + pos] = (unsigned short)(v2 >> 16);
+            }
+        }
+    }
+}
+
+// One half's 9 key tiles onto the running (o, mrun) of the item.
+template <int D>
+__device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int half, const u32x4 (&qb)[2][3],
+                                                  f32x16& o, float& mrun)
+{
+    using X = AttnXOcaShape<D>;
+    constexpr int NKT = X::NK / 32;
+    const unsigned short* Kp = (const unsigned short*)lds;
+    const unsigned short* Vp = Kp + 3 * X::KPL;
+    const float* Tb = (const float*)(Vp + 3 * X::VPL);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ql = lane & 31, h = lane >> 5;
+    const int q = wave * 32 + ql;
+    const int qy = q >> 4, qx = q & 15;
+    // idx = (ky*39 + kx) - (qy*39 + qx) + 600 on the rotated table (attn.hip)
+    const int oca_base = 600 - (qy * 39 + qx);
+    const unsigned short* vrow = Vp + (ql < D ? ql : D) * X::VS + 8 * h;
+    const unsigned short* krow = Kp + ql * X::KS + 8 * h;
+#pragma unroll 1
+    for (int kt = 0; kt < NKT; ++kt) {
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int key = half * X::NK + kt * 32 + (i >> 2) * 8 + (i & 3) + 4 * h;
+            const int ky = (int)((unsigned)key / 24u);
+            s[i] = Tb[oca_base + key + 15 * ky];
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            u32x4 ka[3];
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) ka[pl] = *(const u32x4*)(krow + pl * X::KPL + kt * 32 * X::KS + 16 * st);
+            s = mfma6(ka, qb[st], s);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        if ((half == 0 && kt == 0) || __any(mx > mrun + 8.0f)) {  // wave-uniform
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mnew = fmaxf(mrun, mx);
+            const float corr = fast_exp2(mrun - mnew);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[i] *= corr;
+            mrun = mnew;
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(s[8 * st + j] - mrun);
+            u32x4 pb[3], va[3];
+            split3_x8(pv, pb);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) va[pl] = *(const u32x4*)(vrow + pl * X::VPL + kt * 32 + 16 * st);
+            o = mfma6(va, pb, o);
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned char* lds)
+{
+    using X = AttnXOcaShape<D>;
+    unsigned short* Kp = (unsigned short*)lds;
+    unsigned short* Vp = Kp + 3 * X::KPL;
+    float* Tb = (float*)(Vp + 3 * X::VPL);
+    const int nw = p.nx * p.ny, nitems = nw * p.heads;
+    int item = blockIdx.x;
+    if (item >= nitems) return;  // whole block, before any barrier
+    // Written once: row D of V^T (ones in the high plane), K dims 30, 31 (D = 30).
+    for (int e = threadIdx.x; e < 3 * (X::NK / 2); e += 512) {
+        const int pl = e / (X::NK / 2), k2 = e - pl * (X::NK / 2);
+        *(unsigned*)(Vp + pl * X::VPL + D * X::VS + 2 * k2) = pl == 0 ? 0x3f803f80u : 0u;
+    }
+    if (D == 30) {
+        for (int e = threadIdx.x; e < 3 * X::NK; e += 512) {
+            const int pl = e / X::NK, k = e - pl * X::NK;
+            *(unsigned*)(Kp + pl * X::KPL + k * X::KS + 30) = 0u;
+        }
+    }
+    const int lane = threadIdx.x & 63;
+    const int ql = lane & 31, h = lane >> 5;
+    constexpr int RH = (D % 8) / 4, RR = (D / 8) * 4 + D % 4;
+    typename X::vec ks[X::NE], vs[X::NE];
+    int head = item / nw, wi = item - head * nw;
+    attnx_oca_fetch<D>(p, wi, head, 0, ks, vs);
+    u32x4 qb[2][3];
+    int qpix = attnx_query<D>(p, wi, head, qb);
+    int table_head = -1;
+    f32x16 o;
+    float mrun = -INFINITY;
+    while (true) {
+        const int next = item + gridDim.x;
+        const int nhead = next / nw, nwi = next - nhead * nw;
+#pragma unroll 1
+        for (int half = 0; half < 2; ++half) {
+            __syncthreads();  // every read of the previous half's LDS is done
+            attnx_oca_stash<D>(Kp, Vp, ks, vs);
+            if (head != table_head) {  // block-uniform
+                attn_table<D, true>(p, Tb, head);
+                table_head = head;
+            }
+            __syncthreads();
+            if (half == 0) attnx_oca_fetch<D>(p, wi, head, 1, ks, vs);
+            else if (next < nitems) attnx_oca_fetch<D>(p, nwi, nhead, 0, ks, vs);
+            if (half == 0) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+                mrun = -INFINITY;
+            }
+            attnx_oca_compute<D>(lds, half, qb, o, mrun);
+        }
+        const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
+        const float inv = 1.0f / ltot;
+        float* orow = p.out + (size_t)qpix * p.C + head * D;
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const int d0 = 8 * i4 + 4 * h;
+            if (D % 4 == 0) {
+                if (d0 + 3 < D)
+                    *(float4*)(orow + d0) = make_float4(o[i4 * 4] * inv, o[i4 * 4 + 1] * inv,
+                                                        o[i4 * 4 + 2] * inv, o[i4 * 4 + 3] * inv);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (d0 + j < D) orow[d0 + j] = o[i4 * 4 + j] * inv;
+            }
+        }
+        if (next >= nitems) break;
+        item = next;
+        head = nhead;
+        wi = nwi;
+        qpix = attnx_query<D>(p, wi, head, qb);
+    }
+}
+
+#define ATTNX_OCA_INST(NAME, D)                                                                 \
+    extern "C" __global__ __launch_bounds__(512, 2) void NAME(AttnArgs p)                       \
+    {                                                                                           \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[AttnXOcaShape<D>::LDS_BYTES]; \
+        attnx_oca_kernel<D>(p, lds);                                                            \
+    }
+
+ATTNX_OCA_INST(hat_attnx_oca_d24, 24)
+ATTNX_OCA_INST(hat_attnx_oca_d30, 30)
+
 #define ATTNX_INST(NAME, D, OCC)                                                             \
     extern "C" __global__ __launch_bounds__(512, OCC) void NAME(AttnArgs p)                  \
     {                                                                                        \

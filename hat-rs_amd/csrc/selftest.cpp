@@ -196,10 +196,10 @@ int gpu_selftest(std::string* err)
                     p.qscale = (float)(1.0 / std::sqrt((double)D) * 1.4426950408889634);
                     std::vector<double> want = attn_twin(qkv, tab, hp, wp, heads, D, oca, shift);
                     // SW: the FP32-MFMA kernel and the split-bf16 one
-                    for (const char* fam : {oca ? "hat_attn_oca_d" : "hat_attn_sw_d", oca ? "" : "hat_attnx_sw_d"}) {
-                        if (!*fam) continue;
+                    for (const char* fam : {oca ? "hat_attn_oca_d" : "hat_attn_sw_d", oca ? "hat_attnx_oca_d" : "hat_attnx_sw_d"}) {
                         std::string k = std::string(fam) + std::to_string(D);
-                        if (attn_persistent(D, oca))  // 3 blocks, so a block walks several items
+                        const bool xk = k.find("attnx") != std::string::npos;
+                        if (xk ? attnx_persistent(oca) : attn_persistent(D, oca))  // 3 blocks, so a block walks several items
                             launch(s, k.c_str(), 3, 1, 1, 512, p);
                         else
                             launch(s, k.c_str(), pl.nw(), heads, 1, 512, p);
