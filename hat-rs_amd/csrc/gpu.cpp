@@ -23,6 +23,47 @@ std::vector<float> pack_linear(const float* w, int N, int K, int* Kp)
     return out;
 }
 
+namespace {
+// float -> bf16, round to nearest even (NaN kept a NaN)
+unsigned short bf16_rne(float x)
+{
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (unsigned short)(u >> 16);
+}
+float bf16_float(unsigned short h)
+{
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+}  // namespace
+
+std::vector<unsigned short> pack_linear_x(const float* w, int N, int K)
+{
+    constexpr int BN = 144, KS = 152;
+    // per slice: 3 planes of [BN][KS], zero-padded to whole 1 KB loads
+    constexpr size_t SLICE = ((size_t)3 * BN * KS / 8 + 63) / 64 * 64 * 8;
+    if (K != 144 || N % BN != 0) throw Error("pack_linear_x: needs K = 144 and N a multiple of 144");
+    std::vector<unsigned short> out((size_t)(N / BN) * SLICE, 0);
+    for (int n = 0; n < N; ++n)
+        for (int k = 0; k < K; ++k) {
+            const float x = w[(size_t)n * K + k];
+            const unsigned short h0 = bf16_rne(x);
+            const float r1 = x - bf16_float(h0);
+            const unsigned short h1 = bf16_rne(r1);
+            const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+            const size_t base = (size_t)(n / BN) * SLICE + (size_t)(n % BN) * KS + k;
+            out[base] = h0;
+            out[base + (size_t)BN * KS] = h1;
+            out[base + (size_t)2 * BN * KS] = h2;
+        }
+    return out;
+}
+
 // [CO][CI][3][3] -> [CIp/16][9][COp][16]; with r > 0 the output channels are
 // permuted so that channel o = c*r*r + i*r + j lands at o' = (i*r + j)*Cf + c
 // (Cf = CO / r^2), which lets the conv store four consecutive o' as four
@@ -187,6 +228,14 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
     p.hdim = hdim;
     p.cscale = cscale;
     p.eps = 1e-5f;
+    if (epi == EPI_QKV && L.wx && L.K == 144 && L.N == 432 && heads == 6 && hdim == 24 && lda == 144) {
+        // split-bf16 qkv (gemmx.hip): one block per CU walking 256-token tiles
+        static const int cus = std::max(1, Runtime::get().cu_count());
+        p.w = (const float*)L.wx;
+        const long ntiles = (M + 255) / 256;
+        launch(s, "hat_gemmx_qkv", (unsigned)std::max(1L, std::min<long>(ntiles, cus)), 1, 1, 512, p);
+        return;
+    }
     int wbn = 0;
     if (const char* ws = gemm_ws_kernel(L, epi, &wbn)) {
         // One block per CU (its 85 or 150 KB weight slice fills the LDS); the
@@ -654,6 +703,16 @@ float* GpuBackend::upload(const float* src, size_t n)
     return d;
 }
 
+void* GpuBackend::upload_bytes(const void* src, size_t bytes)
+{
+    Runtime& rt = Runtime::get();
+    void* d = rt.alloc(bytes);
+    owned_.push_back(d);
+    rt.h2d(d, src, bytes);
+    weight_bytes_ += bytes;
+    return d;
+}
+
 void GpuBackend::upload_raw(const std::string& name)
 {
     const TensorInfo& ti = wt_.info(name);
@@ -669,6 +728,10 @@ void GpuBackend::upload_linear(const std::string& name)
     std::vector<float> pk = pack_linear(wt_.t(name + ".weight"), L.N, L.K, &L.Kp);
     L.w = upload(pk.data(), pk.size());
     L.b = upload(wt_.t(name + ".bias"), L.N);
+    if (L.K == 144 && L.N == 432 && name.size() > 4 && name.compare(name.size() - 4, 4, ".qkv") == 0) {
+        std::vector<unsigned short> x = pack_linear_x(wt_.t(name + ".weight"), L.N, L.K);
+        L.wx = (unsigned short*)upload_bytes(x.data(), x.size() * sizeof(unsigned short));
+    }
     lin_[name] = L;
 }
 

@@ -26,6 +26,9 @@ public:
 struct DevLinear {
     float* w = nullptr;  // [N][Kp]
     float* b = nullptr;  // [N]
+    // K = 144, N a multiple of 144: the same weights split into three bf16
+    // planes per 144-column slice (pack_linear_x), for the split-bf16 kernels
+    unsigned short* wx = nullptr;
     int N = 0, K = 0, Kp = 0;
 };
 
@@ -55,6 +58,10 @@ struct DevConv {
 
 // Host-side repacking (also used by the selftest and the op entry points).
 std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
+// [N][144] -> per 144-column slice, 3 parts of [144 rows][152] bf16 (then
+// zeros to a multiple of 1 KB): w = p0 + p1 + p2, each part the round-to-
+// nearest bf16 of what the earlier ones leave; columns 144..151 zero.
+std::vector<unsigned short> pack_linear_x(const float* w, int N, int K);
 std::vector<float> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);
@@ -139,6 +146,7 @@ private:
     void free_batch();
 
     float* upload(const float* src, size_t n);
+    void* upload_bytes(const void* src, size_t bytes);
     void upload_raw(const std::string& name);
     void upload_linear(const std::string& name);
     void upload_conv(const std::string& name, int r = 0);

@@ -6,6 +6,7 @@
 #include "attnx.hip"
 #include "conv.hip"
 #include "gemm.hip"
+#include "gemmx.hip"
 #include "mlp.hip"
 #include "habtail.hip"
 #include "convw.hip"

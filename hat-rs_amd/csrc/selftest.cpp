@@ -296,6 +296,19 @@ int gpu_selftest(std::string* err)
                 check_close(k + " C " + std::to_string(C), dout.get(), want, 3e-5);
                 if (lnout) check_close(k + " C " + std::to_string(C) + " layernorm", dxn.get(), wxn, 5e-5);
                 note(k + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
+                if (ws && C == 144 && epi == EPI_QKV) {
+                    // the split-bf16 form on the same inputs: 2 blocks over 3
+                    // row tiles, the last one partial
+                    std::vector<unsigned short> px = pack_linear_x(w.data(), N, K);
+                    Dev dwx(std::vector<float>((px.size() + 1) / 2)), dout2((size_t)M * N);
+                    rt.h2d(dwx.p, px.data(), px.size() * sizeof(unsigned short));
+                    GemmArgs px2 = p;
+                    px2.w = dwx.p;
+                    px2.out = dout2.p;
+                    launch(s, "hat_gemmx_qkv", 2, 1, 1, 512, px2);
+                    check_close("hat_gemmx_qkv C 144", dout2.get(), want, 3e-5);
+                    note("hat_gemmx_qkv C 144 M " + std::to_string(M) + " K 144");
+                }
         };
         for (int C : {144, 180})
             for (int epi : epis) gemm_case(C, epi, false);
