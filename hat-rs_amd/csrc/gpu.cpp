@@ -42,6 +42,25 @@ float bf16_float(unsigned short h)
 }
 }  // namespace
 
+// Rows [N][K] of w (row stride ldw) as three bf16 planes [N][KS] at dst
+// (plane stride N * KS): x = h0 + h1 + h2, each part the RNE of what the
+// parts before it leave; k >= K stays zero.
+static void split_planes(const float* w, int N, int K, int ldw, int KS, unsigned short* dst)
+{
+    for (int n = 0; n < N; ++n)
+        for (int k = 0; k < K; ++k) {
+            const float x = w[(size_t)n * ldw + k];
+            const unsigned short h0 = bf16_rne(x);
+            const float r1 = x - bf16_float(h0);
+            const unsigned short h1 = bf16_rne(r1);
+            const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+            unsigned short* d = dst + (size_t)n * KS + k;
+            d[0] = h0;
+            d[(size_t)N * KS] = h1;
+            d[(size_t)2 * N * KS] = h2;
+        }
+}
+
 std::vector<unsigned short> pack_linear_x(const float* w, int N, int K)
 {
     constexpr int BN = 144, KS = 152;
@@ -49,19 +68,36 @@ std::vector<unsigned short> pack_linear_x(const float* w, int N, int K)
     constexpr size_t SLICE = ((size_t)3 * BN * KS / 8 + 63) / 64 * 64 * 8;
     if (K != 144 || N % BN != 0) throw Error("pack_linear_x: needs K = 144 and N a multiple of 144");
     std::vector<unsigned short> out((size_t)(N / BN) * SLICE, 0);
-    for (int n = 0; n < N; ++n)
-        for (int k = 0; k < K; ++k) {
-            const float x = w[(size_t)n * K + k];
-            const unsigned short h0 = bf16_rne(x);
-            const float r1 = x - bf16_float(h0);
-            const unsigned short h1 = bf16_rne(r1);
-            const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
-            const size_t base = (size_t)(n / BN) * SLICE + (size_t)(n % BN) * KS + k;
-            out[base] = h0;
-            out[base + (size_t)BN * KS] = h1;
-            out[base + (size_t)2 * BN * KS] = h2;
-        }
+    for (int s = 0; s < N / BN; ++s) split_planes(w + (size_t)s * BN * K, BN, K, K, KS, &out[(size_t)s * SLICE]);
     return out;
+}
+
+// fc1 output tile t, row 4g + r (lane group g, register r) -> hidden unit
+// within a 96-unit third (tailx.hip): fc2's 32-k step s then finds units
+// 32 s + 8 g .. +7 in tiles 2 s and 2 s + 1 of lane group g.
+static int mlpx_unit(int row)
+{
+    const int t = row / 16, g = (row % 16) / 4, r = row % 4;
+    return 32 * (t / 2) + 8 * g + 4 * (t % 2) + r;
+}
+
+void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
+                std::vector<float>* b1x)
+{
+    constexpr int C = 144, H = 288;
+    static_assert(3 * MX_HID * MX_KS1 <= MX_SLICE && 3 * C * MX_KS2 <= MX_SLICE && MX_SLICE % 512 == 0, "slot");
+    std::vector<float> f1((size_t)MX_HID * C);
+    w->assign((size_t)6 * MX_SLICE, 0);
+    b1x->assign(H, 0.0f);
+    for (int q = 0; q < H / MX_HID; ++q) {
+        for (int row = 0; row < MX_HID; ++row) {
+            const int u = q * MX_HID + mlpx_unit(row);
+            memcpy(&f1[(size_t)row * C], w1 + (size_t)u * C, C * sizeof(float));
+            (*b1x)[q * MX_HID + row] = b1[u];
+        }
+        split_planes(f1.data(), MX_HID, C, C, MX_KS1, &(*w)[(size_t)(2 * q) * MX_SLICE]);
+        split_planes(w2 + q * MX_HID, C, MX_HID, H, MX_KS2, &(*w)[(size_t)(2 * q + 1) * MX_SLICE]);
+    }
 }
 
 // [CO][CI][3][3] -> [CIp/16][9][COp][16]; with r > 0 the output channels are
@@ -404,6 +440,52 @@ void run_hab_tail(hipStream_t s, const DevLinear& proj, const DevLinear& fc1, co
     launch(s, cab ? "hat_hab_tail" : "hat_ocab_tail", (unsigned)g, 1, 1, MLP_WAVES * 64, p);
 }
 
+// The tail on split-bf16 (tailx.hip): x' = res + a . Wp^T (+ CAB: the gated
+// conv2 of t1) + bias, xn = norm2(x') [hat_projx(_cab)]; out = x' + MLP(xn)
+// (+ with nw: xn = norm_next(out)) [hat_mlpx(_ln)]. out may alias res.
+void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& mlp, const float* b2, const float* a,
+               const float* res, float* out, float* xn, const float* t1, const float* w2g, const float* bias,
+               const float* n2w, const float* n2b, const float* nw, const float* nb, int H, int W)
+{
+    if (!proj.wx || proj.K != 144 || proj.N != 144) throw Error("tailx: needs the pre-split 144 x 144 projection");
+    if (cab && (!t1 || !w2g)) throw Error("tailx: the CAB form needs t1 and the gated conv2 weights");
+    const long M = (long)H * W;
+    if (M > 0x7fffffffL) throw Error("tailx: too many rows");
+    static const int cus = std::max(1, Runtime::get().cu_count());
+    const unsigned g = (unsigned)std::max(1L, std::min<long>((M + 255) / 256, cus));
+    TailXArgs p{};
+    p.a = a;
+    p.res = res;
+    p.out = out;
+    p.xn = xn;
+    p.w = proj.wx;
+    p.bias = bias;
+    p.w2g = w2g;
+    p.t1 = t1;
+    p.nw = n2w;
+    p.nb = n2b;
+    p.M = (int)M;
+    p.H = H;
+    p.W = W;
+    p.eps = 1e-5f;
+    launch(s, cab ? "hat_projx_cab" : "hat_projx", g, 1, 1, 512, p);
+    TailXArgs q{};
+    q.a = xn;
+    q.res = out;
+    q.out = out;
+    q.xn = nw ? xn : nullptr;
+    q.w = mlp.w;
+    q.bias = mlp.b1;
+    q.b2 = b2;
+    q.nw = nw;
+    q.nb = nb;
+    q.M = (int)M;
+    q.H = H;
+    q.W = W;
+    q.eps = 1e-5f;
+    launch(s, nw ? "hat_mlpx_ln" : "hat_mlpx", g, 1, 1, 512, q);
+}
+
 // The channel-attention gate from the CAB conv's per-tile column sums:
 // reduce in fixed row blocks, then squeeze-excite.
 // With `defer` (C <= 192, sq <= 64), nothing is launched: *defer gets the
@@ -728,11 +810,30 @@ void GpuBackend::upload_linear(const std::string& name)
     std::vector<float> pk = pack_linear(wt_.t(name + ".weight"), L.N, L.K, &L.Kp);
     L.w = upload(pk.data(), pk.size());
     L.b = upload(wt_.t(name + ".bias"), L.N);
-    if (L.K == 144 && L.N == 432 && name.size() > 4 && name.compare(name.size() - 4, 4, ".qkv") == 0) {
+    auto ends = [&](const char* t) {
+        const size_t n = strlen(t);
+        return name.size() >= n && name.compare(name.size() - n, n, t) == 0;
+    };
+    if (L.K == 144 && ((L.N == 432 && ends(".qkv")) || (L.N == 144 && ends("proj")))) {
         std::vector<unsigned short> x = pack_linear_x(wt_.t(name + ".weight"), L.N, L.K);
         L.wx = (unsigned short*)upload_bytes(x.data(), x.size() * sizeof(unsigned short));
     }
     lin_[name] = L;
+}
+
+// The C = 144 MLP, pre-split for hat_mlpx (other widths keep the FP32 kernels).
+void GpuBackend::upload_mlpx(const std::string& name)
+{
+    const TensorInfo& t1 = wt_.info(name + ".fc1.weight");
+    const TensorInfo& t2 = wt_.info(name + ".fc2.weight");
+    if (t1.shape != std::vector<size_t>{288, 144} || t2.shape != std::vector<size_t>{144, 288}) return;
+    std::vector<unsigned short> w;
+    std::vector<float> b1x;
+    pack_mlp_x(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w, &b1x);
+    DevMlpX m;
+    m.w = (unsigned short*)upload_bytes(w.data(), w.size() * sizeof(unsigned short));
+    m.b1 = upload(b1x.data(), b1x.size());
+    mlpx_[name] = m;
 }
 
 void GpuBackend::upload_conv(const std::string& name, int r)
@@ -788,6 +889,7 @@ GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
             upload_linear(p + ".attn.proj");
             upload_linear(p + ".mlp.fc1");
             upload_linear(p + ".mlp.fc2");
+            upload_mlpx(p + ".mlp");
             if (cab_fold_) {
                 const std::string c = p + ".conv_block.cab.";
                 for (const char* n : {"0.bias", "2.weight", "2.bias"}) upload_raw(c + n);
@@ -815,6 +917,7 @@ GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
         upload_linear(p + ".proj");
         upload_linear(p + ".mlp.fc1");
         upload_linear(p + ".mlp.fc2");
+        upload_mlpx(p + ".mlp");
         upload_conv(L + ".conv");
     }
     upload_raw("norm.weight");
@@ -996,6 +1099,14 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
                 a_.w2g, a_.bias2, a_.gate, &gate);
         gemm(lin_.at(p + ".attn.qkv"), a_.xn, C, T, a_.qkv, 0, EPI_QKV);
         attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, &gate);
+        auto mx = mlpx_.find(p + ".mlp");
+        if (proj.wx && mx != mlpx_.end()) {
+            // split-bf16: proj + gated conv2 + shortcut + norm2, then the MLP + next norm1
+            run_tailx(stream_, true, proj, mx->second, lin_.at(p + ".mlp.fc2").b, a_.ao, x_in, x_out, a_.xn, a_.t1,
+                      a_.w2g, a_.bias2, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
+                      raw_.at(next_norm + ".weight"), raw_.at(next_norm + ".bias"), H, W);
+            return;
+        }
         run_hab_tail(stream_, proj, lin_.at(p + ".mlp.fc1"), lin_.at(p + ".mlp.fc2"), a_.ao, x_in, x_out, a_.xn, a_.t1,
                      a_.w2g, a_.bias2, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
                      raw_.at(next_norm + ".weight"), raw_.at(next_norm + ".bias"), H, W);
@@ -1032,6 +1143,13 @@ void GpuBackend::ocab(int stage, float* x)
     attention(p + ".relative_position_bias_table", true, 0);
     const DevLinear& proj = lin_.at(p + ".proj");
     const DevLinear &fc1 = lin_.at(p + ".mlp.fc1"), &fc2 = lin_.at(p + ".mlp.fc2");
+    auto mx = mlpx_.find(p + ".mlp");
+    if (proj.wx && mx != mlpx_.end()) {
+        // split-bf16: projection + shortcut + norm2, then the MLP + residual
+        run_tailx(stream_, false, proj, mx->second, fc2.b, a_.ao, x, x, a_.xn, nullptr, nullptr, proj.b,
+                  raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"), nullptr, nullptr, plan_.hp, plan_.wp);
+        return;
+    }
     if (hab_tail_fits(proj, fc1, fc2)) {
         // projection + shortcut + norm2 + MLP + residual in one kernel
         run_hab_tail(stream_, proj, fc1, fc2, a_.ao, x, x, nullptr, nullptr,

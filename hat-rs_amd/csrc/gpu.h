@@ -49,6 +49,12 @@ struct DevCab {
 // rows 54..63 zero.
 std::vector<float> pack_cab_conv1(const float* w);
 
+// hat_mlpx's weights: the packed slices and b1 in fc1's row order.
+struct DevMlpX {
+    unsigned short* w = nullptr;
+    float* b1 = nullptr;
+};
+
 struct DevConv {
     float* w = nullptr;  // [CIp/16][9][COp][16]
     float* b = nullptr;  // [COp]
@@ -62,6 +68,13 @@ std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
 // zeros to a multiple of 1 KB): w = p0 + p1 + p2, each part the round-to-
 // nearest bf16 of what the earlier ones leave; columns 144..151 zero.
 std::vector<unsigned short> pack_linear_x(const float* w, int N, int K);
+// The C = 144 MLP (fc1 [288][144] + b1, fc2 [144][288]) for hat_mlpx: per
+// third of the hidden layer two MX_SLICE slots of three bf16 planes - fc1's
+// 96 rows [96][MX_KS1], then fc2 on those units [144][MX_KS2] - with fc1's
+// rows (and b1) in the order that leaves its output in fc2's operand layout
+// (tailx.hip).
+void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
+                std::vector<float>* b1x);
 std::vector<float> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);
@@ -107,6 +120,7 @@ private:
     std::map<std::string, DevLinear> lin_;
     std::map<std::string, DevConv> conv_;
     std::map<std::string, DevCab> cab_;
+    std::map<std::string, DevMlpX> mlpx_;  // C = 144 MLPs (blocks and OCABs) for hat_mlpx
     bool cab_fold_ = false;  // the C = 144, 6-channel CAB runs folded
     std::vector<void*> owned_;
     size_t weight_bytes_ = 0;
@@ -150,6 +164,7 @@ private:
     void upload_raw(const std::string& name);
     void upload_linear(const std::string& name);
     void upload_conv(const std::string& name, int r = 0);
+    void upload_mlpx(const std::string& name);
     void ensure_plan(int h, int w);
     void free_plan();
     void run_forward(int h, int w, const float* d_in, float* d_out);

@@ -231,6 +231,35 @@ struct HabTailArgs {
     int ldw1, ldw2;
 };
 
+// The C = 144 HAB / OCAB tail on split-bf16 MFMA as two kernels (tailx.hip):
+// hat_projx(_cab): out = x' = res + a . Wp^T (+ nb(t1) . W2g^T) + bias,
+//                  xn = LN(x') with nw / nb;
+// hat_mlpx(_ln):   out = res + fc2(gelu(fc1(a))) + b2 (+ xn = LN(out)).
+// The split-bf16 MLP (tailx.hip) walks the hidden layer in thirds of 96
+// units: per third one fc1 slice (96 permuted rows x K 144, row stride
+// MX_KS1) and one fc2 slice (144 rows x the third's 96 units, row stride
+// MX_KS2), each three bf16 planes, in MX_SLICE-element slots.
+#define MX_HID 96
+#define MX_KS1 152
+#define MX_KS2 104
+#define MX_SLICE 45056  // >= 3 * max(96 * MX_KS1, 144 * MX_KS2), whole 1 KB loads
+
+struct TailXArgs {
+    const float* a;            // projx: attention output; mlpx: LN2(x') rows
+    const float* res;          // projx: block input; mlpx: x'
+    float* out;                // [M][144] (may alias res)
+    float* xn;                 // projx: LN2(x'); mlpx (LN): the next norm1 (may alias a)
+    const unsigned short* w;   // pre-split weight slices (projx: 1, mlpx: 6)
+    const float* bias;         // projx: bias2 or the projection bias; mlpx: b1, fc1's row order
+    const float* b2;           // mlpx: fc2 bias
+    const float* w2g;          // projx_cab: [144][CAB_K2] gate-scaled conv2 weights
+    const float* t1;           // projx_cab: [M][CAB_CS] CAB conv1 output
+    const float* nw;
+    const float* nb;
+    int M, H, W;               // rows = the H x W plane
+    float eps;
+};
+
 struct LnArgs {
     const float* x;
     float* y;

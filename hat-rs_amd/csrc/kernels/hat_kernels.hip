@@ -7,6 +7,7 @@
 #include "conv.hip"
 #include "gemm.hip"
 #include "gemmx.hip"
+#include "tailx.hip"
 #include "mlp.hip"
 #include "habtail.hip"
 #include "convw.hip"

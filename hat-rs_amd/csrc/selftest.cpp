@@ -625,6 +625,80 @@ int gpu_selftest(std::string* err)
                 const std::vector<float> r2 = dref2.get();
                 check_close("hat_ocab_tail", dout_o.get(), std::vector<double>(r2.begin(), r2.end()), 2e-5);
                 note("hat_ocab_tail (proj + norm2 + MLP) vs the two-kernel path");
+
+                // The split-bf16 tails (tailx.hip) on the same inputs, in place
+                // as the forward runs them (out over the block input, the next
+                // norm over norm2's rows); 2 blocks over 6 row tiles.
+                std::vector<unsigned short> pwx = pack_linear_x(wp.data(), C, C), mwx;
+                std::vector<float> b1x;
+                pack_mlp_x(f1.data(), fb1.data(), f2.data(), &mwx, &b1x);
+                Dev dpwx(std::vector<float>((pwx.size() + 1) / 2)), dmwx(std::vector<float>((mwx.size() + 1) / 2)),
+                    db1x(b1x), dout_x(res), dxn_x((size_t)T * C);
+                Runtime::get().h2d(dpwx.p, pwx.data(), pwx.size() * sizeof(unsigned short));
+                Runtime::get().h2d(dmwx.p, mwx.data(), mwx.size() * sizeof(unsigned short));
+                TailXArgs xa{};
+                xa.a = dao.p;
+                xa.res = dout_x.p;
+                xa.out = dout_x.p;
+                xa.xn = dxn_x.p;
+                xa.w = (const unsigned short*)dpwx.p;
+                xa.bias = dbias2.p;
+                xa.w2g = dw2g.p;
+                xa.t1 = dt1.p;
+                xa.nw = dnw.p;
+                xa.nb = dnb.p;
+                xa.M = T;
+                xa.H = H;
+                xa.W = W;
+                xa.eps = 1e-5f;
+                launch(s, "hat_projx_cab", 2, 1, 1, 512, xa);
+                check_close("hat_projx_cab", dout_x.get(), want, 5e-5);
+                check_close("hat_projx_cab layernorm", dxn_x.get(), wxn, 5e-5);
+                note("hat_projx_cab (split-bf16 proj + folded conv2 + norm2) vs double");
+                TailXArgs xm{};
+                xm.a = dxn_x.p;
+                xm.res = dout_x.p;
+                xm.out = dout_x.p;
+                xm.xn = dxn_x.p;
+                xm.w = (const unsigned short*)dmwx.p;
+                xm.bias = db1x.p;
+                xm.b2 = dfb2.p;
+                xm.nw = dmw.p;
+                xm.nb = dmb.p;
+                xm.M = T;
+                xm.H = H;
+                xm.W = W;
+                xm.eps = 1e-5f;
+                launch(s, "hat_mlpx_ln", 2, 1, 1, 512, xm);
+                check_close("hat_mlpx_ln", dout_x.get(), std::vector<double>(ro.begin(), ro.end()), 2e-5);
+                check_close("hat_mlpx_ln next norm", dxn_x.get(), std::vector<double>(rx.begin(), rx.end()), 2e-5);
+                note("hat_mlpx_ln (split-bf16 MLP + norm) vs the two-kernel path");
+                // The OCAB form over a partial last tile: rows from Mo on stay
+                // the block input.
+                const int Mo = T - 100;
+                Dev dout_ox(res), dxn_ox((size_t)T * C);
+                TailXArgs xo = xa;
+                xo.res = dout_ox.p;
+                xo.out = dout_ox.p;
+                xo.xn = dxn_ox.p;
+                xo.bias = dbp.p;
+                xo.w2g = nullptr;
+                xo.t1 = nullptr;
+                xo.M = Mo;
+                launch(s, "hat_projx", 2, 1, 1, 512, xo);
+                TailXArgs xo2 = xm;
+                xo2.a = dxn_ox.p;
+                xo2.res = dout_ox.p;
+                xo2.out = dout_ox.p;
+                xo2.xn = nullptr;
+                xo2.nw = nullptr;
+                xo2.nb = nullptr;
+                xo2.M = Mo;
+                launch(s, "hat_mlpx", 2, 1, 1, 512, xo2);
+                std::vector<double> wo(r2.begin(), r2.end());
+                for (size_t i = (size_t)Mo * C; i < wo.size(); ++i) wo[i] = res[i];
+                check_close("hat_projx + hat_mlpx", dout_ox.get(), wo, 2e-5);
+                note("hat_projx + hat_mlpx (split-bf16 OCAB tail, partial tile) vs the two-kernel path");
             }
         }
 
