@@ -42,33 +42,35 @@ float bf16_float(unsigned short h)
 }
 }  // namespace
 
-// Rows [N][K] of w (row stride ldw) as three bf16 planes [N][KS] at dst
-// (plane stride N * KS): x = h0 + h1 + h2, each part the RNE of what the
-// parts before it leave; k >= K stays zero.
-static void split_planes(const float* w, int N, int K, int ldw, int KS, unsigned short* dst)
+// Rows [N][K] of w (row stride ldw), N <= 144, as weight chunks at dst: per
+// 32-k step s, three bf16 planes [N][WC_KS] (plane stride N * WC_KS) holding
+// k = 32 s + j for j < 32: x = h0 + h1 + h2, each part the RNE of what the
+// parts before it leave; k >= K and j >= 32 stay zero.
+static void split_chunks(const float* w, int N, int K, int ldw, unsigned short* dst)
 {
-    for (int n = 0; n < N; ++n)
-        for (int k = 0; k < K; ++k) {
-            const float x = w[(size_t)n * ldw + k];
-            const unsigned short h0 = bf16_rne(x);
-            const float r1 = x - bf16_float(h0);
-            const unsigned short h1 = bf16_rne(r1);
-            const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
-            unsigned short* d = dst + (size_t)n * KS + k;
-            d[0] = h0;
-            d[(size_t)N * KS] = h1;
-            d[(size_t)2 * N * KS] = h2;
-        }
+    for (int s = 0; s * 32 < K; ++s)
+        for (int n = 0; n < N; ++n)
+            for (int j = 0; j < 32 && 32 * s + j < K; ++j) {
+                const float x = w[(size_t)n * ldw + 32 * s + j];
+                const unsigned short h0 = bf16_rne(x);
+                const float r1 = x - bf16_float(h0);
+                const unsigned short h1 = bf16_rne(r1);
+                const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+                unsigned short* d = dst + (size_t)s * WC_CHUNK + (size_t)n * WC_KS + j;
+                d[0] = h0;
+                d[(size_t)N * WC_KS] = h1;
+                d[(size_t)2 * N * WC_KS] = h2;
+            }
 }
 
 std::vector<unsigned short> pack_linear_x(const float* w, int N, int K)
 {
-    constexpr int BN = 144, KS = 152;
-    // per slice: 3 planes of [BN][KS], zero-padded to whole 1 KB loads
-    constexpr size_t SLICE = ((size_t)3 * BN * KS / 8 + 63) / 64 * 64 * 8;
+    constexpr int BN = 144;
     if (K != 144 || N % BN != 0) throw Error("pack_linear_x: needs K = 144 and N a multiple of 144");
-    std::vector<unsigned short> out((size_t)(N / BN) * SLICE, 0);
-    for (int s = 0; s < N / BN; ++s) split_planes(w + (size_t)s * BN * K, BN, K, K, KS, &out[(size_t)s * SLICE]);
+    const int steps = (K + 31) / 32;
+    std::vector<unsigned short> out((size_t)(N / BN) * steps * WC_CHUNK, 0);
+    for (int sl = 0; sl < N / BN; ++sl)
+        split_chunks(w + (size_t)sl * BN * K, BN, K, K, &out[(size_t)sl * steps * WC_CHUNK]);
     return out;
 }
 
@@ -85,9 +87,9 @@ void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<u
                 std::vector<float>* b1x)
 {
     constexpr int C = 144, H = 288;
-    static_assert(3 * MX_HID * MX_KS1 <= MX_SLICE && 3 * C * MX_KS2 <= MX_SLICE && MX_SLICE % 512 == 0, "slot");
+    static_assert(3 * C * WC_KS <= WC_CHUNK && WC_CHUNK % 512 == 0 && H % MX_HID == 0, "chunks");
     std::vector<float> f1((size_t)MX_HID * C);
-    w->assign((size_t)6 * MX_SLICE, 0);
+    w->assign((size_t)24 * WC_CHUNK, 0);
     b1x->assign(H, 0.0f);
     for (int q = 0; q < H / MX_HID; ++q) {
         for (int row = 0; row < MX_HID; ++row) {
@@ -95,8 +97,8 @@ void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<u
             memcpy(&f1[(size_t)row * C], w1 + (size_t)u * C, C * sizeof(float));
             (*b1x)[q * MX_HID + row] = b1[u];
         }
-        split_planes(f1.data(), MX_HID, C, C, MX_KS1, &(*w)[(size_t)(2 * q) * MX_SLICE]);
-        split_planes(w2 + q * MX_HID, C, MX_HID, H, MX_KS2, &(*w)[(size_t)(2 * q + 1) * MX_SLICE]);
+        split_chunks(f1.data(), MX_HID, C, C, &(*w)[(size_t)(8 * q) * WC_CHUNK]);
+        split_chunks(w2 + q * MX_HID, C, MX_HID, H, &(*w)[(size_t)(8 * q + 5) * WC_CHUNK]);
     }
 }
 
@@ -265,11 +267,9 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
     p.cscale = cscale;
     p.eps = 1e-5f;
     if (epi == EPI_QKV && L.wx && L.K == 144 && L.N == 432 && heads == 6 && hdim == 24 && lda == 144) {
-        // split-bf16 qkv (gemmx.hip): one block per CU walking 256-token tiles
-        static const int cus = std::max(1, Runtime::get().cu_count());
+        // split-bf16 qkv (gemmx.hip): a block per 128-token tile and slice
         p.w = (const float*)L.wx;
-        const long ntiles = (M + 255) / 256;
-        launch(s, "hat_gemmx_qkv", (unsigned)std::max(1L, std::min<long>(ntiles, cus)), 1, 1, 512, p);
+        launch(s, "hat_gemmx_qkv", (unsigned)gemmx_qkv_blocks(p.M), 1, 1, WX_THREADS, p);
         return;
     }
     int wbn = 0;
@@ -349,7 +349,7 @@ void run_mlp(hipStream_t s, const DevLinear& fc1, const DevLinear& fc2, const fl
 // is not launched: its arguments go to *defer, for the attention launch to run.
 void run_cab(hipStream_t s, const DevCab& cb, const float* xn, int H, int W, const float* bproj,
              float cscale, int sq, float* t1, float* partial, float* w2g, float* bias2, float* gate,
-             CabGateArgs* defer = nullptr)
+             unsigned short* w2gx, CabGateArgs* defer = nullptr)
 {
     if (H % 16 != 0 || W % 16 != 0 || H < 16 || W < 16) throw Error("CAB: plane must be 16-aligned");
     if (sq < 1 || sq > 64) throw Error("CAB: squeeze width must be 1..64");
@@ -382,6 +382,7 @@ void run_cab(hipStream_t s, const DevCab& cb, const float* xn, int H, int W, con
     g.gate = gate;
     g.cscale = cscale;
     g.sq = sq;
+    g.w2gx = w2gx;
     if (defer) {
         *defer = g;
         return;
@@ -444,15 +445,14 @@ void run_hab_tail(hipStream_t s, const DevLinear& proj, const DevLinear& fc1, co
 // conv2 of t1) + bias, xn = norm2(x') [hat_projx(_cab)]; out = x' + MLP(xn)
 // (+ with nw: xn = norm_next(out)) [hat_mlpx(_ln)]. out may alias res.
 void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& mlp, const float* b2, const float* a,
-               const float* res, float* out, float* xn, const float* t1, const float* w2g, const float* bias,
+               const float* res, float* out, float* xn, const float* t1, const unsigned short* w2gx, const float* bias,
                const float* n2w, const float* n2b, const float* nw, const float* nb, int H, int W)
 {
     if (!proj.wx || proj.K != 144 || proj.N != 144) throw Error("tailx: needs the pre-split 144 x 144 projection");
-    if (cab && (!t1 || !w2g)) throw Error("tailx: the CAB form needs t1 and the gated conv2 weights");
+    if (cab && (!t1 || !w2gx)) throw Error("tailx: the CAB form needs t1 and the gated conv2 weight chunks");
     const long M = (long)H * W;
     if (M > 0x7fffffffL) throw Error("tailx: too many rows");
-    static const int cus = std::max(1, Runtime::get().cu_count());
-    const unsigned g = (unsigned)std::max(1L, std::min<long>((M + 255) / 256, cus));
+    const unsigned g = (unsigned)wx_tiles((int)M);  // a block per 128-token tile
     TailXArgs p{};
     p.a = a;
     p.res = res;
@@ -460,7 +460,7 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
     p.xn = xn;
     p.w = proj.wx;
     p.bias = bias;
-    p.w2g = w2g;
+    p.w2gx = w2gx;
     p.t1 = t1;
     p.nw = n2w;
     p.nb = n2b;
@@ -468,7 +468,7 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
     p.H = H;
     p.W = W;
     p.eps = 1e-5f;
-    launch(s, cab ? "hat_projx_cab" : "hat_projx", g, 1, 1, 512, p);
+    launch(s, cab ? "hat_projx_cab" : "hat_projx", g, 1, 1, WX_THREADS, p);
     TailXArgs q{};
     q.a = xn;
     q.res = out;
@@ -483,7 +483,7 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
     q.H = H;
     q.W = W;
     q.eps = 1e-5f;
-    launch(s, nw ? "hat_mlpx_ln" : "hat_mlpx", g, 1, 1, 512, q);
+    launch(s, nw ? "hat_mlpx_ln" : "hat_mlpx", g, 1, 1, WX_THREADS, q);
 }
 
 // The channel-attention gate from the CAB conv's per-tile column sums:
@@ -994,6 +994,7 @@ std::vector<std::pair<float**, size_t>> GpuBackend::layout(const Weights& wt_, c
         {&a.t1, T * t1_stride},
         {&a.cab_part, cab_fold_ ? (size_t)(p.hp / 16) * (p.wp / 16) * CAB_NSUM * CAB_CS : 0},
         {&a.w2g, cab_fold_ ? C * CAB_K2 : 0},
+        {&a.w2gx, cab_fold_ ? WC_CHUNK : 0},  // 2 chunks of bf16
         {&a.bias2, cab_fold_ ? C : 0},
         {&a.t2, cab_fold_ ? 0 : T * C},
         {&a.partial, cab_fold_ ? 0 : nblk * C},
@@ -1096,14 +1097,14 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
         const DevLinear& proj = lin_.at(p + ".attn.proj");
         CabGateArgs gate{};
         run_cab(stream_, cab_.at(p), a_.xn, H, W, proj.b, wt_.conv_scale, wt_.squeezed, a_.t1, a_.cab_part,
-                a_.w2g, a_.bias2, a_.gate, &gate);
+                a_.w2g, a_.bias2, a_.gate, (unsigned short*)a_.w2gx, &gate);
         gemm(lin_.at(p + ".attn.qkv"), a_.xn, C, T, a_.qkv, 0, EPI_QKV);
         attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, &gate);
         auto mx = mlpx_.find(p + ".mlp");
         if (proj.wx && mx != mlpx_.end()) {
             // split-bf16: proj + gated conv2 + shortcut + norm2, then the MLP + next norm1
             run_tailx(stream_, true, proj, mx->second, lin_.at(p + ".mlp.fc2").b, a_.ao, x_in, x_out, a_.xn, a_.t1,
-                      a_.w2g, a_.bias2, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
+                      (const unsigned short*)a_.w2gx, a_.bias2, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
                       raw_.at(next_norm + ".weight"), raw_.at(next_norm + ".bias"), H, W);
             return;
         }

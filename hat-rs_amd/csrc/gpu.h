@@ -64,15 +64,15 @@ struct DevConv {
 
 // Host-side repacking (also used by the selftest and the op entry points).
 std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
-// [N][144] -> per 144-column slice, 3 parts of [144 rows][152] bf16 (then
-// zeros to a multiple of 1 KB): w = p0 + p1 + p2, each part the round-to-
-// nearest bf16 of what the earlier ones leave; columns 144..151 zero.
+// [N][144] -> per 144-row slice, five weight chunks (one per 32-k step) of
+// three bf16 planes [144][WC_KS]: w = p0 + p1 + p2, each part the round-to-
+// nearest bf16 of what the earlier ones leave; k 144..159 and the plane
+// padding zero.
 std::vector<unsigned short> pack_linear_x(const float* w, int N, int K);
 // The C = 144 MLP (fc1 [288][144] + b1, fc2 [144][288]) for hat_mlpx: per
-// third of the hidden layer two MX_SLICE slots of three bf16 planes - fc1's
-// 96 rows [96][MX_KS1], then fc2 on those units [144][MX_KS2] - with fc1's
-// rows (and b1) in the order that leaves its output in fc2's operand layout
-// (tailx.hip).
+// third of the hidden layer eight weight chunks - five of fc1's 96 rows, then
+// three of fc2 on those units - with fc1's rows (and b1) in the order that
+// leaves its output in fc2's operand layout (tailx.hip).
 void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
                 std::vector<float>* b1x);
 std::vector<float> pack_wino(const float* w, int CO, int CI, int r);
@@ -132,7 +132,7 @@ private:
         float *x0 = nullptr, *body = nullptr, *xa = nullptr, *xb = nullptr, *xn = nullptr, *t1 = nullptr,
               *t2 = nullptr, *partial = nullptr, *red = nullptr, *gate = nullptr, *qkv = nullptr, *ao = nullptr,
               *hidden = nullptr, *head0 = nullptr, *head1 = nullptr, *din = nullptr, *dout = nullptr,
-              *cab_part = nullptr, *w2g = nullptr, *bias2 = nullptr;
+              *cab_part = nullptr, *w2g = nullptr, *w2gx = nullptr, *bias2 = nullptr;
     };
     // Each buffer of plan p and its size in floats (0: not used by this
     // network); host_io adds the staging buffers of the host-memory forward.

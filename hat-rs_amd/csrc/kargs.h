@@ -106,6 +106,7 @@ struct CabGateArgs {
     float* gate;         // out: the gate itself [144]
     float cscale;
     int sq;
+    unsigned short* w2gx;  // out (if set): w2g as 2 weight chunks [3][144][WC_KS] for hat_projx_cab
 };
 
 // Implicit-GEMM 3x3 convolution, stride 1, zero padding 1, NHWC.
@@ -235,24 +236,33 @@ struct HabTailArgs {
 // hat_projx(_cab): out = x' = res + a . Wp^T (+ nb(t1) . W2g^T) + bias,
 //                  xn = LN(x') with nw / nb;
 // hat_mlpx(_ln):   out = res + fc2(gelu(fc1(a))) + b2 (+ xn = LN(out)).
-// The split-bf16 MLP (tailx.hip) walks the hidden layer in thirds of 96
-// units: per third one fc1 slice (96 permuted rows x K 144, row stride
-// MX_KS1) and one fc2 slice (144 rows x the third's 96 units, row stride
-// MX_KS2), each three bf16 planes, in MX_SLICE-element slots.
+// Weight chunks of the split-bf16 linears (gemmx.hip, tailx.hip): one 32-k
+// step of up to 144 rows as three bf16 planes [rows][WC_KS] (k 32..39 zero),
+// WC_CHUNK elements apart. A chunk is copied as loads of 1 KB, the same
+// number from every wave of a block: 36 for up to 144 rows, 24 for 96.
+#define WC_KS 40
+#define WC_CHUNK 18432  // 36 x 512 >= 3 x 144 x WC_KS
+// The MLP walks the hidden layer in thirds of MX_HID units: per third five
+// fc1 chunks (96 permuted rows, k = input channel) then three fc2 chunks (144
+// rows, k = the third's hidden units), 24 chunks in all.
 #define MX_HID 96
-#define MX_KS1 152
-#define MX_KS2 104
-#define MX_SLICE 45056  // >= 3 * max(96 * MX_KS1, 144 * MX_KS2), whole 1 KB loads
+// Their launch geometry: blocks of 4 waves, each block one 128-token row tile
+// (hat_gemmx_qkv: one tile and one of q, k, v; ceil(tiles / 8) * 24 blocks so
+// that the three of a tile share an XCD; tailx: one block a tile).
+#define WX_THREADS 256
+#define WX_ROWS 128
+constexpr int wx_tiles(int M) { return (M + WX_ROWS - 1) / WX_ROWS; }
+constexpr int gemmx_qkv_blocks(int M) { return (wx_tiles(M) + 7) / 8 * 24; }
 
 struct TailXArgs {
     const float* a;            // projx: attention output; mlpx: LN2(x') rows
     const float* res;          // projx: block input; mlpx: x'
     float* out;                // [M][144] (may alias res)
     float* xn;                 // projx: LN2(x'); mlpx (LN): the next norm1 (may alias a)
-    const unsigned short* w;   // pre-split weight slices (projx: 1, mlpx: 6)
+    const unsigned short* w;   // weight chunks (projx: 5, mlpx: 24)
     const float* bias;         // projx: bias2 or the projection bias; mlpx: b1, fc1's row order
     const float* b2;           // mlpx: fc2 bias
-    const float* w2g;          // projx_cab: [144][CAB_K2] gate-scaled conv2 weights
+    const unsigned short* w2gx;  // projx_cab: the gate-scaled conv2 weights as 2 chunks (k = tap*6 + ci)
     const float* t1;           // projx_cab: [M][CAB_CS] CAB conv1 output
     const float* nw;
     const float* nb;

@@ -26,48 +26,10 @@
 
 using namespace hatk;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
 __device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
-}
-
-// (a, b) rounded to nearest bf16, packed: a in the low half (element 0).
-__device__ __forceinline__ unsigned pk_bf16(float a, float b)
-{
-    return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2){a, b}, bf16x2));
-}
-
-// The three-way split of a pair: (a, b) = p0 + p1 + p2 (+ below 2^-27 of
-// each), every part a packed pair of bf16, each the round-to-nearest of what
-// the earlier parts leave (x - its rounding is exact in fp32).
-__device__ __forceinline__ void split3_pk(float a, float b, unsigned& p0, unsigned& p1, unsigned& p2)
-{
-    p0 = pk_bf16(a, b);
-    a -= __uint_as_float(p0 << 16);
-    b -= __uint_as_float(p0 & 0xffff0000u);
-    p1 = pk_bf16(a, b);
-    a -= __uint_as_float(p1 << 16);
-    b -= __uint_as_float(p1 & 0xffff0000u);
-    p2 = pk_bf16(a, b);
-}
-
-// Eight consecutive fp32 values as three 8-wide bf16 parts.
-__device__ __forceinline__ void split3_x8(const float (&v)[8], u32x4 (&out)[3])
-{
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        unsigned p0, p1, p2;
-        split3_pk(v[2 * j], v[2 * j + 1], p0, p1, p2);
-        out[0][j] = p0;
-        out[1][j] = p1;
-        out[2][j] = p2;
-    }
 }
 
 // The six products of a 3-part A and a 3-part B into c, smallest first.
@@ -158,7 +120,8 @@ __device__ __forceinline__ void attnx_stash(unsigned short* Kp, unsigned short* 
 template <int D>
 __device__ __forceinline__ int attnx_query(const AttnArgs& p, int wi, int head, u32x4 (&qb)[2][3])
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in a scalar register
     const int ql = lane & 31, h = lane >> 5;
     const int q = wave * 32 + ql, qy = q >> 4, qx = q & 15;
     const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
@@ -207,7 +170,8 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
     const float* Tb = (const float*)(Vp + 3 * X::VPL);
 
     const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in a scalar register
     const int ql = lane & 31, h = lane >> 5;
     const int q = wave * 32 + ql;
     const int qy = q >> 4, qx = q & 15;
@@ -434,7 +398,8 @@ __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int 
     const unsigned short* Kp = (const unsigned short*)lds;
     const unsigned short* Vp = Kp + 3 * X::KPL;
     const float* Tb = (const float*)(Vp + 3 * X::VPL);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in a scalar register
     const int ql = lane & 31, h = lane >> 5;
     const int q = wave * 32 + ql;
     const int qy = q >> 4, qx = q & 15;

@@ -23,6 +23,118 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c)
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// ---- split-bf16 arithmetic (the BF16 MFMA path at fp32 accuracy): an fp32
+// operand as three bf16 parts, a product as the six terms of order <= 2
+// (attnx.hip states the accuracy).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// (a, b) rounded to nearest bf16, packed: a in the low half (element 0).
+__device__ __forceinline__ unsigned pk_bf16(float a, float b)
+{
+    return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+
+// The three-way split of a pair: (a, b) = p0 + p1 + p2 (+ below 2^-27 of
+// each), every part a packed pair of bf16, each the round-to-nearest of what
+// the earlier parts leave (x - its rounding is exact in fp32).
+__device__ __forceinline__ void split3_pk(float a, float b, unsigned& p0, unsigned& p1, unsigned& p2)
+{
+    p0 = pk_bf16(a, b);
+    a -= __uint_as_float(p0 << 16);
+    b -= __uint_as_float(p0 & 0xffff0000u);
+    p1 = pk_bf16(a, b);
+    a -= __uint_as_float(p1 << 16);
+    b -= __uint_as_float(p1 & 0xffff0000u);
+    p2 = pk_bf16(a, b);
+}
+
+// Part pl (0, 1, 2) of x's three-way split, as bf16 bits.
+__device__ __forceinline__ unsigned short split3_part(float x, int pl)
+{
+    unsigned p0, p1, p2;
+    split3_pk(x, 0.0f, p0, p1, p2);
+    return (unsigned short)((pl == 0 ? p0 : pl == 1 ? p1 : p2) & 0xffffu);
+}
+
+// Eight consecutive fp32 values as three 8-wide bf16 parts.
+__device__ __forceinline__ void split3_x8(const float (&v)[8], u32x4 (&out)[3])
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        unsigned p0, p1, p2;
+        split3_pk(v[2 * j], v[2 * j + 1], p0, p1, p2);
+        out[0][j] = p0;
+        out[1][j] = p1;
+        out[2][j] = p2;
+    }
+}
+
+// v_mfma_f32_16x16x32_bf16: A 16x32 (lane l: row l%16, k 8*(l/16) .. +7), B
+// 32x16 (lane l: k 8*(l/16) .. +7, col l%16), D as mfma16's.
+__device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma16x6(const u32x4 (&a)[3], const u32x4 (&b)[3], f32x4 c)
+{
+    c = mfma16_bf16(a[2], b[0], c);
+    c = mfma16_bf16(a[1], b[1], c);
+    c = mfma16_bf16(a[0], b[2], c);
+    c = mfma16_bf16(a[1], b[0], c);
+    c = mfma16_bf16(a[0], b[1], c);
+    return mfma16_bf16(a[0], b[0], c);
+}
+
+// ---- weight chunks for the split-bf16 linears: one 32-k step of up to 144
+// rows as three bf16 planes [rows][WC_KS] (k 32..39 zero), packed on the host
+// WC_CHUNK elements apart. A block copies chunk c + 1 into one of two LDS
+// buffers while its waves multiply chunk c out of the other.
+
+// The NL loads (1 KB each) of one chunk into an LDS buffer, NL / WAVES from
+// every wave: wave w issues loads w, w + WAVES, ...; lane l of a load writes
+// 16 bytes at the load's LDS base + 16 l.
+template <int NL, int WAVES>
+__device__ __forceinline__ void wc_issue(unsigned short* dst, const unsigned short* src, int wave, int lane)
+{
+    static_assert(NL % WAVES == 0 && NL * 512 <= WC_CHUNK, "whole loads per wave, within a chunk");
+#pragma unroll
+    for (int j = 0; j < NL / WAVES; ++j) {
+        const int i = wave + j * WAVES;
+        __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i * 64 + lane) * 8),
+                                         (__attribute__((address_space(3))) void*)(dst + i * 512), 16, 0, 0);
+    }
+}
+
+// acc[mt][nt] += W[rows 16 nt .. +15] . xb[mt] for one chunk of a plane
+// stride PLANE (= rows * WC_KS): the three planes of tile nt + 1 are read
+// while tile nt's 12 MFMAs run (the barriers keep the scheduler from hoisting
+// every tile's reads, which costs more registers than there are).
+template <int NT, int PLANE>
+__device__ __forceinline__ void wc_mma(const unsigned short* Ws, int lr, int lg, const u32x4 (&xb)[2][3],
+                                       f32x4 (&acc)[2][NT])
+{
+    const unsigned short* wr = Ws + lr * WC_KS + lg * 8;
+    u32x4 wa[2][3];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * PLANE);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (nt + 1 < NT) {
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * WC_KS + pl * PLANE);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
+    }
+}
+
 // A compile-time int carried by a value, for generic lambdas: decltype(x)::value.
 template <int V> struct CInt {
     static constexpr int value = V;

@@ -297,15 +297,15 @@ int gpu_selftest(std::string* err)
                 if (lnout) check_close(k + " C " + std::to_string(C) + " layernorm", dxn.get(), wxn, 5e-5);
                 note(k + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
                 if (ws && C == 144 && epi == EPI_QKV) {
-                    // the split-bf16 form on the same inputs: 2 blocks over 3
-                    // row tiles, the last one partial
+                    // the split-bf16 form on the same inputs (the last
+                    // 128-row tile partial)
                     std::vector<unsigned short> px = pack_linear_x(w.data(), N, K);
                     Dev dwx(std::vector<float>((px.size() + 1) / 2)), dout2((size_t)M * N);
                     rt.h2d(dwx.p, px.data(), px.size() * sizeof(unsigned short));
                     GemmArgs px2 = p;
                     px2.w = dwx.p;
                     px2.out = dout2.p;
-                    launch(s, "hat_gemmx_qkv", 2, 1, 1, 512, px2);
+                    launch(s, "hat_gemmx_qkv", (unsigned)gemmx_qkv_blocks(M), 1, 1, WX_THREADS, px2);
                     check_close("hat_gemmx_qkv C 144", dout2.get(), want, 3e-5);
                     note("hat_gemmx_qkv C 144 M " + std::to_string(M) + " K 144");
                 }
@@ -394,7 +394,7 @@ int gpu_selftest(std::string* err)
             const int tiles = (H / 16) * (W / 16);
             Dev dxn(xn), dw1(w1p), db1(b1), dw2(w2), db2(b2), dwa(wa), dba(ba), dwb(wb), dbb(bb), dao(ao),
                 dwp(wpp), dbp(bp), dres(res), dnw(nw), dnb(nb), dt1((size_t)T * CAB_CS),
-                dpart((size_t)tiles * CAB_NSUM * CAB_CS), dw2g((size_t)C * CAB_K2), dbias2(C), dgate(C),
+                dpart((size_t)tiles * CAB_NSUM * CAB_CS), dw2g((size_t)C * CAB_K2), dw2gx(WC_CHUNK), dbias2(C), dgate(C),
                 dout((size_t)T * C), dxo((size_t)T * C);
             CabConvArgs ca{dxn.p, dw1.p, db1.p, dt1.p, dpart.p, H, W};
             launch(s, "hat_cab_conv1", 2, 1, 1, 256, ca);
@@ -416,6 +416,7 @@ int gpu_selftest(std::string* err)
             ga.gate = dgate.p;
             ga.cscale = cscale;
             ga.sq = sq;
+            ga.w2gx = (unsigned short*)dw2gx.p;
             launch(s, "hat_cab_gate", 1, 1, 1, 1024, ga);
             GemmArgs gp{};
             gp.a = dao.p;
@@ -628,7 +629,7 @@ int gpu_selftest(std::string* err)
 
                 // The split-bf16 tails (tailx.hip) on the same inputs, in place
                 // as the forward runs them (out over the block input, the next
-                // norm over norm2's rows); 2 blocks over 6 row tiles.
+                // norm over norm2's rows); 12 row tiles of 128.
                 std::vector<unsigned short> pwx = pack_linear_x(wp.data(), C, C), mwx;
                 std::vector<float> b1x;
                 pack_mlp_x(f1.data(), fb1.data(), f2.data(), &mwx, &b1x);
@@ -643,7 +644,7 @@ int gpu_selftest(std::string* err)
                 xa.xn = dxn_x.p;
                 xa.w = (const unsigned short*)dpwx.p;
                 xa.bias = dbias2.p;
-                xa.w2g = dw2g.p;
+                xa.w2gx = (const unsigned short*)dw2gx.p;
                 xa.t1 = dt1.p;
                 xa.nw = dnw.p;
                 xa.nb = dnb.p;
@@ -651,7 +652,7 @@ int gpu_selftest(std::string* err)
                 xa.H = H;
                 xa.W = W;
                 xa.eps = 1e-5f;
-                launch(s, "hat_projx_cab", 2, 1, 1, 512, xa);
+                launch(s, "hat_projx_cab", (unsigned)wx_tiles(T), 1, 1, WX_THREADS, xa);
                 check_close("hat_projx_cab", dout_x.get(), want, 5e-5);
                 check_close("hat_projx_cab layernorm", dxn_x.get(), wxn, 5e-5);
                 note("hat_projx_cab (split-bf16 proj + folded conv2 + norm2) vs double");
@@ -669,7 +670,7 @@ int gpu_selftest(std::string* err)
                 xm.H = H;
                 xm.W = W;
                 xm.eps = 1e-5f;
-                launch(s, "hat_mlpx_ln", 2, 1, 1, 512, xm);
+                launch(s, "hat_mlpx_ln", (unsigned)wx_tiles(T), 1, 1, WX_THREADS, xm);
                 check_close("hat_mlpx_ln", dout_x.get(), std::vector<double>(ro.begin(), ro.end()), 2e-5);
                 check_close("hat_mlpx_ln next norm", dxn_x.get(), std::vector<double>(rx.begin(), rx.end()), 2e-5);
                 note("hat_mlpx_ln (split-bf16 MLP + norm) vs the two-kernel path");
@@ -682,10 +683,10 @@ int gpu_selftest(std::string* err)
                 xo.out = dout_ox.p;
                 xo.xn = dxn_ox.p;
                 xo.bias = dbp.p;
-                xo.w2g = nullptr;
+                xo.w2gx = nullptr;
                 xo.t1 = nullptr;
                 xo.M = Mo;
-                launch(s, "hat_projx", 2, 1, 1, 512, xo);
+                launch(s, "hat_projx", (unsigned)wx_tiles(Mo), 1, 1, WX_THREADS, xo);
                 TailXArgs xo2 = xm;
                 xo2.a = dxn_ox.p;
                 xo2.res = dout_ox.p;
@@ -694,7 +695,7 @@ int gpu_selftest(std::string* err)
                 xo2.nw = nullptr;
                 xo2.nb = nullptr;
                 xo2.M = Mo;
-                launch(s, "hat_mlpx", 2, 1, 1, 512, xo2);
+                launch(s, "hat_mlpx", (unsigned)wx_tiles(Mo), 1, 1, WX_THREADS, xo2);
                 std::vector<double> wo(r2.begin(), r2.end());
                 for (size_t i = (size_t)Mo * C; i < wo.size(); ++i) wo[i] = res[i];
                 check_close("hat_projx + hat_mlpx", dout_ox.get(), wo, 2e-5);
