@@ -63,14 +63,18 @@ static void split_chunks(const float* w, int N, int K, int ldw, unsigned short* 
             }
 }
 
-std::vector<unsigned short> pack_linear_x(const float* w, int N, int K)
+std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K)
 {
     constexpr int BN = 144;
     if (K != 144 || N % BN != 0) throw Error("pack_linear_x: needs K = 144 and N a multiple of 144");
     const int steps = (K + 31) / 32;
     std::vector<unsigned short> out((size_t)(N / BN) * steps * WC_CHUNK, 0);
-    for (int sl = 0; sl < N / BN; ++sl)
-        split_chunks(w + (size_t)sl * BN * K, BN, K, K, &out[(size_t)sl * steps * WC_CHUNK]);
+    for (int sl = 0; sl < N / BN; ++sl) {
+        unsigned short* dst = &out[(size_t)sl * steps * WC_CHUNK];
+        split_chunks(w + (size_t)sl * BN * K, BN, K, K, dst);
+        // the bias as column k = K (= 144: step 4, j = 16), split like the rest
+        if (bias) split_chunks(bias + (size_t)sl * BN, BN, 1, 1, dst + (size_t)(K / 32) * WC_CHUNK + K % 32);
+    }
     return out;
 }
 
@@ -83,21 +87,22 @@ static int mlpx_unit(int row)
     return 32 * (t / 2) + 8 * g + 4 * (t % 2) + r;
 }
 
-void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
-                std::vector<float>* b1x)
+void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w)
 {
     constexpr int C = 144, H = 288;
     static_assert(3 * C * WC_KS <= WC_CHUNK && WC_CHUNK % 512 == 0 && H % MX_HID == 0, "chunks");
-    std::vector<float> f1((size_t)MX_HID * C);
+    std::vector<float> f1((size_t)MX_HID * C), fb((size_t)MX_HID);
     w->assign((size_t)24 * WC_CHUNK, 0);
-    b1x->assign(H, 0.0f);
     for (int q = 0; q < H / MX_HID; ++q) {
         for (int row = 0; row < MX_HID; ++row) {
             const int u = q * MX_HID + mlpx_unit(row);
             memcpy(&f1[(size_t)row * C], w1 + (size_t)u * C, C * sizeof(float));
-            (*b1x)[q * MX_HID + row] = b1[u];
+            fb[row] = b1[u];
         }
-        split_chunks(f1.data(), MX_HID, C, C, &(*w)[(size_t)(8 * q) * WC_CHUNK]);
+        unsigned short* dst = &(*w)[(size_t)(8 * q) * WC_CHUNK];
+        split_chunks(f1.data(), MX_HID, C, C, dst);
+        // b1 as fc1's column k = 144 (step 4, j = 16)
+        split_chunks(fb.data(), MX_HID, 1, 1, dst + (size_t)(C / 32) * WC_CHUNK + C % 32);
         split_chunks(w2 + q * MX_HID, C, MX_HID, H, &(*w)[(size_t)(8 * q + 5) * WC_CHUNK]);
     }
 }
@@ -475,7 +480,6 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
     q.out = out;
     q.xn = nw ? xn : nullptr;
     q.w = mlp.w;
-    q.bias = mlp.b1;
     q.b2 = b2;
     q.nw = nw;
     q.nb = nb;
@@ -815,7 +819,7 @@ void GpuBackend::upload_linear(const std::string& name)
         return name.size() >= n && name.compare(name.size() - n, n, t) == 0;
     };
     if (L.K == 144 && ((L.N == 432 && ends(".qkv")) || (L.N == 144 && ends("proj")))) {
-        std::vector<unsigned short> x = pack_linear_x(wt_.t(name + ".weight"), L.N, L.K);
+        std::vector<unsigned short> x = pack_linear_x(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K);
         L.wx = (unsigned short*)upload_bytes(x.data(), x.size() * sizeof(unsigned short));
     }
     lin_[name] = L;
@@ -828,11 +832,9 @@ void GpuBackend::upload_mlpx(const std::string& name)
     const TensorInfo& t2 = wt_.info(name + ".fc2.weight");
     if (t1.shape != std::vector<size_t>{288, 144} || t2.shape != std::vector<size_t>{144, 288}) return;
     std::vector<unsigned short> w;
-    std::vector<float> b1x;
-    pack_mlp_x(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w, &b1x);
+    pack_mlp_x(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
     DevMlpX m;
     m.w = (unsigned short*)upload_bytes(w.data(), w.size() * sizeof(unsigned short));
-    m.b1 = upload(b1x.data(), b1x.size());
     mlpx_[name] = m;
 }
 

@@ -51,8 +51,7 @@ std::vector<float> pack_cab_conv1(const float* w);
 
 // hat_mlpx's weights: the packed slices and b1 in fc1's row order.
 struct DevMlpX {
-    unsigned short* w = nullptr;
-    float* b1 = nullptr;
+    unsigned short* w = nullptr;  // 24 weight chunks (pack_mlp_x)
 };
 
 struct DevConv {
@@ -66,15 +65,16 @@ struct DevConv {
 std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
 // [N][144] -> per 144-row slice, five weight chunks (one per 32-k step) of
 // three bf16 planes [144][WC_KS]: w = p0 + p1 + p2, each part the round-to-
-// nearest bf16 of what the earlier ones leave; k 144..159 and the plane
-// padding zero.
-std::vector<unsigned short> pack_linear_x(const float* w, int N, int K);
+// nearest bf16 of what the earlier ones leave; the bias (if given) as column
+// k = 144, split the same way; the rest of k 144..159 and the plane padding
+// zero.
+std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K);
 // The C = 144 MLP (fc1 [288][144] + b1, fc2 [144][288]) for hat_mlpx: per
-// third of the hidden layer eight weight chunks - five of fc1's 96 rows, then
-// three of fc2 on those units - with fc1's rows (and b1) in the order that
-// leaves its output in fc2's operand layout (tailx.hip).
-void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
-                std::vector<float>* b1x);
+// third of the hidden layer eight weight chunks - five of fc1's 96 rows (b1
+// as their column k = 144), then three of fc2 on those units - with fc1's
+// rows in the order that leaves its output in fc2's operand layout
+// (tailx.hip).
+void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
 std::vector<float> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);

@@ -238,10 +238,11 @@ struct HabTailArgs {
 // hat_mlpx(_ln):   out = res + fc2(gelu(fc1(a))) + b2 (+ xn = LN(out)).
 // Weight chunks of the split-bf16 linears (gemmx.hip, tailx.hip): one 32-k
 // step of up to 144 rows as three bf16 planes [rows][WC_KS] (k 32..39 zero),
-// WC_CHUNK elements apart. A chunk is copied as loads of 1 KB, the same
-// number from every wave of a block: 36 for up to 144 rows, 24 for 96.
+// WC_CHUNK elements apart (zeros after the planes). A chunk is copied as
+// loads of 1 KB, the same number from every wave of a block: 144 rows take
+// 34 (36 or 40 to share them out evenly), 96 rows 23 (24).
 #define WC_KS 40
-#define WC_CHUNK 18432  // 36 x 512 >= 3 x 144 x WC_KS
+#define WC_CHUNK 20480  // 40 x 512 >= 3 x 144 x WC_KS
 // The MLP walks the hidden layer in thirds of MX_HID units: per third five
 // fc1 chunks (96 permuted rows, k = input channel) then three fc2 chunks (144
 // rows, k = the third's hidden units), 24 chunks in all.
@@ -260,7 +261,7 @@ struct TailXArgs {
     float* out;                // [M][144] (may alias res)
     float* xn;                 // projx: LN2(x'); mlpx (LN): the next norm1 (may alias a)
     const unsigned short* w;   // weight chunks (projx: 5, mlpx: 24)
-    const float* bias;         // projx: bias2 or the projection bias; mlpx: b1, fc1's row order
+    const float* bias;         // projx: bias2 or the projection bias (mlpx: b1 is in its chunks)
     const float* b2;           // mlpx: fc2 bias
     const unsigned short* w2gx;  // projx_cab: the gate-scaled conv2 weights as 2 chunks (k = tap*6 + ci)
     const float* t1;           // projx_cab: [M][CAB_CS] CAB conv1 output

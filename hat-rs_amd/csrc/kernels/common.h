@@ -102,10 +102,15 @@ template <int NL, int WAVES>
 __device__ __forceinline__ void wc_issue(unsigned short* dst, const unsigned short* src, int wave, int lane)
 {
     static_assert(NL % WAVES == 0 && NL * 512 <= WC_CHUNK, "whole loads per wave, within a chunk");
-#pragma unroll
+    const unsigned loff = (unsigned)lane * 16;  // the lane's bytes within a load: one VGPR for every load
+    // Not unrolled: one load instruction per call site keeps the compiler's
+    // tracking of LDS copies exact (it tracks a few copy instructions by the
+    // LDS object they write and waits for all copies once it runs out).
+#pragma unroll 1
     for (int j = 0; j < NL / WAVES; ++j) {
-        const int i = wave + j * WAVES;
-        __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i * 64 + lane) * 8),
+        const int i = wave + j * WAVES;  // wave-uniform: the load's base goes in scalar registers
+        const char* base = (const char*)src + (size_t)i * 1024;
+        __builtin_amdgcn_global_load_lds((const void*)(base + loff),
                                          (__attribute__((address_space(3))) void*)(dst + i * 512), 16, 0, 0);
     }
 }
@@ -133,6 +138,42 @@ __device__ __forceinline__ void wc_mma(const unsigned short* Ws, int lr, int lg,
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
     }
+}
+
+// wc_mma with other work woven in: side(nt) runs in tile nt's segment, next
+// to its 12 MFMAs (VALU work issued there co-executes with them).
+template <int NT, int PLANE, typename F>
+__device__ __forceinline__ void wc_mma_with(const unsigned short* Ws, int lr, int lg, const u32x4 (&xb)[2][3],
+                                            f32x4 (&acc)[2][NT], F&& side)
+{
+    const unsigned short* wr = Ws + lr * WC_KS + lg * 8;
+    u32x4 wa[2][3];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * PLANE);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (nt + 1 < NT) {
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * WC_KS + pl * PLANE);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
+        side(nt);
+    }
+}
+
+// Pair j (0..7) of the split of a wave's rows pre (mt = j / 4, values
+// 2 (j % 4), +1 of its eight) into xb: eight calls make split_pre(pre, xb).
+__device__ __forceinline__ void split_pair(const f32x4 (&pre)[2][2], u32x4 (&xb)[2][3], int j)
+{
+    const int mt = j >> 2, q = j & 3;
+    unsigned p0, p1, p2;
+    split3_pk(pre[mt][q >> 1][(q & 1) * 2], pre[mt][q >> 1][(q & 1) * 2 + 1], p0, p1, p2);
+    xb[mt][0][q] = p0;
+    xb[mt][1][q] = p1;
+    xb[mt][2][q] = p2;
 }
 
 // A compile-time int carried by a value, for generic lambdas: decltype(x)::value.
@@ -169,6 +210,28 @@ __device__ __forceinline__ float gelu(float v)
 // later waits drain every load; zeroing the value after the load makes it wait
 // for that load at once.
 __device__ __attribute__((aligned(16))) float hat_zero_row[256] = {};
+
+// A 1 then zeros: the activation of a bias column (see WcRows::load_b).
+__device__ __attribute__((aligned(16))) float hat_one_row[4] = {1.0f, 0.0f, 0.0f, 0.0f};
+
+// Where stores of rows past the end of an output go, so that a wave issues
+// the same number of stores whatever the row count (never read).
+__device__ __attribute__((aligned(16))) float hat_sink_row[64];
+
+// s_waitcnt for "at most n vector memory operations of this wave still
+// outstanding, and every LDS operation done" (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8 = 0). Vector
+// memory operations complete in issue order for this count (the compiler's
+// own waits rely on it), so waiting for an operation means waiting until no
+// more than the number issued after it are outstanding.
+constexpr int wc_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70; }
+
+// The workgroup barrier alone. __syncthreads() adds a release fence, which
+// on gfx950 waits for every outstanding vector memory operation - the copies
+// of the next weight chunk and the rows read ahead included; the chunk loops
+// wait for exactly what they need (wc_vmcnt) and then meet here. The memory
+// clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void wc_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // A float4 from p, or zeros (from hat_zero_row) where ok is false.
 __device__ __forceinline__ f32x4 load_or_zero(const float* p, bool ok)

@@ -43,6 +43,7 @@
 
 #define TX_WAVES 4
 #define TX_ROWS (TX_WAVES * 32)
+#define TX_BUF (36 * 512)  // an LDS chunk buffer: 36 loads cover 144 rows
 
 // Row statistics of a token over its 144 channels (36 per lane, the four lane
 // groups of the token reducing with shuffles): two-pass mean, biased variance
@@ -119,15 +120,18 @@ template <bool CAB>
 __device__ __forceinline__ void projx_body(const TailXArgs& p)
 {
     constexpr int NCH = CAB ? 7 : 5, NL = 36;
-    __shared__ __attribute__((aligned(16))) unsigned short Ws[2 * WC_CHUNK];
-    __shared__ __attribute__((aligned(16))) float Cs[3 * 144];  // bias, norm2 w, b
+    // the two chunk buffers as two LDS objects, so that the compiler sees that
+    // reads of one need not wait for the copy into the other
+    __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
+    __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
+    __shared__ __attribute__((aligned(16))) float Cs[3 * 144];  // bias, norm2 w, b (the epilogue's)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
     const int lr = lane & 15, lg = lane >> 4;
     const int M = p.M;
     if ((int)blockIdx.x * TX_ROWS >= M) return;  // whole block, before any barrier
     auto chunk = [&](int c) { return c < 5 ? p.w + (size_t)c * WC_CHUNK : p.w2gx + (size_t)(c - 5) * WC_CHUNK; };
-    wc_issue<NL, TX_WAVES>(Ws, chunk(0), wave, lane);
+    wc_issue<NL, TX_WAVES>(Ws0, chunk(0), wave, lane);
     for (int i = tid; i < 3 * 144; i += TX_WAVES * 64)
         Cs[i] = i < 144 ? p.bias[i] : (i < 288 ? p.nw[i - 144] : p.nb[i - 288]);
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
@@ -165,83 +169,81 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
     for (int c = 0; c < NCH; ++c) {
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk c (and its operands) have landed
         __syncthreads();                // everyone's have, and everyone is done with chunk c - 1
-        if (c + 1 < NCH) wc_issue<NL, TX_WAVES>(Ws + ((c + 1) & 1) * WC_CHUNK, chunk(c + 1), wave, lane);
+        if (c + 1 < NCH) wc_issue<NL, TX_WAVES>(c & 1 ? Ws0 : Ws1, chunk(c + 1), wave, lane);
         u32x4 xb[2][3];
         split_pre(c < 5 ? y[c < 5 ? c : 0] : t1v, xb);
         if (CAB && c >= 4 && c + 1 < NCH) gather_t1(c - 4, t1v);
-        wc_mma<9, 144 * WC_KS>(Ws + (c & 1) * WC_CHUNK, lr, lg, xb, acc);
+        wc_mma<9, 144 * WC_KS>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
     }
     tx_store_rows(acc, Cs, mbase, M, lr, lg, p.eps, p.out, p.xn);
 }
 
 // out = x' + fc2(gelu(fc1(y))) + b2 (+ xn = LN_next(out)); y = p.a, x' = p.res.
-// p.w: 24 chunks (per third: five of fc1's 96 permuted rows, three of fc2 on
-// those units); p.bias: b1 in fc1's permuted row order.
+// p.w: 24 chunks (per third: five of fc1's 96 permuted rows, b1 as their
+// column k = 144, then three of fc2 on those units).
 template <bool LN>
 __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
 {
     constexpr int NL1 = 24, NL2 = 36;
     static_assert(NL1 * 512 >= 3 * MX_HID * WC_KS, "fc1 chunk loads");
-    __shared__ __attribute__((aligned(16))) unsigned short Ws[2 * WC_CHUNK];
-    __shared__ __attribute__((aligned(16))) float Cs[3 * 144 + 288];  // b2, next norm w, b; b1
+    __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
+    __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
+    __shared__ __attribute__((aligned(16))) float Cs[3 * 144];  // b2, next norm w, b (the epilogue's)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
     const int lr = lane & 15, lg = lane >> 4;
     const int M = p.M;
     if ((int)blockIdx.x * TX_ROWS >= M) return;  // whole block, before any barrier
-    wc_issue<NL1, TX_WAVES>(Ws, p.w, wave, lane);
-    for (int i = tid; i < 3 * 144 + 288; i += TX_WAVES * 64) {
+    wc_issue<NL1, TX_WAVES>(Ws0, p.w, wave, lane);
+    for (int i = tid; i < 3 * 144; i += TX_WAVES * 64) {
         float v;
         if (i < 144) v = p.b2[i];
         else if (i < 288) v = LN ? p.nw[i - 144] : 0.0f;
-        else if (i < 432) v = LN ? p.nb[i - 288] : 0.0f;
-        else v = p.bias[i - 432];
+        else v = LN ? p.nb[i - 288] : 0.0f;
         Cs[i] = v;
     }
-    const float* b1 = Cs + 432;
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
     f32x4 acc2[2][9];
     tx_load_res(p.res, mbase, M, lr, lg, acc2);
     WcRows yr;
     yr.init(p.a, mbase, M, lr);
     f32x4 pre[2][2];
-    yr.load(0, lg, pre);
+    yr.load_b(0, lg, pre);
 #pragma unroll 1
     for (int q = 0; q < 3; ++q) {
         const unsigned short* wq = p.w + (size_t)(8 * q) * WC_CHUNK;  // this third's eight chunks
-        // fc1: the third's 96 hidden units (permuted rows), chunks 0..4
+        // fc1: the third's 96 hidden units (permuted rows), chunks 0..4 (even
+        // chunks in buffer 0: eight a third keep the parities fixed)
         f32x4 h[2][6];
-#pragma unroll 1
-        for (int ks = 0; ks < 5; ++ks) {
+#pragma unroll
+        for (int nt = 0; nt < 6; ++nt) h[0][nt] = h[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        auto fc1_step = [&](int ks, auto parv) {
+            constexpr int PAR = decltype(parv)::value;  // = ks & 1
             __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the chunk (and its rows) have landed
             __syncthreads();                // everyone's have, and everyone is done with the one before
-            unsigned short* nbuf = Ws + ((ks + 1) & 1) * WC_CHUNK;
-            if (ks < 4) wc_issue<NL1, TX_WAVES>(nbuf, wq + (size_t)(ks + 1) * WC_CHUNK, wave, lane);
-            else wc_issue<NL2, TX_WAVES>(nbuf, wq + (size_t)5 * WC_CHUNK, wave, lane);
-            if (ks == 0) {
-#pragma unroll
-                for (int nt = 0; nt < 6; ++nt) {
-                    const f32x4 b4 = *(const f32x4*)(b1 + q * MX_HID + nt * 16 + lg * 4);
-                    h[0][nt] = b4;
-                    h[1][nt] = b4;
-                }
-            }
+            if (ks < 4) wc_issue<NL1, TX_WAVES>(PAR ? Ws0 : Ws1, wq + (size_t)(ks + 1) * WC_CHUNK, wave, lane);
+            else wc_issue<NL2, TX_WAVES>(Ws1, wq + (size_t)5 * WC_CHUNK, wave, lane);
             u32x4 xb[2][3];
             split_pre(pre, xb);
-            // the rows of the next fc1 chunk: this third's next k-step, or
-            // k-step 0 for the next third
-            if (ks < 4) yr.load(ks + 1, lg, pre);
-            else if (q < 2) yr.load(0, lg, pre);
-            wc_mma<6, MX_HID * WC_KS>(Ws + (ks & 1) * WC_CHUNK, lr, lg, xb, h);
+            // the rows of the next fc1 chunk: this third's next k-step (k =
+            // 144 carries the 1 of b1's column), or k-step 0 for the next third
+            if (ks < 4) yr.load_b(ks + 1, lg, pre);
+            else if (q < 2) yr.load_b(0, lg, pre);
+            wc_mma<6, MX_HID * WC_KS>(PAR ? Ws1 : Ws0, lr, lg, xb, h);
+        };
+#pragma unroll 1
+        for (int ks = 0; ks < 4; ks += 2) {
+            fc1_step(ks, CInt<0>{});
+            fc1_step(ks + 1, CInt<1>{});
         }
+        fc1_step(4, CInt<0>{});
         // fc2 over the third's units, from registers, chunks 5..7
 #pragma unroll
         for (int s = 0; s < 3; ++s) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            unsigned short* nbuf = Ws + ((s + 6) & 1) * WC_CHUNK;
-            if (s < 2) wc_issue<NL2, TX_WAVES>(nbuf, wq + (size_t)(6 + s) * WC_CHUNK, wave, lane);
-            else if (q < 2) wc_issue<NL1, TX_WAVES>(nbuf, wq + (size_t)8 * WC_CHUNK, wave, lane);
+            if (s < 2) wc_issue<NL2, TX_WAVES>(s & 1 ? Ws1 : Ws0, wq + (size_t)(6 + s) * WC_CHUNK, wave, lane);
+            else if (q < 2) wc_issue<NL1, TX_WAVES>(Ws0, wq + (size_t)8 * WC_CHUNK, wave, lane);
             if (s == 0) {
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt)
@@ -258,7 +260,7 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
                                     h[mt][2 * s + 1][2], h[mt][2 * s + 1][3]};
                 split3_x8(f, xb[mt]);
             }
-            wc_mma<9, 144 * WC_KS>(Ws + ((s + 5) & 1) * WC_CHUNK, lr, lg, xb, acc2);
+            wc_mma<9, 144 * WC_KS>(s & 1 ? Ws0 : Ws1, lr, lg, xb, acc2);
         }
     }
     tx_store_rows(acc2, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);

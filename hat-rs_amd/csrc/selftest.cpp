@@ -299,7 +299,7 @@ int gpu_selftest(std::string* err)
                 if (ws && C == 144 && epi == EPI_QKV) {
                     // the split-bf16 form on the same inputs (the last
                     // 128-row tile partial)
-                    std::vector<unsigned short> px = pack_linear_x(w.data(), N, K);
+                    std::vector<unsigned short> px = pack_linear_x(w.data(), b.data(), N, K);
                     Dev dwx(std::vector<float>((px.size() + 1) / 2)), dout2((size_t)M * N);
                     rt.h2d(dwx.p, px.data(), px.size() * sizeof(unsigned short));
                     GemmArgs px2 = p;
@@ -630,11 +630,10 @@ int gpu_selftest(std::string* err)
                 // The split-bf16 tails (tailx.hip) on the same inputs, in place
                 // as the forward runs them (out over the block input, the next
                 // norm over norm2's rows); 12 row tiles of 128.
-                std::vector<unsigned short> pwx = pack_linear_x(wp.data(), C, C), mwx;
-                std::vector<float> b1x;
-                pack_mlp_x(f1.data(), fb1.data(), f2.data(), &mwx, &b1x);
+                std::vector<unsigned short> pwx = pack_linear_x(wp.data(), nullptr, C, C), mwx;
+                pack_mlp_x(f1.data(), fb1.data(), f2.data(), &mwx);
                 Dev dpwx(std::vector<float>((pwx.size() + 1) / 2)), dmwx(std::vector<float>((mwx.size() + 1) / 2)),
-                    db1x(b1x), dout_x(res), dxn_x((size_t)T * C);
+                    dout_x(res), dxn_x((size_t)T * C);
                 Runtime::get().h2d(dpwx.p, pwx.data(), pwx.size() * sizeof(unsigned short));
                 Runtime::get().h2d(dmwx.p, mwx.data(), mwx.size() * sizeof(unsigned short));
                 TailXArgs xa{};
@@ -662,7 +661,6 @@ int gpu_selftest(std::string* err)
                 xm.out = dout_x.p;
                 xm.xn = dxn_x.p;
                 xm.w = (const unsigned short*)dmwx.p;
-                xm.bias = db1x.p;
                 xm.b2 = dfb2.p;
                 xm.nw = dmw.p;
                 xm.nb = dmb.p;
