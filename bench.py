@@ -16,6 +16,9 @@ Also reported on the same JSON line:
     measured with HIP events on the launch stream over a pass of --steps
     forwards; peak = 157.3 TFLOP/s (MI355X dense FP32 MFMA); traffic = HBM
     bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs;
+    bf16_executed: the BF16-MFMA work the kernel executes for it (six bf16
+    products per fp32 product, padding included; committed counter run)
+    against the dense BF16 peak (2.5 PFLOP/s);
   * norm_roofline: the standalone LayerNorm kernel against HBM peak (8 TB/s);
   * kernels: the same per-kernel event times for every kernel of the forward;
   * pcie: min / median wall time of a forward from and to host memory (the
@@ -43,6 +46,7 @@ sys.path.insert(0, os.path.join(REPO, "oracle"))
 
 METRIC = "output Mpx/s HAT-S x4 512x512 fp32 (1 GPU); window-attn % FP32-MFMA peak"
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense FP32 matrix
+PEAK_BF16_MFMA = 2500.0  # TFLOP/s, MI355X dense BF16 matrix
 PEAK_HBM = 8000.0       # GB/s
 WEIGHT_SEED = 1
 INPUT_SEED = 1
@@ -274,10 +278,18 @@ def main():
     roofline = {"kernel": attn_name, "bound": "mfma", "achieved": round(achieved, 3),
                 "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
                 "flop_per_launch": attn_flop, "mean_launch_ms": round(attn_ms, 5), "traffic": None}
-    traffic_file = os.path.join(REPO, "profiles", "traffic_hat_attn_sw_d24_hats512.json")
-    if os.path.exists(traffic_file) and attn_name == "hat_attn_sw_d24" and h == 512:
+    # The kernel computes on the BF16 matrix path (six bf16 products per fp32
+    # product): the work it executes there, from the committed counter run,
+    # against the dense BF16 peak.
+    traffic_file = os.path.join(REPO, "profiles", "traffic_%s_hats512.json" % attn_name)
+    if os.path.exists(traffic_file) and h == 512 and args.variant == "hat-s":
         with open(traffic_file) as f:
-            roofline["traffic"] = json.load(f)["bytes_per_launch"]
+            tr = json.load(f)
+        roofline["traffic"] = tr["bytes_per_launch"]
+        bf16 = tr["bf16_gflop_executed"] / attn_ms  # GFLOP per ms = TFLOP/s
+        roofline["bf16_executed"] = {"gflop_per_launch": tr["bf16_gflop_executed"], "achieved": round(bf16, 1),
+                                     "peak": PEAK_BF16_MFMA, "unit": "TFLOP/s",
+                                     "frac": round(bf16 / PEAK_BF16_MFMA, 4)}
 
     # HBM reference: the library's plain copy kernel over 1 GiB (read + write),
     # timed with events; rocprof counter runs of this script also see it, which
