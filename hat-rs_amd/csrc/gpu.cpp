@@ -78,6 +78,28 @@ std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int
     return out;
 }
 
+std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, int N, int K)
+{
+    constexpr int BN = 144;
+    if (K != 144 || N % BN != 0) throw Error("pack_linear_ws: needs K = 144 and N a multiple of 144");
+    std::vector<unsigned short> out((size_t)(N / BN) * 5 * WS_CHUNK, 0);
+    for (int n = 0; n < N; ++n)
+        for (int k = 0; k <= K; ++k) {
+            if (k == K && !bias) break;
+            const float x = k < K ? w[(size_t)n * K + k] : bias[n];  // k = K: the bias column
+            const unsigned short h0 = bf16_rne(x);
+            const float r1 = x - bf16_float(h0);
+            const unsigned short h1 = bf16_rne(r1);
+            const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+            const int r = n % BN, s = k / 32, g = (k % 32) / 8, j = k % 8;
+            unsigned short* d = &out[((size_t)(n / BN) * 5 + s) * WS_CHUNK + (size_t)r * 32 + (g ^ ((r >> 2) & 3)) * 8 + j];
+            d[0] = h0;
+            d[(size_t)BN * 32] = h1;
+            d[(size_t)2 * BN * 32] = h2;
+        }
+    return out;
+}
+
 // fc1 output tile t, row 4g + r (lane group g, register r) -> hidden unit
 // within a 96-unit third (tailx.hip): fc2's 32-k step s then finds units
 // 32 s + 8 g .. +7 in tiles 2 s and 2 s + 1 of lane group g.
@@ -272,9 +294,10 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
     p.cscale = cscale;
     p.eps = 1e-5f;
     if (epi == EPI_QKV && L.wx && L.K == 144 && L.N == 432 && heads == 6 && hdim == 24 && lda == 144) {
-        // split-bf16 qkv (gemmx.hip): a block per 128-token tile and slice
+        // split-bf16 qkv (gemmx.hip): weight-stationary, groups of three blocks
+        static const int cus = std::max(1, Runtime::get().cu_count());
         p.w = (const float*)L.wx;
-        launch(s, "hat_gemmx_qkv", (unsigned)gemmx_qkv_blocks(p.M), 1, 1, WX_THREADS, p);
+        launch(s, "hat_gemmx_qkv", (unsigned)(3 * gemmx_qkv_groups(cus)), 1, 1, GX_THREADS, p);
         return;
     }
     int wbn = 0;
@@ -819,7 +842,9 @@ void GpuBackend::upload_linear(const std::string& name)
         return name.size() >= n && name.compare(name.size() - n, n, t) == 0;
     };
     if (L.K == 144 && ((L.N == 432 && ends(".qkv")) || (L.N == 144 && ends("proj")))) {
-        std::vector<unsigned short> x = pack_linear_x(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K);
+        // qkv: the weight-stationary layout of hat_gemmx_qkv; proj: streamed chunks (tailx)
+        std::vector<unsigned short> x = ends(".qkv") ? pack_linear_ws(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K)
+                                                     : pack_linear_x(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K);
         L.wx = (unsigned short*)upload_bytes(x.data(), x.size() * sizeof(unsigned short));
     }
     lin_[name] = L;

@@ -27,7 +27,7 @@ struct DevLinear {
     float* w = nullptr;  // [N][Kp]
     float* b = nullptr;  // [N]
     // K = 144, N a multiple of 144: the same weights split into three bf16
-    // planes per 144-column slice (pack_linear_x), for the split-bf16 kernels
+    // the split-bf16 weights (pack_linear_ws for qkv, pack_linear_x for proj)
     unsigned short* wx = nullptr;
     int N = 0, K = 0, Kp = 0;
 };
@@ -69,6 +69,10 @@ std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
 // k = 144, split the same way; the rest of k 144..159 and the plane padding
 // zero.
 std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K);
+// The same split for hat_gemmx_qkv's weight-stationary slices: per 144-row
+// slice five chunks of three planes [144][32], each row's 16-byte k-groups
+// swizzled (g ^ ((row >> 2) & 3)), WS_CHUNK elements apart; bias at k = 144.
+std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, int N, int K);
 // The C = 144 MLP (fc1 [288][144] + b1, fc2 [144][288]) for hat_mlpx: per
 // third of the hidden layer eight weight chunks - five of fc1's 96 rows (b1
 // as their column k = 144), then three of fc2 on those units - with fc1's

@@ -247,13 +247,20 @@ struct HabTailArgs {
 // fc1 chunks (96 permuted rows, k = input channel) then three fc2 chunks (144
 // rows, k = the third's hidden units), 24 chunks in all.
 #define MX_HID 96
-// Their launch geometry: blocks of 4 waves, each block one 128-token row tile
-// (hat_gemmx_qkv: one tile and one of q, k, v; ceil(tiles / 8) * 24 blocks so
-// that the three of a tile share an XCD; tailx: one block a tile).
+// Their launch geometry (tailx): blocks of 4 waves, one 128-token row tile a block.
 #define WX_THREADS 256
 #define WX_ROWS 128
 constexpr int wx_tiles(int M) { return (M + WX_ROWS - 1) / WX_ROWS; }
-constexpr int gemmx_qkv_blocks(int M) { return (wx_tiles(M) + 7) / 8 * 24; }
+
+// The qkv linear (hat_gemmx_qkv) keeps one 144-column slice in LDS for the
+// whole launch: five chunks of three bf16 planes [144][32], unpadded, each
+// row's four 16-byte k-groups stored at g ^ ((row >> 2) & 3) (so that 16
+// consecutive rows read at one k-group hit distinct banks); WS_CHUNK elements
+// apart (27 loads of 1 KB). Groups of three blocks (one per slice, on one
+// XCD) walk the same 32-token subtiles: GX_GROUPS(cus) groups of 8 waves.
+#define WS_CHUNK (3 * 144 * 32)
+#define GX_THREADS 512
+constexpr int gemmx_qkv_groups(int cus) { return cus >= 24 ? cus / 24 * 8 : 1; }
 
 struct TailXArgs {
     const float* a;            // projx: attention output; mlpx: LN2(x') rows

@@ -11,23 +11,21 @@
 // at k = 144 is 1 and the weights there hold the bias (split like the rest,
 // so it is added exactly), k 145..159 are zeros against zeros.
 //
-// Data flow: a block of 4 waves takes one 128-token row tile through one of
-// the three 144-column slices (q, k or v): its waves hold their 32 token rows
-// in registers for the whole block (all five k-steps, read once) and the
-// slice's five weight chunks (one 32-k step each, pre-split on the host, 40
-// KB) stream through two LDS buffers, chunk c + 1 in flight while chunk c's
-// MFMAs run (common.h). The two buffers are two LDS objects, so that the
-// compiler sees that reading one need not wait for the copy into the other.
-// Two blocks share a CU, so one block's reads overlap the other's MFMAs, and
-// the results leave once, at the block's end. The three blocks of a tile are
-// placed on one XCD (blocks are dealt to the 8 XCDs in turn), so that two of
-// the three reads of the tile's rows hit its L2.
+// Data flow: weight-stationary. A block of 8 waves holds one 144-column
+// slice (q, k or v: five 32-k chunks, 135 KB, unpadded and swizzled) in LDS
+// for the whole launch, loaded once; after that its waves share nothing and
+// meet at no barrier. Each wave walks 32-token subtiles on its own: their rows
+// (five k-steps) in registers, split per k-step, then 108 MFMAs; the next
+// subtile's rows of a k-step are read as soon as that step has been split.
+// The three slices' blocks of a group sit on one XCD (blocks are dealt to the
+// 8 XCDs in turn) and walk the same subtiles in the same order, so that two of
+// a subtile's three reads find its rows in that XCD's L2. Results leave
+// through a wave-private LDS stage as 1.5 KB runs of one head.
 //
-// The host launches it for heads = 6, head_dim = 24 (the slices are q, k, v),
-// on ceil(tiles / 8) * 24 blocks.
+// The host launches 3 * gemmx_qkv_groups(CUs) blocks for heads = 6,
+// head_dim = 24 (the slices are q, k, v).
 
-#define GX_WAVES 4
-#define GX_ROWS (GX_WAVES * 32)  // tokens per tile
+#define GX_WAVES 8
 
 // This wave's 32 token rows of a [M][144] plane, 8 values at k = 32 ks + 8 lg
 // per token, for the B operand (zeros past M and past k = 144).
@@ -77,65 +75,105 @@ __device__ __forceinline__ void split_pre(const f32x4 (&pre)[2][2], u32x4 (&xb)[
     }
 }
 
-extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 2) void hat_gemmx_qkv(GemmArgs p)
+extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv(GemmArgs p)
 {
-    constexpr int NT = 9, QS_S = 52, NL = 36;  // a 144-row chunk as 9 loads from each wave
-    __shared__ __attribute__((aligned(16))) unsigned short Ws0[36 * 512];  // also the results' staging
-    __shared__ __attribute__((aligned(16))) unsigned short Ws1[36 * 512];
+    constexpr int NT = 9, QS_S = 48, NLOAD = 5 * WS_CHUNK / 512;  // 135 loads of 1 KB
+    static_assert(5 * WS_CHUNK % 512 == 0, "whole loads");
+    __shared__ __attribute__((aligned(16))) unsigned short Wsl[5 * WS_CHUNK];  // the slice
+    __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * QS_S];  // per-wave staging
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
     const int lr = lane & 15, lg = lane >> 4;
     const int M = p.M;
-    // block -> (tile, slice): blocks b, b + 8, b + 16 (one XCD) take the three
-    // slices of one tile
-    const int xcd = blockIdx.x & 7, i = blockIdx.x >> 3;
-    const int tile = (i / 3) * 8 + xcd, sl = i - (i / 3) * 3;
-    if (tile * GX_ROWS >= M) return;  // whole block, before any barrier
-    const unsigned short* wx = (const unsigned short*)p.w + (size_t)sl * 5 * WC_CHUNK;  // this slice's chunks
-    wc_issue<NL, GX_WAVES>(Ws0, wx, wave, lane);
-    const int mbase = tile * GX_ROWS + wave * 32;
+    // block -> (group, slice): with a multiple of 8 groups, blocks b, b + 8,
+    // b + 16 (one XCD) are one group's three slices
+    const int G = gridDim.x / 3;
+    int grp, sl;
+    if (G % 8 == 0) {
+        const int i = blockIdx.x >> 3;
+        sl = i % 3;
+        grp = (i / 3) * 8 + (blockIdx.x & 7);
+    } else {
+        sl = blockIdx.x / G;
+        grp = blockIdx.x - sl * G;
+    }
+    {
+        const unsigned short* src = (const unsigned short*)p.w + (size_t)sl * 5 * WS_CHUNK;
+        const unsigned loff = (unsigned)lane * 16;
+#pragma unroll 1
+        for (int i = wave; i < NLOAD; i += GX_WAVES)
+            __builtin_amdgcn_global_load_lds((const void*)((const char*)src + (size_t)i * 1024 + loff),
+                                             (__attribute__((address_space(3))) void*)(Wsl + i * 512), 16, 0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // the slice is in LDS; no barrier after this one
+    }
+    // this lane's A-operand offset: row lr of a 16-row tile, k-group lg swizzled
+    const unsigned short* wl = Wsl + lr * 32 + ((lg ^ ((lr >> 2) & 3)) * 8);
+    float* out = p.out + (size_t)sl * p.heads * M * 24;
+    float* Q = Qs + wave * 16 * QS_S;
+    const int nsub = (M + 31) / 32;
+    const int stride = G * GX_WAVES;
+    int sub = grp * GX_WAVES + wave;
+    if (sub >= nsub) return;
     WcRows xr;
-    xr.init(p.a, mbase, M, lr);
+    xr.init(p.a, sub * 32, M, lr);
     f32x4 y[5][2][2];
 #pragma unroll
     for (int ks = 0; ks < 5; ++ks) xr.load_b(ks, lg, y[ks]);
-    f32x4 acc[2][NT];
+#pragma unroll 1
+    for (; sub < nsub; sub += stride) {
+        // the next subtile's rows, or (past the last) this one's again: the
+        // loads are issued either way, so that their count never depends on
+        // the path and the compiler's waits stay exact
+        xr.init(p.a, (sub + stride < nsub ? sub + stride : sub) * 32, M, lr);
+        f32x4 acc[2][NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[0][nt] = acc[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; ++nt) acc[0][nt] = acc[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 5; ++c) {
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk c (and its rows) have landed
-        __syncthreads();                // everyone's have, and everyone is done with chunk c - 1
-        if (c + 1 < 5) wc_issue<NL, GX_WAVES>(c & 1 ? Ws0 : Ws1, wx + (size_t)(c + 1) * WC_CHUNK, wave, lane);
-        u32x4 xb[2][3];
-        split_pre(y[c], xb);
-        wc_mma<NT, 144 * WC_KS>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
-    }
-    __syncthreads();  // every wave is done with the weights
-    // Two heads at a time go through the wave's LDS region and leave as 16
-    // consecutive rows of each head (1536 contiguous bytes), non-temporal.
-    float* Q = (float*)Ws0 + wave * 16 * QS_S;
+        for (int ks = 0; ks < 5; ++ks) {
+            u32x4 xb[2][3];
+            split_pre(y[ks], xb);
+            xr.load_b(ks, lg, y[ks]);  // the next subtile's rows of this k-step
+            // weight fragments of tile nt + 1 read while tile nt's 12 MFMAs run
+            const unsigned short* wr = wl + ks * WS_CHUNK;
+            u32x4 wa[2][3];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const int mb = mbase + mt * 16;
-        const int mrows = M - mb;
+            for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * 144 * 32);
 #pragma unroll
-        for (int ph = 0; ph < 3; ++ph) {
+            for (int nt = 0; nt < NT; ++nt) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (nt + 1 < NT) {
 #pragma unroll
-            for (int t = 0; t < 3; ++t) *(f32x4*)(Q + lr * QS_S + t * 16 + lg * 4) = acc[mt][3 * ph + t];
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
-#pragma unroll
-            for (int i2 = 0; i2 < 3; ++i2) {
-                const int f = lane + 64 * i2, hh = f / 96, r = (f - hh * 96) / 6, d4 = f - hh * 96 - r * 6;
-                const f32x4 v = *(const f32x4*)(Q + r * QS_S + hh * 24 + d4 * 4);
-                if (r < mrows) {
-                    const int head = 2 * ph + hh;
-                    __builtin_nontemporal_store(
-                        v, (f32x4*)(p.out + ((size_t)(sl * p.heads + head) * M + mb + r) * 24 + d4 * 4));
+                    for (int pl = 0; pl < 3; ++pl)
+                        wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * 32 + pl * 144 * 32);
                 }
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
             }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next phase's writes
+        }
+        // Two heads at a time go through the wave's LDS region and leave as 16
+        // consecutive rows of each head (1536 contiguous bytes), non-temporal.
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int mb = sub * 32 + mt * 16;
+            const int mrows = M - mb;
+#pragma unroll
+            for (int ph = 0; ph < 3; ++ph) {
+#pragma unroll
+                for (int t = 0; t < 3; ++t) *(f32x4*)(Q + lr * QS_S + t * 16 + lg * 4) = acc[mt][3 * ph + t];
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+#pragma unroll
+                for (int i2 = 0; i2 < 3; ++i2) {
+                    const int f = lane + 64 * i2, hh = f / 96, r = (f - hh * 96) / 6, d4 = f - hh * 96 - r * 6;
+                    const f32x4 v = *(const f32x4*)(Q + r * QS_S + hh * 24 + d4 * 4);
+                    // rows past M go to the sink (a store is issued either way)
+                    float* dst = r < mrows ? out + ((size_t)(2 * ph + hh) * M + mb + r) * 24 + d4 * 4
+                                           : hat_sink_row + d4 * 4;
+                    __builtin_nontemporal_store(v, (f32x4*)dst);
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next phase's writes
+            }
         }
     }
 }

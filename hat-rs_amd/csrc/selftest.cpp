@@ -299,13 +299,13 @@ int gpu_selftest(std::string* err)
                 if (ws && C == 144 && epi == EPI_QKV) {
                     // the split-bf16 form on the same inputs (the last
                     // 128-row tile partial)
-                    std::vector<unsigned short> px = pack_linear_x(w.data(), b.data(), N, K);
+                    std::vector<unsigned short> px = pack_linear_ws(w.data(), b.data(), N, K);
                     Dev dwx(std::vector<float>((px.size() + 1) / 2)), dout2((size_t)M * N);
                     rt.h2d(dwx.p, px.data(), px.size() * sizeof(unsigned short));
                     GemmArgs px2 = p;
                     px2.w = dwx.p;
                     px2.out = dout2.p;
-                    launch(s, "hat_gemmx_qkv", (unsigned)gemmx_qkv_blocks(M), 1, 1, WX_THREADS, px2);
+                    launch(s, "hat_gemmx_qkv", 3, 1, 1, GX_THREADS, px2);  // one group: its waves walk all 19 subtiles
                     check_close("hat_gemmx_qkv C 144", dout2.get(), want, 3e-5);
                     note("hat_gemmx_qkv C 144 M " + std::to_string(M) + " K 144");
                 }
