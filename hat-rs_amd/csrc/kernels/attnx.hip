@@ -2,9 +2,9 @@
 // position bias + shift mask + softmax + PV for one (window, head) per block.
 //
 // The same operator as attn.hip (cpu.rs:772-844; hat.cu:246-316) on gfx950's
-// BF16 matrix path, which runs at 13.7x the FP32 MFMA rate and, unlike FP32
-// MFMA, overlaps with VALU work on a SIMD (measured: a BF16 MFMA stream and an
-// independent FMA stream together take the time of the longer one). Every fp32
+// BF16 matrix path, whose peak is 16x the FP32 MFMA rate. VALU and MFMA work
+// share a SIMD's issue time (measured: they do not overlap, from one wave or
+// from two), so the splits and exponentials below cost their full time. Every fp32
 // operand x enters as three bf16 parts, x = x0 + x1 + x2 + e with |e| <=
 // 2^-27 |x| (each part the round-to-nearest of what the earlier ones leave),
 // and a product as the six terms a_i b_j with i + j <= 2, accumulated in fp32
@@ -116,7 +116,9 @@ __device__ __forceinline__ void attnx_stash(unsigned short* Kp, unsigned short* 
 }
 
 // The lane's q, pre-scaled and split: qb[s][part] = dims 16s + 8h .. 16s + 8h
-// + 7 of its query (zeros past D).
+// + 7 of its query (zeros past D). For D = 24 the second step is packed (see
+// AttnxKRows): qb[1][0] = dims 16..23 of part h ? 0 : 2, qb[1][1] = of part
+// h ? 0 : 1.
 template <int D>
 __device__ __forceinline__ int attnx_query(const AttnArgs& p, int wi, int head, u32x4 (&qb)[2][3])
 {
@@ -133,14 +135,14 @@ __device__ __forceinline__ int attnx_query(const AttnArgs& p, int wi, int head, 
     float qv[2][8];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-        const int d0 = 16 * s + 8 * h;
-        if constexpr (D % 4 == 0) {
-            // D = 24: dims 24..31 (s = 1, h = 1) are zero
-            const bool live = d0 + 8 <= D;
-            const f32x4 a = load_or_zero(Qg + d0, live), b = load_or_zero(Qg + d0 + 4, live);
+        if constexpr (D == 24) {
+            // both halves of the packed second step hold dims 16..23
+            const int d0 = s == 0 ? 8 * h : 16;
+            const f32x4 a = *(const f32x4*)(Qg + d0), b = *(const f32x4*)(Qg + d0 + 4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) qv[s][j] = a[j], qv[s][4 + j] = b[j];
         } else {
+            const int d0 = 16 * s + 8 * h;
 #pragma unroll
             for (int j = 0; j < 8; j += 2) {
                 const bool live = d0 + j + 2 <= D;
@@ -156,8 +158,50 @@ __device__ __forceinline__ int attnx_query(const AttnArgs& p, int wi, int head, 
         for (int j = 0; j < 8; ++j) qv[s][j] *= p.qscale;
         split3_x8(qv[s], qb[s]);
     }
+    if constexpr (D == 24) {
+        const u32x4 q0 = qb[1][0], q1 = qb[1][1], q2 = qb[1][2];
+        qb[1][0] = h ? q0 : q2;
+        qb[1][1] = h ? q0 : q1;
+    }
     return qpix;
 }
+
+// The lane's K rows for S^T = K Q^T over 32-key tiles of three planes [keys][KS]
+// (A = 32 keys x 16 dims: lane l gives key l % 32, dims 8h .. 8h + 7 of the step).
+// Step 0 (dims 0..15) is the six products of mfma6. For D = 24, step 1 has only
+// dims 16..23, so each MFMA carries two of the six products, one per lane half:
+// [k1 | k2] . [q1 | q0], [k0 | k1] . [q2 | q0], [k0 | k0] . [q1 | q0] (half 0 |
+// half 1): the same terms in three MFMAs instead of six. For D = 30 step 1 is
+// dims 16..31 (30, 31 zero) as step 0.
+template <int D, int KS, int KPL>
+struct AttnxKRows {
+    const unsigned short *r0, *r12, *r3;
+    __device__ __forceinline__ void init(const unsigned short* Kp, int ql, int h)
+    {
+        r0 = Kp + ql * KS + 8 * h;
+        r12 = Kp + ql * KS + 16 + h * KPL;  // plane h (+1)
+        r3 = Kp + ql * KS + 16;             // plane 0
+    }
+    // s += K Q^T for the tile whose first key row is koff elements in
+    __device__ __forceinline__ f32x16 qk(int koff, const u32x4 (&qb)[2][3], f32x16 s) const
+    {
+        u32x4 ka[3];
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) ka[pl] = *(const u32x4*)(r0 + pl * KPL + koff);
+        s = mfma6(ka, qb[0], s);
+        if constexpr (D == 24) {
+            const u32x4 a12 = *(const u32x4*)(r12 + KPL + koff), a01 = *(const u32x4*)(r12 + koff),
+                        a00 = *(const u32x4*)(r3 + koff);
+            s = mfma_bf16(a12, qb[1][1], s);
+            s = mfma_bf16(a01, qb[1][0], s);
+            return mfma_bf16(a00, qb[1][1], s);
+        } else {
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) ka[pl] = *(const u32x4*)(r0 + pl * KPL + koff + 16);
+            return mfma6(ka, qb[1], s);
+        }
+    }
+};
 
 template <int D, bool MASKED>
 __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned char* lds, int wi, int head,
@@ -187,10 +231,10 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
     constexpr int RH = (D % 8) / 4, RR = (D / 8) * 4 + D % 4;
 
     // The lane's V^T row (dims past D read row D: their outputs are not used)
-    // and K row. For D = 24 the second step's upper lane half reads the next
-    // key's first dims, multiplied by the zeros of its q operand.
+    // and K rows.
     const unsigned short* vrow = Vp + (ql < D ? ql : D) * X::VS + 8 * h;
-    const unsigned short* krow = Kp + ql * X::KS + 8 * h;
+    AttnxKRows<D, X::KS, X::KPL> kr;
+    kr.init(Kp, ql, h);
 
     f32x16 o;
 #pragma unroll
@@ -209,13 +253,7 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
             if (MASKED) b += madd[(ky >> 3) & 1][(kx >> 3) & 1];
             s[i] = b;
         }
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            u32x4 ka[3];
-#pragma unroll
-            for (int pl = 0; pl < 3; ++pl) ka[pl] = *(const u32x4*)(krow + pl * X::KPL + kt * 32 * X::KS + 16 * st);
-            s = mfma6(ka, qb[st], s);
-        }
+        s = kr.qk(kt * 32 * X::KS, qb, s);
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
@@ -406,7 +444,8 @@ __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int 
     // idx = (ky*39 + kx) - (qy*39 + qx) + 600 on the rotated table (attn.hip)
     const int oca_base = 600 - (qy * 39 + qx);
     const unsigned short* vrow = Vp + (ql < D ? ql : D) * X::VS + 8 * h;
-    const unsigned short* krow = Kp + ql * X::KS + 8 * h;
+    AttnxKRows<D, X::KS, X::KPL> kr;
+    kr.init(Kp, ql, h);
 #pragma unroll 1
     for (int kt = 0; kt < NKT; ++kt) {
         f32x16 s;
@@ -416,13 +455,7 @@ __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int 
             const int ky = (int)((unsigned)key / 24u);
             s[i] = Tb[oca_base + key + 15 * ky];
         }
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            u32x4 ka[3];
-#pragma unroll
-            for (int pl = 0; pl < 3; ++pl) ka[pl] = *(const u32x4*)(krow + pl * X::KPL + kt * 32 * X::KS + 16 * st);
-            s = mfma6(ka, qb[st], s);
-        }
+        s = kr.qk(kt * 32 * X::KS, qb, s);
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
