@@ -200,13 +200,27 @@ static bool wino_conv(int CO, int CI, int r)
     return (r == 0 && CI == 144 && (CO == 144 || CO == 64)) || (r == 2 && CI == 64 && CO == 256);
 }
 
-std::vector<float> pack_cab_conv1(const float* w)
+// conv1 [6][144][3][3] as the split A operands of hat_cab_conv1* (CX_WPACK):
+// row r = tap * 6 + co (rows 54..63 zero), each weight as three bf16 parts.
+std::vector<unsigned short> pack_cab_conv1(const float* w)
 {
-    std::vector<float> out((size_t)64 * CAB_C, 0.0f);
-    for (int co = 0; co < CAB_CC; ++co)
-        for (int ci = 0; ci < CAB_C; ++ci)
-            for (int tap = 0; tap < 9; ++tap)
-                out[(size_t)(tap * CAB_CC + co) * CAB_C + ci] = w[((size_t)co * CAB_C + ci) * 9 + tap];
+    std::vector<unsigned short> out(CX_WPACK, 0);
+    for (int ks = 0; ks < 9; ++ks)
+        for (int nt = 0; nt < 2; ++nt)
+            for (int lane = 0; lane < 64; ++lane)
+                for (int j = 0; j < 8; ++j) {
+                    const int r = nt * 32 + lane % 32, ci = ks * 16 + 8 * (lane / 32) + j;
+                    if (r >= 9 * CAB_CC) continue;
+                    const int tap = r / CAB_CC, co = r % CAB_CC;
+                    const float x = w[((size_t)co * CAB_C + ci) * 9 + tap];
+                    const unsigned short h0 = bf16_rne(x);
+                    const float r1 = x - bf16_float(h0);
+                    const unsigned short h1 = bf16_rne(r1);
+                    const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+                    const unsigned short parts[3] = {h0, h1, h2};
+                    for (int part = 0; part < 3; ++part)
+                        out[((size_t)((ks * 2 + nt) * 3 + part) * 64 + lane) * 8 + j] = parts[part];
+                }
     return out;
 }
 
@@ -383,15 +397,11 @@ void run_cab(hipStream_t s, const DevCab& cb, const float* xn, int H, int W, con
     if (sq < 1 || sq > 64) throw Error("CAB: squeeze width must be 1..64");
     static const int cus = std::max(1, Runtime::get().cu_count());
     CabConvArgs a{xn, cb.w1, cb.b1, t1, partial, H, W};
-    // Persistent over the output tiles: 16 wide x 32 tall with one block of 8
-    // waves per CU (137 KB of LDS) when the height allows, else 16 x 16 with
-    // two blocks of 4 waves per CU (73 KB each).
+    // Persistent over the output tiles, one block of 4 waves per CU: 16 wide x
+    // 32 tall when the height allows, else 16 x 16.
     const bool t32 = H % 32 == 0;
     const int tiles = (H / (t32 ? 32 : 16)) * (W / 16);
-    if (t32)
-        launch(s, "hat_cab_conv1_t32", (unsigned)std::min(tiles, cus), 1, 1, 512, a);
-    else
-        launch(s, "hat_cab_conv1", (unsigned)std::min(tiles, 2 * cus), 1, 1, 256, a);
+    launch(s, t32 ? "hat_cab_conv1_t32" : "hat_cab_conv1", (unsigned)std::min(tiles, cus), 1, 1, 256, a);
     CabGateArgs g{};
     g.partial = partial;
     g.t1 = t1;
@@ -920,9 +930,9 @@ GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
             if (cab_fold_) {
                 const std::string c = p + ".conv_block.cab.";
                 for (const char* n : {"0.bias", "2.weight", "2.bias"}) upload_raw(c + n);
-                std::vector<float> w1 = pack_cab_conv1(wt.t(c + "0.weight"));
+                std::vector<unsigned short> w1 = pack_cab_conv1(wt.t(c + "0.weight"));
                 DevCab cb;
-                cb.w1 = upload(w1.data(), w1.size());
+                cb.w1 = (unsigned short*)upload_bytes(w1.data(), w1.size() * sizeof(unsigned short));
                 cb.b1 = raw_.at(c + "0.bias");
                 cb.w2 = raw_.at(c + "2.weight");
                 cb.b2 = raw_.at(c + "2.bias");

@@ -35,7 +35,7 @@ struct DevLinear {
 // The CAB of the compress-to-6 family, in the folded form (conv1 per-tap
 // weights; conv2 and the channel attention as raw tensors for the gate kernel).
 struct DevCab {
-    float* w1 = nullptr;  // [64][144], row tap*6 + co
+    unsigned short* w1 = nullptr;  // conv1 split for hat_cab_conv1* (CX_WPACK bf16)
     float* b1 = nullptr;  // [6]
     float* w2 = nullptr;  // [144][6][3][3]
     float* b2 = nullptr;  // [144]
@@ -47,7 +47,7 @@ struct DevCab {
 
 // conv1 weight [6][144][3][3] -> [64][144]: row tap*6 + co holds w[co][:][tap],
 // rows 54..63 zero.
-std::vector<float> pack_cab_conv1(const float* w);
+std::vector<unsigned short> pack_cab_conv1(const float* w);
 
 // hat_mlpx's weights: the packed slices and b1 in fc1's row order.
 struct DevMlpX {

@@ -79,11 +79,15 @@ struct GemmArgs {
 #define CAB_CC 6             // compressed channels
 #define CAB_CS 8             // t1 channel stride (channels 6, 7 are zero)
 #define CAB_K2 56            // 9 taps x 6 channels (k = tap*6 + ci), 2 zero: 3 x 16 + 8
+// conv1's weights split for hat_cab_conv1*: per 16-channel step ks (9), row
+// tile nt (2 x 32 rows, row tap*6 + co, rows 54.. zero) and part (3), the
+// 32x32x16 A operand of each lane (row l % 32, channels 16 ks + 8 (l / 32) .. +7)
+#define CX_WPACK (9 * 2 * 3 * 64 * 8)
 #define CAB_NSUM 5           // per-tile sums: whole tile, row 0, row H-1, col 0, col W-1
 
 struct CabConvArgs {
     const float* xn;     // [H*W][144]
-    const float* w;      // [64][144]: row tap*6 + co = conv1 weight[co][:][tap]; rows 54.. zero
+    const unsigned short* w;  // [9][2][3][64][8] bf16: step ks, row tile nt, part, lane (CX_WPACK)
     const float* bias;   // [6]
     float* t1;           // [H*W][8]: gelu(conv1(xn))
     float* partial;      // [CAB_NSUM * 8][tiles] (value-major)

@@ -26,23 +26,6 @@
 
 using namespace hatk;
 
-__device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c)
-{
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-}
-
-// The six products of a 3-part A and a 3-part B into c, smallest first.
-__device__ __forceinline__ f32x16 mfma6(const u32x4 (&a)[3], const u32x4 (&b)[3], f32x16 c)
-{
-    c = mfma_bf16(a[2], b[0], c);
-    c = mfma_bf16(a[1], b[1], c);
-    c = mfma_bf16(a[0], b[2], c);
-    c = mfma_bf16(a[1], b[0], c);
-    c = mfma_bf16(a[0], b[1], c);
-    return mfma_bf16(a[0], b[0], c);
-}
-
 template <int D>
 struct AttnXShape {
     static constexpr int NK = 256;

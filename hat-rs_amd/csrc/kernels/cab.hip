@@ -20,176 +20,206 @@
 using namespace hatk;
 
 // ---------------------------------------------------------------------------
-// conv1 (144 -> 6, 3x3, zero padding) + GELU, one 16-wide, TY-tall output tile
-// at a time.
+// conv1 (144 -> 6, 3x3, zero padding) + GELU on split-bf16 MFMA, one 16-wide,
+// TY-tall output tile at a time: persistent over the tiles, one block of four
+// waves per CU.
 //
 // Per-tap products: for each pixel q of the tile's 18 x (TY+2) halo,
 // P[q][tap*6+co] = sum_ci xn[q][ci] * w[co][ci][tap] is a 144-deep product with
-// 54 (padded to 64) outputs - one MFMA row tile of 16 halo pixels x 4 column
-// tiles. The conv output at p is then sum over the 9 taps of
-// P[p + d(tap)][tap*6 + co], read from LDS. The weights (64 x 144) stay in
-// registers for the whole kernel, so a block streams its tiles with no weight
-// traffic.
-//   TY = 16: 4 waves, two blocks per CU (73 KB of LDS each); the halo is 21 row
-//            tiles (one wave has six, the others five).
-//   TY = 32: 8 waves, one block per CU (137 KB); the halo is 39 row tiles (five
-//            per wave, one wave four) for twice the pixels: fewer halo pixels
-//            per output pixel and a better balance across the waves.
-#define CC1_HS 18   // halo width
-#define CC1_PS 56   // LDS row stride of P (54 used)
+// 54 outputs (padded to 64): v_mfma_f32_32x32x16_bf16 with the 64 weight rows as
+// A (two tiles of 32) and 32 halo pixels as B, nine 16-channel steps, every fp32
+// operand as three bf16 parts and every product as the six terms of order <= 2
+// (the arithmetic of the split-bf16 attention, as accurate as FP32 MFMA). The
+// conv output at p is then the sum over the 9 taps of P[p + d(tap)][tap*6 + co],
+// read from LDS in fp32. The split weights (216 registers a lane) stay in
+// registers for the whole kernel, which takes the register file of one wave per
+// SIMD. Each wave streams its 32-pixel halo tiles (TY = 32: 612 pixels in 20
+// tiles, five a wave; TY = 16: 324 in 11), loading the next tile's 144 channels
+// step by step while this one's MFMAs run, across the output tiles too: the
+// barriers here wait for LDS only, so those loads stay in flight through them.
+#define CX_WAVES 4
+#define CX_HS 18  // halo width
+#define CX_PS 60  // LDS row stride of P (56 written, 54 used): a b128 phase's 16 rows on distinct banks
 
 template <int TY>
-struct Cc1Shape {
-    static constexpr int WAVES = TY == 32 ? 8 : 4;
-    static constexpr int THREADS = WAVES * 64;
-    static constexpr int HY = TY + 2;            // halo height
-    static constexpr int HP = CC1_HS * HY;       // halo pixels
-    static constexpr int RT = (HP + 15) / 16;    // row tiles of 16 pixels
-    static_assert(16 * TY == THREADS, "one output pixel per thread");
+struct Cx1Shape {
+    static constexpr int HY = TY + 2;
+    static constexpr int HP = CX_HS * HY;      // halo pixels
+    static constexpr int PT = (HP + 31) / 32;  // 32-pixel halo tiles
+    static constexpr int NPW = (PT + CX_WAVES - 1) / CX_WAVES;  // per wave (past PT: zeros, not stored)
+    static constexpr int NPX = TY / 16;        // output pixels per thread
+    static_assert(16 * TY == CX_WAVES * 64 * NPX, "whole pixels per thread");
 };
 
 template <int TY>
 __device__ __forceinline__ void cab_conv1_body(const CabConvArgs& p)
 {
-    using S = Cc1Shape<TY>;
-    constexpr int WAVES = S::WAVES;
-    __shared__ float Ps[S::HP * CC1_PS];
-    __shared__ float red[WAVES][CAB_NSUM * CAB_CC];
+    using S = Cx1Shape<TY>;
+    __shared__ __attribute__((aligned(16))) float Ps[S::HP * CX_PS];
+    __shared__ float red[CX_WAVES][CAB_NSUM * CAB_CC];
 
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    const int lr = lane & 15;
-    const int lg = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
+    const int pl = lane & 31, h = lane >> 5;
     const int H = p.H, W = p.W;
     const int ntx = W / 16;
     const int ntiles = ntx * (H / TY);
 
-    f32x4 wreg[4][CAB_C / 16];
+    // The split weights go through LDS (the P region, free until the first
+    // halo tile's stores) once per block, then into every wave's registers.
+    constexpr int NWU = CX_WPACK / 8, WIT = (NWU + CX_WAVES * 64 - 1) / (CX_WAVES * 64);  // 16-byte units
+    static_assert(NWU * 16 <= S::HP * CX_PS * 4, "the weights fit the P region");
+    u32x4 stage[WIT];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int kc = 0; kc < CAB_C / 16; ++kc)
-            wreg[nt][kc] = *(const f32x4*)(p.w + (nt * 16 + lr) * CAB_C + kc * 16 + lg * 4);
+    for (int i = 0; i < WIT; ++i) {
+        const int e = min(tid + i * CX_WAVES * 64, NWU - 1);  // the last units again past the end
+        stage[i] = ((const u32x4*)p.w)[e];
+    }
     float bias[CAB_CC];
 #pragma unroll
     for (int co = 0; co < CAB_CC; ++co) bias[co] = p.bias[co];
 
-    // This wave's halo row tiles rt = wave, wave + WAVES, ... of the block's
-    // tiles are walked as one stream of 16-channel chunks (9 per row tile), the
-    // input rows held in nine register slots: chunk kc of the next row tile (of
-    // this tile, or the first of the block's next tile) is loaded as soon as
-    // chunk kc of this one has gone to its MFMAs, a whole row tile (144 MFMAs)
-    // ahead.
-    const int nrt = (S::RT - wave + WAVES - 1) / WAVES;
-    auto src_of = [&](int tl, int i) -> const float* {  // lane's input row of row tile i of tile tl, or null
-        if (tl >= ntiles) return nullptr;
+    // The lane's input row (channels 8h.. of each 16-channel step) for halo
+    // tile i of output tile tl; hat_zero_row outside the plane, past the halo
+    // and past the last tile, so that the loads are issued on every path.
+    auto src_of = [&](int tl, int i) -> const float* {
         const int ty = tl / ntx, tx = tl - ty * ntx;
-        const int hi = (wave + WAVES * i) * 16 + lr;
-        const int hy = hi / CC1_HS, hx = hi - hy * CC1_HS;
+        const int hi = (wave + CX_WAVES * i) * 32 + pl;
+        const int hy = hi / CX_HS, hx = hi - hy * CX_HS;
         const int gy = ty * TY - 1 + hy, gx = tx * 16 - 1 + hx;
-        const bool valid = hi < S::HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
-        return valid ? p.xn + (size_t)(gy * W + gx) * CAB_C + lg * 4 : nullptr;
+        const bool valid = tl < ntiles && hi < S::HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
+        return valid ? p.xn + (size_t)(gy * W + gx) * CAB_C + 8 * h : hat_zero_row;
     };
-    f32x4 xa[CAB_C / 16];
-    auto load = [&](int slot, const float* src, int kc) {
-        f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-        if (src) v = *(const f32x4*)(src + kc * 16);
-        xa[slot] = v;
-    };
+    f32x4 xr[9][2];
     {
         const float* first = src_of(blockIdx.x, 0);
 #pragma unroll
-        for (int s = 0; s < CAB_C / 16; ++s) load(s, first, s);
+        for (int ks = 0; ks < 9; ++ks) {
+            xr[ks][0] = *(const f32x4*)(first + ks * 16);
+            xr[ks][1] = *(const f32x4*)(first + ks * 16 + 4);
+        }
     }
+#pragma unroll
+    for (int i = 0; i < WIT; ++i) ((u32x4*)Ps)[min(tid + i * CX_WAVES * 64, NWU - 1)] = stage[i];
+    lds_barrier();
+    u32x4 wr[9][2][3];
+#pragma unroll
+    for (int ks = 0; ks < 9; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int part = 0; part < 3; ++part)
+                wr[ks][nt][part] = ((const u32x4*)Ps)[((ks * 2 + nt) * 3 + part) * 64 + lane];
+    lds_barrier();  // every wave has its weights before P is written
 
     for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int ty = tile / ntx, tx = tile - ty * ntx;
         const int y0 = ty * TY, x0 = tx * 16;
-#pragma unroll 1
-        for (int i = 0; i < nrt; ++i) {
-            const float* nxt = i + 1 < nrt ? src_of(tile, i + 1) : src_of(tile + gridDim.x, 0);
-            f32x4 acc[4];
+        // unrolled: with no back-edge here, the compiler's waits for the rows
+        // read ahead are exact
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) acc[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < S::NPW; ++i) {
+            const float* nxt = i + 1 < S::NPW ? src_of(tile, i + 1) : src_of(tile + gridDim.x, 0);
+            f32x16 acc[2];
 #pragma unroll
-            for (int kc = 0; kc < CAB_C / 16; ++kc) {
-                const f32x4 a = xa[kc];
-                load(kc, nxt, kc);  // chunk kc of the next row tile
+            for (int j = 0; j < 16; ++j) acc[0][j] = acc[1][j] = 0.0f;
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
+            for (int ks = 0; ks < 9; ++ks) {
+                const float f[8] = {xr[ks][0][0], xr[ks][0][1], xr[ks][0][2], xr[ks][0][3],
+                                    xr[ks][1][0], xr[ks][1][1], xr[ks][1][2], xr[ks][1][3]};
+                u32x4 xb[3];
+                split3_x8(f, xb);
+                xr[ks][0] = *(const f32x4*)(nxt + ks * 16);  // step ks of the next halo tile
+                xr[ks][1] = *(const f32x4*)(nxt + ks * 16 + 4);
 #pragma unroll
-                    for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16(wreg[nt][kc][s], a[s], acc[nt]);
+                for (int nt = 0; nt < 2; ++nt) acc[nt] = mfma6(wr[ks][nt], xb, acc[nt]);
+                __builtin_amdgcn_sched_barrier(0);  // the loads stay in their step
             }
-            // lane (lr, lg) holds P[hi][16nt + 4lg .. +3]; columns 56.. are not stored
-            const int hi = (wave + WAVES * i) * 16 + lr;
+            // lane (pl, h) holds P[hi][32 nt + 8 g + 4 h .. +3] in acc[nt][4g .. 4g+3];
+            // columns 56.. (nt = 1, g = 3) are not stored
+            const int hi = (wave + CX_WAVES * i) * 32 + pl;
             if (hi < S::HP) {
 #pragma unroll
-                for (int nt = 0; nt < 4; ++nt)
-                    if (nt * 16 + lg * 4 < CC1_PS) *(f32x4*)(Ps + hi * CC1_PS + nt * 16 + lg * 4) = acc[nt];
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int g = 0; g < (nt == 0 ? 4 : 3); ++g)
+                        *(f32x4*)(Ps + hi * CX_PS + 32 * nt + 8 * g + 4 * h) =
+                            (f32x4){acc[nt][4 * g], acc[nt][4 * g + 1], acc[nt][4 * g + 2], acc[nt][4 * g + 3]};
             }
         }
-        __syncthreads();
+        lds_barrier();  // P complete
 
-        // One output pixel per thread: the 9 taps from the halo products.
-        const int oy = tid >> 4, ox = tid & 15;
-        float v[CAB_CC];
+        // The 9 taps from the halo products, NPX output pixels per thread
+        // (rows oy, oy + 16).
+        const int ox = tid & 15;
+        float v[S::NPX][CAB_CC];
 #pragma unroll
-        for (int co = 0; co < CAB_CC; ++co) v[co] = bias[co];
+        for (int r = 0; r < S::NPX; ++r) {
+            const int oy = (tid >> 4) + 16 * r;
 #pragma unroll
-        for (int ky = 0; ky < 3; ++ky)
+            for (int co = 0; co < CAB_CC; ++co) v[r][co] = bias[co];
 #pragma unroll
-            for (int kx = 0; kx < 3; ++kx) {
-                const float* q = Ps + ((oy + ky) * CC1_HS + ox + kx) * CC1_PS + (ky * 3 + kx) * CAB_CC;
+            for (int ky = 0; ky < 3; ++ky)
 #pragma unroll
-                for (int j = 0; j < CAB_CC / 2; ++j) {
-                    const float2 t = *(const float2*)(q + 2 * j);
-                    v[2 * j] += t.x;
-                    v[2 * j + 1] += t.y;
+                for (int kx = 0; kx < 3; ++kx) {
+                    const float* q = Ps + ((oy + ky) * CX_HS + ox + kx) * CX_PS + (ky * 3 + kx) * CAB_CC;
+#pragma unroll
+                    for (int j = 0; j < CAB_CC / 2; ++j) {
+                        const float2 t = *(const float2*)(q + 2 * j);
+                        v[r][2 * j] += t.x;
+                        v[r][2 * j + 1] += t.y;
+                    }
                 }
-            }
 #pragma unroll
-        for (int co = 0; co < CAB_CC; ++co) v[co] = gelu(v[co]);
-        const int gy = y0 + oy, gx = x0 + ox;
-        float* dst = p.t1 + ((size_t)gy * W + gx) * CAB_CS;
-        *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
-        *(float4*)(dst + 4) = make_float4(v[4], v[5], 0.f, 0.f);
+            for (int co = 0; co < CAB_CC; ++co) v[r][co] = gelu(v[r][co]);
+            float* dst = p.t1 + ((size_t)(y0 + oy) * W + x0 + ox) * CAB_CS;
+            *(float4*)dst = make_float4(v[r][0], v[r][1], v[r][2], v[r][3]);
+            *(float4*)(dst + 4) = make_float4(v[r][4], v[r][5], 0.f, 0.f);
+        }
 
         // Per-tile sums: the tile, and its pixels on row 0, row H-1, col 0,
         // col W-1 - only tiles on the plane's border have any of the latter.
+        // A thread adds its pixels in row order, then the wave tree.
         const bool border = y0 == 0 || y0 + TY == H || x0 == 0 || x0 + 16 == W;  // tile-uniform
-        const bool line[CAB_NSUM] = {true, gy == 0, gy == H - 1, gx == 0, gx == W - 1};
 #pragma unroll
         for (int l = 0; l < CAB_NSUM; ++l) {
             if (l > 0 && !border) break;
 #pragma unroll
             for (int co = 0; co < CAB_CC; ++co) {
-                const float s = wave_sum(line[l] ? v[co] : 0.0f);
+                float s = 0.0f;
+#pragma unroll
+                for (int r = 0; r < S::NPX; ++r) {
+                    const int gy = y0 + (tid >> 4) + 16 * r, gx = x0 + ox;
+                    const bool on = l == 0 || (l == 1 && gy == 0) || (l == 2 && gy == H - 1) ||
+                                    (l == 3 && gx == 0) || (l == 4 && gx == W - 1);
+                    s += on ? v[r][co] : 0.0f;
+                }
+                s = wave_sum_dpp(s);
                 if (lane == 0) red[wave][l * CAB_CC + co] = s;
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (tid < CAB_NSUM * CAB_CS) {
             const int l = tid / CAB_CS, co = tid - l * CAB_CS;
             float s = 0.0f;
             if (co < CAB_CC && (l == 0 || border)) {
-                const int i = l * CAB_CC + co;
+                const int k = l * CAB_CC + co;
 #pragma unroll
-                for (int w = 0; w < WAVES; ++w) s += red[w][i];  // waves in order
+                for (int w = 0; w < CX_WAVES; ++w) s += red[w][k];  // waves in order
             }
             p.partial[(size_t)tid * ntiles + tile] = s;  // value-major: [40][tiles]
         }
         // The next tile's P stores come after this barrier; every read of Ps
         // and red above precedes it.
-        __syncthreads();
+        lds_barrier();
     }
 }
 
-extern "C" __global__ __launch_bounds__(256, 2) void hat_cab_conv1(CabConvArgs p)
+extern "C" __global__ __launch_bounds__(CX_WAVES * 64, 1) void hat_cab_conv1(CabConvArgs p)
 {
     cab_conv1_body<16>(p);
 }
-extern "C" __global__ __launch_bounds__(512, 1) void hat_cab_conv1_t32(CabConvArgs p)
+extern "C" __global__ __launch_bounds__(CX_WAVES * 64, 1) void hat_cab_conv1_t32(CabConvArgs p)
 {
     cab_conv1_body<32>(p);
 }

@@ -90,6 +90,24 @@ __device__ __forceinline__ f32x4 mfma16x6(const u32x4 (&a)[3], const u32x4 (&b)[
     return mfma16_bf16(a[0], b[0], c);
 }
 
+// The same on v_mfma_f32_32x32x16_bf16 (lane l: row / column l % 32, k 8 (l / 32)
+// .. +7; D: column l % 32, rows 8 (i / 4) + 4 (l / 32) + i % 4).
+__device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma6(const u32x4 (&a)[3], const u32x4 (&b)[3], f32x16 c)
+{
+    c = mfma_bf16(a[2], b[0], c);
+    c = mfma_bf16(a[1], b[1], c);
+    c = mfma_bf16(a[0], b[2], c);
+    c = mfma_bf16(a[1], b[0], c);
+    c = mfma_bf16(a[0], b[1], c);
+    return mfma_bf16(a[0], b[0], c);
+}
+
 // ---- weight chunks for the split-bf16 linears: one 32-k step of up to 144
 // rows as three bf16 planes [rows][WC_KS] (k 32..39 zero), packed on the host
 // WC_CHUNK elements apart. A block copies chunk c + 1 into one of two LDS
@@ -226,12 +244,12 @@ __device__ __attribute__((aligned(16))) float hat_sink_row[64];
 // more than the number issued after it are outstanding.
 constexpr int wc_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70; }
 
-// The workgroup barrier alone. __syncthreads() adds a release fence, which
-// on gfx950 waits for every outstanding vector memory operation - the copies
-// of the next weight chunk and the rows read ahead included; the chunk loops
-// wait for exactly what they need (wc_vmcnt) and then meet here. The memory
-// clobber keeps the compiler from moving memory accesses across it.
-__device__ __forceinline__ void wc_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// A workgroup barrier for LDS data only: this wave's LDS accesses complete,
+// then the barrier. __syncthreads() adds a release fence, which on gfx950 waits
+// for every outstanding vector memory operation as well - global loads issued
+// ahead for later use included. The memory clobber keeps the compiler from
+// moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // A float4 from p, or zeros (from hat_zero_row) where ok is false.
 __device__ __forceinline__ f32x4 load_or_zero(const float* p, bool ok)
@@ -244,4 +262,20 @@ __device__ __forceinline__ float wave_sum(float v)
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
+}
+
+// The wave's sum in registers alone (DPP, no LDS round trips), wave-uniform:
+// pairs, quads, 8 (half-row mirror), 16 (row mirror), then row 0 into row 1
+// and row 2 into row 3 (row_bcast:15), rows 0-1 into row 3 (row_bcast:31);
+// lane 63 ends with the total. A fixed order, so the result does not depend on
+// timing.
+__device__ __forceinline__ float wave_sum_dpp(float v)
+{
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }

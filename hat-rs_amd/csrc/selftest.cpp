@@ -388,15 +388,16 @@ int gpu_selftest(std::string* err)
                                ao = rng.vec((size_t)T * C, 1.0f), wp = rng.vec((size_t)C * C, 0.05f),
                                bp = rng.vec(C, 0.1f), res = rng.vec((size_t)T * C, 1.0f),
                                nw = rng.vec(C, 1.0f), nb = rng.vec(C, 0.1f);
-            std::vector<float> w1p = pack_cab_conv1(w1.data());
+            std::vector<unsigned short> w1p = pack_cab_conv1(w1.data());
             int Kp = 0;
             std::vector<float> wpp = pack_linear(wp.data(), C, C, &Kp);
             const int tiles = (H / 16) * (W / 16);
-            Dev dxn(xn), dw1(w1p), db1(b1), dw2(w2), db2(b2), dwa(wa), dba(ba), dwb(wb), dbb(bb), dao(ao),
+            Dev dxn(xn), dw1(w1p.size() / 2), db1(b1), dw2(w2), db2(b2), dwa(wa), dba(ba), dwb(wb), dbb(bb), dao(ao),
                 dwp(wpp), dbp(bp), dres(res), dnw(nw), dnb(nb), dt1((size_t)T * CAB_CS),
                 dpart((size_t)tiles * CAB_NSUM * CAB_CS), dw2g((size_t)C * CAB_K2), dw2gx(WC_CHUNK), dbias2(C), dgate(C),
                 dout((size_t)T * C), dxo((size_t)T * C);
-            CabConvArgs ca{dxn.p, dw1.p, db1.p, dt1.p, dpart.p, H, W};
+            Runtime::get().h2d(dw1.p, w1p.data(), w1p.size() * sizeof(unsigned short));
+            CabConvArgs ca{dxn.p, (const unsigned short*)dw1.p, db1.p, dt1.p, dpart.p, H, W};
             launch(s, "hat_cab_conv1", 2, 1, 1, 256, ca);
             CabGateArgs ga{};
             ga.partial = dpart.p;
@@ -509,8 +510,8 @@ int gpu_selftest(std::string* err)
                 const int tiles32 = (H / 32) * (W / 16);
                 Dev dt1b((size_t)T * CAB_CS), dpartb((size_t)tiles32 * CAB_NSUM * CAB_CS), dw2gb((size_t)C * CAB_K2),
                     dbias2b(C), dgateb(C);
-                CabConvArgs cb2{dxn.p, dw1.p, db1.p, dt1b.p, dpartb.p, H, W};
-                launch(s, "hat_cab_conv1_t32", 2, 1, 1, 512, cb2);
+                CabConvArgs cb2{dxn.p, (const unsigned short*)dw1.p, db1.p, dt1b.p, dpartb.p, H, W};
+                launch(s, "hat_cab_conv1_t32", 2, 1, 1, 256, cb2);
                 CabGateArgs gb = ga;
                 gb.partial = dpartb.p;
                 gb.t1 = dt1b.p;
