@@ -167,10 +167,11 @@ std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int
 // r > 0 the output channels are permuted as pack_conv permutes them.
 std::vector<float> pack_wino(const float* w, int CO, int CI, int r)
 {
-    if (CO % 16 != 0 || CI % 16 != 0) throw Error("pack_wino: channel counts must be multiples of 16");
+    if (r > 0 && CO % 16 != 0) throw Error("pack_wino: shuffled output channels must come in 16s");
     static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
-    const int NTT = CO / 16, Cf = r > 0 ? CO / (r * r) : 0;
-    std::vector<float> out((size_t)16 * CO * CI);
+    // channels padded to 16s with zeros (60 -> 64, 180 -> 192)
+    const int NTT = (CO + 15) / 16, NKC = (CI + 15) / 16, Cf = r > 0 ? CO / (r * r) : 0;
+    std::vector<float> out((size_t)16 * (16 * NTT) * (16 * NKC), 0.0f);
     for (int o2 = 0; o2 < CO; ++o2) {
         int o = o2;
         if (r > 0) {
@@ -193,11 +194,13 @@ std::vector<float> pack_wino(const float* w, int CO, int CI, int r)
     return out;
 }
 
-// Which convs have a Winograd kernel (hat_convwino_*): the 144 -> 144 trunk
-// convs, conv_before_upsample 144 -> 64 and the x2 upsample convs 64 -> 256.
+// Which convs have a Winograd kernel (hat_convwino_*): the 144 -> 144 and
+// 180 -> 180 trunk convs, conv_before_upsample 144 / 180 -> 64, the x2
+// upsample convs 64 -> 256 and the unfolded CAB's 180 -> 60 and 60 -> 180.
 static bool wino_conv(int CO, int CI, int r)
 {
-    return (r == 0 && CI == 144 && (CO == 144 || CO == 64)) || (r == 2 && CI == 64 && CO == 256);
+    return (r == 0 && (CI == 144 || CI == 180) && (CO == CI || CO == 64)) || (r == 2 && CI == 64 && CO == 256) ||
+           (r == 0 && CI == 180 && CO == 60) || (r == 0 && CI == 60 && CO == 180);
 }
 
 // conv1 [6][144][3][3] as the split A operands of hat_cab_conv1* (CX_WPACK):
@@ -568,12 +571,13 @@ void run_se(hipStream_t s, const float* partial, int nblk, int C, float* red, fl
     launch(s, "hat_se_gate", 1, 1, 1, 256, se);
 }
 
-// The C = 180 CAB conv2 (CO in (144, 192]) and its column sums run on the
-// wide-tile kernel: one partial row per 16x16 tile; every other CEPI_COLSUM
-// conv leaves one per 8x16 tile.
+// The C = 180 CAB conv2 60 -> 180 and its column sums run on the Winograd
+// kernel (hat_convwino_cab2_180, one partial row per 8x16 tile); other CO in
+// (144, 192] on the wide-tile kernel (one per 16x16 tile); every other
+// CEPI_COLSUM conv leaves one per 8x16 tile.
 bool colsum_wide(int CO, int H, int W, int co_stride)
 {
-    return CO > 144 && CO <= 192 && H % 16 == 0 && W % 16 == 0 && CO % 4 == 0 && co_stride % 4 == 0;
+    return CO > 144 && CO <= 192 && CO != 180 && H % 16 == 0 && W % 16 == 0 && CO % 4 == 0 && co_stride % 4 == 0;
 }
 int colsum_rows(int CO, int H, int W, int co_stride)
 {
@@ -666,6 +670,24 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
         }
         if (epi == CEPI_SHUFFLE && C.r == 2 && C.CO == 256 && C.CI == 64 && co_stride >= 64) {
             launch(s, "hat_convwino_n8_shuffle", 2 * tiles, 1, 1, 512, p);
+            return;
+        }
+        // the C = 180 family (the residual epilogue's planes are 180 wide)
+        if (epi == CEPI_STORE && act == 2 && C.CO == 64 && C.CI == 180 && co_stride >= 64) {
+            launch(s, "hat_convwino_n4_store180", tiles, 1, 1, 512, p);
+            return;
+        }
+        if (epi == CEPI_STORE && act == 1 && C.CO == 60 && C.CI == 180 && co_stride >= 60) {
+            launch(s, "hat_convwino_cab1_180", tiles, 1, 1, 512, p);
+            return;
+        }
+        if (epi == CEPI_COLSUM && C.CO == 180 && C.CI == 60 && co_stride >= 180) {
+            launch(s, "hat_convwino_cab2_180", 2 * tiles, 1, 1, 512, p);
+            return;
+        }
+        if (epi == CEPI_RESID && C.CO == 180 && C.CI == 180 && co_stride == 180) {
+            if (in == out) throw Error("conv: the output must not overlap the input");
+            launch(s, "hat_convwino_resid180", 2 * tiles, 1, 1, 512, p);
             return;
         }
     }

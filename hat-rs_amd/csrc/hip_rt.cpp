@@ -28,7 +28,8 @@ const std::vector<std::string>& required_kernels()
         "hat_gemmws_qkv",      "hat_gemmws_gelu",     "hat_gemmws_resid_ln", "hat_gemmws_hab_ln",
         "hat_gemmws12_qkv",    "hat_gemmws12_gelu",   "hat_gemmws12_resid_ln", "hat_gemmws12_hab_ln",
         "hat_mlp_resid",       "hat_mlp_resid_ln",    "hat_mlp12_resid",    "hat_mlp12_resid_ln",    "hat_gemmws_cab_ln",  "hat_cab_conv1",  "hat_cab_conv1_t32",
-        "hat_cab_gate",        "hat_convw_n9_store_ln", "hat_convw_n9_resid_ln", "hat_convwino_resid", "hat_convwino_n4_store", "hat_convwino_n8_shuffle", "hat_convw_n9_resid",
+        "hat_cab_gate",        "hat_convw_n9_store_ln", "hat_convw_n9_resid_ln", "hat_convwino_resid", "hat_convwino_n4_store", "hat_convwino_n8_shuffle", "hat_convwino_resid180", "hat_convwino_n4_store180",
+        "hat_convwino_cab1_180", "hat_convwino_cab2_180", "hat_convw_n9_resid",
         "hat_convw_n4_store",  "hat_convw_n8_shuffle", "hat_convw_n6_resid", "hat_convw_n6_colsum", "hat_hab_tail", "hat_ocab_tail",
         "hat_layernorm",       "hat_pre",             "hat_colsum_reduce",  "hat_se_gate",
         "hat_copy",

@@ -1,7 +1,7 @@
 // 3x3 convolution (stride 1, zero padding 1, NHWC) by Winograd's minimal
 // filtering F(2x2, 3x3) (Lavin & Gray, "Fast Algorithms for Convolutional
-// Neural Networks", 2016), for the convs whose input channels come in 16s
-// and output channels in blocks of 16 NT:
+// Neural Networks", 2016), input channels in chunks of 16 and output channels
+// in blocks of 16 NT (channels past CI read as zeros, past CO not stored):
 //   - the 144 -> 144 trunk convs with the bias and the residual in the
 //     epilogue: the reference's RHAG conv and conv_after_body,
 //     lg_conv3x3_winograd (gpu.rs:605, 742) then lg_add (cuda.rs:227-248).
@@ -11,7 +11,11 @@
 //     HBM-bound pass over rows still in the last-level cache;
 //   - the head's conv_before_upsample (144 -> 64, LeakyReLU) and upsample
 //     convs (64 -> 256 into the PixelShuffle'd plane, two 128-channel column
-//     blocks), gpu.rs:622-653.
+//     blocks), gpu.rs:622-653;
+//   - the C = 180 family's trunk convs (180 -> 180 + residual, two 96-channel
+//     column blocks) and its unfolded CAB: conv1 180 -> 60 + GELU and conv2
+//     60 -> 180 with per-tile column sums for the squeeze-excite gate
+//     (lg_conv3x3 + lg_channel_mean's first stage, cuda.rs:171-183, 259-272).
 //
 // For each 2x2 output tile with the 4x4 input patch d (rows y-1 .. y+2):
 //   Y = A^T [ U (.) V ] A,   U = G g G^T (per co, ci),   V = B^T d B (per ci)
@@ -46,17 +50,19 @@
 #define WG_MS 20                           // LDS row stride of an M slice entry (16 used)
 
 // NT: output channel tiles per block (column block cb), NTT: all of
-// them (the U layout), NKC: 16-channel input chunks. EPI_RESID (NT = NTT = 9)
-// adds the bias and the residual when HEAD is -1, else
-// HEAD = CEPI_STORE (LeakyReLU 0.01) or CEPI_SHUFFLE (into the shuffled plane,
-// channels pre-permuted as for the direct convs).
-template <int NT, int NTT, int NKC, int EPI, int HEAD>
+// them (the U layout), NKC: 16-channel input chunks; CI, CO: the real channel
+// counts (CO is also the row width of the residual epilogue's planes). HEAD
+// -1 adds the bias and the residual; CEPI_STORE applies p.act (1 GELU, 2
+// LeakyReLU 0.01); CEPI_SHUFFLE writes into the shuffled plane (channels
+// pre-permuted as for the direct convs); CEPI_COLSUM stores and leaves the
+// 8 x 16 tile's column sums, one partial row per tile.
+template <int NT, int NTT, int NKC, int CI, int CO, int HEAD>
 __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 {
-    constexpr int C = 144;  // the residual epilogue's row width
-    static_assert(HEAD == CEPI_STORE || HEAD == CEPI_SHUFFLE || EPI == EPI_RESID,
-                  "residual, store or shuffle epilogues");
-    static_assert(HEAD >= 0 || (NT == 9 && NTT == 9), "the residual epilogue covers 144 channels");
+    static_assert(HEAD == -1 || HEAD == CEPI_STORE || HEAD == CEPI_SHUFFLE || HEAD == CEPI_COLSUM,
+                  "residual, store, shuffle or column-sum epilogues");
+    static_assert(NTT % NT == 0 && 16 * NTT >= CO && 16 * (NTT - 1) < CO, "the column blocks cover CO");
+    static_assert(16 * NKC >= CI && 16 * (NKC - 1) < CI && CI % 4 == 0, "the chunks cover CI");
     __shared__ __attribute__((aligned(16))) float Pb0[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Pb1[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Ms0[16 * 32 * WG_MS];
@@ -77,14 +83,14 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     const int y0 = (tile / tiles_x) * WG_TH;
     const int x0 = (tile % tiles_x) * WG_TW;
 
-    for (int i = tid; i < 16 * NT; i += 512) Cs[i] = p.bias[16 * NT * cb + i];
+    for (int i = tid; i < 16 * NT; i += 512) Cs[i] = 16 * NT * cb + i < CO ? p.bias[16 * NT * cb + i] : 0.0f;
 
     // The patch is channel-quad-major: float4 slot q * 180 + pix holds
     // channels 4q .. 4q+3 of halo pixel pix, so a lane's reads sit at one
     // lane offset plus wave-uniform ones. The two slots this thread stages per
     // chunk (the second for waves 0..3 only): element offsets of the quad in
     // chunk 0, or -1 for slots outside the plane or past the 720 used.
-    int soff[2];
+    int soff[2], squad[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int s = r * 512 + tid;
@@ -93,13 +99,16 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
         const bool ok = s < WG_PPX * 4 && gy >= 0 && gy < H && gx >= 0 && gx < W;
         soff[r] = ok ? (gy * W + gx) * p.cin_stride + q * 4 : -1;
+        squad[r] = 4 * q;
     }
     auto fetch = [&](int kc, auto bufc) {
         float* B = decltype(bufc)::value ? Pb1 : Pb0;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             if (r == 1 && wave >= 4) break;  // wave-uniform
-            const float* src = soff[r] >= 0 ? p.in + soff[r] + kc * 16 : hat_zero_row;
+            // quads past CI (the last chunk of CI = 60, 180) read zeros
+            const bool cin = CI % 16 == 0 || kc * 16 + squad[r] < CI;
+            const float* src = soff[r] >= 0 && cin ? p.in + soff[r] + kc * 16 : hat_zero_row;
             __builtin_amdgcn_global_load_lds((const void*)src,
                                              (__attribute__((address_space(3))) void*)(B + (r * 512 + wave * 64) * 4),
                                              16, 0, 0);
@@ -207,16 +216,19 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     const int et = tid >> 4, ec = tid & 15;
     const int ety = et >> 3, etx = et & 7;
     const int py = y0 + 2 * ety, px = x0 + 2 * etx;
-    // element offsets of the thread's four pixels (the plane is below 2^31
-    // elements: checked at launch)
-    const int pix0 = ((py * W) + px) * C, prow = W * C;
+    // element offsets of the thread's four pixels in the residual epilogue's
+    // planes (below 2^31 elements: checked at launch)
+    const int pix0 = ((py * W) + px) * CO, prow = W * CO;
+    const int ocb = 16 * NT * cb + ec;  // the thread's channel in slice 0
+    constexpr bool PADCO = 16 * NTT != CO;  // channels past CO in the last column block
     float y[NT][4];
     auto out_slice = [&](int nt, auto bufc) {
         float* Ms = decltype(bufc)::value ? Ms1 : Ms0;
         // the slice's residual, loaded under the barrier and the transforms
+        const bool live = PADCO ? ocb + 16 * nt < CO : true;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            y[nt][q] = HEAD < 0 ? p.res[pix0 + (q >> 1) * prow + (q & 1) * C + nt * 16 + ec] : 0.0f;
+            y[nt][q] = HEAD < 0 ? p.res[live ? pix0 + (q >> 1) * prow + (q & 1) * CO + ocb + nt * 16 : 0] : 0.0f;
 #pragma unroll
         for (int e = 0; e < 2; ++e)
 #pragma unroll
@@ -246,18 +258,21 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     if constexpr (NT % 2 == 1) out_slice(NT - 1, CInt<0>{});
 
     if constexpr (HEAD >= 0) {
-        // Channel o = 16 NT cb + 16 nt + c of pixel (y, x): CEPI_STORE writes it
-        // there (LeakyReLU 0.01); CEPI_SHUFFLE writes o = (i r + jj) Cf + c' to
-        // pixel (y r + i, x r + jj), channel c' of the r-times larger plane.
+        // Channel o = 16 NT cb + 16 nt + c of pixel (y, x): CEPI_STORE and
+        // CEPI_COLSUM write it there (CEPI_STORE after p.act); CEPI_SHUFFLE
+        // writes o = (i r + jj) Cf + c' to pixel (y r + i, x r + jj), channel c'
+        // of the r-times larger plane.
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            const int o = 16 * NT * cb + 16 * nt + ec;
+            const int o = ocb + 16 * nt;
+            if (PADCO && o >= CO) continue;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int yy = py + (q >> 1), xx = px + (q & 1);
                 float v = y[nt][q];
-                if (HEAD == CEPI_STORE) {
-                    v = v < 0.0f ? v * 0.01f : v;
+                if (HEAD == CEPI_STORE || HEAD == CEPI_COLSUM) {
+                    if (HEAD == CEPI_STORE && p.act == 2) v = v < 0.0f ? v * 0.01f : v;
+                    if (HEAD == CEPI_STORE && p.act == 1) v = gelu(v);
                     p.out[(yy * W + xx) * p.co_stride + o] = v;
                 } else {
                     const int r = p.r, Cf = p.CO / (r * r);
@@ -266,26 +281,74 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
                 }
             }
         }
+        if constexpr (HEAD == CEPI_COLSUM) {
+            // Column sums of the tile's 128 pixels: the thread's four, the four
+            // tiles of the wave with this channel (lanes ec + 16 k), then the
+            // eight waves in order through LDS (Ms0, free after this barrier);
+            // one partial row per 8 x 16 tile, [tile][co_stride].
+            float cs[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                float v = (y[nt][0] + y[nt][1]) + (y[nt][2] + y[nt][3]);
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                cs[nt] = v;
+            }
+            __syncthreads();
+            if (lane < 16) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) Ms0[wave * 16 * NT + nt * 16 + ec] = cs[nt];
+            }
+            __syncthreads();
+            if (tid < 16 * NT) {
+                const int o = 16 * NT * cb + tid;
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 8; ++w) v += Ms0[w * 16 * NT + tid];
+                if (o < CO) p.partial[(size_t)tile * p.co_stride + o] = v;
+            }
+        }
         return;
     }
 
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int nt = 0; nt < NT; ++nt) {
+        if (PADCO && ocb + 16 * nt >= CO) continue;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) p.out[pix0 + (q >> 1) * prow + (q & 1) * C + nt * 16 + ec] = y[nt][q];
+        for (int q = 0; q < 4; ++q) p.out[pix0 + (q >> 1) * prow + (q & 1) * CO + ocb + nt * 16] = y[nt][q];
+    }
 }
 
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid(ConvArgs p)
 {
-    convwino_body<9, 9, 9, EPI_RESID, -1>(p);
+    convwino_body<9, 9, 9, 144, 144, -1>(p);
 }
 // conv_before_upsample: 144 -> 64, LeakyReLU
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_n4_store(ConvArgs p)
 {
-    convwino_body<4, 4, 9, EPI_STORE, CEPI_STORE>(p);
+    convwino_body<4, 4, 9, 144, 64, CEPI_STORE>(p);
 }
 // upsample convs: 64 -> 256 in two 128-channel column blocks, PixelShuffle(2)
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_n8_shuffle(ConvArgs p)
 {
-    convwino_body<8, 16, 4, EPI_STORE, CEPI_SHUFFLE>(p);
+    convwino_body<8, 16, 4, 64, 256, CEPI_SHUFFLE>(p);
+}
+// The C = 180 family: trunk convs 180 -> 180 + residual (two 96-channel column
+// blocks), conv_before_upsample 180 -> 64, CAB conv1 180 -> 60 (+ GELU) and
+// conv2 60 -> 180 with column sums (two column blocks).
+extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid180(ConvArgs p)
+{
+    convwino_body<6, 12, 12, 180, 180, -1>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void hat_convwino_n4_store180(ConvArgs p)
+{
+    convwino_body<4, 4, 12, 180, 64, CEPI_STORE>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void hat_convwino_cab1_180(ConvArgs p)
+{
+    convwino_body<4, 4, 12, 180, 60, CEPI_STORE>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void hat_convwino_cab2_180(ConvArgs p)
+{
+    convwino_body<6, 12, 4, 60, 180, CEPI_COLSUM>(p);
 }

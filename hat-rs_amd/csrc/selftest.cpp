@@ -785,6 +785,7 @@ int gpu_selftest(std::string* err)
             {180, 180, CEPI_RESID, 0, 0, "rhag conv 180->180 + residual"},
             {3, 144, CEPI_STORE, 0, 0, "conv_first 3->144"},
             {144, 64, CEPI_STORE, 2, 0, "conv_before_upsample 144->64 + leaky"},
+            {180, 64, CEPI_STORE, 2, 0, "conv_before_upsample 180->64 + leaky"},
             {64, 256, CEPI_SHUFFLE, 0, 2, "upsample 64->256 + shuffle 2"},
             {64, 576, CEPI_SHUFFLE, 0, 3, "upsample 64->576 + shuffle 3"},
             {64, 3, CEPI_FINAL, 0, 0, "conv_last 64->3 + crop/denorm"},
@@ -929,17 +930,37 @@ int gpu_selftest(std::string* err)
             }
             // The Winograd kernels serve conv_before_upsample and the x2 upsample
             // convs (8 x 16 tiles; the shuffle in two 128-channel column blocks).
+            // For the C = 180 family they serve the trunk conv and both CAB convs
+            // (180 -> 180 and 60 -> 180 in two 96-channel column blocks).
             const char* wino = cc.epi == CEPI_STORE && cc.act == 2 && cc.CI == 144 && cc.CO == 64
                                    ? "hat_convwino_n4_store"
                                : cc.epi == CEPI_SHUFFLE && cc.r == 2 && cc.CI == 64 && cc.CO == 256
                                    ? "hat_convwino_n8_shuffle"
-                                   : nullptr;
+                               : cc.epi == CEPI_STORE && cc.act == 2 && cc.CI == 180 && cc.CO == 64
+                                   ? "hat_convwino_n4_store180"
+                               : cc.epi == CEPI_STORE && cc.act == 1 && cc.CI == 180 && cc.CO == 60
+                                   ? "hat_convwino_cab1_180"
+                               : cc.epi == CEPI_COLSUM && cc.CI == 60 && cc.CO == 180 ? "hat_convwino_cab2_180"
+                               : cc.epi == CEPI_RESID && cc.CI == 180 && cc.CO == 180 ? "hat_convwino_resid180"
+                                                                                      : nullptr;
             if (wino) {
-                Dev dwu(pack_wino(w.data(), cc.CO, cc.CI, cc.r)), dout4(out_n);
+                const int ncb = cc.CO == 256 ? 2 : cc.CO == 180 ? 2 : 1;
+                Dev dwu(pack_wino(w.data(), cc.CO, cc.CI, cc.r)), dout4(out_n), dpart4((size_t)nblk * cc.CO);
                 p.out = dout4.p;
+                p.partial = dpart4.p;
                 p.wu = dwu.p;
-                launch(s, wino, (W / 16) * (H / 8) * (cc.CO / 128 > 1 ? cc.CO / 128 : 1), 1, 1, 512, p);
+                launch(s, wino, (W / 16) * (H / 8) * ncb, 1, 1, 512, p);
                 check_close(std::string(wino) + " " + cc.what, dout4.get(), want, 5e-5);
+                if (cc.epi == CEPI_COLSUM) {
+                    // one partial row per 8x16 tile
+                    std::vector<double> ps((size_t)nblk * cc.CO, 0.0);
+                    for (int y = 0; y < H; ++y)
+                        for (int x = 0; x < W; ++x) {
+                            const int blk = (y / 8) * (W / 16) + x / 16;
+                            for (int o = 0; o < cc.CO; ++o) ps[(size_t)blk * cc.CO + o] += full[((size_t)y * W + x) * cc.CO + o];
+                        }
+                    check_close(std::string(wino) + " partial sums", dpart4.get(), ps, 5e-4);
+                }
                 note(std::string(wino) + "  " + cc.what + "  32x48");
             }
             // conv_last by per-tap products: 16 x 32 tiles, so W = 48 leaves a
