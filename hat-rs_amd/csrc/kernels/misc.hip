@@ -14,54 +14,71 @@ __device__ __align__(256) unsigned char hat_scratch[SCRATCH_BYTES];
 // w + b; y may alias x. For C % 4 == 0, C <= 192 (the models' 144 and 180): a
 // row per 16 lanes, four rows per wave, each lane holding up to three float4 of
 // its row, the sums reduced within the 16 lanes. y goes out with non-temporal
-// stores (a streaming pass); x comes in with ordinary loads: in the forward it
+// stores (a streaming pass) when a wave's four rows are whole 128-byte lines
+// (C % 8 == 0, C = 144); otherwise (C = 180: 2880 bytes, 22.5 lines) lines
+// split between waves are written partially, which non-temporal stores turn
+// into a loss (measured at 262144 rows: 124 us cold / 82 us warm against 72 /
+// 66 us with ordinary stores). x comes in with ordinary loads: in the forward it
 // was written by the kernel just before, and the part of it still held in
 // MI355X's 256 MB last-level cache (MALL) is read from there (measured in the
 // HAT-S 512 forward: 51 us against 56 us with non-temporal loads, which are
 // faster only on data that is cold). Otherwise one wave per row.
+// The 16-lanes-per-row form; NTS: non-temporal stores.
+template <bool NTS>
+__device__ __forceinline__ void ln_rows16(const LnArgs& p, int lane, int C)
+{
+    const int g = lane & 15;
+    const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+    if (row >= p.rows) return;  // whole 16-lane groups leave together
+    const int n4 = C >> 2;
+    const f32x4* x = (const f32x4*)(p.x + (size_t)row * C);
+    f32x4 v[3];
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        const int k = g + 16 * t;
+        v[t] = k < n4 ? x[k] : (f32x4){0.f, 0.f, 0.f, 0.f};
+        s += (v[t].x + v[t].y) + (v[t].z + v[t].w);
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    const float mean = s / (float)C;
+    float q = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        if (g + 16 * t < n4) {
+            const float a = v[t].x - mean, b = v[t].y - mean, c = v[t].z - mean, d = v[t].w - mean;
+            q += (a * a + b * b) + (c * c + d * d);
+        }
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
+    const float rstd = 1.0f / sqrtf(q / (float)C + p.eps);
+    f32x4* y = (f32x4*)(p.y + (size_t)row * C);
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        const int k = g + 16 * t;
+        if (k < n4) {
+            const f32x4 w = ((const f32x4*)p.w)[k], b = ((const f32x4*)p.b)[k];
+            const f32x4 o = {(v[t].x - mean) * rstd * w.x + b.x, (v[t].y - mean) * rstd * w.y + b.y,
+                             (v[t].z - mean) * rstd * w.z + b.z, (v[t].w - mean) * rstd * w.w + b.w};
+            if (NTS)
+                __builtin_nontemporal_store(o, y + k);
+            else
+                y[k] = o;
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void hat_layernorm(LnArgs p)
 {
     const int lane = threadIdx.x & 63;
     const int C = p.C;
     if ((C & 3) == 0 && C <= 192) {
-        const int g = lane & 15;
-        const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
-        if (row >= p.rows) return;  // whole 16-lane groups leave together
-        const int n4 = C >> 2;
-        const f32x4* x = (const f32x4*)(p.x + (size_t)row * C);
-        f32x4 v[3];
-        float s = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 3; ++t) {
-            const int k = g + 16 * t;
-            v[t] = k < n4 ? x[k] : (f32x4){0.f, 0.f, 0.f, 0.f};
-            s += (v[t].x + v[t].y) + (v[t].z + v[t].w);
-        }
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-        const float mean = s / (float)C;
-        float q = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 3; ++t) {
-            if (g + 16 * t < n4) {
-                const float a = v[t].x - mean, b = v[t].y - mean, c = v[t].z - mean, d = v[t].w - mean;
-                q += (a * a + b * b) + (c * c + d * d);
-            }
-        }
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, 64);
-        const float rstd = 1.0f / sqrtf(q / (float)C + p.eps);
-        f32x4* y = (f32x4*)(p.y + (size_t)row * C);
-#pragma unroll
-        for (int t = 0; t < 3; ++t) {
-            const int k = g + 16 * t;
-            if (k < n4) {
-                const f32x4 w = ((const f32x4*)p.w)[k], b = ((const f32x4*)p.b)[k];
-                const f32x4 o = {(v[t].x - mean) * rstd * w.x + b.x, (v[t].y - mean) * rstd * w.y + b.y,
-                                 (v[t].z - mean) * rstd * w.z + b.z, (v[t].w - mean) * rstd * w.w + b.w};
-                __builtin_nontemporal_store(o, y + k);
-            }
-        }
+        if ((C & 7) == 0)
+            ln_rows16<true>(p, lane, C);
+        else
+            ln_rows16<false>(p, lane, C);
         return;
     }
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
