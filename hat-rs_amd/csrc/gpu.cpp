@@ -162,16 +162,17 @@ std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int
 
 // [CO][CI][3][3] -> the Winograd F(2x2, 3x3) weights U[xi] = G g G^T of the
 // hat_convwino_* kernels, G = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2; 0 0 1],
-// formed in double and arranged [kc][xi][nt][lane][4]: lane r + 16 g of
-// (kc, xi, nt) holds U[xi][16 nt + r][16 kc + 4 g .. 16 kc + 4 g + 3]. With
-// r > 0 the output channels are permuted as pack_conv permutes them.
-std::vector<float> pack_wino(const float* w, int CO, int CI, int r)
+// formed in double, rounded to fp32 and split into three bf16 parts, arranged
+// [kc][xi][nt][part][lane][8]: lane r + 16 g of (kc, xi, nt) holds part `part`
+// of U[xi][16 nt + r][32 kc + 8 g .. +7]; channels past CO and CI are zero
+// (CO padded to 16s, CI to 32s). With r > 0 the output channels are permuted
+// as pack_conv permutes them.
+std::vector<unsigned short> pack_wino(const float* w, int CO, int CI, int r)
 {
     if (r > 0 && CO % 16 != 0) throw Error("pack_wino: shuffled output channels must come in 16s");
     static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
-    // channels padded to 16s with zeros (60 -> 64, 180 -> 192)
-    const int NTT = (CO + 15) / 16, NKC = (CI + 15) / 16, Cf = r > 0 ? CO / (r * r) : 0;
-    std::vector<float> out((size_t)16 * (16 * NTT) * (16 * NKC), 0.0f);
+    const int NTT = (CO + 15) / 16, NKC = (CI + 31) / 32, Cf = r > 0 ? CO / (r * r) : 0;
+    std::vector<unsigned short> out((size_t)NKC * 16 * NTT * 3 * 512, 0);
     for (int o2 = 0; o2 < CO; ++o2) {
         int o = o2;
         if (r > 0) {
@@ -185,9 +186,17 @@ std::vector<float> pack_wino(const float* w, int CO, int CI, int r)
                     double u = 0.0;
                     for (int a = 0; a < 3; ++a)
                         for (int b = 0; b < 3; ++b) u += G[i][a] * (double)g[a * 3 + b] * G[j][b];
-                    const int xi = 4 * i + j, kc = ci / 16, c16 = ci % 16, nt = o2 / 16, rr = o2 % 16;
-                    const int lane = rr + 16 * (c16 / 4);
-                    out[((((size_t)kc * 16 + xi) * NTT + nt) * 64 + lane) * 4 + c16 % 4] = (float)u;
+                    const float x = (float)u;
+                    const unsigned short h0 = bf16_rne(x);
+                    const float r1 = x - bf16_float(h0);
+                    const unsigned short h1 = bf16_rne(r1);
+                    const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+                    const int xi = 4 * i + j, kc = ci / 32, c32 = ci % 32, nt = o2 / 16, rr = o2 % 16;
+                    const int lane = rr + 16 * (c32 / 8);
+                    const size_t at = ((((size_t)kc * 16 + xi) * NTT + nt) * 3 * 64 + lane) * 8 + c32 % 8;
+                    out[at] = h0;
+                    out[at + 512] = h1;
+                    out[at + 1024] = h2;
                 }
         }
     }
@@ -908,8 +917,8 @@ void GpuBackend::upload_conv(const std::string& name, int r)
     C.w = upload(pk.data(), pk.size());
     C.b = upload(bias.data(), bias.size());
     if (wino_conv(C.CO, C.CI, r)) {
-        std::vector<float> wu = pack_wino(wt_.t(name + ".weight"), C.CO, C.CI, r);
-        C.wu = upload(wu.data(), wu.size());
+        std::vector<unsigned short> wu = pack_wino(wt_.t(name + ".weight"), C.CO, C.CI, r);
+        C.wu = (unsigned short*)upload_bytes(wu.data(), wu.size() * sizeof(unsigned short));
     }
     conv_[name] = C;
 }

@@ -57,7 +57,7 @@ struct DevMlpX {
 struct DevConv {
     float* w = nullptr;  // [CIp/16][9][COp][16]
     float* b = nullptr;  // [COp]
-    float* wu = nullptr; // 144 -> 144 convs: Winograd weights (pack_wino)
+    unsigned short* wu = nullptr;  // convs with a Winograd kernel: split U (pack_wino)
     int CI = 0, CIp = 0, CO = 0, COp = 0, r = 0;
 };
 
@@ -79,7 +79,7 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
 // rows in the order that leaves its output in fc2's operand layout
 // (tailx.hip).
 void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
-std::vector<float> pack_wino(const float* w, int CO, int CI, int r);
+std::vector<unsigned short> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);
 

@@ -142,9 +142,10 @@ struct ConvArgs {
     const float* nw;
     const float* nb;
     float eps;
-    // hat_convwino_*: Winograd F(2x2,3x3) weights U = G g G^T, arranged
-    // [kc 9][xi 16][nt 9][lane 64][4] (lane r + 16 g: co 16 nt + r, ci 16 kc + 4 g ..)
-    const float* wu;
+    // hat_convwino_*: Winograd F(2x2,3x3) weights U = G g G^T split into three
+    // bf16 parts, arranged [kc][xi 16][nt][part 3][lane 64][8] (lane r + 16 g:
+    // co 16 nt + r, ci 32 kc + 8 g .. +7; channels padded to 16s and 32s)
+    const unsigned short* wu;
 };
 
 // Squeeze-excite gate: gate[c] = sigmoid(b2 + W2 relu(b1 + W1 mean)).

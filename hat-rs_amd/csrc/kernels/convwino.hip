@@ -27,13 +27,15 @@
 // column tiles) and 16 NT output channels. Wave w computes the two transform
 // points xi = 2w, 2w + 1 (B^T row i = w / 2, columns j = 2 (w % 2) + {0, 1}),
 // accumulating M[xi] (co 16 NT x tile 32) in 16 NT registers per lane (144
-// for the trunk convs). Input channels go in chunks of 16: the chunk's
-// 10 x 18 halo patch is staged
-// in LDS (global_load_lds, double-buffered, channel-quad-major); each lane
-// forms V for its
-// (tile, four channels) from the patch and feeds it to the MFMAs as the B
-// operand. U (pre-transformed on the host, 1.33 MB at 144 -> 144, L2-resident) streams
-// from global memory as the A operand, two steps ahead of its MFMAs.
+// for the trunk convs), on split-bf16 MFMA (v_mfma_f32_16x16x32_bf16, each
+// fp32 operand as three bf16 parts and each product as the six terms of
+// order <= 2, as accurate as FP32 MFMA; the split-bf16 attention explains the
+// arithmetic). Input channels go in chunks of 32: the chunk's 10 x 18 halo
+// patch is staged in LDS (global_load_lds, double-buffered, channel-quad-major);
+// each lane forms V for its (tile, eight channels) from the patch, splits it
+// and feeds it to the MFMAs as the B operand. U (pre-transformed and split on
+// the host, 2.2 MB at 144 -> 144 with the channels padded to 160, L2-resident)
+// streams from global memory as the A operand, two steps ahead of its MFMAs.
 //
 // Epilogue, per 16-channel slice: the waves write their M slices to LDS, then
 // each thread forms the 2x2 outputs of one (tile, channel) from the 16 points.
@@ -46,11 +48,11 @@
 #define WG_PH (WG_TH + 2)                  // 10 halo rows
 #define WG_PW (WG_TW + 2)                  // 18 halo columns
 #define WG_PPX (WG_PH * WG_PW)             // 180 halo pixels
-#define WG_SLOTS 768                       // float4 slots per patch buffer (720 used)
+#define WG_SLOTS 1536                      // float4 slots per patch buffer (1440 used)
 #define WG_MS 20                           // LDS row stride of an M slice entry (16 used)
 
 // NT: output channel tiles per block (column block cb), NTT: all of
-// them (the U layout), NKC: 16-channel input chunks; CI, CO: the real channel
+// them (the U layout), NKC: 32-channel input chunks; CI, CO: the real channel
 // counts (CO is also the row width of the residual epilogue's planes). HEAD
 // -1 adds the bias and the residual; CEPI_STORE applies p.act (1 GELU, 2
 // LeakyReLU 0.01); CEPI_SHUFFLE writes into the shuffled plane (channels
@@ -62,7 +64,7 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     static_assert(HEAD == -1 || HEAD == CEPI_STORE || HEAD == CEPI_SHUFFLE || HEAD == CEPI_COLSUM,
                   "residual, store, shuffle or column-sum epilogues");
     static_assert(NTT % NT == 0 && 16 * NTT >= CO && 16 * (NTT - 1) < CO, "the column blocks cover CO");
-    static_assert(16 * NKC >= CI && 16 * (NKC - 1) < CI && CI % 4 == 0, "the chunks cover CI");
+    static_assert(32 * NKC >= CI && 32 * (NKC - 1) < CI && CI % 4 == 0, "the 32-channel chunks cover CI");
     __shared__ __attribute__((aligned(16))) float Pb0[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Pb1[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Ms0[16 * 32 * WG_MS];
@@ -85,42 +87,51 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 
     for (int i = tid; i < 16 * NT; i += 512) Cs[i] = 16 * NT * cb + i < CO ? p.bias[16 * NT * cb + i] : 0.0f;
 
-    // The patch is channel-quad-major: float4 slot q * 180 + pix holds
-    // channels 4q .. 4q+3 of halo pixel pix, so a lane's reads sit at one
-    // lane offset plus wave-uniform ones. The two slots this thread stages per
-    // chunk (the second for waves 0..3 only): element offsets of the quad in
-    // chunk 0, or -1 for slots outside the plane or past the 720 used.
-    int soff[2], squad[2];
+    // The patch of a 32-channel chunk is channel-quad-major: float4 slot
+    // q * 180 + pix holds channels 4q .. 4q+3 of halo pixel pix (1440 of
+    // WG_SLOTS used), so a lane's reads sit at one lane offset plus
+    // wave-uniform ones. The three slots this thread stages per chunk (the
+    // third for waves 0..6 only): element offsets of the quad in chunk 0, or
+    // -1 for slots outside the plane or past the 1440 used.
+    int soff[3], squad[3];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < 3; ++r) {
         const int s = r * 512 + tid;
         const int q = s / WG_PPX, pix = s - q * WG_PPX;
         const int hy = pix / WG_PW, hx = pix - hy * WG_PW;
         const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
-        const bool ok = s < WG_PPX * 4 && gy >= 0 && gy < H && gx >= 0 && gx < W;
+        const bool ok = s < WG_PPX * 8 && gy >= 0 && gy < H && gx >= 0 && gx < W;
         soff[r] = ok ? (gy * W + gx) * p.cin_stride + q * 4 : -1;
         squad[r] = 4 * q;
     }
     auto fetch = [&](int kc, auto bufc) {
         float* B = decltype(bufc)::value ? Pb1 : Pb0;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            if (r == 1 && wave >= 4) break;  // wave-uniform
-            // quads past CI (the last chunk of CI = 60, 180) read zeros
-            const bool cin = CI % 16 == 0 || kc * 16 + squad[r] < CI;
-            const float* src = soff[r] >= 0 && cin ? p.in + soff[r] + kc * 16 : hat_zero_row;
+        for (int r = 0; r < 3; ++r) {
+            if (r == 2 && wave >= 7) break;  // wave-uniform: slots 1472.. are not used
+            // quads past CI (the last chunk of CI = 60, 144, 180) read zeros
+            const bool cin = CI % 32 == 0 || kc * 32 + squad[r] < CI;
+            const float* src = soff[r] >= 0 && cin ? p.in + soff[r] + kc * 32 : hat_zero_row;
             __builtin_amdgcn_global_load_lds((const void*)src,
                                              (__attribute__((address_space(3))) void*)(B + (r * 512 + wave * 64) * 4),
                                              16, 0, 0);
         }
     };
 
-    // U, pre-arranged as [kc][xi][nt][lane] float4: lane (r, g) of step (e, nt)
-    // holds U[2w + e][16 nt + r][16 kc + 4 g .. +3], the MFMA A operand.
-    const float* ubase = p.wu + ((size_t)(2 * wave) * NTT + NT * cb) * 256 + lane * 4;
-    auto ldu = [&](int kc, int t) -> f32x4 {
+    // U, split on the host and arranged [kc][xi][nt][part][lane][8] bf16: lane
+    // (r, g) of step (e, nt) holds part `part` of U[2w + e][16 nt + r][32 kc +
+    // 8 g .. +7], the MFMA A operand.
+    const unsigned short* ubase = p.wu + ((size_t)(2 * wave) * NTT + NT * cb) * 3 * 512 + lane * 8;
+    struct U3 {
+        u32x4 v[3];
+    };
+    auto ldu = [&](int kc, int t) -> U3 {
         const int e = t / NT, nt = t - e * NT;
-        return *(const f32x4*)(ubase + ((size_t)(kc * 16 + e) * NTT + nt) * 256);
+        const unsigned short* u = ubase + ((size_t)(kc * 16 + e) * NTT + nt) * 3 * 512;
+        U3 r;
+#pragma unroll
+        for (int part = 0; part < 3; ++part) r.v[part] = *(const u32x4*)(u + part * 512);
+        return r;
     };
 
     // The lane's B^T row / column pattern: R(col) = d[ra][col] + sr d[rb][col],
@@ -131,13 +142,13 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     const float sr = bi == 1 ? 1.0f : -1.0f;
     const int cA = jp ? 2 : 0, cB = jp ? 1 : 2, cC = 1, cD = jp ? 3 : 2;
     const float sc = jp ? -1.0f : 1.0f;
-    // LDS float offsets: the lane's tile origin (tile 16 nt2 + lr, quad lg)
-    // and the wave's rows / columns
+    // LDS float offsets: the lane's tile origin (tile 16 nt2 + lr, quads 2 lg
+    // and 2 lg + 1, 180 slots apart) and the wave's rows / columns
     int pbase[2];
 #pragma unroll
     for (int nt2 = 0; nt2 < 2; ++nt2) {
         const int n = nt2 * 16 + lr, ty = n >> 3, tx = n & 7;
-        pbase[nt2] = (lg * WG_PPX + 2 * ty * WG_PW + 2 * tx) * 4;
+        pbase[nt2] = (2 * lg * WG_PPX + 2 * ty * WG_PW + 2 * tx) * 4;
     }
     const int cols[4] = {cA, cB, cC, cD};
     int uoff[4][2];  // [column A..D][row a / b]
@@ -155,46 +166,52 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 #pragma unroll
             for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    f32x4 ur[2];
+    U3 ur[2];
     fetch(0, CInt<0>{});
     ur[0] = ldu(0, 0);
     ur[1] = ldu(0, 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    // Chunk kc from patch buffer Q; U steps t = e * NT + nt, the load of step
-    // t + 2 (the next chunk's first two at the end) issued ahead of step t.
+    // Chunk kc from patch buffer Q. Transform point e's V (the lane's tile, 8
+    // channels) is formed and split just before its NT steps t = e * NT + nt;
+    // the U load of step t + 2 (the next chunk's first two at the end) is
+    // issued ahead of step t.
     auto chunk = [&](int kc, auto bufc, auto lastc) {
         constexpr int Q = decltype(bufc)::value;
         constexpr bool LAST = decltype(lastc)::value;
         const float* B = Q ? Pb1 : Pb0;
-        f32x4 v[2][2];
-#pragma unroll
-        for (int nt2 = 0; nt2 < 2; ++nt2) {
-            f32x4 R[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const f32x4 da = *(const f32x4*)(B + pbase[nt2] + uoff[c][0]);
-                const f32x4 db = *(const f32x4*)(B + pbase[nt2] + uoff[c][1]);
-                R[c] = da + sr * db;
-            }
-            v[0][nt2] = R[0] - R[1];
-            v[1][nt2] = R[2] + sc * R[3];
-        }
         const int kn = LAST ? kc : kc + 1;
 #pragma unroll
-        for (int t = 0; t < 2 * NT; ++t) {
-            // step t's operand out of its slot, step t + 2's load into it (the
-            // step count per chunk is even, so slot t % 2 lines up across chunks)
-            const f32x4 u = ur[t % 2];
-            ur[t % 2] = t + 2 < 2 * NT ? ldu(kc, t + 2) : ldu(kn, t + 2 - 2 * NT);
-            if (!LAST && t == 0) fetch(kc + 1, CInt<Q ^ 1>{});
-            __builtin_amdgcn_sched_barrier(0);
-            const int e = t / NT, nt = t - e * NT;
+        for (int e = 0; e < 2; ++e) {
+            u32x4 vb[2][3];
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+            for (int nt2 = 0; nt2 < 2; ++nt2) {
+                float f[8];
 #pragma unroll
-                for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = mfma16(u[s], v[e][nt2][s], acc[e][nt][nt2]);
+                for (int hq = 0; hq < 2; ++hq) {
+                    const float* P = B + pbase[nt2] + hq * WG_PPX * 4;
+                    const int c0 = e == 0 ? 0 : 2, c1 = c0 + 1;
+                    const f32x4 r0 = *(const f32x4*)(P + uoff[c0][0]) + sr * *(const f32x4*)(P + uoff[c0][1]);
+                    const f32x4 r1 = *(const f32x4*)(P + uoff[c1][0]) + sr * *(const f32x4*)(P + uoff[c1][1]);
+                    const f32x4 v = e == 0 ? r0 - r1 : r0 + sc * r1;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) f[4 * hq + j] = v[j];
+                }
+                split3_x8(f, vb[nt2]);
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int t = e * NT + nt;
+                if (!LAST && t == 0) fetch(kc + 1, CInt<Q ^ 1>{});
+#pragma unroll
+                for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = mfma16x6(ur[t % 2].v, vb[nt2], acc[e][nt][nt2]);
+                // step t + 2's load into the slot step t's MFMAs have read (the
+                // step count per chunk is even, so slot t % 2 lines up across
+                // chunks)
+                ur[t % 2] = t + 2 < 2 * NT ? ldu(kc, t + 2) : ldu(kn, t + 2 - 2 * NT);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -321,34 +338,34 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid(ConvArgs p)
 {
-    convwino_body<9, 9, 9, 144, 144, -1>(p);
+    convwino_body<9, 9, 5, 144, 144, -1>(p);
 }
 // conv_before_upsample: 144 -> 64, LeakyReLU
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_n4_store(ConvArgs p)
 {
-    convwino_body<4, 4, 9, 144, 64, CEPI_STORE>(p);
+    convwino_body<4, 4, 5, 144, 64, CEPI_STORE>(p);
 }
 // upsample convs: 64 -> 256 in two 128-channel column blocks, PixelShuffle(2)
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_n8_shuffle(ConvArgs p)
 {
-    convwino_body<8, 16, 4, 64, 256, CEPI_SHUFFLE>(p);
+    convwino_body<8, 16, 2, 64, 256, CEPI_SHUFFLE>(p);
 }
 // The C = 180 family: trunk convs 180 -> 180 + residual (two 96-channel column
 // blocks), conv_before_upsample 180 -> 64, CAB conv1 180 -> 60 (+ GELU) and
 // conv2 60 -> 180 with column sums (two column blocks).
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid180(ConvArgs p)
 {
-    convwino_body<6, 12, 12, 180, 180, -1>(p);
+    convwino_body<6, 12, 6, 180, 180, -1>(p);
 }
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_n4_store180(ConvArgs p)
 {
-    convwino_body<4, 4, 12, 180, 64, CEPI_STORE>(p);
+    convwino_body<4, 4, 6, 180, 64, CEPI_STORE>(p);
 }
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_cab1_180(ConvArgs p)
 {
-    convwino_body<4, 4, 12, 180, 60, CEPI_STORE>(p);
+    convwino_body<4, 4, 6, 180, 60, CEPI_STORE>(p);
 }
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_cab2_180(ConvArgs p)
 {
-    convwino_body<6, 12, 4, 60, 180, CEPI_COLSUM>(p);
+    convwino_body<6, 12, 2, 60, 180, CEPI_COLSUM>(p);
 }

@@ -724,7 +724,10 @@ int gpu_selftest(std::string* err)
                 int CIp = 0, COp = 0;
                 std::vector<float> pk = pack_conv(w.data(), b.data(), CO, c.CI, 0, &bias, &CIp, &COp);
                 Dev din(in), dw(pk), db(bias), dres(res), dnw(nw), dnb(nb), dxn((size_t)HW * CO);
-                Dev dwu(c.wino ? pack_wino(w.data(), CO, c.CI, 0) : std::vector<float>(4, 0.0f));
+                const std::vector<unsigned short> wux = c.wino ? pack_wino(w.data(), CO, c.CI, 0)
+                                                               : std::vector<unsigned short>(8, 0);
+                Dev dwu((wux.size() + 1) / 2);
+                Runtime::get().h2d(dwu.p, wux.data(), wux.size() * sizeof(unsigned short));
                 ConvArgs p{};
                 p.in = din.p;
                 p.w = dw.p;
@@ -743,7 +746,7 @@ int gpu_selftest(std::string* err)
                 p.nw = dnw.p;
                 p.nb = dnb.p;
                 p.eps = 1e-5f;
-                p.wu = dwu.p;
+                p.wu = (const unsigned short*)dwu.p;
                 if (c.wino) launch(s, c.k, (W / 16) * (H / 8), 1, 1, 512, p);
                 else launch(s, c.k, (W / 16) * (H / 16), 1, 1, c.waves * 64, p);
                 std::vector<double> want((size_t)HW * CO), wxn((size_t)HW * CO);
@@ -945,10 +948,12 @@ int gpu_selftest(std::string* err)
                                                                                       : nullptr;
             if (wino) {
                 const int ncb = cc.CO == 256 ? 2 : cc.CO == 180 ? 2 : 1;
-                Dev dwu(pack_wino(w.data(), cc.CO, cc.CI, cc.r)), dout4(out_n), dpart4((size_t)nblk * cc.CO);
+                const std::vector<unsigned short> wux = pack_wino(w.data(), cc.CO, cc.CI, cc.r);
+                Dev dwu((wux.size() + 1) / 2), dout4(out_n), dpart4((size_t)nblk * cc.CO);
+                Runtime::get().h2d(dwu.p, wux.data(), wux.size() * sizeof(unsigned short));
                 p.out = dout4.p;
                 p.partial = dpart4.p;
-                p.wu = dwu.p;
+                p.wu = (const unsigned short*)dwu.p;
                 launch(s, wino, (W / 16) * (H / 8) * ncb, 1, 1, 512, p);
                 check_close(std::string(wino) + " " + cc.what, dout4.get(), want, 5e-5);
                 if (cc.epi == CEPI_COLSUM) {
