@@ -784,15 +784,14 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
         throw Error("attention: shift " + std::to_string(shift) + " is not supported (0" +
                     (oca ? "" : " or " + std::to_string(pl.shift)) + ")");
     const char* name = nullptr;
-    // The split-bf16 kernels (attnx.hip), except OCA at head_dim 30, whose
-    // persistent split-bf16 form spills: there the FP32-MFMA item kernel (attn.hip).
+    // The split-bf16 kernels (attnx.hip), one (window, head) item per block.
     bool persistent = false;
     if (D == 24) {
         name = oca ? "hat_attnx_oca_d24" : "hat_attnx_sw_d24";
         persistent = attnx_persistent(oca);
     } else if (D == 30) {
-        name = oca ? "hat_attn_oca_d30" : "hat_attnx_sw_d30";
-        persistent = oca ? attn_persistent(D, oca) : attnx_persistent(oca);
+        name = oca ? "hat_attnx_oca_d30" : "hat_attnx_sw_d30";
+        persistent = attnx_persistent(oca);
     } else {
         throw Error("attention: head_dim " + std::to_string(D) + " has no kernel (24 and 30 do)");
     }

@@ -321,18 +321,19 @@ __device__ __forceinline__ void attnx_item_kernel(const AttnArgs& p, unsigned ch
 // ---------------------------------------------------------------------------
 // OCA (overlapping cross-attention: 576 keys of the 24x24 unfold with padding
 // 4, zero outside the plane, biased and unmasked; hat_arch.py:373-427,
-// cpu.rs:852-900). The three-plane K and V^T of 576 keys would need 177 KB of
-// LDS, so an item runs as two halves of 288 keys (key rows 0-11, 12-23) that
-// share the online softmax. The kernel is persistent (one block per CU) over
-// the items, head-major: while one half computes, the next half's K and V
-// travel through registers, and go to LDS between two barriers; the bias
-// table is reloaded only when the head changes.
+// cpu.rs:852-900), one (window, head) item per block. The three-plane K and
+// V^T of 576 keys would need 177 KB of LDS, so an item runs as parts of NK
+// keys (D = 24: three of 192, key rows 0-7, 8-15, 16-23; D = 30: six of 96)
+// that share the online softmax; each part is fetched, split into LDS between
+// two barriers and computed. At most 80 KB of LDS and 128 VGPRs, so that two
+// blocks share a CU and one's staging overlaps the other's MFMAs.
 
-template <int D>
+template <int D, int NK>
 struct AttnXOcaShape {
-    static constexpr int NK = 288;                    // keys per half
+    static_assert(576 % NK == 0 && NK % 32 == 0, "whole 32-key tiles, whole parts");
+    static constexpr int NPART = 576 / NK;
     static constexpr int KS = D == 24 ? 24 : 40;
-    static constexpr int VS = NK + 8;
+    static constexpr int VS = NK + 8;                 // V^T row stride: 16 rows of a phase on distinct banks
     static constexpr int KPL = NK * KS, VPL = (D + 1) * VS;
     static constexpr int TROWS = 1521;
     static constexpr int LDS_BYTES = 2 * 3 * (KPL + VPL) + 4 * TROWS;
@@ -341,13 +342,13 @@ struct AttnXOcaShape {
     using vec = typename pick_t<U == 4, float4, float2>::type;
 };
 
-// This thread's share of half `half` of item (wi, head): K and V units.
-template <int D>
-__device__ __forceinline__ void attnx_oca_fetch(const AttnArgs& p, int wi, int head, int half,
-                                                typename AttnXOcaShape<D>::vec (&ks)[AttnXOcaShape<D>::NE],
-                                                typename AttnXOcaShape<D>::vec (&vs)[AttnXOcaShape<D>::NE])
+// This thread's share of part `part` of item (wi, head): K and V units.
+template <int D, int NK>
+__device__ __forceinline__ void attnx_oca_fetch(const AttnArgs& p, int wi, int head, int part,
+                                                typename AttnXOcaShape<D, NK>::vec (&ks)[AttnXOcaShape<D, NK>::NE],
+                                                typename AttnXOcaShape<D, NK>::vec (&vs)[AttnXOcaShape<D, NK>::NE])
 {
-    using X = AttnXOcaShape<D>;
+    using X = AttnXOcaShape<D, NK>;
     using vec = typename X::vec;
     constexpr int PER_KEY = D / X::U;
     const float* Kg = p.qkv + (size_t)(p.heads + head) * p.T * D;
@@ -356,9 +357,9 @@ __device__ __forceinline__ void attnx_oca_fetch(const AttnArgs& p, int wi, int h
     for (int i = 0; i < X::NE; ++i) {
         const int e = threadIdx.x + i * 512;
         vec kv{}, vv{};
-        if (e < X::NK * PER_KEY) {
+        if (e < NK * PER_KEY) {
             const int kl = e / PER_KEY, d = (e - kl * PER_KEY) * X::U;
-            const int pix = attn_key_pixel<true>(p, wi, half * X::NK + kl);
+            const int pix = attn_key_pixel<true>(p, wi, part * NK + kl);
             if (pix >= 0) {
                 kv = *(const vec*)(Kg + (size_t)pix * D + d);
                 vv = *(const vec*)(Vg + (size_t)pix * D + d);
@@ -369,17 +370,17 @@ __device__ __forceinline__ void attnx_oca_fetch(const AttnArgs& p, int wi, int h
     }
 }
 
-template <int D>
+template <int D, int NK>
 __device__ __forceinline__ void attnx_oca_stash(unsigned short* Kp, unsigned short* Vp,
-                                                const typename AttnXOcaShape<D>::vec (&ks)[AttnXOcaShape<D>::NE],
-                                                const typename AttnXOcaShape<D>::vec (&vs)[AttnXOcaShape<D>::NE])
+                                                const typename AttnXOcaShape<D, NK>::vec (&ks)[AttnXOcaShape<D, NK>::NE],
+                                                const typename AttnXOcaShape<D, NK>::vec (&vs)[AttnXOcaShape<D, NK>::NE])
 {
-    using X = AttnXOcaShape<D>;
+    using X = AttnXOcaShape<D, NK>;
     constexpr int PER_KEY = D / X::U;
 #pragma unroll
     for (int i = 0; i < X::NE; ++i) {
         const int e = threadIdx.x + i * 512;
-        if (e < X::NK * PER_KEY) {
+        if (e < NK * PER_KEY) {
             const int k = e / PER_KEY, d = (e - k * PER_KEY) * X::U;
             float kv[4], vv[4];
             if constexpr (X::U == 4) {
@@ -409,13 +410,13 @@ __device__ __forceinline__ void attnx_oca_stash(unsigned short* Kp, unsigned sho
     }
 }
 
-// One half's 9 key tiles onto the running (o, mrun) of the item.
-template <int D>
-__device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int half, const u32x4 (&qb)[2][3],
+// One part's key tiles onto the running (o, mrun) of the item.
+template <int D, int NK>
+__device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int part, const u32x4 (&qb)[2][3],
                                                   f32x16& o, float& mrun)
 {
-    using X = AttnXOcaShape<D>;
-    constexpr int NKT = X::NK / 32;
+    using X = AttnXOcaShape<D, NK>;
+    constexpr int NKT = NK / 32;
     const unsigned short* Kp = (const unsigned short*)lds;
     const unsigned short* Vp = Kp + 3 * X::KPL;
     const float* Tb = (const float*)(Vp + 3 * X::VPL);
@@ -434,7 +435,7 @@ __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int 
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int key = half * X::NK + kt * 32 + (i >> 2) * 8 + (i & 3) + 4 * h;
+            const int key = part * NK + kt * 32 + (i >> 2) * 8 + (i & 3) + 4 * h;
             const int ky = (int)((unsigned)key / 24u);
             s[i] = Tb[oca_base + key + 15 * ky];
         }
@@ -442,7 +443,7 @@ __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int 
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
-        if ((half == 0 && kt == 0) || __any(mx > mrun + 8.0f)) {  // wave-uniform
+        if ((part == 0 && kt == 0) || __any(mx > mrun + 8.0f)) {  // wave-uniform
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float mnew = fmaxf(mrun, mx);
             const float corr = fast_exp2(mrun - mnew);
@@ -464,24 +465,23 @@ __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int 
     }
 }
 
-template <int D>
+template <int D, int NK>
 __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned char* lds)
 {
-    using X = AttnXOcaShape<D>;
+    using X = AttnXOcaShape<D, NK>;
+    const int wi = blockIdx.x, head = blockIdx.y;
     unsigned short* Kp = (unsigned short*)lds;
     unsigned short* Vp = Kp + 3 * X::KPL;
     float* Tb = (float*)(Vp + 3 * X::VPL);
-    const int nw = p.nx * p.ny, nitems = nw * p.heads;
-    int item = blockIdx.x;
-    if (item >= nitems) return;  // whole block, before any barrier
-    // Written once: row D of V^T (ones in the high plane), K dims 30, 31 (D = 30).
-    for (int e = threadIdx.x; e < 3 * (X::NK / 2); e += 512) {
-        const int pl = e / (X::NK / 2), k2 = e - pl * (X::NK / 2);
+    // Written once (no part's staging touches them): row D of V^T (ones in the
+    // high plane), K dims 30, 31 (D = 30).
+    for (int e = threadIdx.x; e < 3 * (NK / 2); e += 512) {
+        const int pl = e / (NK / 2), k2 = e - pl * (NK / 2);
         *(unsigned*)(Vp + pl * X::VPL + D * X::VS + 2 * k2) = pl == 0 ? 0x3f803f80u : 0u;
     }
     if (D == 30) {
-        for (int e = threadIdx.x; e < 3 * X::NK; e += 512) {
-            const int pl = e / X::NK, k = e - pl * X::NK;
+        for (int e = threadIdx.x; e < 3 * NK; e += 512) {
+            const int pl = e / NK, k = e - pl * NK;
             *(unsigned*)(Kp + pl * X::KPL + k * X::KS + 30) = 0u;
         }
     }
@@ -489,67 +489,57 @@ __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned cha
     const int ql = lane & 31, h = lane >> 5;
     constexpr int RH = (D % 8) / 4, RR = (D / 8) * 4 + D % 4;
     typename X::vec ks[X::NE], vs[X::NE];
-    int head = item / nw, wi = item - head * nw;
-    attnx_oca_fetch<D>(p, wi, head, 0, ks, vs);
     u32x4 qb[2][3];
-    int qpix = attnx_query<D>(p, wi, head, qb);
-    int table_head = -1;
-    f32x16 o;
-    float mrun = -INFINITY;
-    while (true) {
-        const int next = item + gridDim.x;
-        const int nhead = next / nw, nwi = next - nhead * nw;
-#pragma unroll 1
-        for (int half = 0; half < 2; ++half) {
-            __syncthreads();  // every read of the previous half's LDS is done
-            attnx_oca_stash<D>(Kp, Vp, ks, vs);
-            if (head != table_head) {  // block-uniform
-                attn_table<D, true>(p, Tb, head);
-                table_head = head;
-            }
-            __syncthreads();
-            if (half == 0) attnx_oca_fetch<D>(p, wi, head, 1, ks, vs);
-            else if (next < nitems) attnx_oca_fetch<D>(p, nwi, nhead, 0, ks, vs);
-            if (half == 0) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[i] = 0.0f;
-                mrun = -INFINITY;
-            }
-            attnx_oca_compute<D>(lds, half, qb, o, mrun);
-        }
-        const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
-        const float inv = 1.0f / ltot;
-        float* orow = p.out + (size_t)qpix * p.C + head * D;
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-            const int d0 = 8 * i4 + 4 * h;
-            if (D % 4 == 0) {
-                if (d0 + 3 < D)
-                    *(float4*)(orow + d0) = make_float4(o[i4 * 4] * inv, o[i4 * 4 + 1] * inv,
-                                                        o[i4 * 4 + 2] * inv, o[i4 * 4 + 3] * inv);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (d0 + j < D) orow[d0 + j] = o[i4 * 4 + j] * inv;
-            }
-        }
-        if (next >= nitems) break;
-        item = next;
-        head = nhead;
-        wi = nwi;
+    int qpix;
+    {
+        attnx_oca_fetch<D, NK>(p, wi, head, 0, ks, vs);
+        AttnTableRegs<D, true> tr;
+        attn_table_load<D, true>(p, head, tr);
         qpix = attnx_query<D>(p, wi, head, qb);
+        attn_table_store<D, true>(Tb, tr);
+    }
+    f32x16 o;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+    float mrun = -INFINITY;
+#pragma unroll 1
+    for (int part = 0; part < X::NPART; ++part) {
+        if (part > 0) {
+            attnx_oca_fetch<D, NK>(p, wi, head, part, ks, vs);
+            __syncthreads();  // every read of the previous part's K and V is done
+        }
+        attnx_oca_stash<D, NK>(Kp, Vp, ks, vs);
+        __syncthreads();
+        attnx_oca_compute<D, NK>(lds, part, qb, o, mrun);
+    }
+    const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
+    const float inv = 1.0f / ltot;
+    float* orow = p.out + (size_t)qpix * p.C + head * D;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+        const int d0 = 8 * i4 + 4 * h;
+        if (D % 4 == 0) {
+            if (d0 + 3 < D)
+                *(float4*)(orow + d0) = make_float4(o[i4 * 4] * inv, o[i4 * 4 + 1] * inv,
+                                                    o[i4 * 4 + 2] * inv, o[i4 * 4 + 3] * inv);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (d0 + j < D) orow[d0 + j] = o[i4 * 4 + j] * inv;
+        }
     }
 }
 
-#define ATTNX_OCA_INST(NAME, D)                                                                 \
-    extern "C" __global__ __launch_bounds__(512, 2) void NAME(AttnArgs p)                       \
-    {                                                                                           \
-        __shared__ __attribute__((aligned(16))) unsigned char lds[AttnXOcaShape<D>::LDS_BYTES]; \
-        attnx_oca_kernel<D>(p, lds);                                                            \
+#define ATTNX_OCA_INST(NAME, D, NK)                                                                 \
+    extern "C" __global__ __launch_bounds__(512, 4) void NAME(AttnArgs p)                           \
+    {                                                                                               \
+        static_assert(AttnXOcaShape<D, NK>::LDS_BYTES <= 80 * 1024, "two blocks per CU");           \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[AttnXOcaShape<D, NK>::LDS_BYTES]; \
+        attnx_oca_kernel<D, NK>(p, lds);                                                            \
     }
 
-ATTNX_OCA_INST(hat_attnx_oca_d24, 24)
-ATTNX_OCA_INST(hat_attnx_oca_d30, 30)
+ATTNX_OCA_INST(hat_attnx_oca_d24, 24, 192)
+ATTNX_OCA_INST(hat_attnx_oca_d30, 30, 96)
 
 #define ATTNX_INST(NAME, D, OCC)                                                             \
     extern "C" __global__ __launch_bounds__(512, OCC) void NAME(AttnArgs p)                  \
