@@ -258,28 +258,28 @@ extern "C" __global__ __launch_bounds__(CL_WAVES * 64) void hat_conv_last3(ConvA
             wreg[nt][kc] = v;
         }
     }
-    const int nrt = (CL_RT - wave + CL_WAVES - 1) / CL_WAVES;
-    auto src_of = [&](int i) -> const float* {  // lane's input row of row tile i, or null
-        if (i >= nrt) return nullptr;
+    // Every wave walks NPW row tiles (the last one past the 39 for wave 7:
+    // zeros, not stored). The lane's input row of row tile i: hat_zero_row
+    // outside the plane and past the halo, so that the loads are issued on every
+    // path, and the loop is unrolled, so that the compiler's waits for the rows
+    // read ahead are exact (a loop back-edge would make them vmcnt(0)).
+    constexpr int NPW = (CL_RT + CL_WAVES - 1) / CL_WAVES;
+    auto src_of = [&](int i) -> const float* {
         const int hi = (wave + CL_WAVES * i) * 16 + lr;
         const int hy = hi / CL_HW, hx = hi - hy * CL_HW;
         const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
-        const bool valid = hi < CL_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
-        return valid ? p.in + ((size_t)gy * W + gx) * p.cin_stride + lg * 4 : nullptr;
+        const bool valid = i < NPW && hi < CL_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
+        return valid ? p.in + ((size_t)gy * W + gx) * p.cin_stride + lg * 4 : hat_zero_row;
     };
     f32x4 xa[4];
-    auto load = [&](int kc, const float* src) {
-        f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-        if (src) v = *(const f32x4*)(src + kc * 16);
-        xa[kc] = v;
-    };
+    auto load = [&](int kc, const float* src) { xa[kc] = *(const f32x4*)(src + kc * 16); };
     {
         const float* first = src_of(0);
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) load(kc, first);
     }
-#pragma unroll 1
-    for (int i = 0; i < nrt; ++i) {
+#pragma unroll
+    for (int i = 0; i < NPW; ++i) {
         const float* nxt = src_of(i + 1);
         f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -290,6 +290,7 @@ extern "C" __global__ __launch_bounds__(CL_WAVES * 64) void hat_conv_last3(ConvA
             for (int s = 0; s < 4; ++s)
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) acc[nt] = mfma16(wreg[nt][kc][s], a[s], acc[nt]);
+            __builtin_amdgcn_sched_barrier(0);  // the loads stay in their chunk
         }
         // lane (lr, lg) holds P[hi][16nt + 4lg .. +3]; columns 28.. are not stored
         const int hi = (wave + CL_WAVES * i) * 16 + lr;
