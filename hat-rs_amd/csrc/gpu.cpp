@@ -80,9 +80,13 @@ std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int
 
 std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, int N, int K)
 {
-    constexpr int BN = 144;
-    if (K != 144 || N % BN != 0) throw Error("pack_linear_ws: needs K = 144 and N a multiple of 144");
-    std::vector<unsigned short> out((size_t)(N / BN) * 5 * WS_CHUNK, 0);
+    // C = 144: slices of 144 rows (q, k, v), five k-steps; C = 180: slices of
+    // 90 rows (three heads of 30) padded to 96, six k-steps
+    if (!((K == 144 && N == 432) || (K == 180 && N == 540)))
+        throw Error("pack_linear_ws: needs the qkv shapes K = 144, N = 432 or K = 180, N = 540");
+    const int real = K == 144 ? 144 : 90, rows = K == 144 ? 144 : 96, ks_n = (K + 32) / 32;
+    const size_t chunk = (size_t)3 * rows * 32;
+    std::vector<unsigned short> out((size_t)(N / real) * ks_n * chunk, 0);
     for (int n = 0; n < N; ++n)
         for (int k = 0; k <= K; ++k) {
             if (k == K && !bias) break;
@@ -91,11 +95,11 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
             const float r1 = x - bf16_float(h0);
             const unsigned short h1 = bf16_rne(r1);
             const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
-            const int r = n % BN, s = k / 32, g = (k % 32) / 8, j = k % 8;
-            unsigned short* d = &out[((size_t)(n / BN) * 5 + s) * WS_CHUNK + (size_t)r * 32 + (g ^ ((r >> 2) & 3)) * 8 + j];
+            const int r = n % real, s = k / 32, g = (k % 32) / 8, j = k % 8;
+            unsigned short* d = &out[((size_t)(n / real) * ks_n + s) * chunk + (size_t)r * 32 + (g ^ ((r >> 2) & 3)) * 8 + j];
             d[0] = h0;
-            d[(size_t)BN * 32] = h1;
-            d[(size_t)2 * BN * 32] = h2;
+            d[(size_t)rows * 32] = h1;
+            d[(size_t)2 * rows * 32] = h2;
         }
     return out;
 }
@@ -323,7 +327,14 @@ void run_gemm(hipStream_t s, const DevLinear& L, const float* a, int lda, long M
         // split-bf16 qkv (gemmx.hip): weight-stationary, groups of three blocks
         static const int cus = std::max(1, Runtime::get().cu_count());
         p.w = (const float*)L.wx;
-        launch(s, "hat_gemmx_qkv", (unsigned)(3 * gemmx_qkv_groups(cus)), 1, 1, GX_THREADS, p);
+        launch(s, "hat_gemmx_qkv", (unsigned)(3 * gemmx_qkv_groups(cus, 3)), 1, 1, GX_THREADS, p);
+        return;
+    }
+    if (epi == EPI_QKV && L.wx && L.K == 180 && L.N == 540 && heads == 6 && hdim == 30 && lda == 180) {
+        // the same for C = 180: groups of six blocks (96-column slices)
+        static const int cus = std::max(1, Runtime::get().cu_count());
+        p.w = (const float*)L.wx;
+        launch(s, "hat_gemmx_qkv180", (unsigned)(6 * gemmx_qkv_groups(cus, 6)), 1, 1, GX_THREADS, p);
         return;
     }
     int wbn = 0;
@@ -881,7 +892,7 @@ void GpuBackend::upload_linear(const std::string& name)
         const size_t n = strlen(t);
         return name.size() >= n && name.compare(name.size() - n, n, t) == 0;
     };
-    if (L.K == 144 && ((L.N == 432 && ends(".qkv")) || (L.N == 144 && ends("proj")))) {
+    if ((L.K == 180 && L.N == 540 && ends(".qkv")) || (L.K == 144 && ((L.N == 432 && ends(".qkv")) || (L.N == 144 && ends("proj"))))) {
         // qkv: the weight-stationary layout of hat_gemmx_qkv; proj: streamed chunks (tailx)
         std::vector<unsigned short> x = ends(".qkv") ? pack_linear_ws(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K)
                                                      : pack_linear_x(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K);

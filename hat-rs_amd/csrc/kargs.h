@@ -256,15 +256,18 @@ struct HabTailArgs {
 #define WX_ROWS 128
 constexpr int wx_tiles(int M) { return (M + WX_ROWS - 1) / WX_ROWS; }
 
-// The qkv linear (hat_gemmx_qkv) keeps one 144-column slice in LDS for the
-// whole launch: five chunks of three bf16 planes [144][32], unpadded, each
-// row's four 16-byte k-groups stored at g ^ ((row >> 2) & 3) (so that 16
-// consecutive rows read at one k-group hit distinct banks); WS_CHUNK elements
-// apart (27 loads of 1 KB). Groups of three blocks (one per slice, on one
-// XCD) walk the same 32-token subtiles: GX_GROUPS(cus) groups of 8 waves.
+// The qkv linear (hat_gemmx_qkv, hat_gemmx_qkv180) keeps one column slice in
+// LDS for the whole launch: per 32-k step three bf16 planes [rows][32],
+// unpadded, each row's four 16-byte k-groups stored at g ^ ((row >> 2) & 3)
+// (so that 16 consecutive rows read at one k-group hit distinct banks),
+// WS_CHUNK elements apart. C = 144: three slices (q, k, v) of 144 rows, five
+// k-steps; C = 180: six slices of 96 rows (three heads of 30, rows 90..95
+// zero), six k-steps (WS_CHUNK180). Groups of NS blocks (one per slice, on one
+// XCD) walk the same 32-token subtiles: gemmx_qkv_groups(cus, NS) groups.
 #define WS_CHUNK (3 * 144 * 32)
+#define WS_CHUNK180 (3 * 96 * 32)
 #define GX_THREADS 512
-constexpr int gemmx_qkv_groups(int cus) { return cus >= 24 ? cus / 24 * 8 : 1; }
+constexpr int gemmx_qkv_groups(int cus, int ns) { return cus >= 8 * ns ? cus / (8 * ns) * 8 : 1; }
 
 struct TailXArgs {
     const float* a;            // projx: attention output; mlpx: LN2(x') rows

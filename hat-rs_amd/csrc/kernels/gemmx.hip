@@ -1,35 +1,41 @@
-// The qkv linear of the C = 144 family on split-bf16 MFMA: out = A . Wqkv^T +
-// b scattered head-major into q, k, v ([3][heads][T][24]), as hat_gemmws_qkv
-// (lg_linear + lg_extract_rows of the reference, cuda.rs:428-453).
+// The qkv linear on split-bf16 MFMA: out = A . Wqkv^T + b scattered head-major
+// into q, k, v ([3][heads][T][head_dim]), as hat_gemmws_qkv (lg_linear +
+// lg_extract_rows of the reference, cuda.rs:428-453), for the C = 144 family
+// (head_dim 24) and the C = 180 family (head_dim 30).
 //
 // Arithmetic: every fp32 operand as three bf16 parts and each product as the
 // six terms of order <= 2 (attnx.hip explains the split and its accuracy), on
 // v_mfma_f32_16x16x32_bf16 with the weight rows as the A operand and the
 // token rows as B: a lane's four accumulators are four consecutive output
-// columns of one token, the layout of the FP32 kernels, so the epilogue is
-// theirs. K = 144 runs as five 32-k steps; in the last one the activation
-// at k = 144 is 1 and the weights there hold the bias (split like the rest,
-// so it is added exactly), k 145..159 are zeros against zeros.
+// columns of one token, the layout of the FP32 kernels. K runs as 32-k steps
+// (144: five, 180: six); in the last one the activation at k = K is 1 and the
+// weights there hold the bias (split like the rest, so it is added exactly),
+// the k past it are zeros against zeros.
 //
-// Data flow: weight-stationary. A block of 8 waves holds one 144-column
-// slice (q, k or v: five 32-k chunks, 135 KB, unpadded and swizzled) in LDS
-// for the whole launch, loaded once; after that its waves share nothing and
-// meet at no barrier. Each wave walks 32-token subtiles on its own: their rows
-// (five k-steps) in registers, split per k-step, then 108 MFMAs; the next
+// Data flow: weight-stationary. A block of 8 waves holds one column slice in
+// LDS for the whole launch, loaded once (C = 144: 144 columns, one of q, k,
+// v, 135 KB; C = 180: 96 columns holding three heads of 30, 108 KB, two
+// slices per q, k and v); after that its waves share nothing and meet at no
+// barrier. Each wave walks 32-token subtiles on its own: their rows in
+// registers, split per k-step, then 12 MFMAs per 16-column tile; the next
 // subtile's rows of a k-step are read as soon as that step has been split.
-// The three slices' blocks of a group sit on one XCD (blocks are dealt to the
-// 8 XCDs in turn) and walk the same subtiles in the same order, so that two of
-// a subtile's three reads find its rows in that XCD's L2. Results leave
-// through a wave-private LDS stage as 1.5 KB runs of one head.
+// The NS slices' blocks of a group sit on one XCD (blocks are dealt to the
+// 8 XCDs in turn) and walk the same subtiles in the same order, so that all
+// but one of a subtile's NS reads find its rows in that XCD's L2. Results
+// leave through a wave-private LDS stage as runs of one head (16 rows:
+// 1.5 KB for head_dim 24, 1.9 KB for 30).
 //
-// The host launches 3 * gemmx_qkv_groups(CUs) blocks for heads = 6,
-// head_dim = 24 (the slices are q, k, v).
+// The host launches NS * gemmx_qkv_groups(CUs, NS) blocks.
 
 #define GX_WAVES 8
 
-// This wave's 32 token rows of a [M][144] plane, 8 values at k = 32 ks + 8 lg
-// per token, for the B operand (zeros past M and past k = 144).
+// This wave's 32 token rows of a [M][K] plane, 8 values at k = 32 ks + 8 lg
+// per token, for the B operand: zeros past M and past k = K, with load_b the
+// 1 at k = K that multiplies the bias column (read from hat_one_row like the
+// rest, so that nothing waits for the loads here).
+template <int K>
 struct WcRows {
+    static_assert(K % 4 == 0, "float4 units");
     const float* rows[2];
     bool alive[2];
     __device__ __forceinline__ void init(const float* base, int mbase, int M, int lr)
@@ -38,30 +44,28 @@ struct WcRows {
         for (int mt = 0; mt < 2; ++mt) {
             const int m = mbase + mt * 16 + lr;
             alive[mt] = m < M;
-            rows[mt] = base + (size_t)(alive[mt] ? m : 0) * 144;
+            rows[mt] = base + (size_t)(alive[mt] ? m : 0) * K;
         }
     }
+    // zeros from k = K on (for a bias added elsewhere)
     __device__ __forceinline__ void load(int ks, int lg, f32x4 (&dst)[2][2]) const
     {
         const int k0 = ks * 32 + lg * 8;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const bool kin = alive[mt] && k0 < 144;
-            dst[mt][0] = load_or_zero(rows[mt] + k0, kin);
-            dst[mt][1] = load_or_zero(rows[mt] + k0 + 4, kin);
-        }
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) dst[mt][j] = load_or_zero(rows[mt] + k0 + 4 * j, alive[mt] && k0 + 4 * j < K);
     }
-    // load, with the 1 at k = 144 that multiplies the bias column (read from
-    // memory like the rest, so that nothing waits for the loads here)
     __device__ __forceinline__ void load_b(int ks, int lg, f32x4 (&dst)[2][2]) const
     {
         const int k0 = ks * 32 + lg * 8;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const bool kin = alive[mt] && k0 < 144;
-            dst[mt][0] = *(const f32x4*)(kin ? rows[mt] + k0 : (k0 == 144 ? hat_one_row : hat_zero_row));
-            dst[mt][1] = load_or_zero(rows[mt] + k0 + 4, kin);
-        }
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int kq = k0 + 4 * j;
+                dst[mt][j] = *(const f32x4*)(alive[mt] && kq < K ? rows[mt] + kq : (kq == K ? hat_one_row : hat_zero_row));
+            }
     }
 };
 
@@ -75,31 +79,37 @@ __device__ __forceinline__ void split_pre(const f32x4 (&pre)[2][2], u32x4 (&xb)[
     }
 }
 
-extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv(GemmArgs p)
+// K: input width; NT: 16-column tiles per slice; NS: slices; HD: head_dim;
+// NH: heads per slice (HD * NH <= 16 NT columns are real, the rest zero).
+template <int K, int NT, int NS, int HD, int NH>
+__device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short* Wsl, float* Qs)
 {
-    constexpr int NT = 9, QS_S = 48, NLOAD = 5 * WS_CHUNK / 512;  // 135 loads of 1 KB
-    static_assert(5 * WS_CHUNK % 512 == 0, "whole loads");
-    __shared__ __attribute__((aligned(16))) unsigned short Wsl[5 * WS_CHUNK];  // the slice
-    __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * QS_S];  // per-wave staging
+    constexpr int KS = (K + 32) / 32;             // 32-k steps, the bias column included
+    constexpr int ROWS = 16 * NT;                 // slice rows in LDS
+    constexpr int CHUNK = 3 * ROWS * 32;          // one k-step: three bf16 planes [ROWS][32]
+    constexpr int NLOAD = KS * CHUNK / 512;       // 1 KB loads
+    constexpr int QS_S = HD == 24 ? 48 : 96;      // staging row stride (floats)
+    static_assert(KS * CHUNK % 512 == 0, "whole loads");
+    static_assert(HD * NH <= ROWS, "the heads fit the slice");
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
     const int lr = lane & 15, lg = lane >> 4;
     const int M = p.M;
     // block -> (group, slice): with a multiple of 8 groups, blocks b, b + 8,
-    // b + 16 (one XCD) are one group's three slices
-    const int G = gridDim.x / 3;
+    // ..., b + 8 (NS - 1) (one XCD) are one group's slices
+    const int G = gridDim.x / NS;
     int grp, sl;
     if (G % 8 == 0) {
         const int i = blockIdx.x >> 3;
-        sl = i % 3;
-        grp = (i / 3) * 8 + (blockIdx.x & 7);
+        sl = i % NS;
+        grp = (i / NS) * 8 + (blockIdx.x & 7);
     } else {
         sl = blockIdx.x / G;
         grp = blockIdx.x - sl * G;
     }
     {
-        const unsigned short* src = (const unsigned short*)p.w + (size_t)sl * 5 * WS_CHUNK;
+        const unsigned short* src = (const unsigned short*)p.w + (size_t)sl * KS * CHUNK;
         const unsigned loff = (unsigned)lane * 16;
 #pragma unroll 1
         for (int i = wave; i < NLOAD; i += GX_WAVES)
@@ -110,17 +120,17 @@ extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv(Gem
     }
     // this lane's A-operand offset: row lr of a 16-row tile, k-group lg swizzled
     const unsigned short* wl = Wsl + lr * 32 + ((lg ^ ((lr >> 2) & 3)) * 8);
-    float* out = p.out + (size_t)sl * p.heads * M * 24;
+    float* out = p.out + (size_t)sl * NH * M * HD;  // the slice's first head
     float* Q = Qs + wave * 16 * QS_S;
     const int nsub = (M + 31) / 32;
     const int stride = G * GX_WAVES;
     int sub = grp * GX_WAVES + wave;
     if (sub >= nsub) return;
-    WcRows xr;
+    WcRows<K> xr;
     xr.init(p.a, sub * 32, M, lr);
-    f32x4 y[5][2][2];
+    f32x4 y[KS][2][2];
 #pragma unroll
-    for (int ks = 0; ks < 5; ++ks) xr.load_b(ks, lg, y[ks]);
+    for (int ks = 0; ks < KS; ++ks) xr.load_b(ks, lg, y[ks]);
 #pragma unroll 1
     for (; sub < nsub; sub += stride) {
         // the next subtile's rows, or (past the last) this one's again: the
@@ -131,49 +141,89 @@ extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv(Gem
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[0][nt] = acc[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 5; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
             u32x4 xb[2][3];
             split_pre(y[ks], xb);
             xr.load_b(ks, lg, y[ks]);  // the next subtile's rows of this k-step
             // weight fragments of tile nt + 1 read while tile nt's 12 MFMAs run
-            const unsigned short* wr = wl + ks * WS_CHUNK;
+            const unsigned short* wr = wl + ks * CHUNK;
             u32x4 wa[2][3];
 #pragma unroll
-            for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * 144 * 32);
+            for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * ROWS * 32);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 __builtin_amdgcn_sched_barrier(0);
                 if (nt + 1 < NT) {
 #pragma unroll
                     for (int pl = 0; pl < 3; ++pl)
-                        wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * 32 + pl * 144 * 32);
+                        wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * 32 + pl * ROWS * 32);
                 }
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
             }
         }
-        // Two heads at a time go through the wave's LDS region and leave as 16
-        // consecutive rows of each head (1536 contiguous bytes), non-temporal.
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             const int mb = sub * 32 + mt * 16;
             const int mrows = M - mb;
+            if constexpr (HD == 24) {
+                // Two heads at a time go through the wave's LDS region and leave
+                // as 16 consecutive rows of each head (1536 contiguous bytes),
+                // non-temporal.
 #pragma unroll
-            for (int ph = 0; ph < 3; ++ph) {
+                for (int ph = 0; ph < 3; ++ph) {
 #pragma unroll
-                for (int t = 0; t < 3; ++t) *(f32x4*)(Q + lr * QS_S + t * 16 + lg * 4) = acc[mt][3 * ph + t];
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+                    for (int t = 0; t < 3; ++t) *(f32x4*)(Q + lr * QS_S + t * 16 + lg * 4) = acc[mt][3 * ph + t];
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
 #pragma unroll
-                for (int i2 = 0; i2 < 3; ++i2) {
-                    const int f = lane + 64 * i2, hh = f / 96, r = (f - hh * 96) / 6, d4 = f - hh * 96 - r * 6;
-                    const f32x4 v = *(const f32x4*)(Q + r * QS_S + hh * 24 + d4 * 4);
-                    // rows past M go to the sink (a store is issued either way)
-                    float* dst = r < mrows ? out + ((size_t)(2 * ph + hh) * M + mb + r) * 24 + d4 * 4
-                                           : hat_sink_row + d4 * 4;
-                    __builtin_nontemporal_store(v, (f32x4*)dst);
+                    for (int i2 = 0; i2 < 3; ++i2) {
+                        const int f = lane + 64 * i2, hh = f / 96, r = (f - hh * 96) / 6, d4 = f - hh * 96 - r * 6;
+                        const f32x4 v = *(const f32x4*)(Q + r * QS_S + hh * 24 + d4 * 4);
+                        // rows past M go to the sink (a store is issued either way)
+                        float* dst = r < mrows ? out + ((size_t)(2 * ph + hh) * M + mb + r) * 24 + d4 * 4
+                                               : hat_sink_row + d4 * 4;
+                        __builtin_nontemporal_store(v, (f32x4*)dst);
+                    }
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next phase's writes
                 }
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next phase's writes
+            } else {
+                // All NH heads at once: 16 rows x 16 NT columns into the stage,
+                // then 16 consecutive rows of each head (30 floats, 1920
+                // contiguous bytes) leave as float2 pairs (a pair never
+                // straddles a row: head_dim is even), non-temporal.
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) *(f32x4*)(Q + lr * QS_S + nt * 16 + lg * 4) = acc[mt][nt];
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+                // lane l < 4 PR: pair l % PR of row l / PR in each group of four
+                // rows; group i2 is rows 4 (i2 % 4) .. +3 of head i2 / 4
+                constexpr int PR = HD / 2;
+                static_assert(4 * PR <= 64, "four rows of pairs per wave");
+                const int rq = lane / PR, d2 = lane - rq * PR;
+#pragma unroll
+                for (int i2 = 0; i2 < 4 * NH; ++i2) {
+                    const int hh = i2 / 4, r = 4 * (i2 % 4) + rq;
+                    const f32x2 v = *(const f32x2*)(Q + (lane < 4 * PR ? r * QS_S + hh * HD + d2 * 2 : 0));
+                    // lanes past the pairs and rows past M go to the sink
+                    float* dst = lane < 4 * PR && r < mrows ? out + ((size_t)hh * M + mb + r) * HD + d2 * 2
+                                                            : hat_sink_row + (lane & 31) * 2;
+                    __builtin_nontemporal_store(v, (f32x2*)dst);
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next tile's writes
             }
         }
     }
+}
+
+extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv(GemmArgs p)
+{
+    __shared__ __attribute__((aligned(16))) unsigned short Wsl[5 * WS_CHUNK];  // the slice
+    __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * 48];    // per-wave staging
+    gemmx_qkv_body<144, 9, 3, 24, 6>(p, Wsl, Qs);
+}
+
+extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv180(GemmArgs p)
+{
+    __shared__ __attribute__((aligned(16))) unsigned short Wsl[6 * WS_CHUNK180];  // the slice
+    __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * 96];        // per-wave staging
+    gemmx_qkv_body<180, 6, 6, 30, 3>(p, Wsl, Qs);
 }

@@ -139,7 +139,7 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
     tx_load_res(p.res, mbase, M, lr, lg, acc);
     f32x4 y[5][2][2];
     {
-        WcRows ar;
+        WcRows<144> ar;
         ar.init(p.a, mbase, M, lr);
 #pragma unroll
         for (int ks = 0; ks < 5; ++ks) ar.load(ks, lg, y[ks]);
@@ -205,7 +205,7 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
     f32x4 acc2[2][9];
     tx_load_res(p.res, mbase, M, lr, lg, acc2);
-    WcRows yr;
+    WcRows<144> yr;
     yr.init(p.a, mbase, M, lr);
     f32x4 pre[2][2];
     yr.load_b(0, lg, pre);

@@ -296,18 +296,20 @@ int gpu_selftest(std::string* err)
                 check_close(k + " C " + std::to_string(C), dout.get(), want, 3e-5);
                 if (lnout) check_close(k + " C " + std::to_string(C) + " layernorm", dxn.get(), wxn, 5e-5);
                 note(k + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
-                if (ws && C == 144 && epi == EPI_QKV) {
+                if (ws && epi == EPI_QKV) {
                     // the split-bf16 form on the same inputs (the last
-                    // 128-row tile partial)
+                    // 32-row subtile partial), one group: its waves walk all 19
+                    // subtiles
                     std::vector<unsigned short> px = pack_linear_ws(w.data(), b.data(), N, K);
                     Dev dwx(std::vector<float>((px.size() + 1) / 2)), dout2((size_t)M * N);
                     rt.h2d(dwx.p, px.data(), px.size() * sizeof(unsigned short));
                     GemmArgs px2 = p;
                     px2.w = dwx.p;
                     px2.out = dout2.p;
-                    launch(s, "hat_gemmx_qkv", 3, 1, 1, GX_THREADS, px2);  // one group: its waves walk all 19 subtiles
-                    check_close("hat_gemmx_qkv C 144", dout2.get(), want, 3e-5);
-                    note("hat_gemmx_qkv C 144 M " + std::to_string(M) + " K 144");
+                    const char* kx = C == 144 ? "hat_gemmx_qkv" : "hat_gemmx_qkv180";
+                    launch(s, kx, C == 144 ? 3 : 6, 1, 1, GX_THREADS, px2);
+                    check_close(std::string(kx) + " C " + std::to_string(C), dout2.get(), want, 3e-5);
+                    note(std::string(kx) + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
                 }
         };
         for (int C : {144, 180})
