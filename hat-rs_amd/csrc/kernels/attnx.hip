@@ -224,7 +224,8 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
     for (int i = 0; i < 16; ++i) o[i] = 0.0f;
     float mrun = -INFINITY;
 
-#pragma unroll 1
+// unrolled: the K, V and bias addresses of every tile are immediate offsets
+#pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
         // S^T = bias (+ mask) + K Q^T
         f32x16 s;
