@@ -113,7 +113,7 @@ def extra_configs(hat_amd, np, td, steps):
     tf = flop / (ams / 1e3) / 1e12
     out["cfg3_ocab"] = {
         "workload": "OCAB op 128x128 C=180 576 keys (norm1 + qkv + attention + proj + MLP)",
-        "op_ms": round(ms, 4), "attn_kernel": "hat_attn_oca_d30", "attn_ms": round(ams, 4),
+        "op_ms": round(ms, 4), "attn_kernel": "hat_attnx_oca_d30", "attn_ms": round(ams, 4),
         "attn_flop": flop, "attn_tflops": round(tf, 2), "attn_frac": round(tf / PEAK_FP32_MFMA, 4)}
 
     for name, variant, size, seed in (("cfg4_hat_x4_256", "hat", 256, 4), ("cfg5_hatl_x4_512", "hat-l", 512, 5)):
