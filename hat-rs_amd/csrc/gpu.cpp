@@ -133,6 +133,49 @@ void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<u
     }
 }
 
+// One 32-k step of `rows` weight rows (value(r, kk), kk < 32) split into three
+// bf16 planes [rows][32] in the swizzled layout of the weight-stationary
+// kernels (row r's k-group g at g ^ ((r >> 2) & 3)).
+template <typename F>
+static void split_ws_step(int rows, F value, unsigned short* dst)
+{
+    for (int r = 0; r < rows; ++r)
+        for (int kk = 0; kk < 32; ++kk) {
+            const float x = value(r, kk);
+            const unsigned short h0 = bf16_rne(x);
+            const float r1 = x - bf16_float(h0);
+            const unsigned short h1 = bf16_rne(r1);
+            const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+            unsigned short* d = dst + (size_t)r * 32 + ((kk / 8) ^ ((r >> 2) & 3)) * 8 + kk % 8;
+            d[0] = h0;
+            d[(size_t)rows * 32] = h1;
+            d[(size_t)2 * rows * 32] = h2;
+        }
+}
+
+// The C = 180 MLP (fc1 [360][180] + b1, fc2 [180][360]) for hat_mlpx180: per
+// part of 64 hidden units, six fc1 k-steps (rows permuted by mlpx_unit, b1 at
+// k = 180) and two fc2 k-steps (192 rows, 180 real, the part's units in
+// natural order), MX180_SLOT elements apart.
+void pack_mlp_x180(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w)
+{
+    constexpr int C = 180, H = 360, NP = 6;
+    w->assign((size_t)8 * NP * MX180_SLOT, 0);
+    for (int q = 0; q < NP; ++q) {
+        for (int ks = 0; ks < 6; ++ks)
+            split_ws_step(MX180_HID, [&](int r, int kk) {
+                const int u = q * MX180_HID + mlpx_unit(r), k = ks * 32 + kk;
+                if (u >= H) return 0.0f;
+                return k < C ? w1[(size_t)u * C + k] : (k == C ? b1[u] : 0.0f);
+            }, &(*w)[(size_t)(8 * q + ks) * MX180_SLOT]);
+        for (int st = 0; st < 2; ++st)
+            split_ws_step(192, [&](int n, int kk) {
+                const int u = q * MX180_HID + st * 32 + kk;
+                return n < C && u < H ? w2[(size_t)n * H + u] : 0.0f;
+            }, &(*w)[(size_t)(8 * q + 6 + st) * MX180_SLOT]);
+    }
+}
+
 // [CO][CI][3][3] -> [CIp/16][9][COp][16]; with r > 0 the output channels are
 // permuted so that channel o = c*r*r + i*r + j lands at o' = (i*r + j)*Cf + c
 // (Cf = CO / r^2), which lets the conv store four consecutive o' as four
@@ -906,10 +949,17 @@ void GpuBackend::upload_mlpx(const std::string& name)
 {
     const TensorInfo& t1 = wt_.info(name + ".fc1.weight");
     const TensorInfo& t2 = wt_.info(name + ".fc2.weight");
-    if (t1.shape != std::vector<size_t>{288, 144} || t2.shape != std::vector<size_t>{144, 288}) return;
     std::vector<unsigned short> w;
-    pack_mlp_x(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
     DevMlpX m;
+    if (t1.shape == std::vector<size_t>{288, 144} && t2.shape == std::vector<size_t>{144, 288}) {
+        pack_mlp_x(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
+        m.C = 144;
+    } else if (t1.shape == std::vector<size_t>{360, 180} && t2.shape == std::vector<size_t>{180, 360}) {
+        pack_mlp_x180(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
+        m.C = 180;
+    } else {
+        return;
+    }
     m.w = (unsigned short*)upload_bytes(w.data(), w.size() * sizeof(unsigned short));
     mlpx_[name] = m;
 }
@@ -1133,8 +1183,37 @@ void GpuBackend::gemm(const DevLinear& L, const float* a, int lda, long M, float
 }
 
 // x = x + fc2(gelu(fc1(a_.xn))), in place; with a norm also a_.xn = norm(x).
+// The split-bf16 C = 180 MLP: out = x + fc2(gelu(fc1(xn))) + b2 (+ xn = LN(out)).
+void run_mlpx180(hipStream_t s, const DevMlpX& m, const float* b2, const float* xn_in, float* x, float* xn_out,
+                 const float* nw, const float* nb, long M)
+{
+    if (m.C != 180) throw Error("mlpx180: needs the pre-split C = 180 MLP");
+    if (M > 0x7fffffffL) throw Error("mlpx180: too many rows");
+    TailXArgs q{};
+    q.a = xn_in;
+    q.res = x;
+    q.out = x;
+    q.xn = nw ? xn_out : nullptr;
+    q.w = m.w;
+    q.b2 = b2;
+    q.nw = nw;
+    q.nb = nb;
+    q.M = (int)M;
+    q.eps = 1e-5f;
+    launch(s, nw ? "hat_mlpx180_ln" : "hat_mlpx180", (unsigned)wx_tiles((int)M), 1, 1, WX_THREADS, q);
+}
+
 void GpuBackend::mlp(const std::string& prefix, float* x, int epi, const std::string& norm)
 {
+    auto mx = mlpx_.find(prefix);
+    if (mx != mlpx_.end() && mx->second.C == 180) {
+        // a_.xn is read (fc1's input) and, with a norm, rewritten: every block
+        // reads its own rows before it writes them
+        run_mlpx180(stream_, mx->second, lin_.at(prefix + ".fc2").b, a_.xn, x, a_.xn,
+                    norm.empty() ? nullptr : raw_.at(norm + ".weight"), norm.empty() ? nullptr : raw_.at(norm + ".bias"),
+                    plan_.tokens());
+        return;
+    }
     GemmEpilogue e;
     if (!norm.empty()) {
         e.xn = a_.xn;

@@ -51,7 +51,8 @@ std::vector<unsigned short> pack_cab_conv1(const float* w);
 
 // hat_mlpx's weights: the packed slices and b1 in fc1's row order.
 struct DevMlpX {
-    unsigned short* w = nullptr;  // 24 weight chunks (pack_mlp_x)
+    unsigned short* w = nullptr;  // C = 144: 24 weight chunks (pack_mlp_x); 180: 48 (pack_mlp_x180)
+    int C = 144;
 };
 
 struct DevConv {
@@ -79,6 +80,7 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
 // rows in the order that leaves its output in fc2's operand layout
 // (tailx.hip).
 void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
+void pack_mlp_x180(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
 std::vector<unsigned short> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);

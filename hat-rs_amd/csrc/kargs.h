@@ -251,6 +251,13 @@ struct HabTailArgs {
 // fc1 chunks (96 permuted rows, k = input channel) then three fc2 chunks (144
 // rows, k = the third's hidden units), 24 chunks in all.
 #define MX_HID 96
+// The C = 180 MLP (hat_mlpx180*) walks its 360 hidden units (384 with 24
+// zero units) in six parts of MX180_HID: per part six fc1 chunks (64 permuted
+// rows, k = input channel, b1 at k = 180) and two fc2 chunks (192 rows, 180
+// real, k = the part's units), 48 chunks in the swizzled [rows][32] layout of
+// the weight-stationary kernels, MX180_SLOT elements apart.
+#define MX180_HID 64
+#define MX180_SLOT (3 * 192 * 32)
 // Their launch geometry (tailx): blocks of 4 waves, one 128-token row tile a block.
 #define WX_THREADS 256
 #define WX_ROWS 128

@@ -158,6 +158,32 @@ __device__ __forceinline__ void wc_mma(const unsigned short* Ws, int lr, int lg,
     }
 }
 
+// wc_mma for a chunk in the swizzled layout of the weight-stationary kernels:
+// three planes [ROWS][32] (plane stride ROWS * 32), row r's four 16-byte
+// k-groups g stored at g ^ ((r >> 2) & 3), so that 16 consecutive rows read at
+// one k-group hit distinct banks without padding (a 192-row chunk fits
+// TX_BUF).
+template <int NT, int ROWS>
+__device__ __forceinline__ void ws_mma(const unsigned short* Ws, int lr, int lg, const u32x4 (&xb)[2][3],
+                                       f32x4 (&acc)[2][NT])
+{
+    const unsigned short* wr = Ws + lr * 32 + ((lg ^ ((lr >> 2) & 3)) * 8);
+    u32x4 wa[2][3];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * ROWS * 32);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (nt + 1 < NT) {
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * 32 + pl * ROWS * 32);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
+    }
+}
+
 // wc_mma with other work woven in: side(nt) runs in tile nt's segment, next
 // to its 12 MFMAs (VALU work issued there co-executes with them).
 template <int NT, int PLANE, typename F>

@@ -45,71 +45,88 @@
 #define TX_ROWS (TX_WAVES * 32)
 #define TX_BUF (36 * 512)  // an LDS chunk buffer: 36 loads cover 144 rows
 
-// Row statistics of a token over its 144 channels (36 per lane, the four lane
-// groups of the token reducing with shuffles): two-pass mean, biased variance
-// (cpu.rs:563-581); returns (mean, rstd).
-__device__ __forceinline__ float2 tx_row_stats(const f32x4 (&v)[9], float eps)
+// Row statistics of a token over its C channels (C = 144: 36 per lane, 180:
+// 45; NT = ceil(C / 16) tiles of which the last holds C % 16 real channels in
+// lane group 0), the four lane groups of the token reducing with shuffles:
+// two-pass mean, biased variance (cpu.rs:563-581); returns (mean, rstd).
+template <int C>
+__device__ __forceinline__ bool tx_live(int nt, int lg)
 {
+    constexpr int NT = (C + 15) / 16;
+    return C % 16 == 0 || nt < NT - 1 || lg * 4 < C % 16;
+}
+template <int C>
+__device__ __forceinline__ float2 tx_row_stats(const f32x4 (&v)[(C + 15) / 16], int lg, float eps)
+{
+    constexpr int NT = (C + 15) / 16;
     float s = 0.0f;
 #pragma unroll
-    for (int nt = 0; nt < 9; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s += v[nt][j];
+        for (int j = 0; j < 4; ++j) s += v[nt][j];  // zeros past C
     s += __shfl_xor(s, 16, 64);
     s += __shfl_xor(s, 32, 64);
-    const float mean = s / 144.0f;
+    const float mean = s / (float)C;
     float q = 0.0f;
 #pragma unroll
-    for (int nt = 0; nt < 9; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float d = v[nt][j] - mean;
+            const float d = tx_live<C>(nt, lg) ? v[nt][j] - mean : 0.0f;
             q += d * d;
         }
     q += __shfl_xor(q, 16, 64);
     q += __shfl_xor(q, 32, 64);
-    return make_float2(mean, 1.0f / sqrtf(q / 144.0f + eps));
+    return make_float2(mean, 1.0f / sqrtf(q / (float)C + eps));
 }
 
-// acc = the 32 rows of res from mbase (zeros past M).
-__device__ __forceinline__ void tx_load_res(const float* res, int mbase, int M, int lr, int lg, f32x4 (&acc)[2][9])
+// acc = the 32 rows of res [M][C] from mbase (zeros past M and past C).
+template <int C>
+__device__ __forceinline__ void tx_load_res(const float* res, int mbase, int M, int lr, int lg,
+                                            f32x4 (&acc)[2][(C + 15) / 16])
 {
+    constexpr int NT = (C + 15) / 16;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         const int m = mbase + mt * 16 + lr;
         const bool alive = m < M;
-        const float* row = alive ? res + (size_t)m * 144 + lg * 4 : hat_zero_row;
+        const float* row = alive ? res + (size_t)m * C + lg * 4 : hat_zero_row;
 #pragma unroll
-        for (int nt = 0; nt < 9; ++nt) acc[mt][nt] = *(const f32x4*)(row + (alive ? nt * 16 : 0));
+        for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] = *(const f32x4*)(alive && tx_live<C>(nt, lg) ? row + nt * 16 : hat_zero_row);
     }
 }
 
-// v = acc + bias (Cs); out = v; with xn: xn = LN(v) by (nw, nb) = (Cs + 144, Cs + 288).
-__device__ __forceinline__ void tx_store_rows(const f32x4 (&acc)[2][9], const float* Cs, int mbase, int M, int lr,
-                                              int lg, float eps, float* out, float* xn)
+// v = acc + bias (Cs); out = v; with xn: xn = LN(v) by (nw, nb) = (Cs + 16 NT,
+// Cs + 32 NT) (Cs zero past C).
+template <int C>
+__device__ __forceinline__ void tx_store_rows(const f32x4 (&acc)[2][(C + 15) / 16], const float* Cs, int mbase,
+                                              int M, int lr, int lg, float eps, float* out, float* xn)
 {
+    constexpr int NT = (C + 15) / 16;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         const int m = mbase + mt * 16 + lr;
-        f32x4 v[9];
+        f32x4 v[NT];
 #pragma unroll
-        for (int nt = 0; nt < 9; ++nt) v[nt] = acc[mt][nt] + *(const f32x4*)(Cs + nt * 16 + lg * 4);
+        for (int nt = 0; nt < NT; ++nt) v[nt] = acc[mt][nt] + *(const f32x4*)(Cs + nt * 16 + lg * 4);
         float2 st = make_float2(0.f, 0.f);
-        if (xn) st = tx_row_stats(v, eps);
+        if (xn) st = tx_row_stats<C>(v, lg, eps);
         if (m >= M) continue;
-        float* orow = out + (size_t)m * 144 + lg * 4;
+        float* orow = out + (size_t)m * C + lg * 4;
 #pragma unroll
-        for (int nt = 0; nt < 9; ++nt) *(f32x4*)(orow + nt * 16) = v[nt];
+        for (int nt = 0; nt < NT; ++nt)
+            if (tx_live<C>(nt, lg)) *(f32x4*)(orow + nt * 16) = v[nt];
         if (xn) {
-            float* nrow = xn + (size_t)m * 144 + lg * 4;
+            float* nrow = xn + (size_t)m * C + lg * 4;
 #pragma unroll
-            for (int nt = 0; nt < 9; ++nt) {
-                const f32x4 w4 = *(const f32x4*)(Cs + 144 + nt * 16 + lg * 4);
-                const f32x4 b4 = *(const f32x4*)(Cs + 288 + nt * 16 + lg * 4);
+            for (int nt = 0; nt < NT; ++nt) {
+                const f32x4 w4 = *(const f32x4*)(Cs + 16 * NT + nt * 16 + lg * 4);
+                const f32x4 b4 = *(const f32x4*)(Cs + 32 * NT + nt * 16 + lg * 4);
                 f32x4 y;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) y[j] = (v[nt][j] - st.x) * st.y * w4[j] + b4[j];
-                *(f32x4*)(nrow + nt * 16) = y;
+                if (tx_live<C>(nt, lg)) *(f32x4*)(nrow + nt * 16) = y;
             }
         }
     }
@@ -136,7 +153,7 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
         Cs[i] = i < 144 ? p.bias[i] : (i < 288 ? p.nw[i - 144] : p.nb[i - 288]);
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
     f32x4 acc[2][9];
-    tx_load_res(p.res, mbase, M, lr, lg, acc);
+    tx_load_res<144>(p.res, mbase, M, lr, lg, acc);
     f32x4 y[5][2][2];
     {
         WcRows<144> ar;
@@ -175,7 +192,7 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
         if (CAB && c >= 4 && c + 1 < NCH) gather_t1(c - 4, t1v);
         wc_mma<9, 144 * WC_KS>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
     }
-    tx_store_rows(acc, Cs, mbase, M, lr, lg, p.eps, p.out, p.xn);
+    tx_store_rows<144>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, p.xn);
 }
 
 // out = x' + fc2(gelu(fc1(y))) + b2 (+ xn = LN_next(out)); y = p.a, x' = p.res.
@@ -204,7 +221,7 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
     }
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
     f32x4 acc2[2][9];
-    tx_load_res(p.res, mbase, M, lr, lg, acc2);
+    tx_load_res<144>(p.res, mbase, M, lr, lg, acc2);
     WcRows<144> yr;
     yr.init(p.a, mbase, M, lr);
     f32x4 pre[2][2];
@@ -263,10 +280,101 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
             wc_mma<9, 144 * WC_KS>(s & 1 ? Ws0 : Ws1, lr, lg, xb, acc2);
         }
     }
-    tx_store_rows(acc2, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
+    tx_store_rows<144>(acc2, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
+}
+
+// The C = 180 MLP: out = x' + fc2(gelu(fc1(y))) + b2 (+ xn = LN_next(out)),
+// y = p.a [M][180], x' = p.res. The hidden layer in six parts of 64 units (the
+// last 40 real), so that fc2's 192 accumulator columns (96 registers), fc1's
+// output of a part (32) and the operands fit a lane. p.w: 48 chunks
+// MX180_SLOT apart, per part six fc1 k-steps (64 permuted rows, b1 at k = 180)
+// then two fc2 k-steps (192 rows); the swizzled [rows][32] layout (ws_mma).
+template <bool LN>
+__device__ __forceinline__ void mlpx180_body(const TailXArgs& p)
+{
+    constexpr int C = 180, NT = 12, NP = 6, NL1 = 12, NL2 = 36;
+    static_assert(NL1 * 512 == 3 * MX180_HID * 32 && NL2 * 512 == MX180_SLOT && MX180_SLOT <= TX_BUF, "chunk loads");
+    __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
+    __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
+    __shared__ __attribute__((aligned(16))) float Cs[3 * 16 * NT];  // b2, next norm w, b (zero past 180)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
+    const int lr = lane & 15, lg = lane >> 4;
+    const int M = p.M;
+    if ((int)blockIdx.x * TX_ROWS >= M) return;  // whole block, before any barrier
+    wc_issue<NL1, TX_WAVES>(Ws0, p.w, wave, lane);
+    for (int i = tid; i < 3 * 16 * NT; i += TX_WAVES * 64) {
+        const int part = i / (16 * NT), c = i - part * 16 * NT;
+        float v = 0.0f;
+        if (c < C) v = part == 0 ? p.b2[c] : (LN ? (part == 1 ? p.nw[c] : p.nb[c]) : 0.0f);
+        Cs[i] = v;
+    }
+    const int mbase = blockIdx.x * TX_ROWS + wave * 32;
+    f32x4 acc2[2][NT];
+    tx_load_res<C>(p.res, mbase, M, lr, lg, acc2);
+    WcRows<C> yr;
+    yr.init(p.a, mbase, M, lr);
+    f32x4 pre[2][2];
+    yr.load_b(0, lg, pre);
+#pragma unroll 1
+    for (int q = 0; q < NP; ++q) {
+        const unsigned short* wq = p.w + (size_t)(8 * q) * MX180_SLOT;  // this part's eight chunks
+        // fc1: the part's 64 hidden units (permuted rows), chunks 0..5 (even
+        // chunks in buffer 0: eight a part keep the parities fixed)
+        f32x4 h[2][4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) h[0][nt] = h[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        auto fc1_step = [&](int ks, auto parv) {
+            constexpr int PAR = decltype(parv)::value;  // = ks & 1
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the chunk (and its rows) have landed
+            __syncthreads();                // everyone's have, and everyone is done with the one before
+            if (ks < 5) wc_issue<NL1, TX_WAVES>(PAR ? Ws0 : Ws1, wq + (size_t)(ks + 1) * MX180_SLOT, wave, lane);
+            else wc_issue<NL2, TX_WAVES>(Ws0, wq + (size_t)6 * MX180_SLOT, wave, lane);
+            u32x4 xb[2][3];
+            split_pre(pre, xb);
+            // the rows of the next fc1 chunk: this part's next k-step (k =
+            // 180 carries the 1 of b1's column), or k-step 0 for the next part
+            if (ks < 5) yr.load_b(ks + 1, lg, pre);
+            else if (q < NP - 1) yr.load_b(0, lg, pre);
+            ws_mma<4, MX180_HID>(PAR ? Ws1 : Ws0, lr, lg, xb, h);
+        };
+#pragma unroll 1
+        for (int ks = 0; ks < 6; ks += 2) {
+            fc1_step(ks, CInt<0>{});
+            fc1_step(ks + 1, CInt<1>{});
+        }
+        // fc2 over the part's units, from registers, chunks 6, 7
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (s == 0) wc_issue<NL2, TX_WAVES>(Ws1, wq + (size_t)7 * MX180_SLOT, wave, lane);
+            else if (q < NP - 1) wc_issue<NL1, TX_WAVES>(Ws0, wq + (size_t)8 * MX180_SLOT, wave, lane);
+            if (s == 0) {
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) h[mt][nt][j] = gelu(h[mt][nt][j]);
+            }
+            u32x4 xb[2][3];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const float f[8] = {h[mt][2 * s][0],     h[mt][2 * s][1],     h[mt][2 * s][2],
+                                    h[mt][2 * s][3],     h[mt][2 * s + 1][0], h[mt][2 * s + 1][1],
+                                    h[mt][2 * s + 1][2], h[mt][2 * s + 1][3]};
+                split3_x8(f, xb[mt]);
+            }
+            ws_mma<NT, 16 * NT>(s == 0 ? Ws0 : Ws1, lr, lg, xb, acc2);
+        }
+    }
+    tx_store_rows<C>(acc2, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
 }
 
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx_cab(TailXArgs p) { projx_body<true>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx(TailXArgs p) { projx_body<false>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx_ln(TailXArgs p) { mlpx_body<true>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx(TailXArgs p) { mlpx_body<false>(p); }
+extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx180_ln(TailXArgs p) { mlpx180_body<true>(p); }
+extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx180(TailXArgs p) { mlpx180_body<false>(p); }

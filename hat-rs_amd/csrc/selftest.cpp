@@ -374,6 +374,30 @@ int gpu_selftest(std::string* err)
             check_close(std::string(k), dx.get(), want, 5e-5);
             if (epi == EPI_RESID_LN) check_close(std::string(k) + " layernorm", da.get(), wxn, 5e-5);
             note(std::string(k) + " C " + std::to_string(C) + " M 600 (in place)");
+            if (C == 180) {
+                // the split-bf16 form, in place the same way, 5 tiles of 128
+                // (the last partial)
+                std::vector<unsigned short> mw;
+                pack_mlp_x180(w1.data(), b1.data(), w2.data(), &mw);
+                Dev da2(a), dx2(res), dmw((mw.size() + 1) / 2);
+                Runtime::get().h2d(dmw.p, mw.data(), mw.size() * sizeof(unsigned short));
+                TailXArgs q{};
+                q.a = da2.p;
+                q.res = dx2.p;
+                q.out = dx2.p;
+                q.xn = epi == EPI_RESID_LN ? da2.p : nullptr;
+                q.w = (const unsigned short*)dmw.p;
+                q.b2 = db2.p;
+                q.nw = dnw.p;
+                q.nb = dnb.p;
+                q.M = M;
+                q.eps = 1e-5f;
+                const char* kx = epi == EPI_RESID_LN ? "hat_mlpx180_ln" : "hat_mlpx180";
+                launch(s, kx, (unsigned)wx_tiles(M), 1, 1, WX_THREADS, q);
+                check_close(kx, dx2.get(), want, 5e-5);
+                if (epi == EPI_RESID_LN) check_close(std::string(kx) + " layernorm", da2.get(), wxn, 5e-5);
+                note(std::string(kx) + " C 180 M 600 (split-bf16, in place)");
+            }
         }
 
         // ---- folded CAB (144 -> 6 -> 144) against the unfolded computation:
