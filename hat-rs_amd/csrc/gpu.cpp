@@ -153,6 +153,20 @@ static void split_ws_step(int rows, F value, unsigned short* dst)
         }
 }
 
+// The C = 180 projection [180][180] for hat_projx180*: six 32-k steps of 192
+// rows (180 real; the bias is added in the epilogue), MX180_SLOT apart.
+std::vector<unsigned short> pack_linear_x180(const float* w)
+{
+    constexpr int C = 180;
+    std::vector<unsigned short> out((size_t)6 * MX180_SLOT, 0);
+    for (int ks = 0; ks < 6; ++ks)
+        split_ws_step(192, [&](int n, int kk) {
+            const int k = ks * 32 + kk;
+            return n < C && k < C ? w[(size_t)n * C + k] : 0.0f;
+        }, &out[(size_t)ks * MX180_SLOT]);
+    return out;
+}
+
 // The C = 180 MLP (fc1 [360][180] + b1, fc2 [180][360]) for hat_mlpx180: per
 // part of 64 hidden units, six fc1 k-steps (rows permuted by mlpx_unit, b1 at
 // k = 180) and two fc2 k-steps (192 rows, 180 real, the part's units in
@@ -935,6 +949,11 @@ void GpuBackend::upload_linear(const std::string& name)
         const size_t n = strlen(t);
         return name.size() >= n && name.compare(name.size() - n, n, t) == 0;
     };
+    if (L.K == 180 && L.N == 180 && ends("proj")) {
+        // the C = 180 projection tails (hat_projx180*)
+        std::vector<unsigned short> x = pack_linear_x180(wt_.t(name + ".weight"));
+        L.wx = (unsigned short*)upload_bytes(x.data(), x.size() * sizeof(unsigned short));
+    }
     if ((L.K == 180 && L.N == 540 && ends(".qkv")) || (L.K == 144 && ((L.N == 432 && ends(".qkv")) || (L.N == 144 && ends("proj"))))) {
         // qkv: the weight-stationary layout of hat_gemmx_qkv; proj: streamed chunks (tailx)
         std::vector<unsigned short> x = ends(".qkv") ? pack_linear_ws(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K)
@@ -1183,6 +1202,30 @@ void GpuBackend::gemm(const DevLinear& L, const float* a, int lda, long M, float
 }
 
 // x = x + fc2(gelu(fc1(a_.xn))), in place; with a norm also a_.xn = norm(x).
+// The split-bf16 C = 180 projection tail: out = res + ao . Wp^T + bias (with
+// aux: + aux * gate * cscale), xn = LN2(out) by (nw, nb).
+void run_projx180(hipStream_t s, const DevLinear& proj, const float* ao, const float* res, float* out, float* xn,
+                  const float* nw, const float* nb, const float* aux, const float* gate, float cscale, long M)
+{
+    if (!proj.wx || proj.K != 180 || proj.N != 180) throw Error("projx180: needs the pre-split 180 x 180 projection");
+    if (M > 0x7fffffffL) throw Error("projx180: too many rows");
+    TailXArgs q{};
+    q.a = ao;
+    q.res = res;
+    q.out = out;
+    q.xn = xn;
+    q.w = proj.wx;
+    q.bias = proj.b;
+    q.nw = nw;
+    q.nb = nb;
+    q.M = (int)M;
+    q.eps = 1e-5f;
+    q.aux = aux;
+    q.gate = gate;
+    q.cscale = cscale;
+    launch(s, aux ? "hat_projx180_hab" : "hat_projx180", (unsigned)wx_tiles((int)M), 1, 1, WX_THREADS, q);
+}
+
 // The split-bf16 C = 180 MLP: out = x + fc2(gelu(fc1(xn))) + b2 (+ xn = LN(out)).
 void run_mlpx180(hipStream_t s, const DevMlpX& m, const float* b2, const float* xn_in, float* x, float* xn_out,
                  const float* nw, const float* nb, long M)
@@ -1258,7 +1301,7 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
         gemm(lin_.at(p + ".attn.qkv"), a_.xn, C, T, a_.qkv, 0, EPI_QKV);
         attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, &gate);
         auto mx = mlpx_.find(p + ".mlp");
-        if (proj.wx && mx != mlpx_.end()) {
+        if (proj.wx && C == 144 && mx != mlpx_.end()) {
             // split-bf16: proj + gated conv2 + shortcut + norm2, then the MLP + next norm1
             run_tailx(stream_, true, proj, mx->second, lin_.at(p + ".mlp.fc2").b, a_.ao, x_in, x_out, a_.xn, a_.t1,
                       (const unsigned short*)a_.w2gx, a_.bias2, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
@@ -1285,8 +1328,12 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
     // proj's epilogue adds the shortcut and the gated conv branch, then norm2.
     gemm(lin_.at(p + ".attn.qkv"), a_.xn, C, T, a_.qkv, 0, EPI_QKV);
     attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, nullptr, &se);
-    gemm(lin_.at(p + ".attn.proj"), a_.ao, C, T, x_out, C, EPI_HAB_LN, x_in, a_.t2, a_.gate, a_.xn,
-         p + ".norm2");
+    const DevLinear& proj = lin_.at(p + ".attn.proj");
+    if (proj.wx && C == 180)
+        run_projx180(stream_, proj, a_.ao, x_in, x_out, a_.xn, raw_.at(p + ".norm2.weight"),
+                     raw_.at(p + ".norm2.bias"), a_.t2, a_.gate, wt_.conv_scale, T);
+    else
+        gemm(proj, a_.ao, C, T, x_out, C, EPI_HAB_LN, x_in, a_.t2, a_.gate, a_.xn, p + ".norm2");
     mlp(p + ".mlp", x_out, EPI_RESID_LN, next_norm);
 }
 
@@ -1302,7 +1349,7 @@ void GpuBackend::ocab(int stage, float* x)
     const DevLinear& proj = lin_.at(p + ".proj");
     const DevLinear &fc1 = lin_.at(p + ".mlp.fc1"), &fc2 = lin_.at(p + ".mlp.fc2");
     auto mx = mlpx_.find(p + ".mlp");
-    if (proj.wx && mx != mlpx_.end()) {
+    if (proj.wx && C == 144 && mx != mlpx_.end()) {
         // split-bf16: projection + shortcut + norm2, then the MLP + residual
         run_tailx(stream_, false, proj, mx->second, fc2.b, a_.ao, x, x, a_.xn, nullptr, nullptr, proj.b,
                   raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"), nullptr, nullptr, plan_.hp, plan_.wp);
@@ -1315,7 +1362,11 @@ void GpuBackend::ocab(int stage, float* x)
                      plan_.hp, plan_.wp);
         return;
     }
-    gemm(proj, a_.ao, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, a_.xn, p + ".norm2");
+    if (proj.wx && C == 180)
+        run_projx180(stream_, proj, a_.ao, x, x, a_.xn, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
+                     nullptr, nullptr, 0.0f, T);
+    else
+        gemm(proj, a_.ao, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, a_.xn, p + ".norm2");
     mlp(p + ".mlp", x, EPI_RESID, "");
 }
 

@@ -80,6 +80,7 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
 // rows in the order that leaves its output in fc2's operand layout
 // (tailx.hip).
 void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
+std::vector<unsigned short> pack_linear_x180(const float* w);
 void pack_mlp_x180(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
 std::vector<unsigned short> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,

@@ -290,6 +290,11 @@ struct TailXArgs {
     const float* nb;
     int M, H, W;               // rows = the H x W plane
     float eps;
+    // hat_projx180_hab (the unfolded CAB of the C = 180 family): out = x +
+    // proj + bias + aux * gate * cscale (aux: conv2's output [M][180])
+    const float* aux;
+    const float* gate;
+    float cscale;
 };
 
 struct LnArgs {

@@ -283,6 +283,66 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
     tx_store_rows<144>(acc2, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
 }
 
+// The C = 180 projection tail: out = x + ao . Wp^T + bias (HAB: + aux * gate *
+// cscale, the unfolded CAB's gated conv2), xn = LN2(out). p.w: six chunks
+// MX180_SLOT apart, k-steps of the 192-row (180 real) projection in the
+// swizzled [rows][32] layout (ws_mma); ao's rows are read one k-step ahead.
+template <bool HAB>
+__device__ __forceinline__ void projx180_body(const TailXArgs& p)
+{
+    constexpr int C = 180, NT = 12, NL = 36;
+    static_assert(NL * 512 == MX180_SLOT && MX180_SLOT <= TX_BUF, "chunk loads");
+    __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
+    __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
+    __shared__ __attribute__((aligned(16))) float Cs[4 * 16 * NT];  // bias, norm2 w, b, gate * cscale (zero past 180)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
+    const int lr = lane & 15, lg = lane >> 4;
+    const int M = p.M;
+    if ((int)blockIdx.x * TX_ROWS >= M) return;  // whole block, before any barrier
+    wc_issue<NL, TX_WAVES>(Ws0, p.w, wave, lane);
+    for (int i = tid; i < 4 * 16 * NT; i += TX_WAVES * 64) {
+        const int part = i / (16 * NT), c = i - part * 16 * NT;
+        float v = 0.0f;
+        if (c < C) v = part == 0 ? p.bias[c] : part == 1 ? p.nw[c] : part == 2 ? p.nb[c] : (HAB ? p.gate[c] * p.cscale : 0.0f);
+        Cs[i] = v;
+    }
+    const int mbase = blockIdx.x * TX_ROWS + wave * 32;
+    f32x4 acc[2][NT];
+    tx_load_res<C>(p.res, mbase, M, lr, lg, acc);
+    WcRows<C> ar;
+    ar.init(p.a, mbase, M, lr);
+    f32x4 pre[2][2];
+    ar.load(0, lg, pre);
+#pragma unroll
+    for (int c = 0; c < 6; ++c) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk c (and its rows) have landed
+        __syncthreads();                // everyone's have, and everyone is done with chunk c - 1
+        if (c + 1 < 6) wc_issue<NL, TX_WAVES>(c & 1 ? Ws0 : Ws1, p.w + (size_t)(c + 1) * MX180_SLOT, wave, lane);
+        u32x4 xb[2][3];
+        split_pre(pre, xb);
+        if (c + 1 < 6) ar.load(c + 1, lg, pre);
+        ws_mma<NT, 16 * NT>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
+    }
+    if constexpr (HAB) {
+        // + conv2's output times gate * cscale, one 16-row tile at a time
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int m = mbase + mt * 16 + lr;
+            const float* arow = m < M ? p.aux + (size_t)m * C + lg * 4 : hat_zero_row;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const f32x4 a4 = *(const f32x4*)(m < M && tx_live<C>(nt, lg) ? arow + nt * 16 : hat_zero_row);
+                const f32x4 g4 = *(const f32x4*)(Cs + 48 * NT + nt * 16 + lg * 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[mt][nt][j] += a4[j] * g4[j];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    tx_store_rows<C>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, p.xn);
+}
+
 // The C = 180 MLP: out = x' + fc2(gelu(fc1(y))) + b2 (+ xn = LN_next(out)),
 // y = p.a [M][180], x' = p.res. The hidden layer in six parts of 64 units (the
 // last 40 real), so that fc2's 192 accumulator columns (96 registers), fc1's
@@ -378,3 +438,5 @@ extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx_ln(TailX
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx(TailXArgs p) { mlpx_body<false>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx180_ln(TailXArgs p) { mlpx180_body<true>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx180(TailXArgs p) { mlpx180_body<false>(p); }
+extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx180_hab(TailXArgs p) { projx180_body<true>(p); }
+extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx180(TailXArgs p) { projx180_body<false>(p); }

@@ -400,6 +400,54 @@ int gpu_selftest(std::string* err)
             }
         }
 
+        // ---- the split-bf16 C = 180 projection tails against double: out =
+        // res + a . Wp^T + b (+ aux * gate * cscale), xn = LN(out), in place
+        // over the residual, 600 rows (the last tile partial).
+        for (int hab : {1, 0}) {
+            const int M = 600, C = 180;
+            const float cscale = 0.01f;
+            std::vector<float> a = rng.vec((size_t)M * C, 1.0f), w = rng.vec((size_t)C * C, 0.08f),
+                               b = rng.vec(C, 0.1f), res = rng.vec((size_t)M * C, 1.0f), aux = rng.vec((size_t)M * C, 1.0f),
+                               gate = rng.vec(C, 1.0f), nw = rng.vec(C, 1.0f), nb = rng.vec(C, 0.1f);
+            std::vector<unsigned short> wx = pack_linear_x180(w.data());
+            Dev da(a), db(b), dx(res), daux(aux), dg(gate), dnw(nw), dnb(nb), dxn((size_t)M * C), dw((wx.size() + 1) / 2);
+            Runtime::get().h2d(dw.p, wx.data(), wx.size() * sizeof(unsigned short));
+            TailXArgs q{};
+            q.a = da.p;
+            q.res = dx.p;
+            q.out = dx.p;
+            q.xn = dxn.p;
+            q.w = (const unsigned short*)dw.p;
+            q.bias = db.p;
+            q.nw = dnw.p;
+            q.nb = dnb.p;
+            q.M = M;
+            q.eps = 1e-5f;
+            q.aux = hab ? daux.p : nullptr;
+            q.gate = hab ? dg.p : nullptr;
+            q.cscale = cscale;
+            const char* k = hab ? "hat_projx180_hab" : "hat_projx180";
+            launch(s, k, (unsigned)wx_tiles(M), 1, 1, WX_THREADS, q);
+            std::vector<double> want((size_t)M * C), wxn((size_t)M * C);
+            for (int m = 0; m < M; ++m) {
+                double mean = 0, var = 0;
+                for (int n = 0; n < C; ++n) {
+                    double v = b[n];
+                    for (int c = 0; c < C; ++c) v += (double)a[(size_t)m * C + c] * w[(size_t)n * C + c];
+                    v += res[(size_t)m * C + n];
+                    if (hab) v += (double)aux[(size_t)m * C + n] * gate[n] * cscale;
+                    want[(size_t)m * C + n] = v;
+                    mean += v / C;
+                }
+                for (int n = 0; n < C; ++n) var += (want[(size_t)m * C + n] - mean) * (want[(size_t)m * C + n] - mean) / C;
+                for (int n = 0; n < C; ++n)
+                    wxn[(size_t)m * C + n] = (want[(size_t)m * C + n] - mean) / std::sqrt(var + 1e-5) * nw[n] + nb[n];
+            }
+            check_close(k, dx.get(), want, 3e-5);
+            check_close(std::string(k) + " layernorm", dxn.get(), wxn, 5e-5);
+            note(std::string(k) + " C 180 M 600 (split-bf16, in place)");
+        }
+
         // ---- folded CAB (144 -> 6 -> 144) against the unfolded computation:
         // conv1 + GELU, conv2 in full, its pixel mean, squeeze-excite, gate, and
         // shortcut + proj + gated conv2 * cscale + LayerNorm - in double. A 32 x 48
