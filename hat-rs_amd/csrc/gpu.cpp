@@ -42,25 +42,27 @@ float bf16_float(unsigned short h)
 }
 }  // namespace
 
-// Rows [N][K] of w (row stride ldw), N <= 144, as weight chunks at dst: per
-// 32-k step s, three bf16 planes [N][WC_KS] (plane stride N * WC_KS) holding
-// k = 32 s + j for j < 32: x = h0 + h1 + h2, each part the RNE of what the
-// parts before it leave; k >= K and j >= 32 stay zero.
-static void split_chunks(const float* w, int N, int K, int ldw, unsigned short* dst)
+// Rows [N][K] of w (row stride ldw), N <= 192, as weight chunks at dst: the
+// value at (n, k) is column kbase + k, which lands in 32-k step s = (kbase +
+// k) / 32, WC_CHUNK elements apart, as three bf16 planes [N][32] (plane stride
+// N * 32) with row n's 16-byte k-groups g stored at g ^ ((n >> 2) & 3) (so that
+// 16 consecutive rows read at one k-group hit distinct banks): x = h0 + h1 +
+// h2, each part the RNE of what the parts before it leave; the rest stays zero.
+static void split_chunks(const float* w, int N, int K, int ldw, unsigned short* dst, int kbase = 0)
 {
-    for (int s = 0; s * 32 < K; ++s)
-        for (int n = 0; n < N; ++n)
-            for (int j = 0; j < 32 && 32 * s + j < K; ++j) {
-                const float x = w[(size_t)n * ldw + 32 * s + j];
-                const unsigned short h0 = bf16_rne(x);
-                const float r1 = x - bf16_float(h0);
-                const unsigned short h1 = bf16_rne(r1);
-                const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
-                unsigned short* d = dst + (size_t)s * WC_CHUNK + (size_t)n * WC_KS + j;
-                d[0] = h0;
-                d[(size_t)N * WC_KS] = h1;
-                d[(size_t)2 * N * WC_KS] = h2;
-            }
+    for (int n = 0; n < N; ++n)
+        for (int k = 0; k < K; ++k) {
+            const float x = w[(size_t)n * ldw + k];
+            const unsigned short h0 = bf16_rne(x);
+            const float r1 = x - bf16_float(h0);
+            const unsigned short h1 = bf16_rne(r1);
+            const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+            const int s = (kbase + k) / 32, kk = (kbase + k) % 32;
+            unsigned short* d = dst + (size_t)s * WC_CHUNK + (size_t)n * 32 + ((kk / 8) ^ ((n >> 2) & 3)) * 8 + kk % 8;
+            d[0] = h0;
+            d[(size_t)N * 32] = h1;
+            d[(size_t)2 * N * 32] = h2;
+        }
 }
 
 std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K)
@@ -73,7 +75,7 @@ std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int
         unsigned short* dst = &out[(size_t)sl * steps * WC_CHUNK];
         split_chunks(w + (size_t)sl * BN * K, BN, K, K, dst);
         // the bias as column k = K (= 144: step 4, j = 16), split like the rest
-        if (bias) split_chunks(bias + (size_t)sl * BN, BN, 1, 1, dst + (size_t)(K / 32) * WC_CHUNK + K % 32);
+        if (bias) split_chunks(bias + (size_t)sl * BN, BN, 1, 1, dst, K);
     }
     return out;
 }
@@ -116,7 +118,7 @@ static int mlpx_unit(int row)
 void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w)
 {
     constexpr int C = 144, H = 288;
-    static_assert(3 * C * WC_KS <= WC_CHUNK && WC_CHUNK % 512 == 0 && H % MX_HID == 0, "chunks");
+    static_assert(3 * C * 32 <= WC_CHUNK && WC_CHUNK % 512 == 0 && H % MX_HID == 0, "chunks");
     std::vector<float> f1((size_t)MX_HID * C), fb((size_t)MX_HID);
     w->assign((size_t)24 * WC_CHUNK, 0);
     for (int q = 0; q < H / MX_HID; ++q) {
@@ -128,7 +130,7 @@ void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<u
         unsigned short* dst = &(*w)[(size_t)(8 * q) * WC_CHUNK];
         split_chunks(f1.data(), MX_HID, C, C, dst);
         // b1 as fc1's column k = 144 (step 4, j = 16)
-        split_chunks(fb.data(), MX_HID, 1, 1, dst + (size_t)(C / 32) * WC_CHUNK + C % 32);
+        split_chunks(fb.data(), MX_HID, 1, 1, dst, C);
         split_chunks(w2 + q * MX_HID, C, MX_HID, H, &(*w)[(size_t)(8 * q + 5) * WC_CHUNK]);
     }
 }

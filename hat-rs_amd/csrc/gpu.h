@@ -65,10 +65,10 @@ struct DevConv {
 // Host-side repacking (also used by the selftest and the op entry points).
 std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
 // [N][144] -> per 144-row slice, five weight chunks (one per 32-k step) of
-// three bf16 planes [144][WC_KS]: w = p0 + p1 + p2, each part the round-to-
-// nearest bf16 of what the earlier ones leave; the bias (if given) as column
-// k = 144, split the same way; the rest of k 144..159 and the plane padding
-// zero.
+// three bf16 planes [144][32] (k-groups swizzled as in pack_linear_ws): w =
+// p0 + p1 + p2, each part the round-to-nearest bf16 of what the earlier ones
+// leave; the bias (if given) as column k = 144, split the same way; the rest
+// of k 144..159 zero.
 std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K);
 // The same split for hat_gemmx_qkv's weight-stationary slices: per 144-row
 // slice five chunks of three planes [144][32], each row's 16-byte k-groups

@@ -110,7 +110,7 @@ struct CabGateArgs {
     float* gate;         // out: the gate itself [144]
     float cscale;
     int sq;
-    unsigned short* w2gx;  // out (if set): w2g as 2 weight chunks [3][144][WC_KS] for hat_projx_cab
+    unsigned short* w2gx;  // out (if set): w2g as 2 weight chunks [3][144][32] (swizzled) for hat_projx_cab
 };
 
 // Implicit-GEMM 3x3 convolution, stride 1, zero padding 1, NHWC.
@@ -240,13 +240,13 @@ struct HabTailArgs {
 // hat_projx(_cab): out = x' = res + a . Wp^T (+ nb(t1) . W2g^T) + bias,
 //                  xn = LN(x') with nw / nb;
 // hat_mlpx(_ln):   out = res + fc2(gelu(fc1(a))) + b2 (+ xn = LN(out)).
-// Weight chunks of the split-bf16 linears (gemmx.hip, tailx.hip): one 32-k
-// step of up to 144 rows as three bf16 planes [rows][WC_KS] (k 32..39 zero),
-// WC_CHUNK elements apart (zeros after the planes). A chunk is copied as
-// loads of 1 KB, the same number from every wave of a block: 144 rows take
-// 34 (36 or 40 to share them out evenly), 96 rows 23 (24).
-#define WC_KS 40
-#define WC_CHUNK 20480  // 40 x 512 >= 3 x 144 x WC_KS
+// Weight chunks of the split-bf16 tails (tailx.hip): one 32-k step of up to
+// 192 rows as three bf16 planes [rows][32], each row's four 16-byte k-groups g
+// stored at g ^ ((row >> 2) & 3) (ws_mma), WC_CHUNK elements apart (zeros after
+// the planes). A chunk is copied as loads of 1 KB, the same number from every
+// wave of a block: 144 rows take 27 (28 to share them out evenly), 96 rows 18
+// (20), 192 rows 36.
+#define WC_CHUNK 20480  // 40 x 512 >= 3 x 192 x 32
 // The MLP walks the hidden layer in thirds of MX_HID units: per third five
 // fc1 chunks (96 permuted rows, k = input channel) then three fc2 chunks (144
 // rows, k = the third's hidden units), 24 chunks in all.

@@ -301,17 +301,18 @@ __device__ __forceinline__ void cab_gate_body(const CabGateArgs& p, float* lds)
         if (tap < 9) v = (p.cscale * s_gate[c]) * p.w2[(c * CAB_CC + ci) * 9 + tap];
         p.w2g[i] = v;
     }
-    // the same weights as hat_projx_cab's two weight chunks: [s][plane][c][WC_KS],
-    // k = 32 s + j (j < 32), zeros elsewhere
+    // the same weights as hat_projx_cab's two weight chunks: [s][plane][c][32],
+    // row c's k-group g at g ^ ((c >> 2) & 3), k = 32 s + j, zeros elsewhere
     if (p.w2gx) {
-        constexpr int PLANE = CAB_C * WC_KS;
+        constexpr int PLANE = CAB_C * 32;
         for (int i = tid; i < 2 * WC_CHUNK; i += WAVES * 64) {
             const int s = i / WC_CHUNK, r = i - s * WC_CHUNK;
             unsigned short h = 0;
             if (r < 3 * PLANE) {
-                const int pl = r / PLANE, c = (r - pl * PLANE) / WC_KS, j = r - pl * PLANE - c * WC_KS;
+                const int pl = r / PLANE, c = (r - pl * PLANE) / 32, pos = r - pl * PLANE - c * 32;
+                const int j = (((pos >> 3) ^ ((c >> 2) & 3)) << 3) | (pos & 7);
                 const int k = 32 * s + j, tap = k / CAB_CC, ci = k - tap * CAB_CC;
-                const float v = j < 32 && tap < 9 ? (p.cscale * s_gate[c]) * p.w2[(c * CAB_CC + ci) * 9 + tap] : 0.0f;
+                const float v = tap < 9 ? (p.cscale * s_gate[c]) * p.w2[(c * CAB_CC + ci) * 9 + tap] : 0.0f;
                 h = split3_part(v, pl);
             }
             p.w2gx[i] = h;

@@ -108,10 +108,10 @@ __device__ __forceinline__ f32x16 mfma6(const u32x4 (&a)[3], const u32x4 (&b)[3]
     return mfma_bf16(a[0], b[0], c);
 }
 
-// ---- weight chunks for the split-bf16 linears: one 32-k step of up to 144
-// rows as three bf16 planes [rows][WC_KS] (k 32..39 zero), packed on the host
-// WC_CHUNK elements apart. A block copies chunk c + 1 into one of two LDS
-// buffers while its waves multiply chunk c out of the other.
+// ---- weight chunks for the split-bf16 linears: one 32-k step of up to 192
+// rows as three bf16 planes [rows][32] with swizzled k-groups (ws_mma), packed
+// on the host WC_CHUNK elements apart. A block copies chunk c + 1 into one of
+// two LDS buffers while its waves multiply chunk c out of the other.
 
 // The NL loads (1 KB each) of one chunk into an LDS buffer, NL / WAVES from
 // every wave: wave w issues loads w, w + WAVES, ...; lane l of a load writes
@@ -133,32 +133,8 @@ __device__ __forceinline__ void wc_issue(unsigned short* dst, const unsigned sho
     }
 }
 
-// acc[mt][nt] += W[rows 16 nt .. +15] . xb[mt] for one chunk of a plane
-// stride PLANE (= rows * WC_KS): the three planes of tile nt + 1 are read
-// while tile nt's 12 MFMAs run (the barriers keep the scheduler from hoisting
-// every tile's reads, which costs more registers than there are).
-template <int NT, int PLANE>
-__device__ __forceinline__ void wc_mma(const unsigned short* Ws, int lr, int lg, const u32x4 (&xb)[2][3],
-                                       f32x4 (&acc)[2][NT])
-{
-    const unsigned short* wr = Ws + lr * WC_KS + lg * 8;
-    u32x4 wa[2][3];
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * PLANE);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        __builtin_amdgcn_sched_barrier(0);
-        if (nt + 1 < NT) {
-#pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-                wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * WC_KS + pl * PLANE);
-        }
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
-    }
-}
-
-// wc_mma for a chunk in the swizzled layout of the weight-stationary kernels:
+// acc[mt][nt] += W[rows 16 nt .. +15] . xb[mt] for one chunk in the swizzled
+// layout of the weight-stationary kernels:
 // three planes [ROWS][32] (plane stride ROWS * 32), row r's four 16-byte
 // k-groups g stored at g ^ ((r >> 2) & 3), so that 16 consecutive rows read at
 // one k-group hit distinct banks without padding (a 192-row chunk fits
@@ -182,42 +158,6 @@ __device__ __forceinline__ void ws_mma(const unsigned short* Ws, int lr, int lg,
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
     }
-}
-
-// wc_mma with other work woven in: side(nt) runs in tile nt's segment, next
-// to its 12 MFMAs (VALU work issued there co-executes with them).
-template <int NT, int PLANE, typename F>
-__device__ __forceinline__ void wc_mma_with(const unsigned short* Ws, int lr, int lg, const u32x4 (&xb)[2][3],
-                                            f32x4 (&acc)[2][NT], F&& side)
-{
-    const unsigned short* wr = Ws + lr * WC_KS + lg * 8;
-    u32x4 wa[2][3];
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * PLANE);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        __builtin_amdgcn_sched_barrier(0);
-        if (nt + 1 < NT) {
-#pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-                wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * WC_KS + pl * PLANE);
-        }
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
-        side(nt);
-    }
-}
-
-// Pair j (0..7) of the split of a wave's rows pre (mt = j / 4, values
-// 2 (j % 4), +1 of its eight) into xb: eight calls make split_pre(pre, xb).
-__device__ __forceinline__ void split_pair(const f32x4 (&pre)[2][2], u32x4 (&xb)[2][3], int j)
-{
-    const int mt = j >> 2, q = j & 3;
-    unsigned p0, p1, p2;
-    split3_pk(pre[mt][q >> 1][(q & 1) * 2], pre[mt][q >> 1][(q & 1) * 2 + 1], p0, p1, p2);
-    xb[mt][0][q] = p0;
-    xb[mt][1][q] = p1;
-    xb[mt][2][q] = p2;
 }
 
 // A compile-time int carried by a value, for generic lambdas: decltype(x)::value.

@@ -43,7 +43,7 @@
 
 #define TX_WAVES 4
 #define TX_ROWS (TX_WAVES * 32)
-#define TX_BUF (36 * 512)  // an LDS chunk buffer: 36 loads cover 144 rows
+#define TX_BUF (36 * 512)  // an LDS chunk buffer: 36 loads cover 192 rows
 
 // Row statistics of a token over its C channels (C = 144: 36 per lane, 180:
 // 45; NT = ceil(C / 16) tiles of which the last holds C % 16 real channels in
@@ -136,7 +136,8 @@ __device__ __forceinline__ void tx_store_rows(const f32x4 (&acc)[2][(C + 15) / 1
 template <bool CAB>
 __device__ __forceinline__ void projx_body(const TailXArgs& p)
 {
-    constexpr int NCH = CAB ? 7 : 5, NL = 36;
+    constexpr int NCH = CAB ? 7 : 5, NL = 28;
+    static_assert(NL * 512 >= 3 * 144 * 32, "chunk loads");
     // the two chunk buffers as two LDS objects, so that the compiler sees that
     // reads of one need not wait for the copy into the other
     __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
@@ -190,7 +191,7 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
         u32x4 xb[2][3];
         split_pre(c < 5 ? y[c < 5 ? c : 0] : t1v, xb);
         if (CAB && c >= 4 && c + 1 < NCH) gather_t1(c - 4, t1v);
-        wc_mma<9, 144 * WC_KS>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
+        ws_mma<9, 144>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
     }
     tx_store_rows<144>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, p.xn);
 }
@@ -201,8 +202,8 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
 template <bool LN>
 __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
 {
-    constexpr int NL1 = 24, NL2 = 36;
-    static_assert(NL1 * 512 >= 3 * MX_HID * WC_KS, "fc1 chunk loads");
+    constexpr int NL1 = 20, NL2 = 28;
+    static_assert(NL1 * 512 >= 3 * MX_HID * 32 && NL2 * 512 >= 3 * 144 * 32, "chunk loads");
     __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
     __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
     __shared__ __attribute__((aligned(16))) float Cs[3 * 144];  // b2, next norm w, b (the epilogue's)
@@ -246,7 +247,7 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
             // 144 carries the 1 of b1's column), or k-step 0 for the next third
             if (ks < 4) yr.load_b(ks + 1, lg, pre);
             else if (q < 2) yr.load_b(0, lg, pre);
-            wc_mma<6, MX_HID * WC_KS>(PAR ? Ws1 : Ws0, lr, lg, xb, h);
+            ws_mma<6, MX_HID>(PAR ? Ws1 : Ws0, lr, lg, xb, h);
         };
 #pragma unroll 1
         for (int ks = 0; ks < 4; ks += 2) {
@@ -277,7 +278,7 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
                                     h[mt][2 * s + 1][2], h[mt][2 * s + 1][3]};
                 split3_x8(f, xb[mt]);
             }
-            wc_mma<9, 144 * WC_KS>(s & 1 ? Ws0 : Ws1, lr, lg, xb, acc2);
+            ws_mma<9, 144>(s & 1 ? Ws0 : Ws1, lr, lg, xb, acc2);
         }
     }
     tx_store_rows<144>(acc2, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
