@@ -3,6 +3,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 
 #include "kargs.h"
 #include "tile.h"
@@ -855,13 +856,10 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
                     (oca ? "" : " or " + std::to_string(pl.shift)) + ")");
     const char* name = nullptr;
     // The split-bf16 kernels (attnx.hip), one (window, head) item per block.
-    bool persistent = false;
     if (D == 24) {
         name = oca ? "hat_attnx_oca_d24" : "hat_attnx_sw_d24";
-        persistent = attnx_persistent(oca);
     } else if (D == 30) {
         name = oca ? "hat_attnx_oca_d30" : "hat_attnx_sw_d30";
-        persistent = attnx_persistent(oca);
     } else {
         throw Error("attention: head_dim " + std::to_string(D) + " has no kernel (24 and 30 do)");
     }
@@ -889,13 +887,7 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
         p.with_se = 1;
         p.se = *se;
     }
-    if (persistent) {
-        static const int cus = std::max(1, Runtime::get().cu_count());
-        const long items = (long)pl.nw() * heads;
-        launch(s, name, (unsigned)std::min<long>(items, cus), 1, 1, 512, p);
-    } else {
-        launch(s, name, (unsigned)pl.nw(), (unsigned)heads, 1, 512, p);
-    }
+    launch(s, name, (unsigned)pl.nw(), (unsigned)heads, 1, 512, p);
 }
 
 void run_ln(hipStream_t s, const float* x, float* y, const float* w, const float* b, long rows, int C)
@@ -1671,20 +1663,64 @@ struct DevBuf {
     DevBuf& operator=(const DevBuf&) = delete;
 };
 
+// Device copy of a host bf16 array (DevBuf's units are floats).
+static std::unique_ptr<DevBuf> dev_u16(const std::vector<unsigned short>& v)
+{
+    std::unique_ptr<DevBuf> d(new DevBuf((v.size() + 1) / 2));
+    Runtime::get().h2d(d->p, v.data(), v.size() * sizeof(unsigned short));
+    return d;
+}
+
+// A linear of the op entry points, packed as the backend packs it
+// (upload_linear): the FP32 rows, and for the shapes a split-bf16 kernel
+// takes (the qkv of 144 / 180 channels, the 144 / 180 projection) the split
+// weights too, so that an op runs the forward's kernels.
 struct OpLinear {
+    enum Split { kNone, kQkv, kProj };
     DevBuf w, b;
+    std::unique_ptr<DevBuf> x;
     DevLinear L;
-    OpLinear(const float* wt, const float* bias, int N, int K, std::vector<float> pk = {})
-        : w(1), b(bias, N)
+    OpLinear(const float* wt, const float* bias, int N, int K, Split sp = kNone) : w(1), b(bias, N)
     {
         L.N = N;
         L.K = K;
-        pk = pack_linear(wt, N, K, &L.Kp);
+        std::vector<float> pk = pack_linear(wt, N, K, &L.Kp);
         Runtime::get().free(w.p);
         w.p = (float*)Runtime::get().alloc(pk.size() * sizeof(float));
         Runtime::get().h2d(w.p, pk.data(), pk.size() * sizeof(float));
         L.w = w.p;
         L.b = b.p;
+        std::vector<unsigned short> xs;
+        if (sp == kQkv && ((N == 432 && K == 144) || (N == 540 && K == 180)))
+            xs = pack_linear_ws(wt, bias, N, K);
+        else if (sp == kProj && N == 144 && K == 144)
+            xs = pack_linear_x(wt, bias, N, K);
+        else if (sp == kProj && N == 180 && K == 180)
+            xs = pack_linear_x180(wt);
+        if (!xs.empty()) {
+            x = dev_u16(xs);
+            L.wx = (unsigned short*)x->p;
+        }
+    }
+};
+
+// An op's MLP pre-split for hat_mlpx (C = 144) or hat_mlpx180 (C = 180), as
+// upload_mlpx packs it; other shapes leave m.w null (the FP32 kernels).
+struct OpMlpX {
+    std::unique_ptr<DevBuf> buf;
+    DevMlpX m;
+    OpMlpX(const float* w1, const float* b1, const float* w2, int c, size_t hid)
+    {
+        std::vector<unsigned short> w;
+        if (c == 144 && hid == 288)
+            pack_mlp_x(w1, b1, w2, &w);
+        else if (c == 180 && hid == 360)
+            pack_mlp_x180(w1, b1, w2, &w);
+        else
+            return;
+        m.C = c;
+        buf = dev_u16(w);
+        m.w = (unsigned short*)buf->p;
     }
 };
 
@@ -1728,7 +1764,9 @@ void op_swmsa(const float* x, float* out, int hp, int wp, int c, int heads, int 
     rt.check(api.StreamCreate(&s), "hipStreamCreate");
     {
         DevBuf dx(x, T * c), dq(3 * T * c), dao(T * c), dout(T * c), dtab(table, 961 * (size_t)heads);
-        OpLinear qkv(qkv_w, qkv_b, 3 * c, c), proj(proj_w, proj_b, c, c);
+        // qkv as in the forward; the projection here has no residual, a form the
+        // forward never runs, so it stays on the FP32 store epilogue
+        OpLinear qkv(qkv_w, qkv_b, 3 * c, c, OpLinear::kQkv), proj(proj_w, proj_b, c, c);
         const GemmEpilogue none;
         auto run = [&]() {
             run_gemm(s, qkv.L, dx.p, c, (long)T, dq.p, 0, EPI_QKV, none, heads, D, 0.f);
@@ -1780,22 +1818,31 @@ void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int m
     {
         DevBuf dx(x, T * c), dwork(T * c), dxn(T * c), dq(3 * T * c), dao(T * c), dh(T * hid),
             dtab(table, 1521 * (size_t)heads), d1w(n1w, c), d1b(n1b, c), d2w(n2w, c), d2b(n2b, c);
-        OpLinear qkv(qkv_w, qkv_b, 3 * c, c), proj(proj_w, proj_b, c, c),
+        OpLinear qkv(qkv_w, qkv_b, 3 * c, c, OpLinear::kQkv), proj(proj_w, proj_b, c, c, OpLinear::kProj),
             fc1(fc1_w, fc1_b, (int)hid, c), fc2(fc2_w, fc2_b, c, (int)hid);
+        const OpMlpX mx(fc1_w, fc1_b, fc2_w, c, hid);
         const GemmEpilogue none;
         GemmEpilogue resid_ln;
         resid_ln.res = dx.p;
         resid_ln.xn = dxn.p;
         resid_ln.nw = d2w.p;
         resid_ln.nb = d2b.p;
-        // The backend's OCAB sequence: norm1, qkv, attention, proj + shortcut
-        // (whose epilogue also writes norm2), then the MLP + residual.
+        // The backend's OCAB sequence (GpuBackend::ocab): norm1, qkv, attention,
+        // proj + shortcut (which also writes norm2), then the MLP + residual.
         auto run = [&]() {
             run_ln(s, dx.p, dxn.p, d1w.p, d1b.p, (long)T, c);
             run_gemm(s, qkv.L, dxn.p, c, (long)T, dq.p, 0, EPI_QKV, none, heads, D, 0.f);
             run_attn(s, dq.p, dtab.p, dao.p, pl, heads, D, true, 0);
-            run_gemm(s, proj.L, dao.p, c, (long)T, dwork.p, c, EPI_RESID_LN, resid_ln, heads, D, 0.f);
-            run_mlp(s, fc1.L, fc2.L, dxn.p, (long)T, dwork.p, dwork.p, EPI_RESID, none, dh.p);
+            if (proj.L.wx && mx.m.w && c == 144) {
+                run_tailx(s, false, proj.L, mx.m, fc2.L.b, dao.p, dx.p, dwork.p, dxn.p, nullptr, nullptr, proj.L.b,
+                          d2w.p, d2b.p, nullptr, nullptr, hp, wp);
+            } else if (proj.L.wx && mx.m.w && c == 180) {
+                run_projx180(s, proj.L, dao.p, dx.p, dwork.p, dxn.p, d2w.p, d2b.p, nullptr, nullptr, 0.f, (long)T);
+                run_mlpx180(s, mx.m, fc2.L.b, dxn.p, dwork.p, nullptr, nullptr, nullptr, (long)T);
+            } else {
+                run_gemm(s, proj.L, dao.p, c, (long)T, dwork.p, c, EPI_RESID_LN, resid_ln, heads, D, 0.f);
+                run_mlp(s, fc1.L, fc2.L, dxn.p, (long)T, dwork.p, dwork.p, EPI_RESID, none, dh.p);
+            }
         };
         run();
         rt.check(api.StreamSynchronize(s), "ocab");

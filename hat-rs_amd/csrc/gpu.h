@@ -26,8 +26,9 @@ public:
 struct DevLinear {
     float* w = nullptr;  // [N][Kp]
     float* b = nullptr;  // [N]
-    // K = 144, N a multiple of 144: the same weights split into three bf16
-    // the split-bf16 weights (pack_linear_ws for qkv, pack_linear_x for proj)
+    // The same weights split into three bf16 parts for the split-bf16 kernels
+    // (qkv: pack_linear_ws; projection: pack_linear_x, pack_linear_x180), or
+    // null where the FP32 kernels run.
     unsigned short* wx = nullptr;
     int N = 0, K = 0, Kp = 0;
 };
@@ -45,8 +46,9 @@ struct DevCab {
     float* bb = nullptr;
 };
 
-// conv1 weight [6][144][3][3] -> [64][144]: row tap*6 + co holds w[co][:][tap],
-// rows 54..63 zero.
+// conv1 weight [6][144][3][3] -> 64 rows of 144 (row tap*6 + co holds
+// w[co][:][tap], rows 54..63 zero), each weight as three bf16 parts in
+// hat_cab_conv1's A-operand layout (CX_WPACK elements).
 std::vector<unsigned short> pack_cab_conv1(const float* w);
 
 // hat_mlpx's weights: the packed slices and b1 in fc1's row order.
@@ -80,8 +82,18 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
 // rows in the order that leaves its output in fc2's operand layout
 // (tailx.hip).
 void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
+// The C = 180 projection [180][180] for hat_projx180*: six chunks (one per
+// 32-k step, k 180..191 zero) of three bf16 planes [192][32] (rows 180..191
+// zero), k-groups swizzled as in pack_linear_ws, MX180_SLOT elements apart;
+// the bias stays FP32 (added in the epilogue).
 std::vector<unsigned short> pack_linear_x180(const float* w);
+// The C = 180 MLP (fc1 [360][180] + b1, fc2 [180][360]) for hat_mlpx180: per
+// part of MX180_HID hidden units six fc1 chunks (64 permuted rows, b1 as
+// their column k = 180) then two fc2 chunks (192 rows), 48 chunks in all.
 void pack_mlp_x180(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
+// Winograd U = G g G^T of a 3x3 conv [CO][CI][3][3] (formed in double), split
+// into three bf16 parts in the layout convwino.hip streams:
+// [32-channel chunk][point][16-channel tile][part][lane][8].
 std::vector<unsigned short> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);

@@ -165,8 +165,7 @@ struct SeArgs {
 // for OCA with head_dim 24, persistent blocks walking the (window, head) items
 // head-major (grid: at most one block per CU, gridDim.y = 1).
 constexpr bool attn_persistent(int D, bool oca) { return oca && D == 24; }
-// The split-bf16 kernels (attnx.hip): one item per block, SW and OCA.
-constexpr bool attnx_persistent(bool) { return false; }
+// The split-bf16 kernels (attnx.hip) run one item per block, SW and OCA.
 struct AttnArgs {
     const float* qkv;    // head-major [3][heads][T][D]
     const float* table;  // relative-position bias table [rows][heads]

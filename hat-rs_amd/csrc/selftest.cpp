@@ -199,7 +199,7 @@ int gpu_selftest(std::string* err)
                     for (const char* fam : {oca ? "hat_attn_oca_d" : "hat_attn_sw_d", oca ? "hat_attnx_oca_d" : "hat_attnx_sw_d"}) {
                         std::string k = std::string(fam) + std::to_string(D);
                         const bool xk = k.find("attnx") != std::string::npos;
-                        if (xk ? attnx_persistent(oca) : attn_persistent(D, oca))  // 3 blocks, so a block walks several items
+                        if (!xk && attn_persistent(D, oca))  // 3 blocks, so a block walks several items
                             launch(s, k.c_str(), 3, 1, 1, 512, p);
                         else
                             launch(s, k.c_str(), pl.nw(), heads, 1, 512, p);
