@@ -16,9 +16,12 @@
 // LDS for the whole launch, loaded once (C = 144: 144 columns, one of q, k,
 // v, 135 KB; C = 180: 96 columns holding three heads of 30, 108 KB, two
 // slices per q, k and v); after that its waves share nothing and meet at no
-// barrier. Each wave walks 32-token subtiles on its own: their rows in
-// registers, split per k-step, then 12 MFMAs per 16-column tile; the next
-// subtile's rows of a k-step are read as soon as that step has been split.
+// barrier. Each wave walks subtiles of 16 MT tokens on its own (C = 144: 32,
+// C = 180: 48, the faster in same-box timings): a k-step's rows are split in
+// registers, the next k-step's rows (at the last step the next subtile's
+// first) are read, and 6 MT MFMAs run per 16-column tile while the next
+// tile's weight fragments are read from LDS. Rows read one k-step ahead take
+// 8 MT registers a lane (a whole subtile ahead took 80 at C = 144).
 // The NS slices' blocks of a group sit on one XCD (blocks are dealt to the
 // 8 XCDs in turn) and walk the same subtiles in the same order, so that all
 // but one of a subtile's NS reads find its rows in that XCD's L2. Results
@@ -29,38 +32,38 @@
 
 #define GX_WAVES 8
 
-// This wave's 32 token rows of a [M][K] plane, 8 values at k = 32 ks + 8 lg
+// This wave's 16 MT token rows of a [M][K] plane, 8 values at k = 32 ks + 8 lg
 // per token, for the B operand: zeros past M and past k = K, with load_b the
 // 1 at k = K that multiplies the bias column (read from hat_one_row like the
 // rest, so that nothing waits for the loads here).
-template <int K>
+template <int K, int MT = 2>
 struct WcRows {
     static_assert(K % 4 == 0, "float4 units");
-    const float* rows[2];
-    bool alive[2];
+    const float* rows[MT];
+    bool alive[MT];
     __device__ __forceinline__ void init(const float* base, int mbase, int M, int lr)
     {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
             const int m = mbase + mt * 16 + lr;
             alive[mt] = m < M;
             rows[mt] = base + (size_t)(alive[mt] ? m : 0) * K;
         }
     }
     // zeros from k = K on (for a bias added elsewhere)
-    __device__ __forceinline__ void load(int ks, int lg, f32x4 (&dst)[2][2]) const
+    __device__ __forceinline__ void load(int ks, int lg, f32x4 (&dst)[MT][2]) const
     {
         const int k0 = ks * 32 + lg * 8;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int j = 0; j < 2; ++j) dst[mt][j] = load_or_zero(rows[mt] + k0 + 4 * j, alive[mt] && k0 + 4 * j < K);
     }
-    __device__ __forceinline__ void load_b(int ks, int lg, f32x4 (&dst)[2][2]) const
+    __device__ __forceinline__ void load_b(int ks, int lg, f32x4 (&dst)[MT][2]) const
     {
         const int k0 = ks * 32 + lg * 8;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int kq = k0 + 4 * j;
@@ -69,10 +72,11 @@ struct WcRows {
     }
 };
 
-__device__ __forceinline__ void split_pre(const f32x4 (&pre)[2][2], u32x4 (&xb)[2][3])
+template <int MT>
+__device__ __forceinline__ void split_pre(const f32x4 (&pre)[MT][2], u32x4 (&xb)[MT][3])
 {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
         const float f[8] = {pre[mt][0][0], pre[mt][0][1], pre[mt][0][2], pre[mt][0][3],
                             pre[mt][1][0], pre[mt][1][1], pre[mt][1][2], pre[mt][1][3]};
         split3_x8(f, xb[mt]);
@@ -80,8 +84,10 @@ __device__ __forceinline__ void split_pre(const f32x4 (&pre)[2][2], u32x4 (&xb)[
 }
 
 // K: input width; NT: 16-column tiles per slice; NS: slices; HD: head_dim;
-// NH: heads per slice (HD * NH <= 16 NT columns are real, the rest zero).
-template <int K, int NT, int NS, int HD, int NH>
+// NH: heads per slice (HD * NH <= 16 NT columns are real, the rest zero); MT:
+// 16-token tiles per subtile (each weight fragment read from LDS feeds MT
+// tiles, so MT sets the LDS bytes per MFMA).
+template <int K, int NT, int NS, int HD, int NH, int MT>
 __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short* Wsl, float* Qs)
 {
     constexpr int KS = (K + 32) / 32;             // 32-k steps, the bias column included
@@ -89,6 +95,7 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
     constexpr int CHUNK = 3 * ROWS * 32;          // one k-step: three bf16 planes [ROWS][32]
     constexpr int NLOAD = KS * CHUNK / 512;       // 1 KB loads
     constexpr int QS_S = HD == 24 ? 48 : 96;      // staging row stride (floats)
+    constexpr int TOK = 16 * MT;                  // tokens per subtile
     static_assert(KS * CHUNK % 512 == 0, "whole loads");
     static_assert(HD * NH <= ROWS, "the heads fit the slice");
 
@@ -122,30 +129,36 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
     const unsigned short* wl = Wsl + lr * 32 + ((lg ^ ((lr >> 2) & 3)) * 8);
     float* out = p.out + (size_t)sl * NH * M * HD;  // the slice's first head
     float* Q = Qs + wave * 16 * QS_S;
-    const int nsub = (M + 31) / 32;
+    const int nsub = (M + TOK - 1) / TOK;
     const int stride = G * GX_WAVES;
     int sub = grp * GX_WAVES + wave;
     if (sub >= nsub) return;
-    WcRows<K> xr;
-    xr.init(p.a, sub * 32, M, lr);
-    f32x4 y[KS][2][2];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) xr.load_b(ks, lg, y[ks]);
+    WcRows<K, MT> xr;
+    xr.init(p.a, sub * TOK, M, lr);
+    f32x4 y[MT][2];  // the rows of the next k-step
+    xr.load_b(0, lg, y);
 #pragma unroll 1
     for (; sub < nsub; sub += stride) {
-        // the next subtile's rows, or (past the last) this one's again: the
-        // loads are issued either way, so that their count never depends on
-        // the path and the compiler's waits stay exact
-        xr.init(p.a, (sub + stride < nsub ? sub + stride : sub) * 32, M, lr);
-        f32x4 acc[2][NT];
+        f32x4 acc[MT][NT];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[0][nt] = acc[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            u32x4 xb[2][3];
-            split_pre(y[ks], xb);
-            xr.load_b(ks, lg, y[ks]);  // the next subtile's rows of this k-step
-            // weight fragments of tile nt + 1 read while tile nt's 12 MFMAs run
+            u32x4 xb[MT][3];
+            split_pre(y, xb);
+            if (ks + 1 < KS) {
+                xr.load_b(ks + 1, lg, y);
+            } else {
+                // the next subtile's first k-step, or (past the last) this
+                // one's again: the loads are issued either way, so that their
+                // count never depends on the path and the compiler's waits
+                // stay exact
+                xr.init(p.a, (sub + stride < nsub ? sub + stride : sub) * TOK, M, lr);
+                xr.load_b(0, lg, y);
+            }
+            // weight fragments of tile nt + 1 read while tile nt's 6 MT MFMAs run
             const unsigned short* wr = wl + ks * CHUNK;
             u32x4 wa[2][3];
 #pragma unroll
@@ -159,12 +172,12 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
                         wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * 32 + pl * ROWS * 32);
                 }
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
+                for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
             }
         }
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const int mb = sub * 32 + mt * 16;
+        for (int mt = 0; mt < MT; ++mt) {
+            const int mb = sub * TOK + mt * 16;
             const int mrows = M - mb;
             if constexpr (HD == 24) {
                 // Two heads at a time go through the wave's LDS region and leave
@@ -218,12 +231,12 @@ extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv(Gem
 {
     __shared__ __attribute__((aligned(16))) unsigned short Wsl[5 * WS_CHUNK];  // the slice
     __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * 48];    // per-wave staging
-    gemmx_qkv_body<144, 9, 3, 24, 6>(p, Wsl, Qs);
+    gemmx_qkv_body<144, 9, 3, 24, 6, 2>(p, Wsl, Qs);
 }
 
 extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv180(GemmArgs p)
 {
     __shared__ __attribute__((aligned(16))) unsigned short Wsl[6 * WS_CHUNK180];  // the slice
     __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * 96];        // per-wave staging
-    gemmx_qkv_body<180, 6, 6, 30, 3>(p, Wsl, Qs);
+    gemmx_qkv_body<180, 6, 6, 30, 3, 3>(p, Wsl, Qs);
 }

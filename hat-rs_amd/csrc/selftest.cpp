@@ -298,8 +298,9 @@ int gpu_selftest(std::string* err)
                 note(k + " C " + std::to_string(C) + " M " + std::to_string(M) + " K " + std::to_string(K));
                 if (ws && epi == EPI_QKV) {
                     // the split-bf16 form on the same inputs (the last
-                    // 32-row subtile partial), one group: its waves walk all 19
-                    // subtiles
+                    // subtile partial: 600 rows are 18.75 subtiles of 32 at
+                    // C = 144, 12.5 of 48 at C = 180), one group: its 8 waves
+                    // walk them all
                     std::vector<unsigned short> px = pack_linear_ws(w.data(), b.data(), N, K);
                     Dev dwx(std::vector<float>((px.size() + 1) / 2)), dout2((size_t)M * N);
                     rt.h2d(dwx.p, px.data(), px.size() * sizeof(unsigned short));
