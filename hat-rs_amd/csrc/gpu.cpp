@@ -563,8 +563,9 @@ void run_hab_tail(hipStream_t s, const DevLinear& proj, const DevLinear& fc1, co
 }
 
 // The tail on split-bf16 (tailx.hip): x' = res + a . Wp^T (+ CAB: the gated
-// conv2 of t1) + bias, xn = norm2(x') [hat_projx(_cab)]; out = x' + MLP(xn)
-// (+ with nw: xn = norm_next(out)) [hat_mlpx(_ln)]. out may alias res.
+// conv2 of t1) + bias [hat_projx(_cab)]; out = x' + MLP(norm2(x')), norm2
+// formed in the MLP kernel (+ with nw: xn = norm_next(out)) [hat_mlpx(_ln)].
+// out may alias res.
 void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& mlp, const float* b2, const float* a,
                const float* res, float* out, float* xn, const float* t1, const unsigned short* w2gx, const float* bias,
                const float* n2w, const float* n2b, const float* nw, const float* nb, int H, int W)
@@ -574,11 +575,13 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
     const long M = (long)H * W;
     if (M > 0x7fffffffL) throw Error("tailx: too many rows");
     const unsigned g = (unsigned)wx_tiles((int)M);  // a block per 128-token tile
+    // the projection writes x' only: the MLP forms norm2(x') from the x'
+    // rows it reads
     TailXArgs p{};
     p.a = a;
     p.res = res;
     p.out = out;
-    p.xn = xn;
+    p.xn = nullptr;
     p.w = proj.wx;
     p.bias = bias;
     p.w2gx = w2gx;
@@ -591,7 +594,7 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
     p.eps = 1e-5f;
     launch(s, cab ? "hat_projx_cab" : "hat_projx", g, 1, 1, WX_THREADS, p);
     TailXArgs q{};
-    q.a = xn;
+    q.a = out;
     q.res = out;
     q.out = out;
     q.xn = nw ? xn : nullptr;
@@ -599,6 +602,8 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
     q.b2 = b2;
     q.nw = nw;
     q.nb = nb;
+    q.inw = n2w;
+    q.inb = n2b;
     q.M = (int)M;
     q.H = H;
     q.W = W;

@@ -276,10 +276,11 @@ constexpr int wx_tiles(int M) { return (M + WX_ROWS - 1) / WX_ROWS; }
 constexpr int gemmx_qkv_groups(int cus, int ns) { return cus >= 8 * ns ? cus / (8 * ns) * 8 : 1; }
 
 struct TailXArgs {
-    const float* a;            // projx: attention output; mlpx: LN2(x') rows
+    const float* a;            // projx: attention output; mlpx (C = 144): x' rows, normed in the kernel by
+                               // (inw, inb); mlpx180: LN2(x') rows
     const float* res;          // projx: block input; mlpx: x'
     float* out;                // [M][144] (may alias res)
-    float* xn;                 // projx: LN2(x'); mlpx (LN): the next norm1 (may alias a)
+    float* xn;                 // projx: LN2(x') when non-null; mlpx (LN): the next norm1 (may alias a)
     const unsigned short* w;   // weight chunks (projx: 5, mlpx: 24)
     const float* bias;         // projx: bias2 or the projection bias (mlpx: b1 is in its chunks)
     const float* b2;           // mlpx: fc2 bias
@@ -294,6 +295,9 @@ struct TailXArgs {
     const float* aux;
     const float* gate;
     float cscale;
+    // hat_mlpx(_ln): norm2's weight and bias, applied to the x' rows of a
+    const float* inw;
+    const float* inb;
 };
 
 struct LnArgs {

@@ -196,9 +196,14 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
     tx_store_rows<144>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, p.xn);
 }
 
-// out = x' + fc2(gelu(fc1(y))) + b2 (+ xn = LN_next(out)); y = p.a, x' = p.res.
-// p.w: 24 chunks (per third: five of fc1's 96 permuted rows, b1 as their
-// column k = 144, then three of fc2 on those units).
+// out = x' + fc2(gelu(fc1(y))) + b2 (+ xn = LN_next(out)); x' = p.res = p.a and
+// y = LN2(x') by (p.inw, p.inb), formed from the x' rows as they are read for
+// each third (so that the projection kernel need not write LN2(x') and this
+// one read it three times: the row statistics come from the residual rows,
+// which hold x' in the layout tx_row_stats takes, and the arithmetic is the
+// projection epilogue's, so y is the same to the bit). p.w: 24 chunks (per
+// third: five of fc1's 96 permuted rows, b1 as their column k = 144, then
+// three of fc2 on those units).
 template <bool LN>
 __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
 {
@@ -207,6 +212,9 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
     __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
     __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
     __shared__ __attribute__((aligned(16))) float Cs[3 * 144];  // b2, next norm w, b (the epilogue's)
+    // norm2's w and b over the 160 k of fc1's input: at k = 144 w 0 and b 1
+    // (the 1 that multiplies b1's column comes out as 1), past it zeros
+    __shared__ __attribute__((aligned(16))) float Cn[2 * 160];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
     const int lr = lane & 15, lg = lane >> 4;
@@ -220,9 +228,29 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
         else v = LN ? p.nb[i - 288] : 0.0f;
         Cs[i] = v;
     }
+    for (int i = tid; i < 2 * 160; i += TX_WAVES * 64) {
+        const int k = i < 160 ? i : i - 160;
+        Cn[i] = k < 144 ? (i < 160 ? p.inw[k] : p.inb[k]) : (i >= 160 && k == 144 ? 1.0f : 0.0f);
+    }
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
     f32x4 acc2[2][9];
     tx_load_res<144>(p.res, mbase, M, lr, lg, acc2);
+    // norm2's statistics of the wave's tokens, from x' as the residual holds it
+    float2 st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) st[mt] = tx_row_stats<144>(acc2[mt], lg, p.eps);
+    // y = LN2(x') for k-step ks of the rows in pre, in place
+    auto norm_pre = [&](int ks, f32x4 (&pre)[2][2]) {
+        const float* wk = Cn + ks * 32 + lg * 8;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const f32x4 w4 = *(const f32x4*)(wk + 4 * j), b4 = *(const f32x4*)(wk + 160 + 4 * j);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pre[mt][j][i] = (pre[mt][j][i] - st[mt].x) * st[mt].y * w4[i] + b4[i];
+        }
+    };
     WcRows<144> yr;
     yr.init(p.a, mbase, M, lr);
     f32x4 pre[2][2];
@@ -242,6 +270,7 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
             if (ks < 4) wc_issue<NL1, TX_WAVES>(PAR ? Ws0 : Ws1, wq + (size_t)(ks + 1) * WC_CHUNK, wave, lane);
             else wc_issue<NL2, TX_WAVES>(Ws1, wq + (size_t)5 * WC_CHUNK, wave, lane);
             u32x4 xb[2][3];
+            norm_pre(ks, pre);
             split_pre(pre, xb);
             // the rows of the next fc1 chunk: this third's next k-step (k =
             // 144 carries the 1 of b1's column), or k-step 0 for the next third

@@ -732,7 +732,9 @@ int gpu_selftest(std::string* err)
                 check_close("hat_projx_cab layernorm", dxn_x.get(), wxn, 5e-5);
                 note("hat_projx_cab (split-bf16 proj + folded conv2 + norm2) vs double");
                 TailXArgs xm{};
-                xm.a = dxn_x.p;
+                xm.a = dout_x.p;  // x': the kernel forms norm2 from it
+                xm.inw = dnw.p;
+                xm.inb = dnb.p;
                 xm.res = dout_x.p;
                 xm.out = dout_x.p;
                 xm.xn = dxn_x.p;
@@ -762,7 +764,7 @@ int gpu_selftest(std::string* err)
                 xo.M = Mo;
                 launch(s, "hat_projx", (unsigned)wx_tiles(Mo), 1, 1, WX_THREADS, xo);
                 TailXArgs xo2 = xm;
-                xo2.a = dxn_ox.p;
+                xo2.a = dout_ox.p;
                 xo2.res = dout_ox.p;
                 xo2.out = dout_ox.p;
                 xo2.xn = nullptr;
