@@ -1202,7 +1202,7 @@ void GpuBackend::gemm(const DevLinear& L, const float* a, int lda, long M, float
 
 // x = x + fc2(gelu(fc1(a_.xn))), in place; with a norm also a_.xn = norm(x).
 // The split-bf16 C = 180 projection tail: out = res + ao . Wp^T + bias (with
-// aux: + aux * gate * cscale), xn = LN2(out) by (nw, nb).
+// aux: + aux * gate * cscale), and with xn: xn = LN2(out) by (nw, nb).
 void run_projx180(hipStream_t s, const DevLinear& proj, const float* ao, const float* res, float* out, float* xn,
                   const float* nw, const float* nb, const float* aux, const float* gate, float cscale, long M)
 {
@@ -1225,14 +1225,17 @@ void run_projx180(hipStream_t s, const DevLinear& proj, const float* ao, const f
     launch(s, aux ? "hat_projx180_hab" : "hat_projx180", (unsigned)wx_tiles((int)M), 1, 1, WX_THREADS, q);
 }
 
-// The split-bf16 C = 180 MLP: out = x + fc2(gelu(fc1(xn))) + b2 (+ xn = LN(out)).
-void run_mlpx180(hipStream_t s, const DevMlpX& m, const float* b2, const float* xn_in, float* x, float* xn_out,
-                 const float* nw, const float* nb, long M)
+// The split-bf16 C = 180 MLP: x = x + fc2(gelu(fc1(norm2(x)))) + b2 (+ xn =
+// LN(x)), norm2 by (n2w, n2b) formed in the kernel from the x rows.
+void run_mlpx180(hipStream_t s, const DevMlpX& m, const float* b2, const float* n2w, const float* n2b, float* x,
+                 float* xn_out, const float* nw, const float* nb, long M)
 {
     if (m.C != 180) throw Error("mlpx180: needs the pre-split C = 180 MLP");
     if (M > 0x7fffffffL) throw Error("mlpx180: too many rows");
     TailXArgs q{};
-    q.a = xn_in;
+    q.a = x;
+    q.inw = n2w;
+    q.inb = n2b;
     q.res = x;
     q.out = x;
     q.xn = nw ? xn_out : nullptr;
@@ -1247,15 +1250,6 @@ void run_mlpx180(hipStream_t s, const DevMlpX& m, const float* b2, const float* 
 
 void GpuBackend::mlp(const std::string& prefix, float* x, int epi, const std::string& norm)
 {
-    auto mx = mlpx_.find(prefix);
-    if (mx != mlpx_.end() && mx->second.C == 180) {
-        // a_.xn is read (fc1's input) and, with a norm, rewritten: every block
-        // reads its own rows before it writes them
-        run_mlpx180(stream_, mx->second, lin_.at(prefix + ".fc2").b, a_.xn, x, a_.xn,
-                    norm.empty() ? nullptr : raw_.at(norm + ".weight"), norm.empty() ? nullptr : raw_.at(norm + ".bias"),
-                    plan_.tokens());
-        return;
-    }
     GemmEpilogue e;
     if (!norm.empty()) {
         e.xn = a_.xn;
@@ -1328,11 +1322,19 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
     gemm(lin_.at(p + ".attn.qkv"), a_.xn, C, T, a_.qkv, 0, EPI_QKV);
     attention(p + ".attn.relative_position_bias_table", false, block % 2 == 1 ? plan_.shift : 0, nullptr, &se);
     const DevLinear& proj = lin_.at(p + ".attn.proj");
-    if (proj.wx && C == 180)
-        run_projx180(stream_, proj, a_.ao, x_in, x_out, a_.xn, raw_.at(p + ".norm2.weight"),
+    auto mx = mlpx_.find(p + ".mlp");
+    if (proj.wx && C == 180 && mx != mlpx_.end() && mx->second.C == 180) {
+        // split-bf16: projection + gated conv branch + shortcut (x' only), then
+        // the MLP, which forms norm2(x') from the x' rows, + residual + next norm
+        run_projx180(stream_, proj, a_.ao, x_in, x_out, nullptr, raw_.at(p + ".norm2.weight"),
                      raw_.at(p + ".norm2.bias"), a_.t2, a_.gate, wt_.conv_scale, T);
-    else
-        gemm(proj, a_.ao, C, T, x_out, C, EPI_HAB_LN, x_in, a_.t2, a_.gate, a_.xn, p + ".norm2");
+        run_mlpx180(stream_, mx->second, lin_.at(p + ".mlp.fc2").b, raw_.at(p + ".norm2.weight"),
+                    raw_.at(p + ".norm2.bias"), x_out, a_.xn,
+                    next_norm.empty() ? nullptr : raw_.at(next_norm + ".weight"),
+                    next_norm.empty() ? nullptr : raw_.at(next_norm + ".bias"), T);
+        return;
+    }
+    gemm(proj, a_.ao, C, T, x_out, C, EPI_HAB_LN, x_in, a_.t2, a_.gate, a_.xn, p + ".norm2");
     mlp(p + ".mlp", x_out, EPI_RESID_LN, next_norm);
 }
 
@@ -1361,11 +1363,14 @@ void GpuBackend::ocab(int stage, float* x)
                      plan_.hp, plan_.wp);
         return;
     }
-    if (proj.wx && C == 180)
-        run_projx180(stream_, proj, a_.ao, x, x, a_.xn, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
+    if (proj.wx && C == 180 && mx != mlpx_.end() && mx->second.C == 180) {
+        run_projx180(stream_, proj, a_.ao, x, x, nullptr, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
                      nullptr, nullptr, 0.0f, T);
-    else
-        gemm(proj, a_.ao, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, a_.xn, p + ".norm2");
+        run_mlpx180(stream_, mx->second, fc2.b, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"), x, nullptr,
+                    nullptr, nullptr, T);
+        return;
+    }
+    gemm(proj, a_.ao, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, a_.xn, p + ".norm2");
     mlp(p + ".mlp", x, EPI_RESID, "");
 }
 
@@ -1842,8 +1847,8 @@ void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int m
                 run_tailx(s, false, proj.L, mx.m, fc2.L.b, dao.p, dx.p, dwork.p, dxn.p, nullptr, nullptr, proj.L.b,
                           d2w.p, d2b.p, nullptr, nullptr, hp, wp);
             } else if (proj.L.wx && mx.m.w && c == 180) {
-                run_projx180(s, proj.L, dao.p, dx.p, dwork.p, dxn.p, d2w.p, d2b.p, nullptr, nullptr, 0.f, (long)T);
-                run_mlpx180(s, mx.m, fc2.L.b, dxn.p, dwork.p, nullptr, nullptr, nullptr, (long)T);
+                run_projx180(s, proj.L, dao.p, dx.p, dwork.p, nullptr, d2w.p, d2b.p, nullptr, nullptr, 0.f, (long)T);
+                run_mlpx180(s, mx.m, fc2.L.b, d2w.p, d2b.p, dwork.p, nullptr, nullptr, nullptr, (long)T);
             } else {
                 run_gemm(s, proj.L, dao.p, c, (long)T, dwork.p, c, EPI_RESID_LN, resid_ln, heads, D, 0.f);
                 run_mlp(s, fc1.L, fc2.L, dxn.p, (long)T, dwork.p, dwork.p, EPI_RESID, none, dh.p);

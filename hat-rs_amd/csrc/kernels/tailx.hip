@@ -151,7 +151,7 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
     auto chunk = [&](int c) { return c < 5 ? p.w + (size_t)c * WC_CHUNK : p.w2gx + (size_t)(c - 5) * WC_CHUNK; };
     wc_issue<NL, TX_WAVES>(Ws0, chunk(0), wave, lane);
     for (int i = tid; i < 3 * 144; i += TX_WAVES * 64)
-        Cs[i] = i < 144 ? p.bias[i] : (i < 288 ? p.nw[i - 144] : p.nb[i - 288]);
+        Cs[i] = i < 144 ? p.bias[i] : (!p.xn ? 0.0f : i < 288 ? p.nw[i - 144] : p.nb[i - 288]);  // norm2's when written
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
     f32x4 acc[2][9];
     tx_load_res<144>(p.res, mbase, M, lr, lg, acc);
@@ -334,7 +334,11 @@ __device__ __forceinline__ void projx180_body(const TailXArgs& p)
     for (int i = tid; i < 4 * 16 * NT; i += TX_WAVES * 64) {
         const int part = i / (16 * NT), c = i - part * 16 * NT;
         float v = 0.0f;
-        if (c < C) v = part == 0 ? p.bias[c] : part == 1 ? p.nw[c] : part == 2 ? p.nb[c] : (HAB ? p.gate[c] * p.cscale : 0.0f);
+        // the norm's constants only when norm2 is written here (xn given)
+        if (c < C)
+            v = part == 0 ? p.bias[c]
+                          : part == 1 ? (p.xn ? p.nw[c] : 0.0f)
+                                      : part == 2 ? (p.xn ? p.nb[c] : 0.0f) : (HAB ? p.gate[c] * p.cscale : 0.0f);
         Cs[i] = v;
     }
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
@@ -374,7 +378,8 @@ __device__ __forceinline__ void projx180_body(const TailXArgs& p)
 }
 
 // The C = 180 MLP: out = x' + fc2(gelu(fc1(y))) + b2 (+ xn = LN_next(out)),
-// y = p.a [M][180], x' = p.res. The hidden layer in six parts of 64 units (the
+// x' = p.res = p.a [M][180] and y = LN2(x') by (p.inw, p.inb), formed from the
+// x' rows as hat_mlpx forms it. The hidden layer in six parts of 64 units (the
 // last 40 real), so that fc2's 192 accumulator columns (96 registers), fc1's
 // output of a part (32) and the operands fit a lane. p.w: 48 chunks
 // MX180_SLOT apart, per part six fc1 k-steps (64 permuted rows, b1 at k = 180)
@@ -387,6 +392,9 @@ __device__ __forceinline__ void mlpx180_body(const TailXArgs& p)
     __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
     __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
     __shared__ __attribute__((aligned(16))) float Cs[3 * 16 * NT];  // b2, next norm w, b (zero past 180)
+    // norm2's w and b over the 192 k of fc1's input: at k = 180 w 0 and b 1
+    // (the 1 that multiplies b1's column), past it zeros
+    __shared__ __attribute__((aligned(16))) float Cn[2 * 192];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
     const int lr = lane & 15, lg = lane >> 4;
@@ -399,9 +407,29 @@ __device__ __forceinline__ void mlpx180_body(const TailXArgs& p)
         if (c < C) v = part == 0 ? p.b2[c] : (LN ? (part == 1 ? p.nw[c] : p.nb[c]) : 0.0f);
         Cs[i] = v;
     }
+    for (int i = tid; i < 2 * 192; i += TX_WAVES * 64) {
+        const int k = i < 192 ? i : i - 192;
+        Cn[i] = k < C ? (i < 192 ? p.inw[k] : p.inb[k]) : (i >= 192 && k == C ? 1.0f : 0.0f);
+    }
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
     f32x4 acc2[2][NT];
     tx_load_res<C>(p.res, mbase, M, lr, lg, acc2);
+    // norm2's statistics of the wave's tokens, from x' as the residual holds it
+    float2 st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) st[mt] = tx_row_stats<C>(acc2[mt], lg, p.eps);
+    // y = LN2(x') for k-step ks of the rows in pre, in place
+    auto norm_pre = [&](int ks, f32x4 (&pre)[2][2]) {
+        const float* wk = Cn + ks * 32 + lg * 8;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const f32x4 w4 = *(const f32x4*)(wk + 4 * j), b4 = *(const f32x4*)(wk + 192 + 4 * j);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pre[mt][j][i] = (pre[mt][j][i] - st[mt].x) * st[mt].y * w4[i] + b4[i];
+        }
+    };
     WcRows<C> yr;
     yr.init(p.a, mbase, M, lr);
     f32x4 pre[2][2];
@@ -421,6 +449,7 @@ __device__ __forceinline__ void mlpx180_body(const TailXArgs& p)
             if (ks < 5) wc_issue<NL1, TX_WAVES>(PAR ? Ws0 : Ws1, wq + (size_t)(ks + 1) * MX180_SLOT, wave, lane);
             else wc_issue<NL2, TX_WAVES>(Ws0, wq + (size_t)6 * MX180_SLOT, wave, lane);
             u32x4 xb[2][3];
+            norm_pre(ks, pre);
             split_pre(pre, xb);
             // the rows of the next fc1 chunk: this part's next k-step (k =
             // 180 carries the 1 of b1's column), or k-step 0 for the next part

@@ -377,16 +377,20 @@ int gpu_selftest(std::string* err)
             note(std::string(k) + " C " + std::to_string(C) + " M 600 (in place)");
             if (C == 180) {
                 // the split-bf16 form, in place the same way, 5 tiles of 128
-                // (the last partial)
+                // (the last partial): its fc1 input is norm2 (n2w, n2b) of the
+                // residual rows, formed in the kernel; against double
+                std::vector<float> n2w = rng.vec(C, 1.0f), n2b = rng.vec(C, 0.1f);
                 std::vector<unsigned short> mw;
                 pack_mlp_x180(w1.data(), b1.data(), w2.data(), &mw);
-                Dev da2(a), dx2(res), dmw((mw.size() + 1) / 2);
+                Dev dx2(res), dxn2((size_t)M * C), dn2w(n2w), dn2b(n2b), dmw((mw.size() + 1) / 2);
                 Runtime::get().h2d(dmw.p, mw.data(), mw.size() * sizeof(unsigned short));
                 TailXArgs q{};
-                q.a = da2.p;
+                q.a = dx2.p;
+                q.inw = dn2w.p;
+                q.inb = dn2b.p;
                 q.res = dx2.p;
                 q.out = dx2.p;
-                q.xn = epi == EPI_RESID_LN ? da2.p : nullptr;
+                q.xn = epi == EPI_RESID_LN ? dxn2.p : nullptr;
                 q.w = (const unsigned short*)dmw.p;
                 q.b2 = db2.p;
                 q.nw = dnw.p;
@@ -395,9 +399,36 @@ int gpu_selftest(std::string* err)
                 q.eps = 1e-5f;
                 const char* kx = epi == EPI_RESID_LN ? "hat_mlpx180_ln" : "hat_mlpx180";
                 launch(s, kx, (unsigned)wx_tiles(M), 1, 1, WX_THREADS, q);
-                check_close(kx, dx2.get(), want, 5e-5);
-                if (epi == EPI_RESID_LN) check_close(std::string(kx) + " layernorm", da2.get(), wxn, 5e-5);
-                note(std::string(kx) + " C 180 M 600 (split-bf16, in place)");
+                std::vector<double> want2((size_t)M * C), wxn2((size_t)M * C), y(C);
+                for (int m = 0; m < M; ++m) {
+                    const float* r = &res[(size_t)m * C];
+                    double mu = 0, va = 0;
+                    for (int c = 0; c < C; ++c) mu += r[c];
+                    mu /= C;
+                    for (int c = 0; c < C; ++c) va += (r[c] - mu) * (r[c] - mu);
+                    va /= C;
+                    for (int c = 0; c < C; ++c) y[c] = (r[c] - mu) / std::sqrt(va + 1e-5) * n2w[c] + n2b[c];
+                    for (int j = 0; j < H; ++j) {
+                        double v = b1[j];
+                        for (int c = 0; c < C; ++c) v += y[c] * w1[(size_t)j * C + c];
+                        hid[j] = gelu_d(v);
+                    }
+                    double mean = 0, var = 0;
+                    for (int n = 0; n < C; ++n) {
+                        double v = b2[n];
+                        for (int j = 0; j < H; ++j) v += hid[j] * w2[(size_t)n * H + j];
+                        want2[(size_t)m * C + n] = r[n] + v;
+                        mean += want2[(size_t)m * C + n];
+                    }
+                    mean /= C;
+                    for (int n = 0; n < C; ++n) var += (want2[(size_t)m * C + n] - mean) * (want2[(size_t)m * C + n] - mean);
+                    var /= C;
+                    for (int n = 0; n < C; ++n)
+                        wxn2[(size_t)m * C + n] = (want2[(size_t)m * C + n] - mean) / std::sqrt(var + 1e-5) * nw[n] + nb[n];
+                }
+                check_close(kx, dx2.get(), want2, 5e-5);
+                if (epi == EPI_RESID_LN) check_close(std::string(kx) + " layernorm", dxn2.get(), wxn2, 5e-5);
+                note(std::string(kx) + " C 180 M 600 (split-bf16 with norm2 in the kernel, in place) vs double");
             }
         }
 
