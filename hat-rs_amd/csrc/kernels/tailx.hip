@@ -1,12 +1,15 @@
-// The second half of a HAB (and of an OCAB), C = 144, on split-bf16 MFMA, as
-// two kernels (hat_arch.py HAB.forward / OCAB.forward; cpu.rs hab 1090-1166,
-// ocab 983-1055; the reference GPU graph's proj, CAB conv2 and channel scale,
-// adds, norm2, fc1 + GELU + fc2 and the next norm1, src/gpu.rs:469-588):
+// The second half of a HAB (and of an OCAB), C = 144 and 180, on split-bf16
+// MFMA, as two kernels (hat_arch.py HAB.forward / OCAB.forward; cpu.rs hab
+// 1090-1166, ocab 983-1055; the reference GPU graph's proj, CAB conv2 and
+// channel scale, adds, norm2, fc1 + GELU + fc2 and the next norm1,
+// src/gpu.rs:469-588):
 //
 //   hat_projx_cab / hat_projx:  x' = x + ao . Wp^T (+ nb(t1) . W2g^T) + bias
-//                               out = x',  xn = LN2(x')
-//   hat_mlpx_ln / hat_mlpx:     out = x' + fc2(gelu(fc1(LN2(x')))) + b2
-//                               (xn = LN_next(out))
+//                               out = x' (and xn = LN2(x') when asked)
+//   hat_mlpx_ln / hat_mlpx:     out = x' + fc2(gelu(fc1(LN2(x')))) + b2, LN2
+//                               formed from the x' rows (xn = LN_next(out))
+//   hat_projx180(_hab), hat_mlpx180(_ln): the same at C = 180 (the HAB form
+//                               adds the unfolded CAB's gated conv2 output)
 //
 // ao is the attention output, nb(t1) the 3x3 neighbourhood of the CAB's conv1
 // output (k = tap*6 + ci, 54 values) and W2g / bias the gate-scaled conv2
@@ -29,15 +32,15 @@
 // The MLP walks the hidden layer in thirds of 96 units, so that fc1's output
 // of a third (48 registers) and fc2's accumulators (72) fit a lane next to
 // the operands: per third five fc1 chunks, then three fc2 chunks on those
-// units; its input rows are read one chunk ahead, once per third (the second
-// and third reads hit the caches). fc1's output stays in registers and is
+// units; its input rows are read one chunk ahead, once per third, and normed
+// as they arrive. fc1's output stays in registers and is
 // fc2's B operand: fc1's rows are permuted on the host so that output tile t,
 // row 4g + r (lane group g, register r) is unit 32(t/2) + 8g + 4(t%2) + r of
 // the third; fc2's 32-k step s then finds units 32s + 8g .. +7 in tiles 2s
 // and 2s+1 of lane group g, its weights in natural order.
 //
-// Split in two at x' (written, and LN2(x') with it, then read back by the
-// MLP): one kernel would hold x', LN2(x') and the MLP's registers at once.
+// Split in two at x' (written, then read back by the MLP): one kernel would
+// hold x', LN2(x') and the MLP's registers at once.
 //
 // Included after gemmx.hip (WcRows, split_pre).
 
