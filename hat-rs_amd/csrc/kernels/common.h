@@ -115,29 +115,22 @@ __device__ __forceinline__ f32x16 mfma6(const u32x4 (&a)[3], const u32x4 (&b)[3]
 
 // The NL loads (1 KB each) of one chunk into an LDS buffer, NL / WAVES from
 // every wave: wave w issues loads w, w + WAVES, ...; lane l of a load writes
-// 16 bytes at the load's LDS base + 16 l. UNROLL: the loads as straight-line
-// code; as a loop, the per-load scalar bookkeeping (M0, the address, the
-// counter and the branch) cost the C = 144 tails 3-4% (same-box timings),
-// while the C = 180 tails (up to nine loads a wave) measured no better
-// unrolled. The compiler's waits stay where they were either way: the callers
-// wait for the copies explicitly before reading a buffer.
-template <int NL, int WAVES, bool UNROLL = false>
+// 16 bytes at the load's LDS base + 16 l. Straight-line code: as a loop, the
+// per-load scalar bookkeeping (M0, the address, the counter and the branch)
+// cost the tails 1-4% (same-box timings). The compiler's waits stay where
+// they were: the callers wait for the copies explicitly before reading a
+// buffer.
+template <int NL, int WAVES>
 __device__ __forceinline__ void wc_issue(unsigned short* dst, const unsigned short* src, int wave, int lane)
 {
     static_assert(NL % WAVES == 0 && NL * 512 <= WC_CHUNK, "whole loads per wave, within a chunk");
     const unsigned loff = (unsigned)lane * 16;  // the lane's bytes within a load: one VGPR for every load
-    auto one = [&](int j) {
+#pragma unroll
+    for (int j = 0; j < NL / WAVES; ++j) {
         const int i = wave + j * WAVES;  // wave-uniform: the load's base goes in scalar registers
         const char* base = (const char*)src + (size_t)i * 1024;
         __builtin_amdgcn_global_load_lds((const void*)(base + loff),
                                          (__attribute__((address_space(3))) void*)(dst + i * 512), 16, 0, 0);
-    };
-    if constexpr (UNROLL) {
-#pragma unroll
-        for (int j = 0; j < NL / WAVES; ++j) one(j);
-    } else {
-#pragma unroll 1
-        for (int j = 0; j < NL / WAVES; ++j) one(j);
     }
 }
 

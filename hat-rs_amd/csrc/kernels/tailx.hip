@@ -152,7 +152,7 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
     const int M = p.M;
     if ((int)blockIdx.x * TX_ROWS >= M) return;  // whole block, before any barrier
     auto chunk = [&](int c) { return c < 5 ? p.w + (size_t)c * WC_CHUNK : p.w2gx + (size_t)(c - 5) * WC_CHUNK; };
-    wc_issue<NL, TX_WAVES, true>(Ws0, chunk(0), wave, lane);
+    wc_issue<NL, TX_WAVES>(Ws0, chunk(0), wave, lane);
     for (int i = tid; i < 3 * 144; i += TX_WAVES * 64)
         Cs[i] = i < 144 ? p.bias[i] : (!p.xn ? 0.0f : i < 288 ? p.nw[i - 144] : p.nb[i - 288]);  // norm2's when written
     const int mbase = blockIdx.x * TX_ROWS + wave * 32;
@@ -190,7 +190,7 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
     for (int c = 0; c < NCH; ++c) {
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk c (and its operands) have landed
         __syncthreads();                // everyone's have, and everyone is done with chunk c - 1
-        if (c + 1 < NCH) wc_issue<NL, TX_WAVES, true>(c & 1 ? Ws0 : Ws1, chunk(c + 1), wave, lane);
+        if (c + 1 < NCH) wc_issue<NL, TX_WAVES>(c & 1 ? Ws0 : Ws1, chunk(c + 1), wave, lane);
         u32x4 xb[2][3];
         split_pre(c < 5 ? y[c < 5 ? c : 0] : t1v, xb);
         if (CAB && c >= 4 && c + 1 < NCH) gather_t1(c - 4, t1v);
@@ -223,7 +223,7 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
     const int lr = lane & 15, lg = lane >> 4;
     const int M = p.M;
     if ((int)blockIdx.x * TX_ROWS >= M) return;  // whole block, before any barrier
-    wc_issue<NL1, TX_WAVES, true>(Ws0, p.w, wave, lane);
+    wc_issue<NL1, TX_WAVES>(Ws0, p.w, wave, lane);
     for (int i = tid; i < 3 * 144; i += TX_WAVES * 64) {
         float v;
         if (i < 144) v = p.b2[i];
@@ -270,8 +270,8 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
             constexpr int PAR = decltype(parv)::value;  // = ks & 1
             __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the chunk (and its rows) have landed
             __syncthreads();                // everyone's have, and everyone is done with the one before
-            if (ks < 4) wc_issue<NL1, TX_WAVES, true>(PAR ? Ws0 : Ws1, wq + (size_t)(ks + 1) * WC_CHUNK, wave, lane);
-            else wc_issue<NL2, TX_WAVES, true>(Ws1, wq + (size_t)5 * WC_CHUNK, wave, lane);
+            if (ks < 4) wc_issue<NL1, TX_WAVES>(PAR ? Ws0 : Ws1, wq + (size_t)(ks + 1) * WC_CHUNK, wave, lane);
+            else wc_issue<NL2, TX_WAVES>(Ws1, wq + (size_t)5 * WC_CHUNK, wave, lane);
             u32x4 xb[2][3];
             norm_pre(ks, pre);
             split_pre(pre, xb);
@@ -292,8 +292,8 @@ __device__ __forceinline__ void mlpx_body(const TailXArgs& p)
         for (int s = 0; s < 3; ++s) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (s < 2) wc_issue<NL2, TX_WAVES, true>(s & 1 ? Ws1 : Ws0, wq + (size_t)(6 + s) * WC_CHUNK, wave, lane);
-            else if (q < 2) wc_issue<NL1, TX_WAVES, true>(Ws0, wq + (size_t)8 * WC_CHUNK, wave, lane);
+            if (s < 2) wc_issue<NL2, TX_WAVES>(s & 1 ? Ws1 : Ws0, wq + (size_t)(6 + s) * WC_CHUNK, wave, lane);
+            else if (q < 2) wc_issue<NL1, TX_WAVES>(Ws0, wq + (size_t)8 * WC_CHUNK, wave, lane);
             if (s == 0) {
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt)
