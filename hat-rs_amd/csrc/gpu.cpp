@@ -46,8 +46,8 @@ float bf16_float(unsigned short h)
 // Rows [N][K] of w (row stride ldw), N <= 192, as weight chunks at dst: the
 // value at (n, k) is column kbase + k, which lands in 32-k step s = (kbase +
 // k) / 32, WC_CHUNK elements apart, as three bf16 planes [N][32] (plane stride
-// N * 32) with row n's 16-byte k-groups g stored at g ^ ((n >> 2) & 3) (so that
-// 16 consecutive rows read at one k-group hit distinct banks): x = h0 + h1 +
+// N * 32) with row n's 16-byte k-groups g stored at slot ws_slot(n, g) (so that
+// reads of one k-group down the rows are free of bank conflicts): x = h0 + h1 +
 // h2, each part the RNE of what the parts before it leave; the rest stays zero.
 static void split_chunks(const float* w, int N, int K, int ldw, unsigned short* dst, int kbase = 0)
 {
@@ -59,7 +59,7 @@ static void split_chunks(const float* w, int N, int K, int ldw, unsigned short* 
             const unsigned short h1 = bf16_rne(r1);
             const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
             const int s = (kbase + k) / 32, kk = (kbase + k) % 32;
-            unsigned short* d = dst + (size_t)s * WC_CHUNK + (size_t)n * 32 + ((kk / 8) ^ ((n >> 2) & 3)) * 8 + kk % 8;
+            unsigned short* d = dst + (size_t)s * WC_CHUNK + (size_t)n * 32 + hatk::ws_slot(n, kk / 8) * 8 + kk % 8;
             d[0] = h0;
             d[(size_t)N * 32] = h1;
             d[(size_t)2 * N * 32] = h2;
@@ -99,7 +99,7 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
             const unsigned short h1 = bf16_rne(r1);
             const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
             const int r = n % real, s = k / 32, g = (k % 32) / 8, j = k % 8;
-            unsigned short* d = &out[((size_t)(n / real) * ks_n + s) * chunk + (size_t)r * 32 + (g ^ ((r >> 2) & 3)) * 8 + j];
+            unsigned short* d = &out[((size_t)(n / real) * ks_n + s) * chunk + (size_t)r * 32 + hatk::ws_slot(r, g) * 8 + j];
             d[0] = h0;
             d[(size_t)rows * 32] = h1;
             d[(size_t)2 * rows * 32] = h2;
@@ -138,7 +138,7 @@ void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<u
 
 // One 32-k step of `rows` weight rows (value(r, kk), kk < 32) split into three
 // bf16 planes [rows][32] in the swizzled layout of the weight-stationary
-// kernels (row r's k-group g at g ^ ((r >> 2) & 3)).
+// kernels (row r's k-group g at slot ws_slot(r, g)).
 template <typename F>
 static void split_ws_step(int rows, F value, unsigned short* dst)
 {
@@ -149,7 +149,7 @@ static void split_ws_step(int rows, F value, unsigned short* dst)
             const float r1 = x - bf16_float(h0);
             const unsigned short h1 = bf16_rne(r1);
             const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
-            unsigned short* d = dst + (size_t)r * 32 + ((kk / 8) ^ ((r >> 2) & 3)) * 8 + kk % 8;
+            unsigned short* d = dst + (size_t)r * 32 + hatk::ws_slot(r, kk / 8) * 8 + kk % 8;
             d[0] = h0;
             d[(size_t)rows * 32] = h1;
             d[(size_t)2 * rows * 32] = h2;

@@ -74,7 +74,7 @@ std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
 std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K);
 // The same split for hat_gemmx_qkv's weight-stationary slices: per 144-row
 // slice five chunks of three planes [144][32], each row's 16-byte k-groups
-// swizzled (g ^ ((row >> 2) & 3)), WS_CHUNK elements apart; bias at k = 144.
+// swizzled (ws_slot), WS_CHUNK elements apart; bias at k = 144.
 std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, int N, int K);
 // The C = 144 MLP (fc1 [288][144] + b1, fc2 [144][288]) for hat_mlpx: per
 // third of the hidden layer eight weight chunks - five of fc1's 96 rows (b1

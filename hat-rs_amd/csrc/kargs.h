@@ -241,11 +241,18 @@ struct HabTailArgs {
 // hat_mlpx(_ln):   out = res + fc2(gelu(fc1(a))) + b2 (+ xn = LN(out)).
 // Weight chunks of the split-bf16 tails (tailx.hip): one 32-k step of up to
 // 192 rows as three bf16 planes [rows][32], each row's four 16-byte k-groups g
-// stored at g ^ ((row >> 2) & 3) (ws_mma), WC_CHUNK elements apart (zeros after
+// stored at slot ws_slot(row, g) (ws_mma), WC_CHUNK elements apart (zeros after
 // the planes). A chunk is copied as loads of 1 KB, the same number from every
 // wave of a block: 144 rows take 27 (28 to share them out evenly), 96 rows 18
 // (20), 192 rows 36.
 #define WC_CHUNK 20480  // 40 x 512 >= 3 x 192 x 32
+// The slot of row r's 16-byte k-group g in a 64-byte row of those planes. An
+// MFMA fragment read has lane i take rows r0 + i at one k-group, 16 bytes a
+// lane, and the LDS serves such reads 8 consecutive lanes at a time over its
+// 32 four-byte banks; two 64-byte rows fill the banks once, so the XOR by
+// (r >> 1) & 3 gives the four row pairs of every 8 lanes four distinct slots
+// and the reads have no bank conflicts without padding (measured: none).
+constexpr int ws_slot(int r, int g) { return g ^ ((r >> 1) & 3); }
 // The MLP walks the hidden layer in thirds of MX_HID units: per third five
 // fc1 chunks (96 permuted rows, k = input channel) then three fc2 chunks (144
 // rows, k = the third's hidden units), 24 chunks in all.
@@ -264,8 +271,8 @@ constexpr int wx_tiles(int M) { return (M + WX_ROWS - 1) / WX_ROWS; }
 
 // The qkv linear (hat_gemmx_qkv, hat_gemmx_qkv180) keeps one column slice in
 // LDS for the whole launch: per 32-k step three bf16 planes [rows][32],
-// unpadded, each row's four 16-byte k-groups stored at g ^ ((row >> 2) & 3)
-// (so that 16 consecutive rows read at one k-group hit distinct banks),
+// unpadded, each row's four 16-byte k-groups stored at slot ws_slot(row, g)
+// (so that reads of one k-group down the rows are free of bank conflicts),
 // WS_CHUNK elements apart. C = 144: three slices (q, k, v) of 144 rows, five
 // k-steps; C = 180: six slices of 96 rows (three heads of 30, rows 90..95
 // zero), six k-steps (WS_CHUNK180). Groups of NS blocks (one per slice, on one

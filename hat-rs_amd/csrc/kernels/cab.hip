@@ -302,7 +302,7 @@ __device__ __forceinline__ void cab_gate_body(const CabGateArgs& p, float* lds)
         p.w2g[i] = v;
     }
     // the same weights as hat_projx_cab's two weight chunks: [s][plane][c][32],
-    // row c's k-group g at g ^ ((c >> 2) & 3), k = 32 s + j, zeros elsewhere
+    // row c's k-group g at slot ws_slot(c, g), k = 32 s + j, zeros elsewhere
     if (p.w2gx) {
         constexpr int PLANE = CAB_C * 32;
         for (int i = tid; i < 2 * WC_CHUNK; i += WAVES * 64) {
@@ -310,7 +310,7 @@ __device__ __forceinline__ void cab_gate_body(const CabGateArgs& p, float* lds)
             unsigned short h = 0;
             if (r < 3 * PLANE) {
                 const int pl = r / PLANE, c = (r - pl * PLANE) / 32, pos = r - pl * PLANE - c * 32;
-                const int j = (((pos >> 3) ^ ((c >> 2) & 3)) << 3) | (pos & 7);
+                const int j = (ws_slot(c, pos >> 3) << 3) | (pos & 7);
                 const int k = 32 * s + j, tap = k / CAB_CC, ci = k - tap * CAB_CC;
                 const float v = tap < 9 ? (p.cscale * s_gate[c]) * p.w2[(c * CAB_CC + ci) * 9 + tap] : 0.0f;
                 h = split3_part(v, pl);

@@ -137,14 +137,14 @@ __device__ __forceinline__ void wc_issue(unsigned short* dst, const unsigned sho
 // acc[mt][nt] += W[rows 16 nt .. +15] . xb[mt] for one chunk in the swizzled
 // layout of the weight-stationary kernels:
 // three planes [ROWS][32] (plane stride ROWS * 32), row r's four 16-byte
-// k-groups g stored at g ^ ((r >> 2) & 3), so that 16 consecutive rows read at
-// one k-group hit distinct banks without padding (a 192-row chunk fits
-// TX_BUF).
+// k-groups g stored at slot ws_slot(r, g), so that the fragment reads down the
+// rows at one k-group are free of bank conflicts without padding (a 192-row
+// chunk fits TX_BUF).
 template <int NT, int ROWS>
 __device__ __forceinline__ void ws_mma(const unsigned short* Ws, int lr, int lg, const u32x4 (&xb)[2][3],
                                        f32x4 (&acc)[2][NT])
 {
-    const unsigned short* wr = Ws + lr * 32 + ((lg ^ ((lr >> 2) & 3)) * 8);
+    const unsigned short* wr = Ws + lr * 32 + (hatk::ws_slot(lr, lg) * 8);
     u32x4 wa[2][3];
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl) wa[0][pl] = *(const u32x4*)(wr + pl * ROWS * 32);

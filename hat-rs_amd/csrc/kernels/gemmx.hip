@@ -83,6 +83,10 @@ __device__ __forceinline__ void split_pre(const f32x4 (&pre)[MT][2], u32x4 (&xb)
     }
 }
 
+// The epilogue's staging rows (floats): 48 at head_dim 24 (two heads of a
+// 16-row tile at a time), 100 at 30 (all 96 columns, padded).
+constexpr int gx_stage_stride(int hd) { return hd == 24 ? 48 : 100; }
+
 // K: input width; NT: 16-column tiles per slice; NS: slices; HD: head_dim;
 // NH: heads per slice (HD * NH <= 16 NT columns are real, the rest zero); MT:
 // 16-token tiles per subtile (each weight fragment read from LDS feeds MT
@@ -94,7 +98,7 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
     constexpr int ROWS = 16 * NT;                 // slice rows in LDS
     constexpr int CHUNK = 3 * ROWS * 32;          // one k-step: three bf16 planes [ROWS][32]
     constexpr int NLOAD = KS * CHUNK / 512;       // 1 KB loads
-    constexpr int QS_S = HD == 24 ? 48 : 96;      // staging row stride (floats)
+    constexpr int QS_S = gx_stage_stride(HD);     // staging row stride (floats)
     constexpr int TOK = 16 * MT;                  // tokens per subtile
     static_assert(KS * CHUNK % 512 == 0, "whole loads");
     static_assert(HD * NH <= ROWS, "the heads fit the slice");
@@ -126,7 +130,7 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
         __syncthreads();  // the slice is in LDS; no barrier after this one
     }
     // this lane's A-operand offset: row lr of a 16-row tile, k-group lg swizzled
-    const unsigned short* wl = Wsl + lr * 32 + ((lg ^ ((lr >> 2) & 3)) * 8);
+    const unsigned short* wl = Wsl + lr * 32 + (hatk::ws_slot(lr, lg) * 8);
     float* out = p.out + (size_t)sl * NH * M * HD;  // the slice's first head
     float* Q = Qs + wave * 16 * QS_S;
     const int nsub = (M + TOK - 1) / TOK;
@@ -182,16 +186,22 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
             if constexpr (HD == 24) {
                 // Two heads at a time go through the wave's LDS region and leave
                 // as 16 consecutive rows of each head (1536 contiguous bytes),
-                // non-temporal.
+                // non-temporal. Row r's twelve float4 slots are rotated by
+                // r >> 1, so that the writes (8 lanes: rows r0 .. r0 + 7 at one
+                // slot) meet no bank conflicts in the 48-float rows.
+                auto slot = [](int r, int s) {
+                    const int v = s + (r >> 1);
+                    return (v >= 12 ? v - 12 : v) * 4;
+                };
 #pragma unroll
                 for (int ph = 0; ph < 3; ++ph) {
 #pragma unroll
-                    for (int t = 0; t < 3; ++t) *(f32x4*)(Q + lr * QS_S + t * 16 + lg * 4) = acc[mt][3 * ph + t];
+                    for (int t = 0; t < 3; ++t) *(f32x4*)(Q + lr * QS_S + slot(lr, t * 4 + lg)) = acc[mt][3 * ph + t];
                     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
 #pragma unroll
                     for (int i2 = 0; i2 < 3; ++i2) {
                         const int f = lane + 64 * i2, hh = f / 96, r = (f - hh * 96) / 6, d4 = f - hh * 96 - r * 6;
-                        const f32x4 v = *(const f32x4*)(Q + r * QS_S + hh * 24 + d4 * 4);
+                        const f32x4 v = *(const f32x4*)(Q + r * QS_S + slot(r, hh * 6 + d4));
                         // rows past M go to the sink (a store is issued either way)
                         float* dst = r < mrows ? out + ((size_t)(2 * ph + hh) * M + mb + r) * 24 + d4 * 4
                                                : hat_sink_row + d4 * 4;
@@ -200,10 +210,12 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
                     __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next phase's writes
                 }
             } else {
-                // All NH heads at once: 16 rows x 16 NT columns into the stage,
-                // then 16 consecutive rows of each head (30 floats, 1920
-                // contiguous bytes) leave as float2 pairs (a pair never
-                // straddles a row: head_dim is even), non-temporal.
+                // All NH heads at once: 16 rows x 16 NT columns into the stage
+                // (rows 100 floats apart, so that the writes, 8 lanes at rows
+                // r0 .. r0 + 7, meet no bank conflicts), then 16 consecutive
+                // rows of each head (30 floats, 1920 contiguous bytes) leave as
+                // float2 pairs (a pair never straddles a row: head_dim is
+                // even), non-temporal.
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) *(f32x4*)(Q + lr * QS_S + nt * 16 + lg * 4) = acc[mt][nt];
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
@@ -230,13 +242,13 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
 extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv(GemmArgs p)
 {
     __shared__ __attribute__((aligned(16))) unsigned short Wsl[5 * WS_CHUNK];  // the slice
-    __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * 48];    // per-wave staging
+    __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * gx_stage_stride(24)];  // per-wave staging
     gemmx_qkv_body<144, 9, 3, 24, 6, 2>(p, Wsl, Qs);
 }
 
 extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv180(GemmArgs p)
 {
     __shared__ __attribute__((aligned(16))) unsigned short Wsl[6 * WS_CHUNK180];  // the slice
-    __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * 96];        // per-wave staging
+    __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * gx_stage_stride(30)];  // per-wave staging
     gemmx_qkv_body<180, 6, 6, 30, 3, 3>(p, Wsl, Qs);
 }
