@@ -88,17 +88,24 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     for (int i = tid; i < 16 * NT; i += 512) Cs[i] = 16 * NT * cb + i < CO ? p.bias[16 * NT * cb + i] : 0.0f;
 
     // The patch of a 32-channel chunk is channel-quad-major: float4 slot
-    // q * 180 + pix holds channels 4q .. 4q+3 of halo pixel pix (1440 of
-    // WG_SLOTS used), so a lane's reads sit at one lane offset plus
-    // wave-uniform ones. The three slots this thread stages per chunk (the
+    // q * 180 + 18 hy + c holds channels 4q .. 4q+3 of halo pixel (hy, hx),
+    // 1440 of WG_SLOTS used. With PSPLIT the even columns come first (c = hx
+    // / 2) and then the odd ones (c = 9 + hx / 2), so that the 8 lanes that
+    // LDS serves together (tiles tx = 0 .. 7 of a row, columns 2 tx + j) read
+    // 8 consecutive slots, free of bank conflicts; without it c = hx and the
+    // reads are 2-way conflicted. The 144-channel trunk conv (NT = 9, 144
+    // accumulator registers) keeps c = hx: with the split columns the compiler
+    // spills 32 registers there instead of 16, which costs more than the
+    // conflicts. A lane's reads sit at one lane offset plus wave-uniform ones. The three slots this thread stages per chunk (the
     // third for waves 0..6 only): element offsets of the quad in chunk 0, or
     // -1 for slots outside the plane or past the 1440 used.
+    constexpr bool PSPLIT = NT != 9;
     int soff[3], squad[3];
 #pragma unroll
     for (int r = 0; r < 3; ++r) {
         const int s = r * 512 + tid;
         const int q = s / WG_PPX, pix = s - q * WG_PPX;
-        const int hy = pix / WG_PW, hx = pix - hy * WG_PW;
+        const int hy = pix / WG_PW, c = pix - hy * WG_PW, hx = !PSPLIT ? c : c < 9 ? 2 * c : 2 * c - 17;
         const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
         const bool ok = s < WG_PPX * 8 && gy >= 0 && gy < H && gx >= 0 && gx < W;
         soff[r] = ok ? (gy * W + gx) * p.cin_stride + q * 4 : -1;
@@ -148,14 +155,16 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 #pragma unroll
     for (int nt2 = 0; nt2 < 2; ++nt2) {
         const int n = nt2 * 16 + lr, ty = n >> 3, tx = n & 7;
-        pbase[nt2] = (2 * lg * WG_PPX + 2 * ty * WG_PW + 2 * tx) * 4;
+        pbase[nt2] = (2 * lg * WG_PPX + 2 * ty * WG_PW + (PSPLIT ? tx : 2 * tx)) * 4;
     }
     const int cols[4] = {cA, cB, cC, cD};
     int uoff[4][2];  // [column A..D][row a / b]
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        uoff[c][0] = (ra * WG_PW + cols[c]) * 4;
-        uoff[c][1] = (rb * WG_PW + cols[c]) * 4;
+        // column 2 tx + cols[c]'s slot, less the lane's part
+        const int cs = PSPLIT ? (cols[c] & 1) * 9 + (cols[c] >> 1) : cols[c];
+        uoff[c][0] = (ra * WG_PW + cs) * 4;
+        uoff[c][1] = (rb * WG_PW + cs) * 4;
     }
 
     f32x4 acc[2][NT][2];
@@ -231,6 +240,14 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     // ---- epilogue. Thread (tile = tid / 16, c = tid % 16): outputs of tile
     // (ty, tx) for channels 16 nt + c.
     const int et = tid >> 4, ec = tid & 15;
+    // An M slice entry (a row of 16 floats) keeps its four float4s at slots
+    // ws_slot(row, g), so that the waves' writes (8 lanes: rows r0 .. r0 + 7)
+    // and the reads here (16 lanes a row, two rows at a time) meet no bank
+    // conflicts; row x * 32 + et has (row >> 1) & 3 == (et >> 1) & 3.
+    // (The NT = 9 trunk conv keeps plain rows of WG_MS floats, 2-way conflicted
+    // reads: the swizzle's offset register makes the compiler spill more.)
+    constexpr int MS = PSPLIT ? 16 : WG_MS;
+    const int moff = PSPLIT ? 4 * ws_slot(et, ec >> 2) + (ec & 3) : ec;
     const int ety = et >> 3, etx = et & 7;
     const int py = y0 + 2 * ety, px = x0 + 2 * etx;
     // element offsets of the thread's four pixels in the residual epilogue's
@@ -250,11 +267,12 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         for (int e = 0; e < 2; ++e)
 #pragma unroll
             for (int nt2 = 0; nt2 < 2; ++nt2)
-                *(f32x4*)(Ms + ((2 * wave + e) * 32 + nt2 * 16 + lr) * WG_MS + 4 * lg) = acc[e][nt][nt2];
+                *(f32x4*)(Ms + ((2 * wave + e) * 32 + nt2 * 16 + lr) * MS + 4 * (PSPLIT ? ws_slot(lr, lg) : lg)) =
+                    acc[e][nt][nt2];
         __syncthreads();
         float m[16];
 #pragma unroll
-        for (int x = 0; x < 16; ++x) m[x] = Ms[(x * 32 + et) * WG_MS + ec];
+        for (int x = 0; x < 16; ++x) m[x] = Ms[(x * 32 + et) * MS + moff];
         float t0[4], t1[4];  // T[i][0], T[i][1] = M[i] A
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
