@@ -190,6 +190,10 @@ void run(const Args& a)
         if (tile >= std::max(w, h)) printf("  whole-image pass fits in free VRAM\n");
         else printf("  free VRAM -> tile %zupx (margin %zu)\n", tile, margin);
     } else if (a.have_mem) {
+        // The per-pixel cost is this backend's own per-plan device bytes at the
+        // image's padded size. The reference divides Cpu::footprint_floats by the
+        // plan's tokens for either device (main.rs:244-245); this build has no CPU
+        // backend, and its device buffers are what a tile must fit.
         hat_mem_plan mp;
         if (hat_gpu_plan(wt, h, w, &mp) != 0) throw CliError{last_error()};
         const size_t hp = (h + win - 1) / win * win, wp = (w + win - 1) / win * win;
@@ -209,8 +213,10 @@ void run(const Args& a)
     std::vector<float> out(3 * w * s * h * s);
     hat_tiling ti;
     if (hat_tile_forward(be, h, w, img.data(), out.data(), tile, margin, &ti) != 0) throw CliError{last_error()};
+    // "largest" is the biggest sub-image as height x width (main.rs:278-280 prints
+    // tile.rs's `largest`, which is (sh, sw))
     printf("  tiled %zux%zu into %zu tiles (%zupx cores, %zupx margin, largest %zux%zu)\n", w, h, ti.tiles,
-           ti.tile, ti.margin, ti.largest_w, ti.largest_h);
+           ti.tile, ti.margin, ti.largest_h, ti.largest_w);
     const double sec = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     printf("  gpu forward in %.1f ms (%.2f MP/s)\n", sec * 1e3, (double)(w * h) / 1e6 / sec);
     if (hat_png_save(a.output.c_str(), w * s, h * s, out.data()) != 0) throw CliError{last_error()};

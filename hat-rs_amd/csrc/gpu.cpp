@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <thread>
 
 #include "kargs.h"
 #include "tile.h"
@@ -911,6 +912,10 @@ void run_ln(hipStream_t s, const float* x, float* y, const float* w, const float
 
 float* GpuBackend::upload(const float* src, size_t n)
 {
+    if (count_only_) {
+        weight_bytes_ += n * sizeof(float);
+        return nullptr;
+    }
     Runtime& rt = Runtime::get();
     float* d = (float*)rt.alloc(n * sizeof(float));
     owned_.push_back(d);
@@ -921,6 +926,10 @@ float* GpuBackend::upload(const float* src, size_t n)
 
 void* GpuBackend::upload_bytes(const void* src, size_t bytes)
 {
+    if (count_only_) {
+        weight_bytes_ += bytes;
+        return nullptr;
+    }
     Runtime& rt = Runtime::get();
     void* d = rt.alloc(bytes);
     owned_.push_back(d);
@@ -1017,6 +1026,27 @@ GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
         if (d < 1) throw Error("every stage needs at least one HAB");
     cab_fold_ = cab_folded(wt);
     rt.check(rt.api().StreamCreate(&stream_), "hipStreamCreate");
+    upload_all();
+    if (!wt.device_bytes_cache) wt.device_bytes_cache = weight_bytes_;
+}
+
+GpuBackend::GpuBackend(const Weights& wt, CountOnly) : wt_(wt), count_only_(true)
+{
+    cab_fold_ = cab_folded(wt);
+    upload_all();
+}
+
+size_t GpuBackend::device_weight_bytes(const Weights& wt)
+{
+    if (!wt.device_bytes_cache) wt.device_bytes_cache = GpuBackend(wt, CountOnly{}).weight_bytes_;
+    return wt.device_bytes_cache;
+}
+
+// Every tensor of the network, packed as the kernels read it (Gpu::new's upload,
+// gpu.rs:372-386).
+void GpuBackend::upload_all()
+{
+    const Weights& wt = wt_;
     upload_conv("conv_first");
     upload_raw("patch_embed.norm.weight");
     upload_raw("patch_embed.norm.bias");
@@ -1078,6 +1108,7 @@ GpuBackend::GpuBackend(const Weights& wt) : wt_(wt)
 
 GpuBackend::~GpuBackend()
 {
+    if (count_only_) return;
     try {
         Runtime& rt = Runtime::get();
         rt.api().StreamSynchronize(stream_);
@@ -1092,6 +1123,7 @@ GpuBackend::~GpuBackend()
 void GpuBackend::free_plan()
 {
     Runtime& rt = Runtime::get();
+    free_stage();
     for (void* p : acts_) rt.free(p);
     acts_.clear();
     acts_bytes_ = 0;
@@ -1646,17 +1678,81 @@ void GpuBackend::forward_batch(int n, int h, int w, const float* in, float* out)
     }
 }
 
-// Backend::forward: host [3][h][w] in, host [3][h*s][w*s] out.
+void GpuBackend::free_stage()
+{
+    Runtime& rt = Runtime::get();
+    if (stage_in_) rt.api().HostFree(stage_in_);
+    if (stage_out_) rt.api().HostFree(stage_out_);
+    for (hipEvent_t e : stage_ev_) rt.api().EventDestroy(e);
+    stage_in_ = stage_out_ = nullptr;
+    stage_in_n_ = stage_out_n_ = 0;
+    stage_ev_.clear();
+}
+
+namespace {
+// Output chunks of Backend::forward's download, and the host threads that copy
+// them out of pinned memory while later chunks are still on the bus.
+constexpr size_t kStageChunk = 2u << 20;  // bytes
+constexpr unsigned kStageThreads = 8;
+}  // namespace
+
+// Backend::forward (backend.rs:29-36, gpu.rs:759-803): host [3][h][w] in, host
+// [3][h*s][w*s] out. The input goes up through a pinned buffer; the output comes
+// back into a pinned buffer in 2 MiB chunks, each with an event, and up to eight
+// host threads copy each chunk to `out` as soon as its event fires, so the
+// host-side copy runs beside the DMA instead of after it (a pageable hipMemcpy
+// stages through the runtime's own bounce buffers one piece at a time).
 void GpuBackend::forward(int h, int w, const float* in, float* out)
 {
     if (h <= 0 || w <= 0) throw Error(std::to_string(h) + "x" + std::to_string(w) + " is empty");
+    if (!in || !out) throw Error("forward: null argument");
     ensure_plan(h, w);
     Runtime& rt = Runtime::get();
+    const HipApi& api = rt.api();
     const size_t s2 = (size_t)wt_.scale * wt_.scale;
-    rt.h2d(a_.din, in, 3 * (size_t)h * w * sizeof(float));
-    forward_device(h, w, a_.din, a_.dout);
-    rt.check(rt.api().StreamSynchronize(stream_), "forward");
-    rt.d2h(out, a_.dout, 3 * (size_t)h * w * s2 * sizeof(float));
+    const size_t in_n = 3 * (size_t)h * w, out_n = in_n * s2;
+    const size_t out_bytes = out_n * sizeof(float);
+    const size_t chunks = (out_bytes + kStageChunk - 1) / kStageChunk;
+    if (stage_in_n_ != in_n || stage_out_n_ != out_n) {
+        free_stage();
+        rt.check(api.HostMalloc((void**)&stage_in_, in_n * sizeof(float), 0), "hipHostMalloc");
+        stage_in_n_ = in_n;
+        rt.check(api.HostMalloc((void**)&stage_out_, out_bytes, 0), "hipHostMalloc");
+        stage_out_n_ = out_n;
+        stage_ev_.assign(chunks, nullptr);
+        for (hipEvent_t& e : stage_ev_) rt.check(api.EventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+    }
+    memcpy(stage_in_, in, in_n * sizeof(float));
+    rt.check(api.MemcpyAsync(a_.din, stage_in_, in_n * sizeof(float), hipMemcpyHostToDevice, stream_),
+             "hipMemcpyAsync H2D");
+    run_forward(h, w, a_.din, a_.dout);
+    for (size_t k = 0; k < chunks; ++k) {
+        const size_t off = k * kStageChunk, len = std::min(kStageChunk, out_bytes - off);
+        rt.check(api.MemcpyAsync((char*)stage_out_ + off, (const char*)a_.dout + off, len, hipMemcpyDeviceToHost,
+                                 stream_),
+                 "hipMemcpyAsync D2H");
+        rt.check(api.EventRecord(stage_ev_[k], stream_), "hipEventRecord");
+    }
+    // Thread t copies chunks t, t + n, ... in the order they arrive.
+    const unsigned n = (unsigned)std::min<size_t>(kStageThreads, chunks);
+    std::vector<hipError_t> err(n, hipSuccess);
+    auto copy_out = [&](unsigned t) {
+        for (size_t k = t; k < chunks; k += n) {
+            const hipError_t e = api.EventSynchronize(stage_ev_[k]);
+            if (e != hipSuccess) {
+                err[t] = e;
+                return;
+            }
+            const size_t off = k * kStageChunk, len = std::min(kStageChunk, out_bytes - off);
+            memcpy((char*)out + off, (const char*)stage_out_ + off, len);
+        }
+    };
+    std::vector<std::thread> pool;
+    for (unsigned t = 1; t < n; ++t) pool.emplace_back(copy_out, t);
+    copy_out(0);
+    for (std::thread& th : pool) th.join();
+    rt.check(api.StreamSynchronize(stream_), "forward");
+    for (hipError_t e : err) rt.check(e, "forward: download");
 }
 
 // ---------------------------------------------------------------------------

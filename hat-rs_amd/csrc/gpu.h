@@ -121,6 +121,10 @@ public:
     // Device bytes of the per-plan buffers a backend over `wt` allocates for an
     // h x w forward (gpu.rs:78-290 footprint_floats), computed without a device.
     static size_t plan_bytes(const Weights& wt, int h, int w, bool host_io);
+    // Device bytes the weight upload of a backend over `wt` allocates (the
+    // packed FP32 tensors and their split-bf16 copies), computed without a
+    // device by running the upload's packers in a counting pass; cached in wt.
+    static size_t device_weight_bytes(const Weights& wt);
     static bool cab_folded(const Weights& wt);
     // HAB.forward of one block (gpu.rs:469-520 `hab`) on a window-multiple
     // hp x wp plane: host x, out token-major [hp*wp][embed]; with the block's
@@ -133,7 +137,11 @@ public:
     const Weights& weights() const { return wt_; }
 
 private:
+    struct CountOnly {};
+    GpuBackend(const Weights& wt, CountOnly);  // the counting pass: packs, uploads nothing
+    void upload_all();
     const Weights& wt_;
+    bool count_only_ = false;
     hipStream_t stream_ = nullptr;
     std::map<std::string, float*> raw_;
     std::map<std::string, DevLinear> lin_;
@@ -177,6 +185,13 @@ private:
     Plan batch_plan_;
     std::vector<void*> batch_dev_;
     void free_batch();
+
+    // Backend::forward's host staging, kept for the plan: pinned input and
+    // output buffers and one event per output chunk.
+    float *stage_in_ = nullptr, *stage_out_ = nullptr;
+    size_t stage_in_n_ = 0, stage_out_n_ = 0;
+    std::vector<hipEvent_t> stage_ev_;
+    void free_stage();
 
     float* upload(const float* src, size_t n);
     void* upload_bytes(const void* src, size_t bytes);

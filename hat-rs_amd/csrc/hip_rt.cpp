@@ -122,6 +122,7 @@ Runtime::Runtime()
     sym(l, api_.StreamDestroy, "hipStreamDestroy");
     sym(l, api_.StreamSynchronize, "hipStreamSynchronize");
     sym(l, api_.EventCreate, "hipEventCreate");
+    sym(l, api_.EventCreateWithFlags, "hipEventCreateWithFlags");
     sym(l, api_.EventDestroy, "hipEventDestroy");
     sym(l, api_.EventRecord, "hipEventRecord");
     sym(l, api_.EventSynchronize, "hipEventSynchronize");

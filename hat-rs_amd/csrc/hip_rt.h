@@ -49,6 +49,7 @@ struct HipApi {
     hipError_t (*StreamDestroy)(hipStream_t);
     hipError_t (*StreamSynchronize)(hipStream_t);
     hipError_t (*EventCreate)(hipEvent_t*);
+    hipError_t (*EventCreateWithFlags)(hipEvent_t*, unsigned);
     hipError_t (*EventDestroy)(hipEvent_t);
     hipError_t (*EventRecord)(hipEvent_t, hipStream_t);
     hipError_t (*EventSynchronize)(hipEvent_t);

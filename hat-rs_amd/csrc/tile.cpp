@@ -88,7 +88,9 @@ MemPlan gpu_plan(const Weights& wt, size_t h, size_t w)
 {
     MemPlan p;
     p.activations = GpuBackend::plan_bytes(wt, (int)h, (int)w, true);
-    p.weights = wt.file_bytes;
+    // what the upload allocates: the packed tensors and their split-bf16 copies
+    // (the reference's backend uploads the file's tensors as they are, wt.bytes)
+    p.weights = GpuBackend::device_weight_bytes(wt);
     p.base = kBase;
     p.need = (uint64_t)((double)p.activations * kSlack) + p.weights + p.base;
     std::string why;
@@ -124,10 +126,11 @@ void check_gpu_weights(const Weights& wt)
     if (!gpu_available(&why)) return;
     size_t fr = 0, tot = 0;
     if (Runtime::get().api().MemGetInfo(&fr, &tot) != hipSuccess) return;
-    const uint64_t need = wt.file_bytes + kBase;
+    const uint64_t dev = GpuBackend::device_weight_bytes(wt);
+    const uint64_t need = dev + kBase;
     if (need > fr)
         throw Error("not enough video memory for the checkpoint alone\nhat: " + wt.variant + " uploads as " +
-                    fmt_bytes(wt.file_bytes) + " of tensors, and " + fmt_bytes(fr) +
+                    fmt_bytes(dev) + " of tensors, and " + fmt_bytes(fr) +
                     " is free on the device\nhat: a smaller checkpoint is what fits");
 }
 

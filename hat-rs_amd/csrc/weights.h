@@ -42,6 +42,9 @@ public:
     float mean[3] = {0.f, 0.f, 0.f};
     std::vector<std::string> names;  // file order (sorted, as convert.py writes)
     size_t file_bytes = 0;
+    // What the GPU backend's upload of this checkpoint allocates on the device,
+    // once computed (0 until then; GpuBackend::device_weight_bytes fills it).
+    mutable size_t device_bytes_cache = 0;
 
     bool has(const std::string& name) const { return info_.count(name) != 0; }
     const TensorInfo& info(const std::string& name) const;

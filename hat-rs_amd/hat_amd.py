@@ -249,10 +249,14 @@ class Backend:
     def name(self):
         return lib().hat_backend_name(self.h).decode()
 
-    def forward(self, h, w, img):
+    def forward(self, h, w, img, out=None):
+        """Backend::forward; `out` (optional) is a caller-allocated
+        [3][h*s][w*s] float32 array, as the C ABI's output argument is."""
         img = f32(img).reshape(3, h, w)
         s = self.weights.scale
-        out = np.empty((3, h * s, w * s), dtype=np.float32)
+        if out is None:
+            out = np.empty((3, h * s, w * s), dtype=np.float32)
+        assert out.shape == (3, h * s, w * s) and out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
         _check(lib().hat_backend_forward(self.h, h, w, _fp(img), _fp(out)), "forward")
         return out
 

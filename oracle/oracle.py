@@ -265,3 +265,43 @@ class OracleModel:
         out = np.zeros_like(x)
         lib().or_hab_op(C.byref(self.m), fp(x), fp(out), hp, wp, stage, block)
         return out
+
+
+# ---- tiling -------------------------------------------------------------------------
+
+def _round_up(v, to):
+    return v if to == 0 else (v + to - 1) // to * to
+
+
+def tile_forward(model, h, w, img, tile, margin, win=16, _plant=None):
+    """tile::forward (src/tile.rs:50-107) over the oracle's whole forward.
+
+    Cores of `tile` input pixels rounded up to the window, a halo of `margin`
+    rounded up to the window and clamped to the image (tile.rs:62-66, 80-87),
+    one forward per sub-image, and only each core copied back, at its own
+    position scaled by the model (tile.rs:90-100); no blending. Returns the
+    [3][h*s][w*s] image and (tiles, step, margin, largest_h, largest_w).
+    `_plant` is for the tests that show the tiling checks can fail:
+    "origin" copies each core from the sub-image's corner instead of its own
+    offset, "unrounded" keeps the margin as given.
+    """
+    img = f32(img).reshape(3, h, w)
+    s = model.scale
+    step = max(_round_up(tile, win), win)
+    margin = margin if _plant == "unrounded" else _round_up(margin, win)
+    out = np.zeros((3, h * s, w * s), dtype=np.float32)
+    tiles = largest_h = largest_w = 0
+    for ty in range(-(-h // step)):
+        for tx in range(-(-w // step)):
+            y0, x0 = ty * step, tx * step
+            y1, x1 = min(y0 + step, h), min(x0 + step, w)
+            sy0, sx0 = max(y0 - margin, 0), max(x0 - margin, 0)
+            sy1, sx1 = min(y1 + margin, h), min(x1 + margin, w)
+            sh, sw = sy1 - sy0, sx1 - sx0
+            largest_h, largest_w = max(largest_h, sh), max(largest_w, sw)
+            planes = model.forward(sh, sw, img[:, sy0:sy1, sx0:sx1])
+            dy0, dx0 = (0, 0) if _plant == "origin" else ((y0 - sy0) * s, (x0 - sx0) * s)
+            ch, cw = (y1 - y0) * s, (x1 - x0) * s
+            out[:, y0 * s:y0 * s + ch, x0 * s:x0 * s + cw] = planes[:, dy0:dy0 + ch, dx0:dx0 + cw]
+            tiles += 1
+    return out, (tiles, step, margin, largest_h, largest_w)

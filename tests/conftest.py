@@ -9,8 +9,9 @@ import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(REPO, "tests", "golden")
-# Written by tests/golden/make_x3_checkpoint.py (generated, not committed).
-X3_CHECKPOINT = os.path.join(GOLDEN, "_gen", "hats_x3_seed5.safetensors")
+# Written by tests/golden/make_x3_checkpoint.py and committed as data: the
+# checkpoint behind the reference's own x3 fixture (hats_x3_48x48.bin).
+X3_CHECKPOINT = os.path.join(GOLDEN, "hats_x3_seed5.safetensors")
 sys.path.insert(0, os.path.join(REPO, "hat-rs_amd"))
 sys.path.insert(0, os.path.join(REPO, "oracle"))
 

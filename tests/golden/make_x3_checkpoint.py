@@ -26,9 +26,9 @@ and only then writes
 
   * tests/golden/hats_x3_48x48.bin - the reference's fixture, copied unmodified
     (data: a HATF v1 input and expected output, fixture.rs:44-78);
-  * tests/golden/_gen/hats_x3_seed5.safetensors - the 38 MB checkpoint. It is
-    generated, not committed (.gitignore lists _gen/); the tests that need it
-    skip, saying so, when it is absent.
+  * tests/golden/hats_x3_seed5.safetensors - the 38 MB checkpoint, committed
+    as data (random fp32 weights do not compress: gzip saves 14%), so that the
+    tests that need it run on every checkout; its absence fails them.
 """
 import os
 import shutil
@@ -42,7 +42,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REF = "/root/reference"
 FIXTURE = os.path.join(REF, "tests", "data", "hats_x3_48x48.bin")
 OUT_FIXTURE = os.path.join(HERE, "hats_x3_48x48.bin")
-OUT_CKPT = os.path.join(HERE, "_gen", "hats_x3_seed5.safetensors")
+OUT_CKPT = os.path.join(HERE, "hats_x3_seed5.safetensors")
 
 sys.path.insert(0, os.path.join(REF, "tools"))
 import timm_shim  # noqa: E402

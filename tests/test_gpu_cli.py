@@ -7,7 +7,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from conftest import GOLDEN, make_weights
+from conftest import FWD_MEAN_TOL, FWD_TOL, GOLDEN, make_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -30,6 +30,13 @@ def small(hl, tmp_path_factory):
     return wp, W, hl.Backend(W)
 
 
+def test_admission_counts_the_weights_the_upload_allocates(small):
+    """The memory plan's weights term is what the backend's upload allocated
+    (packed tensors and split-bf16 copies), computed without a device."""
+    wp, W, be = small
+    assert be.weight_bytes() == W.gpu_plan(64, 64)["weights"] > 2 * W.file_bytes()
+
+
 def test_a_tile_that_covers_the_image_is_one_tile(small):
     """tests/tiling.rs:65-83: one tile reproduces the whole-image pass bit for bit."""
     _, W, be = small
@@ -41,35 +48,70 @@ def test_a_tile_that_covers_the_image_is_one_tile(small):
         assert np.array_equal(got, whole)
 
 
+def _fwd_ok(got, exp, what):
+    d = np.abs(got - exp)
+    _say(f"  {what}: worst {d.max():.3e}, mean {d.mean():.3e}")
+    assert d.max() < FWD_TOL and d.mean() < FWD_MEAN_TOL, what
+
+
 def test_a_covering_margin_is_exact_and_the_margin_bounds_the_seam(small):
     """tests/tiling.rs:86-144: a margin that reaches the image's edges from every
     core reproduces the whole image exactly; with less margin the seams differ,
-    and more margin differs less."""
-    _, W, be = small
+    and more margin differs less. The seams themselves (margin 0 and 16, where
+    the tiled output is not the whole pass) are held to the whole-forward bars
+    against the oracle's tiled forward (tile.rs:50-107 geometry over the oracle's
+    forward per sub-image), so a halo or core placement that differs from the
+    reference's shows up."""
+    import oracle
+    wp, W, be = small
     h, w = 64, 64
     img = np.random.default_rng(2).random((3, h, w), dtype=np.float32)
     whole = be.forward(h, w, img)
     got, info = be.tile_forward(h, w, img, 32, 64)
     assert info["tiles"] == 4 and info["largest_h"] == 64
     assert np.array_equal(got, whole)
+    M = oracle.OracleModel(wp)
     errs = []
     for margin in (0, 16):
         got, info = be.tile_forward(h, w, img, 32, margin)
         assert info["tiles"] == 4 and info["margin"] == margin
+        exp, oinfo = oracle.tile_forward(M, h, w, img, 32, margin)
+        assert (info["tiles"], info["tile"], info["margin"], info["largest_h"], info["largest_w"]) == oinfo
+        _fwd_ok(got, exp, f"tiled margin {margin} vs the oracle's tiled forward")
         errs.append(float(np.abs(got - whole).max()))
-    _say(f"  seam worst |diff|: margin 0 {errs[0]:.3e}, margin 16 {errs[1]:.3e}")
-    assert errs[0] > 0 and errs[1] < errs[0]
+    _say(f"  seam worst |diff| vs the whole pass: margin 0 {errs[0]:.3e}, margin 16 {errs[1]:.3e}")
+    assert errs[0] > 1e-4 and errs[1] < errs[0]
+
+
+def test_a_non_square_tiling_matches_the_oracle(small):
+    """Ragged cores (the last row and column of tiles shorter than the step) on a
+    non-square, non-window-multiple image, against the oracle's tiled forward."""
+    import oracle
+    wp, W, be = small
+    h, w = 45, 70
+    img = np.random.default_rng(6).random((3, h, w), dtype=np.float32)
+    got, info = be.tile_forward(h, w, img, 20, 10)
+    exp, oinfo = oracle.tile_forward(oracle.OracleModel(wp), h, w, img, 20, 10)
+    assert (info["tiles"], info["tile"], info["margin"], info["largest_h"], info["largest_w"]) == oinfo
+    # step round_up(20, 16) = 32, margin 16: 2 x 3 cores, the last ones 13 and 6 wide
+    assert (info["tiles"], info["tile"], info["margin"]) == (6, 32, 16)
+    _fwd_ok(got, exp, "45x70 tile 20 margin 10 vs the oracle")
 
 
 @pytest.mark.parametrize("n,h,w", [(5, 48, 32), (2, 16, 16), (9, 17, 23)])
 def test_batch_equals_one_image_at_a_time(small, n, h, w):
     """forward_batch runs up to 4 images at once on separate streams with their
-    own buffers: each result is bit-identical to that image's own forward."""
-    _, W, be = small
+    own buffers: each result is bit-identical to that image's own forward, and
+    every image of the batch is held to the whole-forward bars against the
+    oracle's forward of that image."""
+    import oracle
+    wp, W, be = small
+    M = oracle.OracleModel(wp)
     imgs = np.random.default_rng(n).random((n, 3, h, w), dtype=np.float32)
     got = be.forward_batch(n, h, w, imgs)
     for i in range(n):
         assert np.array_equal(got[i], be.forward(h, w, imgs[i])), i
+        _fwd_ok(got[i], M.forward(h, w, imgs[i]), f"batch image {i} of {n} ({h}x{w}) vs the oracle")
 
 
 def _cli(hl, *args):
@@ -95,9 +137,13 @@ def test_cli_upscales_a_png(hl, small, tmp_path):
     ref = str(tmp_path / "ref.png")
     hl.png_save(ref, be.forward(37, 45, planes))
     assert open(dst, "rb").read() == open(ref, "rb").read()
-    # --mem picks a tile; the run still writes an image of the right size
-    r = _cli(hl, "-m", wp, "-i", src, "-o", dst, "--mem", "300")
-    assert r.returncode == 0 and "--mem 300 MiB -> tile" in r.stdout
+    # --mem picks a tile (the pick is pinned on the CPU by
+    # test_mem_budget_picks_the_tile_from_this_backends_plan); the tiled line
+    # names the largest sub-image as height x width, as main.rs:278-280 does
+    r = _cli(hl, "-m", wp, "-i", src, "-o", dst, "--mem", "100")
+    assert r.returncode == 0
+    assert "  --mem 100 MiB -> tile 32px (margin 32)" in r.stdout.splitlines()
+    assert "  tiled 45x37 into 4 tiles (32px cores, 32px margin, largest 37x45)" in r.stdout.splitlines()
     assert hl.png_load(dst).shape == (3, 148, 180)
 
 

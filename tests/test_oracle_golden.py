@@ -119,13 +119,11 @@ def test_hab_bar_sees_a_slip(weights_dir, o, plant):
         assert np.abs(M.hab(x, hh, ww, 0, blk) - ref[f"hab{blk}"]).max() > 5 * OP_TOL
 
 
-@pytest.mark.skipif(not os.path.exists(X3_CHECKPOINT),
-                    reason="the seed-5 HAT-S x3 checkpoint is generated, not committed: "
-                           "run tests/golden/make_x3_checkpoint.py in the build container")
 def test_oracle_matches_the_reference_x3_fixture():
     """The reference's own whole-forward fixture (tests/data/hats_x3_48x48.bin,
     made by its tools/make_fixture.py from a torch-seeded HAT-S x3, recipe at
     tests/parity.rs:30-37), on the checkpoint rebuilt from that recipe."""
+    assert os.path.exists(X3_CHECKPOINT), f"{X3_CHECKPOINT} is missing from the tree"
     h, w, scale, inp, exp = read_hatf(os.path.join(GOLDEN, "hats_x3_48x48.bin"))
     M = oracle.OracleModel(X3_CHECKPOINT)
     assert (M.scale, h, w) == (3, 48, 48)

@@ -28,15 +28,19 @@ def _run(hl, be, h, w, scale, img, noalloc):
     return d_out.download(out)
 
 
-def test_noalloc_forward_equals_forward_device(weights_dir):
+@pytest.mark.parametrize("variant,sizes", [("hat-s", [(64, 64), (32, 48)]), ("hat", [(48, 48), (16, 32)])])
+def test_noalloc_forward_equals_forward_device(weights_dir, variant, sizes):
+    """HAT-S (C = 144: the folded CAB, the 144-channel tails) and HAT (C = 180:
+    the unfolded CAB's Winograd convs, the 180-channel tails), each on two calls
+    in a row, the second smaller."""
     import hat_amd as hl
     assert hl.gpu_available(), "the HIP runtime or the GPU is missing"
-    wp = make_weights(weights_dir, "hat-s", 4, 1, None)
+    wp = make_weights(weights_dir, variant, 4, 1, None)
     be = hl.Backend(hl.Weights(wp))
     rng = np.random.default_rng(77)
-    for h, w in [(64, 64), (32, 48)]:
+    for h, w in sizes:
         img = rng.random((3, h, w), dtype=np.float32)
-        _say(f"forward_noalloc HAT-S x4 {h}x{w}")
+        _say(f"forward_noalloc {variant} x4 {h}x{w}")
         got = _run(hl, be, h, w, 4, img, True)
         want = _run(hl, be, h, w, 4, img, False)
         assert np.isfinite(got).all()
