@@ -137,6 +137,37 @@ void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<u
     }
 }
 
+// Fused tail input position k = 32 ks + 8 g + j (ks: 32-k step, g: lane group,
+// j < 8) -> channel of x': steps 0..3 hold the lane's accumulator tiles 2 ks
+// and 2 ks + 1 (channels 32 ks + 4 g + j and 32 ks + 16 + 4 g + j - 4), step 4
+// tile 8 (128 + 4 g + j) and b1's 1 at g = 0, j = 4 (-1); -2: an empty position.
+// The device twin is habx_channel (tailx.hip).
+int mlpx_fused_channel(int k)
+{
+    const int ks = k >> 5, g = (k >> 3) & 3, j = k & 7;
+    if (ks < 4) return 32 * ks + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+    if (j < 4) return 128 + 4 * g + j;
+    return g == 0 && j == 4 ? -1 : -2;
+}
+
+void pack_mlp_xf(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w)
+{
+    constexpr int C = 144, H = 288, KP = 160;
+    std::vector<float> f1((size_t)MX_HID * KP);
+    w->assign((size_t)24 * WC_CHUNK, 0);
+    for (int q = 0; q < H / MX_HID; ++q) {
+        for (int row = 0; row < MX_HID; ++row) {
+            const int u = q * MX_HID + mlpx_unit(row);
+            for (int k = 0; k < KP; ++k) {
+                const int c = mlpx_fused_channel(k);
+                f1[(size_t)row * KP + k] = c >= 0 ? w1[(size_t)u * C + c] : c == -1 ? b1[u] : 0.0f;
+            }
+        }
+        split_chunks(f1.data(), MX_HID, KP, KP, &(*w)[(size_t)(8 * q) * WC_CHUNK]);
+        split_chunks(w2 + q * MX_HID, C, MX_HID, H, &(*w)[(size_t)(8 * q + 5) * WC_CHUNK]);
+    }
+}
+
 // One 32-k step of `rows` weight rows (value(r, kk), kk < 32) split into three
 // bf16 planes [rows][32] in the swizzled layout of the weight-stationary
 // kernels (row r's k-group g at slot ws_slot(r, g)).
@@ -576,6 +607,31 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
     const long M = (long)H * W;
     if (M > 0x7fffffffL) throw Error("tailx: too many rows");
     const unsigned g = (unsigned)wx_tiles((int)M);  // a block per 128-token tile
+    if (mlp.wf && cab == (nw != nullptr)) {
+        // one kernel, x' kept on the chip (the forms the network runs: the HAB's
+        // with the next norm, the OCAB's without)
+        TailXArgs f{};
+        f.a = a;
+        f.res = res;
+        f.out = out;
+        f.xn = nw ? xn : nullptr;
+        f.w = proj.wx;
+        f.wm = mlp.wf;
+        f.bias = bias;
+        f.b2 = b2;
+        f.w2gx = w2gx;
+        f.t1 = t1;
+        f.inw = n2w;
+        f.inb = n2b;
+        f.nw = nw;
+        f.nb = nb;
+        f.M = (int)M;
+        f.H = H;
+        f.W = W;
+        f.eps = 1e-5f;
+        launch(s, cab ? "hat_habx_cab_ln" : "hat_habx", g, 1, 1, WX_THREADS, f);
+        return;
+    }
     // the projection writes x' only: the MLP forms norm2(x') from the x'
     // rows it reads
     TailXArgs p{};
@@ -981,6 +1037,9 @@ void GpuBackend::upload_mlpx(const std::string& name)
     if (t1.shape == std::vector<size_t>{288, 144} && t2.shape == std::vector<size_t>{144, 288}) {
         pack_mlp_x(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
         m.C = 144;
+        std::vector<unsigned short> wf;
+        pack_mlp_xf(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &wf);
+        m.wf = (unsigned short*)upload_bytes(wf.data(), wf.size() * sizeof(unsigned short));
     } else if (t1.shape == std::vector<size_t>{360, 180} && t2.shape == std::vector<size_t>{180, 360}) {
         pack_mlp_x180(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
         m.C = 180;
@@ -1813,13 +1872,18 @@ struct OpLinear {
 // An op's MLP pre-split for hat_mlpx (C = 144) or hat_mlpx180 (C = 180), as
 // upload_mlpx packs it; other shapes leave m.w null (the FP32 kernels).
 struct OpMlpX {
-    std::unique_ptr<DevBuf> buf;
+    std::unique_ptr<DevBuf> buf, fbuf;
     DevMlpX m;
     OpMlpX(const float* w1, const float* b1, const float* w2, int c, size_t hid)
     {
         std::vector<unsigned short> w;
-        if (c == 144 && hid == 288)
+        if (c == 144 && hid == 288) {
             pack_mlp_x(w1, b1, w2, &w);
+            std::vector<unsigned short> wf;
+            pack_mlp_xf(w1, b1, w2, &wf);
+            fbuf = dev_u16(wf);
+            m.wf = (unsigned short*)fbuf->p;
+        }
         else if (c == 180 && hid == 360)
             pack_mlp_x180(w1, b1, w2, &w);
         else

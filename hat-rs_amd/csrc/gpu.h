@@ -54,6 +54,7 @@ std::vector<unsigned short> pack_cab_conv1(const float* w);
 // hat_mlpx's weights: the packed slices and b1 in fc1's row order.
 struct DevMlpX {
     unsigned short* w = nullptr;  // C = 144: 24 weight chunks (pack_mlp_x); 180: 48 (pack_mlp_x180)
+    unsigned short* wf = nullptr;  // C = 144: the same in the fused tail's input order (pack_mlp_xf)
     int C = 144;
 };
 
@@ -82,6 +83,11 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
 // rows in the order that leaves its output in fc2's operand layout
 // (tailx.hip).
 void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
+// The same for the fused tails (hat_habx*), whose fc1 reads x' in the order a
+// lane holds the projection's accumulators: input position k = 32 ks + 8 g + j
+// is channel mlpx_fused_channel(k) (b1 at the position that returns -1).
+void pack_mlp_xf(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
+int mlpx_fused_channel(int k);
 // The C = 180 projection [180][180] for hat_projx180*: six chunks (one per
 // 32-k step, k 180..191 zero) of three bf16 planes [192][32] (rows 180..191
 // zero), k-groups swizzled as in pack_linear_ws, MX180_SLOT elements apart;

@@ -305,6 +305,9 @@ struct TailXArgs {
     // hat_mlpx(_ln): norm2's weight and bias, applied to the x' rows of a
     const float* inw;
     const float* inb;
+    // hat_habx*: the MLP's 24 weight chunks in the fused input order (w holds
+    // the projection's)
+    const unsigned short* wm;
 };
 
 struct LnArgs {

@@ -494,6 +494,252 @@ __device__ __forceinline__ void mlpx180_body(const TailXArgs& p)
     tx_store_rows<C>(acc2, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
 }
 
+// The whole second half of a block in one kernel, C = 144 (HAB with the
+// folded CAB, or OCAB):
+//
+//   x' = x + ao . Wp^T (+ nb(t1) . W2g^T) + bias
+//   out = x' + fc2(gelu(fc1(LN2(x')))) + b2, xn = LN_next(out) when asked
+//
+// hat_projx(_cab) followed by hat_mlpx(_ln) with x' kept on the chip: the
+// projection's accumulators are x' in the layout the MLP's residual takes, and
+// they stay in registers for the MLP. The MLP's input for its first third of
+// hidden units comes from the same registers: fc1's input columns are packed
+// in the order a lane holds x' (pack_mlp_xf), so k-step ks of lane group g is
+// the lane's accumulator tiles 2 ks and 2 ks + 1, i.e. channels 32 ks + 4 g +
+// j and 32 ks + 16 + 4 g + j (j < 4), and in the last step channels 128 + 4 g
+// + j with the 1 of b1's column at lane group 0, j = 4. The first third forms
+// y = norm2(x') from them and leaves y in the output rows; the other two
+// thirds read y back (each lane reads exactly the addresses it wrote, so
+// program order is what makes the values visible) and need no norm; those
+// rows are overwritten by the result at the end.
+// Against the two kernels this saves x''s round trip through HBM between them
+// and lets one block's projection (memory-latency bound) overlap another's
+// MLP (issue bound) on the same CU.
+//
+// The chunk buffers: the projection reads chunk c from buffer c & 1 and its
+// last chunk (5 or 7: an odd count) from buffer 0, so the MLP's first chunk
+// goes to buffer 1 during it, and the MLP runs with the buffers' roles
+// swapped (its even chunks in buffer 1).
+
+// fused input position k = 32 ks + 8 g + j -> channel of x' (-1: b1's 1, -2: zero)
+__device__ __forceinline__ int habx_channel(int k)
+{
+    const int ks = k >> 5, g = (k >> 3) & 3, j = k & 7;
+    if (ks < 4) return 32 * ks + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+    if (j < 4) return 128 + 4 * g + j;
+    return g == 0 && j == 4 ? -1 : -2;
+}
+
+template <bool CAB, bool LN>
+__device__ __forceinline__ void habx_body(const TailXArgs& p)
+{
+    constexpr int NCH = CAB ? 7 : 5, NLP = 28, NL1 = 20, NL2 = 28;
+    static_assert(NCH % 2 == 1, "the projection's last chunk is in buffer 0");
+    static_assert(NLP * 512 >= 3 * 144 * 32 && NL1 * 512 >= 3 * MX_HID * 32 && NL2 * 512 >= 3 * 144 * 32,
+                  "chunk loads");
+    __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
+    __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
+    __shared__ __attribute__((aligned(16))) float Cp[144];      // the projection's bias
+    __shared__ __attribute__((aligned(16))) float Cs[3 * 144];  // b2, next norm w, b (the epilogue's)
+    // norm2's w and b over fc1's 160 input positions in the fused order: at
+    // b1's position w 0 and b 1, at the empty ones zeros
+    __shared__ __attribute__((aligned(16))) float Cn[2 * 160];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
+    const int lr = lane & 15, lg = lane >> 4;
+    const int M = p.M;
+    if ((int)blockIdx.x * TX_ROWS >= M) return;  // whole block, before any barrier
+    auto pchunk = [&](int c) { return c < 5 ? p.w + (size_t)c * WC_CHUNK : p.w2gx + (size_t)(c - 5) * WC_CHUNK; };
+    wc_issue<NLP, TX_WAVES>(Ws0, pchunk(0), wave, lane);
+    for (int i = tid; i < 144; i += TX_WAVES * 64) Cp[i] = p.bias[i];
+    for (int i = tid; i < 3 * 144; i += TX_WAVES * 64) {
+        float v;
+        if (i < 144) v = p.b2[i];
+        else if (i < 288) v = LN ? p.nw[i - 144] : 0.0f;
+        else v = LN ? p.nb[i - 288] : 0.0f;
+        Cs[i] = v;
+    }
+    for (int i = tid; i < 2 * 160; i += TX_WAVES * 64) {
+        const int k = i < 160 ? i : i - 160, c = habx_channel(k);
+        Cn[i] = c >= 0 ? (i < 160 ? p.inw[c] : p.inb[c]) : (i >= 160 && c == -1 ? 1.0f : 0.0f);
+    }
+    const int mbase = blockIdx.x * TX_ROWS + wave * 32;
+    f32x4 acc[2][9];
+    tx_load_res<144>(p.res, mbase, M, lr, lg, acc);
+
+    // ---- the projection: acc = x + ao . Wp^T (+ nb(t1) . W2g^T)
+    {
+        f32x4 y[5][2][2];
+        {
+            WcRows<144> ar;
+            ar.init(p.a, mbase, M, lr);
+#pragma unroll
+            for (int ks = 0; ks < 5; ++ks) ar.load(ks, lg, y[ks]);
+        }
+        auto gather_t1 = [&](int s, f32x4 (&dst)[2][2]) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int m = mbase + mt * 16 + lr;
+                const bool alive = m < M;
+                const int yq = m / p.W, xq = m - yq * p.W;
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const int k = s * 32 + lg * 8 + j, tap = k / 6, ci = k - tap * 6;
+                    const int yy = yq + tap / 3 - 1, xx = xq + tap % 3 - 1;
+                    const bool ok = alive && tap < 9 && yy >= 0 && yy < p.H && xx >= 0 && xx < p.W;
+                    const float2 v =
+                        *(const float2*)(ok ? p.t1 + ((size_t)yy * p.W + xx) * CAB_CS + ci : hat_zero_row);
+                    dst[mt][j / 4][j % 4] = v.x;
+                    dst[mt][j / 4][j % 4 + 1] = v.y;
+                }
+            }
+        };
+        f32x4 t1v[2][2];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk c (and its operands) have landed
+            __syncthreads();                // everyone's have, and everyone is done with chunk c - 1
+            if (c + 1 < NCH) wc_issue<NLP, TX_WAVES>(c & 1 ? Ws0 : Ws1, pchunk(c + 1), wave, lane);
+            else wc_issue<NL1, TX_WAVES>(Ws1, p.wm, wave, lane);  // the MLP's first chunk
+            u32x4 xb[2][3];
+            split_pre(c < 5 ? y[c < 5 ? c : 0] : t1v, xb);
+            if (CAB && c >= 4 && c + 1 < NCH) gather_t1(c - 4, t1v);
+            ws_mma<9, 144>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
+        }
+    }
+    // x' = acc + bias, kept in acc; norm2's statistics from it
+    float2 st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < 9; ++nt) acc[mt][nt] += *(const f32x4*)(Cp + nt * 16 + lg * 4);
+        st[mt] = tx_row_stats<144>(acc[mt], lg, p.eps);
+    }
+
+    // ---- the MLP on x' (acc), in thirds of 96 hidden units
+    auto norm_pre = [&](int ks, f32x4 (&pre)[2][2]) {
+        const float* wk = Cn + ks * 32 + lg * 8;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const f32x4 w4 = *(const f32x4*)(wk + 4 * j), b4 = *(const f32x4*)(wk + 160 + 4 * j);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pre[mt][j][i] = (pre[mt][j][i] - st[mt].x) * st[mt].y * w4[i] + b4[i];
+        }
+    };
+    // y = LN2(x') in the fused order for k-step ks: third 0 forms it from the
+    // registers and leaves it in the output rows (the lane's own channels, in
+    // place of x', which stays in acc), thirds 1 and 2 read it back; the last
+    // step's second half is b1's 1 (lane group 0) or zeros
+    float* yrow[2];
+    bool yalive[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = mbase + mt * 16 + lr;
+        yalive[mt] = m < M;
+        yrow[mt] = p.out + (size_t)(yalive[mt] ? m : 0) * 144 + lg * 4;
+    }
+    auto load_y = [&](int ks, f32x4 (&dst)[2][2]) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            dst[mt][0] = *(const f32x4*)(yalive[mt] ? yrow[mt] + 32 * ks : hat_zero_row);
+            dst[mt][1] = *(const f32x4*)(yalive[mt] && ks < 4 ? yrow[mt] + 32 * ks + 16
+                                                               : (ks == 4 && lg == 0 ? hat_one_row : hat_zero_row));
+        }
+    };
+    // fc2 over a third's units from registers: chunks 5..7 of the third
+    auto fc2_third = [&](int q, const unsigned short* wq, f32x4 (&h)[2][6]) {
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            // buffers swapped: the third's chunk 5 + s is in buffer (s & 1 ? 1 : 0)
+            if (s < 2) wc_issue<NL2, TX_WAVES>(s & 1 ? Ws0 : Ws1, wq + (size_t)(6 + s) * WC_CHUNK, wave, lane);
+            else if (q < 2) wc_issue<NL1, TX_WAVES>(Ws1, wq + (size_t)8 * WC_CHUNK, wave, lane);
+            if (s == 0) {
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < 6; ++nt)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) h[mt][nt][j] = gelu(h[mt][nt][j]);
+            }
+            u32x4 xb[2][3];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const float f[8] = {h[mt][2 * s][0],     h[mt][2 * s][1],     h[mt][2 * s][2],
+                                    h[mt][2 * s][3],     h[mt][2 * s + 1][0], h[mt][2 * s + 1][1],
+                                    h[mt][2 * s + 1][2], h[mt][2 * s + 1][3]};
+                split3_x8(f, xb[mt]);
+            }
+            ws_mma<9, 144>(s & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
+        }
+    };
+    // third 0: fc1's input from the registers
+    {
+        const unsigned short* wq = p.wm;
+        f32x4 h[2][6];
+#pragma unroll
+        for (int nt = 0; nt < 6; ++nt) h[0][nt] = h[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 5; ++ks) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (ks < 4) wc_issue<NL1, TX_WAVES>(ks & 1 ? Ws1 : Ws0, wq + (size_t)(ks + 1) * WC_CHUNK, wave, lane);
+            else wc_issue<NL2, TX_WAVES>(Ws0, wq + (size_t)5 * WC_CHUNK, wave, lane);
+            f32x4 pre[2][2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                pre[mt][0] = acc[mt][2 * ks < 9 ? 2 * ks : 8];
+                pre[mt][1] = 2 * ks + 1 < 9 ? acc[mt][2 * ks + 1 < 9 ? 2 * ks + 1 : 8] : (f32x4){0.f, 0.f, 0.f, 0.f};
+            }
+            u32x4 xb[2][3];
+            norm_pre(ks, pre);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                // y for thirds 1 and 2 (rows past M: the sink)
+                float* yr = yalive[mt] ? yrow[mt] + 32 * ks : hat_sink_row;
+                *(f32x4*)yr = pre[mt][0];
+                if (ks < 4) *(f32x4*)(yr + (yalive[mt] ? 16 : 4)) = pre[mt][1];
+            }
+            split_pre(pre, xb);
+            ws_mma<6, MX_HID>(ks & 1 ? Ws0 : Ws1, lr, lg, xb, h);
+        }
+        fc2_third(0, wq, h);
+    }
+    // thirds 1, 2: fc1's input read back from the output rows, one k-step ahead
+    f32x4 pre[2][2];
+    load_y(0, pre);
+#pragma unroll 1
+    for (int q = 1; q < 3; ++q) {
+        const unsigned short* wq = p.wm + (size_t)(8 * q) * WC_CHUNK;
+        f32x4 h[2][6];
+#pragma unroll
+        for (int nt = 0; nt < 6; ++nt) h[0][nt] = h[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        auto fc1_step = [&](int ks, auto parv) {
+            constexpr int PAR = decltype(parv)::value;  // = ks & 1
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (ks < 4) wc_issue<NL1, TX_WAVES>(PAR ? Ws1 : Ws0, wq + (size_t)(ks + 1) * WC_CHUNK, wave, lane);
+            else wc_issue<NL2, TX_WAVES>(Ws0, wq + (size_t)5 * WC_CHUNK, wave, lane);
+            u32x4 xb[2][3];
+            split_pre(pre, xb);
+            if (ks < 4) load_y(ks + 1, pre);
+            else if (q < 2) load_y(0, pre);
+            ws_mma<6, MX_HID>(PAR ? Ws0 : Ws1, lr, lg, xb, h);
+        };
+#pragma unroll 1
+        for (int ks = 0; ks < 4; ks += 2) {
+            fc1_step(ks, CInt<0>{});
+            fc1_step(ks + 1, CInt<1>{});
+        }
+        fc1_step(4, CInt<0>{});
+        fc2_third(q, wq, h);
+    }
+    tx_store_rows<144>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
+}
+
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx_cab(TailXArgs p) { projx_body<true>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx(TailXArgs p) { projx_body<false>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx_ln(TailXArgs p) { mlpx_body<true>(p); }
@@ -502,3 +748,5 @@ extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx180_ln(Ta
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx180(TailXArgs p) { mlpx180_body<false>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx180_hab(TailXArgs p) { projx180_body<true>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx180(TailXArgs p) { projx180_body<false>(p); }
+extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_habx_cab_ln(TailXArgs p) { habx_body<true, true>(p); }
+extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_habx(TailXArgs p) { habx_body<false, false>(p); }

@@ -737,12 +737,15 @@ int gpu_selftest(std::string* err)
                 // The split-bf16 tails (tailx.hip) on the same inputs, in place
                 // as the forward runs them (out over the block input, the next
                 // norm over norm2's rows); 12 row tiles of 128.
-                std::vector<unsigned short> pwx = pack_linear_x(wp.data(), nullptr, C, C), mwx;
+                std::vector<unsigned short> pwx = pack_linear_x(wp.data(), nullptr, C, C), mwx, mwf;
                 pack_mlp_x(f1.data(), fb1.data(), f2.data(), &mwx);
+                pack_mlp_xf(f1.data(), fb1.data(), f2.data(), &mwf);
                 Dev dpwx(std::vector<float>((pwx.size() + 1) / 2)), dmwx(std::vector<float>((mwx.size() + 1) / 2)),
-                    dout_x(res), dxn_x((size_t)T * C);
+                    dmwf(std::vector<float>((mwf.size() + 1) / 2)), dout_x(res), dxn_x((size_t)T * C),
+                    dout_f(res), dxn_f((size_t)T * C);
                 Runtime::get().h2d(dpwx.p, pwx.data(), pwx.size() * sizeof(unsigned short));
                 Runtime::get().h2d(dmwx.p, mwx.data(), mwx.size() * sizeof(unsigned short));
+                Runtime::get().h2d(dmwf.p, mwf.data(), mwf.size() * sizeof(unsigned short));
                 TailXArgs xa{};
                 xa.a = dao.p;
                 xa.res = dout_x.p;
@@ -781,6 +784,22 @@ int gpu_selftest(std::string* err)
                 check_close("hat_mlpx_ln", dout_x.get(), std::vector<double>(ro.begin(), ro.end()), 2e-5);
                 check_close("hat_mlpx_ln next norm", dxn_x.get(), std::vector<double>(rx.begin(), rx.end()), 2e-5);
                 note("hat_mlpx_ln (split-bf16 MLP + norm) vs the two-kernel path");
+                // The fused tail (x' on the chip) on the same inputs, in place,
+                // against the same references.
+                TailXArgs xf = xa;
+                xf.res = dout_f.p;
+                xf.out = dout_f.p;
+                xf.xn = dxn_f.p;
+                xf.wm = (const unsigned short*)dmwf.p;
+                xf.b2 = dfb2.p;
+                xf.inw = dnw.p;
+                xf.inb = dnb.p;
+                xf.nw = dmw.p;
+                xf.nb = dmb.p;
+                launch(s, "hat_habx_cab_ln", (unsigned)wx_tiles(T), 1, 1, WX_THREADS, xf);
+                check_close("hat_habx_cab_ln", dout_f.get(), std::vector<double>(ro.begin(), ro.end()), 2e-5);
+                check_close("hat_habx_cab_ln next norm", dxn_f.get(), std::vector<double>(rx.begin(), rx.end()), 2e-5);
+                note("hat_habx_cab_ln (fused split-bf16 proj + conv2 + MLP + norm) vs the two-kernel path");
                 // The OCAB form over a partial last tile: rows from Mo on stay
                 // the block input.
                 const int Mo = T - 100;
@@ -807,6 +826,20 @@ int gpu_selftest(std::string* err)
                 for (size_t i = (size_t)Mo * C; i < wo.size(); ++i) wo[i] = res[i];
                 check_close("hat_projx + hat_mlpx", dout_ox.get(), wo, 2e-5);
                 note("hat_projx + hat_mlpx (split-bf16 OCAB tail, partial tile) vs the two-kernel path");
+                Dev dout_of(res);
+                TailXArgs xof = xo;
+                xof.res = dout_of.p;
+                xof.out = dout_of.p;
+                xof.xn = nullptr;
+                xof.wm = (const unsigned short*)dmwf.p;
+                xof.b2 = dfb2.p;
+                xof.inw = dnw.p;
+                xof.inb = dnb.p;
+                xof.nw = nullptr;
+                xof.nb = nullptr;
+                launch(s, "hat_habx", (unsigned)wx_tiles(Mo), 1, 1, WX_THREADS, xof);
+                check_close("hat_habx", dout_of.get(), wo, 2e-5);
+                note("hat_habx (fused split-bf16 OCAB tail, partial tile) vs the two-kernel path");
             }
         }
 
