@@ -186,9 +186,17 @@ struct AttnxKRows {
     }
 };
 
-template <int D, bool MASKED>
-__device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned char* lds, int wi, int head,
-                                              const u32x4 (&qb)[2][3], int qpix)
+// O^T (with the softmax denominator in row D) of the lane's query over the
+// item's 256 keys. SAFE: the online softmax (the running base raised when a
+// score exceeds it by more than 8, in log2 units), as the reference subtracts
+// the row maximum (cpu.rs:801-812). Otherwise the base is 0: P = exp2(s)
+// straight from the scores, no maximum, no subtraction, no rescaling (16 VALU
+// a tile fewer); the caller checks the result and runs the SAFE form instead
+// when a sum could have overflowed or lost its range (see attnx_item_done).
+// Either way o / o[row D] is the softmax-weighted sum, the same quantity.
+template <int D, bool MASKED, bool SAFE>
+__device__ __forceinline__ f32x16 attnx_tiles(const AttnArgs& p, const unsigned char* lds, int wi,
+                                              const u32x4 (&qb)[2][3])
 {
     using X = AttnXShape<D>;
     constexpr int NKT = X::NK / 32;
@@ -211,7 +219,6 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
     const float madd[2][2] = {{(r_lo || c_lo) ? NEG : 0.0f, (r_lo || c_hi) ? NEG : 0.0f},
                               {(r_hi || c_lo) ? NEG : 0.0f, (r_hi || c_hi) ? NEG : 0.0f}};
     static_assert(D < 32, "a spare V^T row is needed");
-    constexpr int RH = (D % 8) / 4, RR = (D / 8) * 4 + D % 4;
 
     // The lane's V^T row (dims past D read row D: their outputs are not used)
     // and K rows.
@@ -222,7 +229,7 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
     f32x16 o;
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[i] = 0.0f;
-    float mrun = -INFINITY;
+    float mrun = SAFE ? -INFINITY : 0.0f;
 
 // unrolled: the K, V and bias addresses of every tile are immediate offsets
 #pragma unroll
@@ -238,16 +245,18 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
             s[i] = b;
         }
         s = kr.qk(kt * 32 * X::KS, qb, s);
-        float mx = -INFINITY;
+        if constexpr (SAFE) {
+            float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
-        if (kt == 0 || __any(mx > mrun + 8.0f)) {  // wave-uniform
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(mrun, mx);
-            const float corr = fast_exp2(mrun - mnew);
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+            if (kt == 0 || __any(mx > mrun + 8.0f)) {  // wave-uniform
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mnew = fmaxf(mrun, mx);
+                const float corr = fast_exp2(mrun - mnew);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[i] *= corr;
-            mrun = mnew;
+                for (int i = 0; i < 16; ++i) o[i] *= corr;
+                mrun = mnew;
+            }
         }
         // O^T += V^T P^T, P = exp2(S - base): the B operand of step st is
         // registers 8st .. 8st+7, split.
@@ -255,7 +264,7 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
         for (int st = 0; st < 2; ++st) {
             float pv[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(s[8 * st + j] - mrun);
+            for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(SAFE ? s[8 * st + j] - mrun : s[8 * st + j]);
             u32x4 pb[3], va[3];
             split3_x8(pv, pb);
 #pragma unroll
@@ -263,7 +272,33 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
             o = mfma6(va, pb, o);
         }
     }
+    return o;
+}
 
+// Whether an item's base-0 pass (attnx_tiles with SAFE false) may stand, for
+// every query of the wave: the denominator within [2^-60, 2^100] (no
+// overflow, and far from the range where P's split parts would underflow;
+// with the row maximum subtracted it lies in [1, 256 * 2^8]) and every
+// accumulator finite. Wave-uniform.
+template <int D>
+__device__ __forceinline__ bool attnx_item_done(const f32x16& o)
+{
+    constexpr int RH = (D % 8) / 4, RR = (D / 8) * 4 + D % 4;
+    const int ql = threadIdx.x & 31;
+    const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
+    bool ok = ltot >= 0x1p-60f && ltot <= 0x1p100f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ok = ok && __builtin_isfinite(o[i]);
+    return __all(ok);
+}
+
+// out[query][head * D + d] = O^T[d] / O^T[D] for the lane's query.
+template <int D>
+__device__ __forceinline__ void attnx_store(const AttnArgs& p, int head, int qpix, const f32x16& o)
+{
+    constexpr int RH = (D % 8) / 4, RR = (D / 8) * 4 + D % 4;
+    const int lane = threadIdx.x & 63;
+    const int ql = lane & 31, h = lane >> 5;
     const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
     const float inv = 1.0f / ltot;
     float* orow = p.out + (size_t)qpix * p.C + head * D;
@@ -280,6 +315,21 @@ __device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned 
                 if (d0 + j < D) orow[d0 + j] = o[i4 * 4 + j] * inv;
         }
     }
+}
+
+template <int D, bool MASKED>
+__device__ __forceinline__ void attnx_compute(const AttnArgs& p, const unsigned char* lds, int wi, int head,
+                                              const u32x4 (&qb)[2][3], int qpix)
+{
+    f32x16 o = attnx_tiles<D, MASKED, false>(p, lds, wi, qb);
+    if (!attnx_item_done<D>(o)) {  // wave-uniform
+        // the same LDS through an offset the compiler cannot see is zero, so
+        // that it does not keep the first pass's loaded values for this one
+        int z = 0;
+        asm volatile("" : "+s"(z));
+        o = attnx_tiles<D, MASKED, true>(p, lds + z, wi, qb);
+    }
+    attnx_store<D>(p, head, qpix, o);
 }
 
 template <int D>
@@ -411,8 +461,9 @@ __device__ __forceinline__ void attnx_oca_stash(unsigned short* Kp, unsigned sho
     }
 }
 
-// One part's key tiles onto the running (o, mrun) of the item.
-template <int D, int NK>
+// One part's key tiles onto the running (o, mrun) of the item; SAFE as in
+// attnx_tiles (without it the base stays 0 and mrun is not used).
+template <int D, int NK, bool SAFE>
 __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int part, const u32x4 (&qb)[2][3],
                                                   f32x16& o, float& mrun)
 {
@@ -441,22 +492,24 @@ __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int 
             s[i] = Tb[oca_base + key + 15 * ky];
         }
         s = kr.qk(kt * 32 * X::KS, qb, s);
-        float mx = -INFINITY;
+        if constexpr (SAFE) {
+            float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
-        if ((part == 0 && kt == 0) || __any(mx > mrun + 8.0f)) {  // wave-uniform
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(mrun, mx);
-            const float corr = fast_exp2(mrun - mnew);
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+            if ((part == 0 && kt == 0) || __any(mx > mrun + 8.0f)) {  // wave-uniform
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mnew = fmaxf(mrun, mx);
+                const float corr = fast_exp2(mrun - mnew);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[i] *= corr;
-            mrun = mnew;
+                for (int i = 0; i < 16; ++i) o[i] *= corr;
+                mrun = mnew;
+            }
         }
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             float pv[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(s[8 * st + j] - mrun);
+            for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(SAFE ? s[8 * st + j] - mrun : s[8 * st + j]);
             u32x4 pb[3], va[3];
             split3_x8(pv, pb);
 #pragma unroll
@@ -502,7 +555,8 @@ __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned cha
     f32x16 o;
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[i] = 0.0f;
-    float mrun = -INFINITY;
+    float mrun = 0.0f;
+    // the base-0 pass (see attnx_tiles)
 #pragma unroll 1
     for (int part = 0; part < X::NPART; ++part) {
         if (part > 0) {
@@ -511,7 +565,29 @@ __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned cha
         }
         attnx_oca_stash<D, NK>(Kp, Vp, ks, vs);
         __syncthreads();
-        attnx_oca_compute<D, NK>(lds, part, qb, o, mrun);
+        attnx_oca_compute<D, NK, false>(lds, part, qb, o, mrun);
+    }
+    // The parts are staged by the whole block, so the block redoes the item
+    // with the max-subtracted softmax if any of its waves needs it.
+    __shared__ int item_ok[8];
+    const bool ok = attnx_item_done<D>(o);
+    if (lane == 0) item_ok[threadIdx.x >> 6] = ok;
+    __syncthreads();  // also: every read of the last part's K and V is done
+    bool all_ok = true;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) all_ok = all_ok && item_ok[w];
+    if (!all_ok) {  // block-uniform
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+        mrun = -INFINITY;
+#pragma unroll 1
+        for (int part = 0; part < X::NPART; ++part) {
+            attnx_oca_fetch<D, NK>(p, wi, head, part, ks, vs);
+            if (part > 0) __syncthreads();  // every read of the previous part's K and V is done
+            attnx_oca_stash<D, NK>(Kp, Vp, ks, vs);
+            __syncthreads();
+            attnx_oca_compute<D, NK, true>(lds, part, qb, o, mrun);
+        }
     }
     const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
     const float inv = 1.0f / ltot;

@@ -71,6 +71,53 @@ def test_swmsa_matches_golden_and_oracle(hl, golden_manifest, weights_dir, varia
 
 
 @pytest.mark.parametrize("variant", ["hat", "hat-s"])
+def test_swmsa_scores_out_of_range_take_the_safe_softmax(hl, golden_manifest, weights_dir, variant):
+    """The attention kernels first run the softmax with base 0 (P = exp2(score),
+    no row maximum) and redo an item with the reference's max-subtracted online
+    softmax (cpu.rs:801-812) when a row's sum overflows or underflows. Relative
+    position bias tables shifted by +200 (heads 0, 1: every exp overflows) and
+    -200 (heads 2, 3: every exp underflows) force that path, heads 4, 5 keep
+    the fast one; with the shift mask. Against the oracle, which always
+    subtracts the maximum."""
+    import oracle
+    o = next(x for x in golden_manifest["ops"] if x["variant"] == variant)
+    A = _op_weights(weights_dir, o)
+    hh, ww, c = o["h"], o["w"], o["c"]
+    x = op_input(o["input_seed"], hh * ww, c)
+    p = "layers.0.residual_group.blocks.1.attn"
+    w = [A[p + n].copy() for n in (".qkv.weight", ".qkv.bias", ".proj.weight", ".proj.bias",
+                                   ".relative_position_bias_table")]
+    w[4][:, 0:2] += 200.0
+    w[4][:, 2:4] -= 200.0
+    _say(f"swmsa {variant} 32x32 shift 8 with out-of-range bias tables")
+    got, _, _ = hl.op_swmsa(x, hh, ww, c, 6, 8, *w)
+    orc = oracle.swmsa_op(x, hh, ww, c, 6, 8, *w)
+    assert np.isfinite(got).all()
+    assert np.abs(got - orc).max() < OP_TOL
+
+
+@pytest.mark.parametrize("variant", ["hat", "hat-s"])
+def test_ocab_scores_out_of_range_take_the_safe_softmax(hl, golden_manifest, weights_dir, variant):
+    """The overlapping cross-attention's base-0 softmax and its fallback (the
+    whole block redoes an item, all its key parts, with the maximum subtracted):
+    bias tables shifted by +200 (heads 0, 1) and -200 (heads 2, 3), against
+    the oracle."""
+    import oracle
+    o = next(x for x in golden_manifest["ops"] if x["variant"] == variant)
+    A = _op_weights(weights_dir, o)
+    hh, ww, c = o["h"], o["w"], o["c"]
+    x = op_input(o["input_seed"], hh * ww, c)
+    ws = [A["layers.0.residual_group.overlap_attn" + n].copy() for n in OCAB_NAMES]
+    ws[6][:, 0:2] += 200.0
+    ws[6][:, 2:4] -= 200.0
+    _say(f"ocab {variant} 32x32 with out-of-range bias tables")
+    got, _, _ = hl.op_ocab(x, hh, ww, c, 6, 2, ws)
+    orc = oracle.ocab_op(x, hh, ww, c, 6, 2, ws)
+    assert np.isfinite(got).all()
+    assert np.abs(got - orc).max() < OP_TOL
+
+
+@pytest.mark.parametrize("variant", ["hat", "hat-s"])
 def test_ocab_matches_golden_and_oracle(hl, golden_manifest, weights_dir, variant):
     import oracle
     o = next(x for x in golden_manifest["ops"] if x["variant"] == variant)
