@@ -99,7 +99,7 @@ def extra_configs(hat_amd, np, td, steps):
         tf = flop / (ams / 1e3) / 1e12
         out[f"cfg2_swmsa_shift{shift}"] = {
             "workload": "SW-MSA op 128x128 C=180 6 heads (qkv + attention + proj)",
-            "op_ms": round(ms, 4), "attn_kernel": "hat_attnx_sw_d30", "attn_ms": round(ams, 4),
+            "op_ms": round(ms, 4), "attn_kernel": "hat_attnx_swp_d30", "attn_ms": round(ams, 4),
             "attn_flop": flop, "attn_tflops": round(tf, 2), "attn_frac": round(tf / PEAK_FP32_MFMA, 4)}
     shapes = [(c,), (c,), (3 * c, c), (3 * c,), (c, c), (c,), (1521, heads), (c,), (c,),
               (2 * c, c), (2 * c,), (c, 2 * c), (c,)]
@@ -270,7 +270,7 @@ def main():
 
     T = h * w
     C = W.embed
-    attn_name = "hat_attnx_sw_d24" if W.head_dim == 24 else "hat_attnx_sw_d30"
+    attn_name = "hat_attnx_sw_d24" if W.head_dim == 24 else "hat_attnx_swp_d30"
     n_a, t_a = stats[attn_name]
     attn_ms = t_a / n_a
     attn_flop = 4.0 * T * 256 * C

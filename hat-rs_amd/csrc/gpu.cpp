@@ -921,7 +921,9 @@ void run_attn(hipStream_t s, const float* qkv, const float* table, float* out, c
     if (D == 24) {
         name = oca ? "hat_attnx_oca_d24" : "hat_attnx_sw_d24";
     } else if (D == 30) {
-        name = oca ? "hat_attnx_oca_d30" : "hat_attnx_sw_d30";
+        // SW in four parts of 64 keys (two blocks per CU; the whole-item form
+        // hat_attnx_sw_d30 needs 114 KB of LDS, one block per CU)
+        name = oca ? "hat_attnx_oca_d30" : "hat_attnx_swp_d30";
     } else {
         throw Error("attention: head_dim " + std::to_string(D) + " has no kernel (24 and 30 do)");
     }

@@ -379,14 +379,19 @@ __device__ __forceinline__ void attnx_item_kernel(const AttnArgs& p, unsigned ch
 // two barriers and computed. At most 80 KB of LDS and 128 VGPRs, so that two
 // blocks share a CU and one's staging overlaps the other's MFMAs.
 
-template <int D, int NK>
+// SW: the same part-wise staging for shifted-window attention (256 keys of the
+// rolled window, the shift mask on the last window row and column, the 961-row
+// table), which head_dim 30 needs for two blocks per CU: its whole item, K and
+// V^T in three planes, takes 114 KB of LDS, two parts of 128 keys 60 KB.
+template <int D, int NK, bool SW = false>
 struct AttnXOcaShape {
-    static_assert(576 % NK == 0 && NK % 32 == 0, "whole 32-key tiles, whole parts");
-    static constexpr int NPART = 576 / NK;
+    static constexpr int NKEYS = SW ? 256 : 576;
+    static_assert(NKEYS % NK == 0 && NK % 32 == 0, "whole 32-key tiles, whole parts");
+    static constexpr int NPART = NKEYS / NK;
     static constexpr int KS = D == 24 ? 24 : 40;
     static constexpr int VS = NK + 8;                 // V^T row stride: 16 rows of a phase on distinct banks
     static constexpr int KPL = NK * KS, VPL = (D + 1) * VS;
-    static constexpr int TROWS = 1521;
+    static constexpr int TROWS = SW ? 961 : 1521;
     static constexpr int LDS_BYTES = 2 * 3 * (KPL + VPL) + 4 * TROWS;
     static constexpr int U = D % 4 == 0 ? 4 : 2;       // floats per staging unit
     static constexpr int NE = (NK * D / U + 511) / 512;
@@ -394,12 +399,12 @@ struct AttnXOcaShape {
 };
 
 // This thread's share of part `part` of item (wi, head): K and V units.
-template <int D, int NK>
+template <int D, int NK, bool SW = false>
 __device__ __forceinline__ void attnx_oca_fetch(const AttnArgs& p, int wi, int head, int part,
-                                                typename AttnXOcaShape<D, NK>::vec (&ks)[AttnXOcaShape<D, NK>::NE],
-                                                typename AttnXOcaShape<D, NK>::vec (&vs)[AttnXOcaShape<D, NK>::NE])
+                                                typename AttnXOcaShape<D, NK, SW>::vec (&ks)[AttnXOcaShape<D, NK, SW>::NE],
+                                                typename AttnXOcaShape<D, NK, SW>::vec (&vs)[AttnXOcaShape<D, NK, SW>::NE])
 {
-    using X = AttnXOcaShape<D, NK>;
+    using X = AttnXOcaShape<D, NK, SW>;
     using vec = typename X::vec;
     constexpr int PER_KEY = D / X::U;
     const float* Kg = p.qkv + (size_t)(p.heads + head) * p.T * D;
@@ -410,7 +415,7 @@ __device__ __forceinline__ void attnx_oca_fetch(const AttnArgs& p, int wi, int h
         vec kv{}, vv{};
         if (e < NK * PER_KEY) {
             const int kl = e / PER_KEY, d = (e - kl * PER_KEY) * X::U;
-            const int pix = attn_key_pixel<true>(p, wi, part * NK + kl);
+            const int pix = attn_key_pixel<!SW>(p, wi, part * NK + kl);
             if (pix >= 0) {
                 kv = *(const vec*)(Kg + (size_t)pix * D + d);
                 vv = *(const vec*)(Vg + (size_t)pix * D + d);
@@ -421,12 +426,12 @@ __device__ __forceinline__ void attnx_oca_fetch(const AttnArgs& p, int wi, int h
     }
 }
 
-template <int D, int NK>
+template <int D, int NK, bool SW = false>
 __device__ __forceinline__ void attnx_oca_stash(unsigned short* Kp, unsigned short* Vp,
-                                                const typename AttnXOcaShape<D, NK>::vec (&ks)[AttnXOcaShape<D, NK>::NE],
-                                                const typename AttnXOcaShape<D, NK>::vec (&vs)[AttnXOcaShape<D, NK>::NE])
+                                                const typename AttnXOcaShape<D, NK, SW>::vec (&ks)[AttnXOcaShape<D, NK, SW>::NE],
+                                                const typename AttnXOcaShape<D, NK, SW>::vec (&vs)[AttnXOcaShape<D, NK, SW>::NE])
 {
-    using X = AttnXOcaShape<D, NK>;
+    using X = AttnXOcaShape<D, NK, SW>;
     constexpr int PER_KEY = D / X::U;
 #pragma unroll
     for (int i = 0; i < X::NE; ++i) {
@@ -519,11 +524,97 @@ __device__ __forceinline__ void attnx_oca_compute(const unsigned char* lds, int 
     }
 }
 
-template <int D, int NK>
+// One part of a shifted-window item (the SW form of attnx_oca_compute): the
+// keys part * NK .. + NK - 1 of the rolled window, bias and mask as attnx_tiles.
+template <int D, int NK, bool SAFE, bool MASKED>
+__device__ __forceinline__ void attnx_swp_compute(const AttnArgs& p, const unsigned char* lds, int wi, int part,
+                                                  const u32x4 (&qb)[2][3], f32x16& o, float& mrun)
+{
+    using X = AttnXOcaShape<D, NK, true>;
+    constexpr int NKT = NK / 32;
+    static_assert(NK % 16 == 0, "parts of whole window rows");
+    const unsigned short* Kp = (const unsigned short*)lds;
+    const unsigned short* Vp = Kp + 3 * X::KPL;
+    const float* Tb = (const float*)(Vp + 3 * X::VPL);
+    const int wy = wi / p.nx, wx = wi - (wi / p.nx) * p.nx;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in a scalar register
+    const int ql = lane & 31, h = lane >> 5;
+    const int q = wave * 32 + ql;
+    const int qy = q >> 4, qx = q & 15;
+    // the part's first key row: NK / 16 rows of 31 table entries each
+    const float* Tr = Tb + 960 - ((qy + 15) * 31 + qx + 15 - 4 * h) + part * (NK / 16) * 31;
+    const float NEG = -100.0f * HAT_LOG2E;
+    const bool mrow = MASKED && wy == p.ny - 1;
+    const bool mcol = MASKED && wx == p.nx - 1;
+    const bool r_lo = mrow && (qy & 8), r_hi = mrow && !(qy & 8);
+    const bool c_lo = mcol && (qx & 8), c_hi = mcol && !(qx & 8);
+    const float madd[2][2] = {{(r_lo || c_lo) ? NEG : 0.0f, (r_lo || c_hi) ? NEG : 0.0f},
+                              {(r_hi || c_lo) ? NEG : 0.0f, (r_hi || c_hi) ? NEG : 0.0f}};
+    const unsigned short* vrow = Vp + (ql < D ? ql : D) * X::VS + 8 * h;
+    AttnxKRows<D, X::KS, X::KPL> kr;
+    kr.init(Kp, ql, h);
+#pragma unroll 1
+    for (int kt = 0; kt < NKT; ++kt) {
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kl = kt * 32 + (i >> 2) * 8 + (i & 3);  // key within the part (lane half 0)
+            const int ky = kl >> 4, kx = kl & 15;
+            float b = Tr[ky * 31 + kx];
+            // the mask's row band: the key row within the window, part * NK / 16 + ky
+            if (MASKED) b += madd[((part * (NK / 16) + ky) >> 3) & 1][(kx >> 3) & 1];
+            s[i] = b;
+        }
+        s = kr.qk(kt * 32 * X::KS, qb, s);
+        if constexpr (SAFE) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+            if ((part == 0 && kt == 0) || __any(mx > mrun + 8.0f)) {  // wave-uniform
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mnew = fmaxf(mrun, mx);
+                const float corr = fast_exp2(mrun - mnew);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[i] *= corr;
+                mrun = mnew;
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(SAFE ? s[8 * st + j] - mrun : s[8 * st + j]);
+            u32x4 pb[3], va[3];
+            split3_x8(pv, pb);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) va[pl] = *(const u32x4*)(vrow + pl * X::VPL + kt * 32 + 16 * st);
+            o = mfma6(va, pb, o);
+        }
+    }
+}
+
+template <int D, int NK, bool SW = false>
 __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned char* lds)
 {
-    using X = AttnXOcaShape<D, NK>;
+    using X = AttnXOcaShape<D, NK, SW>;
     const int wi = blockIdx.x, head = blockIdx.y;
+    // SW: the windows of the last row and column of a shifted grid carry the mask
+    const bool masked = SW && p.shift > 0 && (wi / p.nx == p.ny - 1 || wi % p.nx == p.nx - 1);  // block-uniform
+    if constexpr (SW) {
+        // the CAB's gates ride on the SW launch, in its first block, as in
+        // attnx_item_kernel
+        if (p.with_gate && wi == 0 && head == 0) {  // block-uniform
+            static_assert(4 * CAB_GATE_LDS <= X::LDS_BYTES, "the gate's scratch fits the item LDS");
+            cab_gate_body<8>(p.gate, (float*)lds);
+            __syncthreads();
+        }
+        if (p.with_se && wi == 0 && head == 0) {  // block-uniform
+            static_assert(4 * SE_GATE_LDS <= X::LDS_BYTES, "the gate's scratch fits the item LDS");
+            se_gate_body<8>(p.se, (float*)lds);
+            __syncthreads();
+        }
+    }
     unsigned short* Kp = (unsigned short*)lds;
     unsigned short* Vp = Kp + 3 * X::KPL;
     float* Tb = (float*)(Vp + 3 * X::VPL);
@@ -546,11 +637,11 @@ __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned cha
     u32x4 qb[2][3];
     int qpix;
     {
-        attnx_oca_fetch<D, NK>(p, wi, head, 0, ks, vs);
-        AttnTableRegs<D, true> tr;
-        attn_table_load<D, true>(p, head, tr);
+        attnx_oca_fetch<D, NK, SW>(p, wi, head, 0, ks, vs);
+        AttnTableRegs<D, !SW> tr;
+        attn_table_load<D, !SW>(p, head, tr);
         qpix = attnx_query<D>(p, wi, head, qb);
-        attn_table_store<D, true>(Tb, tr);
+        attn_table_store<D, !SW>(Tb, tr);
     }
     f32x16 o;
 #pragma unroll
@@ -560,12 +651,18 @@ __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned cha
 #pragma unroll 1
     for (int part = 0; part < X::NPART; ++part) {
         if (part > 0) {
-            attnx_oca_fetch<D, NK>(p, wi, head, part, ks, vs);
+            attnx_oca_fetch<D, NK, SW>(p, wi, head, part, ks, vs);
             __syncthreads();  // every read of the previous part's K and V is done
         }
-        attnx_oca_stash<D, NK>(Kp, Vp, ks, vs);
+        attnx_oca_stash<D, NK, SW>(Kp, Vp, ks, vs);
         __syncthreads();
-        attnx_oca_compute<D, NK, false>(lds, part, qb, o, mrun);
+        if constexpr (SW) {
+            if (masked) attnx_swp_compute<D, NK, false, true>(p, lds, wi, part, qb, o, mrun);
+            else attnx_swp_compute<D, NK, false, false>(p, lds, wi, part, qb, o, mrun);
+        } else {
+            attnx_oca_compute<D, NK, false>(lds, part, qb, o, mrun);
+        }
+
     }
     // The parts are staged by the whole block, so the block redoes the item
     // with the max-subtracted softmax if any of its waves needs it.
@@ -582,11 +679,16 @@ __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned cha
         mrun = -INFINITY;
 #pragma unroll 1
         for (int part = 0; part < X::NPART; ++part) {
-            attnx_oca_fetch<D, NK>(p, wi, head, part, ks, vs);
+            attnx_oca_fetch<D, NK, SW>(p, wi, head, part, ks, vs);
             if (part > 0) __syncthreads();  // every read of the previous part's K and V is done
-            attnx_oca_stash<D, NK>(Kp, Vp, ks, vs);
+            attnx_oca_stash<D, NK, SW>(Kp, Vp, ks, vs);
             __syncthreads();
-            attnx_oca_compute<D, NK, true>(lds, part, qb, o, mrun);
+            if constexpr (SW) {
+                if (masked) attnx_swp_compute<D, NK, true, true>(p, lds, wi, part, qb, o, mrun);
+                else attnx_swp_compute<D, NK, true, false>(p, lds, wi, part, qb, o, mrun);
+            } else {
+                attnx_oca_compute<D, NK, true>(lds, part, qb, o, mrun);
+            }
         }
     }
     const float ltot = __shfl(o[RR], ql + 32 * RH, 64);
@@ -617,6 +719,19 @@ __device__ __forceinline__ void attnx_oca_kernel(const AttnArgs& p, unsigned cha
 
 ATTNX_OCA_INST(hat_attnx_oca_d24, 24, 192)
 ATTNX_OCA_INST(hat_attnx_oca_d30, 30, 96)
+
+// Shifted-window attention for head_dim 30 in two parts of 128 keys (60 KB of
+// LDS: two blocks per CU), the masked form for the windows of the last row
+// and column of a shifted grid.
+#define ATTNX_SWP_INST(NAME, D, NK)                                                                      \
+    extern "C" __global__ __launch_bounds__(512, 4) void NAME(AttnArgs p)                                \
+    {                                                                                                    \
+        static_assert(AttnXOcaShape<D, NK, true>::LDS_BYTES <= 80 * 1024, "two blocks per CU");          \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[AttnXOcaShape<D, NK, true>::LDS_BYTES]; \
+        attnx_oca_kernel<D, NK, true>(p, lds);                                                           \
+    }
+
+ATTNX_SWP_INST(hat_attnx_swp_d30, 30, 64)
 
 #define ATTNX_INST(NAME, D, OCC)                                                             \
     extern "C" __global__ __launch_bounds__(512, OCC) void NAME(AttnArgs p)                  \

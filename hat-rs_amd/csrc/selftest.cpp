@@ -195,8 +195,11 @@ int gpu_selftest(std::string* err)
                     p.T = T;
                     p.qscale = (float)(1.0 / std::sqrt((double)D) * 1.4426950408889634);
                     std::vector<double> want = attn_twin(qkv, tab, hp, wp, heads, D, oca, shift);
-                    // SW: the FP32-MFMA kernel and the split-bf16 one
-                    for (const char* fam : {oca ? "hat_attn_oca_d" : "hat_attn_sw_d", oca ? "hat_attnx_oca_d" : "hat_attnx_sw_d"}) {
+                    // the FP32-MFMA kernel and the split-bf16 ones (SW head_dim 30:
+                    // the whole-item form and the part-staged one the forward runs)
+                    for (const char* fam : {oca ? "hat_attn_oca_d" : "hat_attn_sw_d", oca ? "hat_attnx_oca_d" : "hat_attnx_sw_d",
+                                            oca ? "" : "hat_attnx_swp_d"}) {
+                        if (!*fam || (std::string(fam) == "hat_attnx_swp_d" && D != 30)) continue;
                         std::string k = std::string(fam) + std::to_string(D);
                         const bool xk = k.find("attnx") != std::string::npos;
                         if (!xk && attn_persistent(D, oca))  // 3 blocks, so a block walks several items
