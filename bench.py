@@ -23,6 +23,8 @@ Also reported on the same JSON line:
   * kernels: the same per-kernel event times for every kernel of the forward;
   * pcie: min / median wall time of a forward from and to host memory (the
     reference's Backend::forward shape), never the headline;
+  * host_peak_rss_mib: the process's peak resident set (VmHWM) after the
+    metric configuration's forwards, as the reference's bench reports it;
   * configs: benchmark configurations 2-5 of the plan as extra figures - the
     SW-MSA op (128 x 128, C = 180, shift 0 and 8) and the OCAB op with their
     head_dim-30 attention kernels' fractions of peak, HAT x4 at 256 x 256 and
@@ -67,6 +69,19 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def host_peak_rss_mib():
+    """The process's peak resident set (VmHWM), as the reference's bench reports it
+    beside the device working set (examples/bench.rs:85-100)."""
+    try:
+        with open("/proc/self/status") as f:
+            for line in f:
+                if line.startswith("VmHWM:"):
+                    return round(int(line.split()[1]) / 1024.0, 1)
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
 
 
 def stats_ms(samples):
@@ -332,6 +347,8 @@ def main():
     pcie["output_mpx_s_at_median"] = round(out_px / 1e6 / (pcie["median"] / 1e3), 3)
     acts_gib = round(be.acts_bytes() / 2**30, 3)
     weights_mib = round(be.weight_bytes() / 2**20, 2)
+    # before the extra configurations and the CPU oracle, which hold their own buffers
+    rss_mib = host_peak_rss_mib()
     d_in.free()
     d_out.free()
     be.close()
@@ -367,6 +384,7 @@ def main():
         "copy_kernel_gbps": round(copy_gbps, 1),
         "acts_gib": acts_gib,
         "weights_mib": weights_mib,
+        "host_peak_rss_mib": rss_mib,
         "device": hat_amd.device_name(),
         "configs": configs,
         "kernels": kernels,
