@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <atomic>
 #include <thread>
 
 #include "kargs.h"
@@ -726,11 +727,18 @@ int colsum_rows(int CO, int H, int W, int co_stride)
     return colsum_wide(CO, H, W, co_stride) ? (W / 16) * (H / 16) : (W / 16) * (H / 8);
 }
 
+// [band_r0, band_r1): with band_r1 >= 0, only that band of tile rows is
+// launched (the host-memory forward's head): 8 input rows of the Winograd
+// upsample conv (hat_convwino_n8_shuffle), 16 output rows of conv_last
+// (hat_conv_last3), the same band indices for the two since the shuffle
+// doubles the rows. Other convs are always whole planes.
 void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, int H, int W,
               float* out, int co_stride, int epi, int act, const float* res, float* partial,
-              int crop_h, int crop_w, float img_range, const float* mean)
+              int crop_h, int crop_w, float img_range, const float* mean, int band_r0, int band_r1)
 {
     if (H % 8 != 0 || W % 16 != 0) throw Error("conv: plane must be a multiple of 8x16");
+    const bool band = band_r1 >= 0;
+    if (band && (band_r0 < 0 || band_r0 >= band_r1)) throw Error("conv: empty band");
     if (cin_stride % 4 != 0 || cin_stride < C.CI) throw Error("conv: bad input channel stride");
     // The wide-tile kernel (16x16 pixels, a whole 64-, 96- or 128-channel
     // column block per block) for the head convs, the 60-channel CAB conv and
@@ -811,9 +819,16 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
             return;
         }
         if (epi == CEPI_SHUFFLE && C.r == 2 && C.CO == 256 && C.CI == 64 && co_stride >= 64) {
-            launch(s, "hat_convwino_n8_shuffle", 2 * tiles, 1, 1, 512, p);
+            unsigned nt = tiles;
+            if (band) {
+                if (band_r1 > H / 8) throw Error("conv: band past the plane");
+                p.tile0 = band_r0 * (W / 16);
+                nt = (unsigned)((band_r1 - band_r0) * (W / 16));
+            }
+            launch(s, "hat_convwino_n8_shuffle", 2 * nt, 1, 1, 512, p);
             return;
         }
+        if (band) throw Error("conv: only the Winograd upsample conv and conv_last run in bands");
         // the C = 180 family (the residual epilogue's planes are 180 wide)
         if (epi == CEPI_STORE && act == 2 && C.CO == 64 && C.CI == 180 && co_stride >= 64) {
             launch(s, "hat_convwino_n4_store180", tiles, 1, 1, 512, p);
@@ -833,6 +848,8 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
             return;
         }
     }
+    if (band && !(epi == CEPI_FINAL && C.CO == 3 && C.CI == 64 && C.CIp == 64 && cin_stride >= 64))
+        throw Error("conv: only the Winograd upsample conv and conv_last run in bands");
     if (wide) {
         launch(s, wide, (unsigned)((W / 16) * (H / 16)), (unsigned)((C.CO + wbn - 1) / wbn), 1,
                (unsigned)(wwaves * 64), p);
@@ -842,7 +859,14 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
         if (crop_h > H || crop_w > W || crop_h < 1 || crop_w < 1) throw Error("conv: bad crop");
         // conv_last 64 -> 3 by per-tap products, 16 x 32 output tiles
         if (C.CO == 3 && C.CI == 64 && C.CIp == 64 && cin_stride >= 64) {
-            launch(s, "hat_conv_last3", (unsigned)(((W + 31) / 32) * ((H + 15) / 16)), 1, 1, 512, p);
+            const int ntx = (W + 31) / 32, nty = (H + 15) / 16;  // 16 x 32 output tiles
+            unsigned nt = (unsigned)(ntx * nty);
+            if (band) {
+                if (band_r1 > nty) throw Error("conv: band past the plane");
+                p.tile0 = band_r0 * ntx;
+                nt = (unsigned)((band_r1 - band_r0) * ntx);
+            }
+            launch(s, "hat_conv_last3", nt, 1, 1, 512, p);
             return;
         }
     }
@@ -1176,6 +1200,9 @@ GpuBackend::~GpuBackend()
         free_batch();
         free_plan();
         for (void* p : owned_) rt.free(p);
+        for (hipEvent_t e : band_ev_) rt.api().EventDestroy(e);
+        for (hipEvent_t e : copy_ev_) rt.api().EventDestroy(e);
+        if (copy_stream_) rt.api().StreamDestroy(copy_stream_);
         rt.api().StreamDestroy(stream_);
     } catch (...) {
     }
@@ -1355,10 +1382,10 @@ void GpuBackend::mlp(const std::string& prefix, float* x, int epi, const std::st
 
 void GpuBackend::conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
                       int co_stride, int epi, int act, const float* res, float* partial,
-                      int crop_h, int crop_w)
+                      int crop_h, int crop_w, int band_r0, int band_r1)
 {
     run_conv(stream_, C, in, cin_stride, H, W, out, co_stride, epi, act, res, partial, crop_h,
-             crop_w, wt_.img_range, wt_.mean);
+             crop_w, wt_.img_range, wt_.mean, band_r0, band_r1);
 }
 
 void GpuBackend::attention(const std::string& table, bool oca, int shift, const CabGateArgs* gate,
@@ -1533,7 +1560,7 @@ void GpuBackend::forward_noalloc(int h, int w, const float* d_in, float* d_out)
 }
 
 // The forward on the current plan's buffers (a_, plan_).
-void GpuBackend::run_forward(int h, int w, const float* d_in, float* d_out)
+void GpuBackend::run_forward(int h, int w, const float* d_in, float* d_out, std::vector<std::pair<int, int>>* bands)
 {
     const long T = plan_.tokens();
     const int C = wt_.embed, H = plan_.hp, W = plan_.wp;
@@ -1590,15 +1617,58 @@ void GpuBackend::run_forward(int h, int w, const float* d_in, float* d_out)
     float* nxt = a_.head1;
     int hh = H, ww = W;
     const auto blocks = wt_.up_blocks();
+    const DevConv& last = conv_.at("conv_last");
+    const int oh = h * wt_.scale, ow = w * wt_.scale;
     for (size_t b = 0; b < blocks.size(); ++b) {
-        conv(conv_.at("upsample." + std::to_string(2 * b)), cur, feat, hh, ww, nxt, feat,
-             CEPI_SHUFFLE, 0);
+        const DevConv& up = conv_.at("upsample." + std::to_string(2 * b));
+        if (bands && b + 1 == blocks.size() && head_bands_fit(up, last, hh, ww, feat)) {
+            // The last upsample conv and conv_last over bands of tile rows
+            // (eighths of the plane, the last one split in two, so that the
+            // first download starts early and the last one is short),
+            // conv_last's band k after the upsample's band k + 1 (its halo
+            // row below), an event after each conv_last band.
+            const int R = hh / 8, step = (R + 7) / 8;  // at most 8 steps + the split: 10 bands
+            std::vector<int> bnd{0};
+            while (bnd.back() + step < R) bnd.push_back(bnd.back() + step);
+            if (R - bnd.back() >= 2) bnd.push_back(bnd.back() + (R - bnd.back()) / 2);
+            bnd.push_back(R);
+            const int nb = (int)bnd.size() - 1;
+            if (nb > (int)band_ev_.size()) throw Error("forward: too many output bands");
+            bands->clear();
+            conv(up, cur, feat, hh, ww, nxt, feat, CEPI_SHUFFLE, 0, nullptr, nullptr, 0, 0, bnd[0], bnd[1]);
+            for (int k = 0; k < nb; ++k) {
+                if (k + 1 < nb)
+                    conv(up, cur, feat, hh, ww, nxt, feat, CEPI_SHUFFLE, 0, nullptr, nullptr, 0, 0, bnd[k + 1],
+                         bnd[k + 2]);
+                conv(last, nxt, feat, 2 * hh, 2 * ww, d_out, 0, CEPI_FINAL, 0, nullptr, nullptr, oh, ow, bnd[k],
+                     bnd[k + 1]);
+                Runtime::get().check(Runtime::get().api().EventRecord(band_ev_[k], stream_), "hipEventRecord");
+                bands->emplace_back(std::min(oh, 16 * bnd[k]), std::min(oh, 16 * bnd[k + 1]));
+            }
+            return;
+        }
+        conv(up, cur, feat, hh, ww, nxt, feat, CEPI_SHUFFLE, 0);
         hh *= blocks[b].first;
         ww *= blocks[b].first;
         std::swap(cur, nxt);
     }
-    conv(conv_.at("conv_last"), cur, feat, hh, ww, d_out, 0, CEPI_FINAL, 0, nullptr, nullptr,
-         h * wt_.scale, w * wt_.scale);
+    conv(last, cur, feat, hh, ww, d_out, 0, CEPI_FINAL, 0, nullptr, nullptr, oh, ow);
+    if (bands) {
+        // one band: the whole output
+        if (band_ev_.empty()) throw Error("forward: no band events");
+        Runtime::get().check(Runtime::get().api().EventRecord(band_ev_[0], stream_), "hipEventRecord");
+        bands->assign(1, {0, oh});
+    }
+}
+
+// Whether the head's last upsample conv (input hh x ww) and conv_last run on
+// the kernels that take bands of tile rows: the Winograd x2 upsample and the
+// 64 -> 3 conv_last, whose 16-row tiles are the upsample's 8-row tiles doubled.
+bool GpuBackend::head_bands_fit(const DevConv& up, const DevConv& last, int hh, int ww, int feat) const
+{
+    return up.wu && up.r == 2 && up.CO == 256 && up.CI == 64 && feat == 64 && hh % 16 == 0 && ww % 16 == 0 &&
+           (size_t)hh * ww * feat < ((size_t)1 << 31) && (size_t)hh * ww * 4 * feat < ((size_t)1 << 31) &&
+           last.CO == 3 && last.CI == 64 && last.CIp == 64;
 }
 
 void GpuBackend::op_hab(int stage, int block, int hp, int wp, const float* x, float* out, int iters,
@@ -1742,27 +1812,30 @@ void GpuBackend::forward_batch(int n, int h, int w, const float* in, float* out)
 void GpuBackend::free_stage()
 {
     Runtime& rt = Runtime::get();
+    if (copy_stream_) rt.api().StreamSynchronize(copy_stream_);
     if (stage_in_) rt.api().HostFree(stage_in_);
     if (stage_out_) rt.api().HostFree(stage_out_);
-    for (hipEvent_t e : stage_ev_) rt.api().EventDestroy(e);
     stage_in_ = stage_out_ = nullptr;
     stage_in_n_ = stage_out_n_ = 0;
-    stage_ev_.clear();
 }
 
 namespace {
-// Output chunks of Backend::forward's download, and the host threads that copy
-// them out of pinned memory while later chunks are still on the bus.
-constexpr size_t kStageChunk = 2u << 20;  // bytes
+// Host threads of Backend::forward: each copies its share of the input into
+// pinned memory, and of every output band out of it.
 constexpr unsigned kStageThreads = 8;
+constexpr int kMaxBands = 10;
 }  // namespace
 
 // Backend::forward (backend.rs:29-36, gpu.rs:759-803): host [3][h][w] in, host
-// [3][h*s][w*s] out. The input goes up through a pinned buffer; the output comes
-// back into a pinned buffer in 2 MiB chunks, each with an event, and up to eight
-// host threads copy each chunk to `out` as soon as its event fires, so the
-// host-side copy runs beside the DMA instead of after it (a pageable hipMemcpy
-// stages through the runtime's own bounce buffers one piece at a time).
+// [3][h*s][w*s] out. Eight host threads copy the input into a pinned buffer
+// (each an eighth), which goes up in one DMA. The head's last convs run in
+// bands of output rows (run_forward), each band downloaded into a pinned buffer
+// on a second stream as soon as its event fires, while the GPU computes the
+// next bands; the threads copy each band to `out` as its download completes.
+// So the 50 MB download of a 512 x 512 x4 forward overlaps the last upsample
+// conv, and only the last band's download and copy (1/16 of the output) follow
+// the forward. (A pageable hipMemcpy would stage through the runtime's own
+// bounce buffers one piece at a time, after the whole forward.)
 void GpuBackend::forward(int h, int w, const float* in, float* out)
 {
     if (h <= 0 || w <= 0) throw Error(std::to_string(h) + "x" + std::to_string(w) + " is empty");
@@ -1770,49 +1843,92 @@ void GpuBackend::forward(int h, int w, const float* in, float* out)
     ensure_plan(h, w);
     Runtime& rt = Runtime::get();
     const HipApi& api = rt.api();
-    const size_t s2 = (size_t)wt_.scale * wt_.scale;
-    const size_t in_n = 3 * (size_t)h * w, out_n = in_n * s2;
-    const size_t out_bytes = out_n * sizeof(float);
-    const size_t chunks = (out_bytes + kStageChunk - 1) / kStageChunk;
-    if (stage_in_n_ != in_n || stage_out_n_ != out_n) {
+    const size_t oh = (size_t)h * wt_.scale, ow = (size_t)w * wt_.scale;
+    const size_t in_bytes = 3 * (size_t)h * w * sizeof(float), plane_bytes = oh * ow * sizeof(float);
+    if (stage_in_n_ != in_bytes || stage_out_n_ != 3 * plane_bytes) {
         free_stage();
-        rt.check(api.HostMalloc((void**)&stage_in_, in_n * sizeof(float), 0), "hipHostMalloc");
-        stage_in_n_ = in_n;
-        rt.check(api.HostMalloc((void**)&stage_out_, out_bytes, 0), "hipHostMalloc");
-        stage_out_n_ = out_n;
-        stage_ev_.assign(chunks, nullptr);
-        for (hipEvent_t& e : stage_ev_) rt.check(api.EventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+        rt.check(api.HostMalloc((void**)&stage_in_, in_bytes, 0), "hipHostMalloc");
+        stage_in_n_ = in_bytes;
+        rt.check(api.HostMalloc((void**)&stage_out_, 3 * plane_bytes, 0), "hipHostMalloc");
+        stage_out_n_ = 3 * plane_bytes;
     }
-    memcpy(stage_in_, in, in_n * sizeof(float));
-    rt.check(api.MemcpyAsync(a_.din, stage_in_, in_n * sizeof(float), hipMemcpyHostToDevice, stream_),
-             "hipMemcpyAsync H2D");
-    run_forward(h, w, a_.din, a_.dout);
-    for (size_t k = 0; k < chunks; ++k) {
-        const size_t off = k * kStageChunk, len = std::min(kStageChunk, out_bytes - off);
-        rt.check(api.MemcpyAsync((char*)stage_out_ + off, (const char*)a_.dout + off, len, hipMemcpyDeviceToHost,
-                                 stream_),
-                 "hipMemcpyAsync D2H");
-        rt.check(api.EventRecord(stage_ev_[k], stream_), "hipEventRecord");
+    if (!copy_stream_) rt.check(api.StreamCreate(&copy_stream_), "hipStreamCreate");
+    while (band_ev_.size() < (size_t)kMaxBands) {
+        hipEvent_t a = nullptr, b = nullptr;
+        rt.check(api.EventCreateWithFlags(&a, hipEventDisableTiming), "hipEventCreate");
+        band_ev_.push_back(a);
+        rt.check(api.EventCreateWithFlags(&b, hipEventDisableTiming), "hipEventCreate");
+        copy_ev_.push_back(b);
     }
-    // Thread t copies chunks t, t + n, ... in the order they arrive.
-    const unsigned n = (unsigned)std::min<size_t>(kStageThreads, chunks);
-    std::vector<hipError_t> err(n, hipSuccess);
+
+    constexpr unsigned T = kStageThreads;
+    std::vector<std::pair<int, int>> bands;  // output rows, in the order they are written
+    std::atomic<unsigned> in_done{0};
+    std::atomic<int> queued{0};  // 1: every band's download is queued; -1: queueing failed
+    std::vector<hipError_t> err(T, hipSuccess);
+    // thread t's share [a, b) of n bytes, in 64-byte units
+    auto share = [](size_t n, unsigned t) {
+        const size_t u = (n + 63) / 64;
+        return std::make_pair(std::min(n, u * t / T * 64), std::min(n, u * (t + 1) / T * 64));
+    };
+    auto copy_in = [&](unsigned t) {
+        const auto r = share(in_bytes, t);
+        memcpy((char*)stage_in_ + r.first, (const char*)in + r.first, r.second - r.first);
+        in_done.fetch_add(1, std::memory_order_release);
+    };
     auto copy_out = [&](unsigned t) {
-        for (size_t k = t; k < chunks; k += n) {
-            const hipError_t e = api.EventSynchronize(stage_ev_[k]);
+        int q;
+        while ((q = queued.load(std::memory_order_acquire)) == 0) std::this_thread::yield();
+        if (q < 0) return;
+        for (size_t k = 0; k < bands.size(); ++k) {
+            const hipError_t e = api.EventSynchronize(copy_ev_[k]);
             if (e != hipSuccess) {
                 err[t] = e;
                 return;
             }
-            const size_t off = k * kStageChunk, len = std::min(kStageChunk, out_bytes - off);
-            memcpy((char*)out + off, (const char*)stage_out_ + off, len);
+            const size_t row = ow * sizeof(float), len = (size_t)(bands[k].second - bands[k].first) * row;
+            const auto r = share(len, t);
+            for (int c = 0; c < 3; ++c) {
+                const size_t off = c * plane_bytes + (size_t)bands[k].first * row + r.first;
+                memcpy((char*)out + off, (const char*)stage_out_ + off, r.second - r.first);
+            }
         }
     };
+    auto worker = [&](unsigned t) {
+        copy_in(t);
+        copy_out(t);
+    };
     std::vector<std::thread> pool;
-    for (unsigned t = 1; t < n; ++t) pool.emplace_back(copy_out, t);
+    for (unsigned t = 1; t < T; ++t) pool.emplace_back(worker, t);
+    try {
+        copy_in(0);
+        while (in_done.load(std::memory_order_acquire) < T) std::this_thread::yield();
+        rt.check(api.MemcpyAsync(a_.din, stage_in_, in_bytes, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync H2D");
+        run_forward(h, w, a_.din, a_.dout, &bands);
+        for (size_t k = 0; k < bands.size(); ++k) {
+            rt.check(api.StreamWaitEvent(copy_stream_, band_ev_[k], 0), "hipStreamWaitEvent");
+            // the band's rows of the three planes: one 2D copy (a copy per
+            // plane measured 25-45 us apart on the copy engine)
+            const size_t row = ow * sizeof(float), len = (size_t)(bands[k].second - bands[k].first) * row;
+            const size_t off = (size_t)bands[k].first * row;
+            if (len > 0)
+                rt.check(api.Memcpy2DAsync((char*)stage_out_ + off, plane_bytes, (const char*)a_.dout + off,
+                                           plane_bytes, len, 3, hipMemcpyDeviceToHost, copy_stream_),
+                         "hipMemcpy2DAsync D2H");
+            rt.check(api.EventRecord(copy_ev_[k], copy_stream_), "hipEventRecord");
+        }
+    } catch (...) {
+        queued.store(-1, std::memory_order_release);
+        for (std::thread& th : pool) th.join();
+        api.StreamSynchronize(stream_);
+        api.StreamSynchronize(copy_stream_);
+        throw;
+    }
+    queued.store(1, std::memory_order_release);
     copy_out(0);
     for (std::thread& th : pool) th.join();
     rt.check(api.StreamSynchronize(stream_), "forward");
+    rt.check(api.StreamSynchronize(copy_stream_), "forward: download");
     for (hipError_t e : err) rt.check(e, "forward: download");
 }
 

@@ -193,10 +193,12 @@ private:
     void free_batch();
 
     // Backend::forward's host staging, kept for the plan: pinned input and
-    // output buffers and one event per output chunk.
+    // output buffers; the stream that downloads the output bands, an event per
+    // band on each stream (computed, downloaded).
     float *stage_in_ = nullptr, *stage_out_ = nullptr;
     size_t stage_in_n_ = 0, stage_out_n_ = 0;
-    std::vector<hipEvent_t> stage_ev_;
+    hipStream_t copy_stream_ = nullptr;
+    std::vector<hipEvent_t> band_ev_, copy_ev_;
     void free_stage();
 
     float* upload(const float* src, size_t n);
@@ -207,7 +209,12 @@ private:
     void upload_mlpx(const std::string& name);
     void ensure_plan(int h, int w);
     void free_plan();
-    void run_forward(int h, int w, const float* d_in, float* d_out);
+    // With bands: the output's row bands [y0, y1) in the order they are
+    // written, band_ev_[k] recorded on the stream after band k (the
+    // host-memory forward downloads each while later ones compute).
+    void run_forward(int h, int w, const float* d_in, float* d_out,
+                     std::vector<std::pair<int, int>>* bands = nullptr);
+    bool head_bands_fit(const DevConv& up, const DevConv& last, int hh, int ww, int feat) const;
 
     void layernorm(const float* x, float* y, const std::string& prefix, long rows);
     void gemm(const DevLinear& L, const float* a, int lda, long M, float* out, int ldo, int epi,
@@ -215,7 +222,7 @@ private:
               float* xn = nullptr, const std::string& norm = "");
     void conv(const DevConv& C, const float* in, int cin_stride, int H, int W, float* out,
               int co_stride, int epi, int act, const float* res = nullptr, float* partial = nullptr,
-              int crop_h = 0, int crop_w = 0);
+              int crop_h = 0, int crop_w = 0, int band_r0 = 0, int band_r1 = -1);
     void attention(const std::string& table, bool oca, int shift, const hatk::CabGateArgs* gate = nullptr,
                    const hatk::SeArgs* se = nullptr);
     void mlp(const std::string& prefix, float* x, int epi, const std::string& norm);

@@ -115,6 +115,7 @@ Runtime::Runtime()
     sym(l, api_.Free, "hipFree");
     sym(l, api_.Memcpy, "hipMemcpy");
     sym(l, api_.MemcpyAsync, "hipMemcpyAsync");
+    sym(l, api_.Memcpy2DAsync, "hipMemcpy2DAsync");
     sym(l, api_.MemGetInfo, "hipMemGetInfo");
     sym(l, api_.HostMalloc, "hipHostMalloc");
     sym(l, api_.HostFree, "hipHostFree");
@@ -125,6 +126,7 @@ Runtime::Runtime()
     sym(l, api_.EventCreateWithFlags, "hipEventCreateWithFlags");
     sym(l, api_.EventDestroy, "hipEventDestroy");
     sym(l, api_.EventRecord, "hipEventRecord");
+    sym(l, api_.StreamWaitEvent, "hipStreamWaitEvent");
     sym(l, api_.EventSynchronize, "hipEventSynchronize");
     sym(l, api_.EventElapsedTime, "hipEventElapsedTime");
 

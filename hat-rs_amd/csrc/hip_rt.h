@@ -42,12 +42,14 @@ struct HipApi {
     hipError_t (*Free)(void*);
     hipError_t (*Memcpy)(void*, const void*, size_t, hipMemcpyKind);
     hipError_t (*MemcpyAsync)(void*, const void*, size_t, hipMemcpyKind, hipStream_t);
+    hipError_t (*Memcpy2DAsync)(void*, size_t, const void*, size_t, size_t, size_t, hipMemcpyKind, hipStream_t);
     hipError_t (*MemGetInfo)(size_t*, size_t*);
     hipError_t (*HostMalloc)(void**, size_t, unsigned int);
     hipError_t (*HostFree)(void*);
     hipError_t (*StreamCreate)(hipStream_t*);
     hipError_t (*StreamDestroy)(hipStream_t);
     hipError_t (*StreamSynchronize)(hipStream_t);
+    hipError_t (*StreamWaitEvent)(hipStream_t, hipEvent_t, unsigned);
     hipError_t (*EventCreate)(hipEvent_t*);
     hipError_t (*EventCreateWithFlags)(hipEvent_t*, unsigned);
     hipError_t (*EventDestroy)(hipEvent_t);

@@ -146,6 +146,9 @@ struct ConvArgs {
     // bf16 parts, arranged [kc][xi 16][nt][part 3][lane 64][8] (lane r + 16 g:
     // co 16 nt + r, ci 32 kc + 8 g .. +7; channels padded to 16s and 32s)
     const unsigned short* wu;
+    // hat_convwino_* and hat_conv_last3 launched over a band of tile rows (the
+    // host-memory forward's head): the band's first tile; 0 for a whole plane
+    int tile0;
 };
 
 // Squeeze-excite gate: gate[c] = sigmoid(b2 + W2 relu(b1 + W1 mean)).

@@ -242,7 +242,8 @@ extern "C" __global__ __launch_bounds__(CL_WAVES * 64) void hat_conv_last3(ConvA
     const int ntx = (W + CL_TW - 1) / CL_TW;
     // Tiles are taken bottom row first: the conv before this one wrote its
     // bottom rows last, so those are the ones still in the last-level cache.
-    const int bt = (int)gridDim.x - 1 - (int)blockIdx.x;
+    // tile0: the first tile of a band of tile rows (0 for the whole plane)
+    const int bt = p.tile0 + (int)gridDim.x - 1 - (int)blockIdx.x;
     const int ty = bt / ntx, tx = bt - ty * ntx;
     const int y0 = ty * CL_TH, x0 = tx * CL_TW;
 

@@ -81,7 +81,8 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     // a tile's column blocks are consecutive blocks, so they read its patch
     // from L2 at about the same time
     constexpr int NCB = NTT / NT;
-    const int tile = (int)blockIdx.x / NCB, cb = (int)blockIdx.x - tile * NCB;
+    const int bt = (int)blockIdx.x / NCB, cb = (int)blockIdx.x - bt * NCB;
+    const int tile = p.tile0 + bt;  // tile0: a band's first tile (0 for the whole plane)
     const int y0 = (tile / tiles_x) * WG_TH;
     const int x0 = (tile % tiles_x) * WG_TW;
 

@@ -263,20 +263,32 @@ def test_plan_cache_and_determinism(hl, weights_dir):
     assert np.isfinite(ya1).all() and np.isfinite(yb).all()
 
 
-def test_host_forward_staging_equals_the_device_pass(hl, weights_dir):
-    """Backend::forward stages through pinned buffers and brings the output back
-    in 2 MiB chunks copied out by host threads: at outputs of 0.28, 1.5 and
-    7.14 chunks, alternating so that the staging
-    is rebuilt, the result is bit-identical to the device-resident pass of the
-    same input."""
-    wp = make_weights(weights_dir, "hat-s", 4, 31, [2])
+@pytest.mark.parametrize("variant,scale,sizes", [
+    # x4: the last upsample conv's input is 2h x 2w, its 8-row tile rows R = h / 4
+    # (padded), in bands of ceil(R / 8) with the last one halved: 300x260 -> R 76,
+    # bands 10 x 7, 3, 3, the last one cropped; 37x45 -> R 12, bands 2 x 5, 1, 1,
+    # the last two cropped away entirely (rows 148..148); 32x48 -> R 8, eight bands
+    # of 1; 128x128 -> R 32; the staging rebuilt in turn
+    ("hat-s", 4, [(300, 260), (37, 45), (32, 48), (128, 128), (300, 260)]),
+    # x2: one upsample conv, banded on the h x w plane (64x80: R 8; 17x33: R 4)
+    ("hat-s", 2, [(64, 80), (17, 33)]),
+    # x3: the r = 3 upsample has no banded kernel: one band after conv_last
+    ("hat", 3, [(48, 64)]),
+])
+def test_host_forward_staging_equals_the_device_pass(hl, weights_dir, variant, scale, sizes):
+    """Backend::forward stages the input through a pinned buffer filled by host
+    threads, runs the head's last upsample conv and conv_last in bands of output
+    rows and downloads each band on a second stream while later bands compute,
+    the threads copying each band out as it lands: the result is bit-identical to
+    the device-resident pass of the same input (whole-plane launches, one
+    stream), whatever the band split and the crop."""
+    wp = make_weights(weights_dir, variant, scale, 31, [2])
     W = hl.Weights(wp)
     be = hl.Backend(W)
     rng = np.random.default_rng(9)
-    # output bytes 3*16*h*w*4: 32x48 -> 0.28 chunks, 128x128 -> 1.5, 300x260 -> 7.14
-    for h, w in [(300, 260), (32, 48), (128, 128), (300, 260)]:
+    for h, w in sizes:
         img = rng.random((3, h, w), dtype=np.float32)
-        out = np.full((3, 4 * h, 4 * w), np.nan, dtype=np.float32)
+        out = np.full((3, scale * h, scale * w), np.nan, dtype=np.float32)
         got = be.forward(h, w, img, out)
         d_in = hl.DeviceBuffer(img.nbytes)
         d_out = hl.DeviceBuffer(out.nbytes)
@@ -284,7 +296,7 @@ def test_host_forward_staging_equals_the_device_pass(hl, weights_dir):
         be.forward_device(h, w, d_in.ptr, d_out.ptr)
         be.synchronize()
         want = d_out.download(np.empty_like(out))
-        _say(f"  staged forward {h}x{w}: {out.nbytes / 2**21:.2f} chunks")
+        _say(f"  staged forward {variant} x{scale} {h}x{w}")
         assert got is out and np.array_equal(got, want), (h, w)
         d_in.free()
         d_out.free()
