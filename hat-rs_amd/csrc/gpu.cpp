@@ -1569,7 +1569,29 @@ void GpuBackend::run_forward(int h, int w, const float* d_in, float* d_out, std:
     const DevConv& cf = conv_.at("conv_first");
     // With 144 channels the trunk convs carry the LayerNorm that follows them.
     const bool fused = convw_fits(cf);
-    if (fused) {
+    if ((C == 144 || C == 180) && cf.CI == 3 && cf.CIp == 16 && cf.CO == C && cf.r == 0 && H % 16 == 0 &&
+        W % 16 == 0) {
+        // conv_first + patch_embed.norm as one K = 27 GEMM (convfirst.hip)
+        ConvArgs p{};
+        p.in = a_.x0;
+        p.w = cf.w;
+        p.bias = cf.b;
+        p.out = a_.body;
+        p.xn = a_.xa;
+        p.nw = raw_.at("patch_embed.norm.weight");
+        p.nb = raw_.at("patch_embed.norm.bias");
+        p.H = H;
+        p.W = W;
+        p.CI = cf.CI;
+        p.CIp = cf.CIp;
+        p.cin_stride = 4;
+        p.CO = C;
+        p.COp = cf.COp;
+        p.co_stride = C;
+        p.eps = 1e-5f;
+        launch(stream_, C == 144 ? "hat_conv_first_ln144" : "hat_conv_first_ln180", (unsigned)((W / 16) * (H / 16)), 1,
+               1, 256, p);
+    } else if (fused) {
         run_convw(stream_, cf, a_.x0, 4, H, W, a_.body, EPI_STORE_LN, nullptr, a_.xa,
                   raw_.at("patch_embed.norm.weight"), raw_.at("patch_embed.norm.bias"));
     } else {

@@ -13,3 +13,4 @@
 #include "convw.hip"
 #include "convwino.hip"
 #include "misc.hip"
+#include "convfirst.hip"

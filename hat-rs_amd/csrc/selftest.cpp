@@ -851,9 +851,12 @@ int gpu_selftest(std::string* err)
         // LayerNorm, and a plain residual; 32 x 48 plane = 6 tiles.
         {
             // wino: the Winograd F(2x2, 3x3) kernels (8 x 16 tiles, 512 threads)
+            // the conv_first kernels (convfirst.hip): 16 x 16 tiles, 4 waves
             struct WCase { int CI, cin_stride, CO, epi; const char* k; int waves; bool wino; };
             const WCase wc[] = {{144, 144, 144, EPI_RESID_LN, "hat_convw_n9_resid_ln", CONVW_WAVES_N9_RESID_LN, false},
                                 {3, 4, 144, EPI_STORE_LN, "hat_convw_n9_store_ln", CONVW_WAVES_N9_STORE_LN, false},
+                                {3, 4, 144, EPI_STORE_LN, "hat_conv_first_ln144", 4, false},
+                                {3, 4, 180, EPI_STORE_LN, "hat_conv_first_ln180", 4, false},
                                 {144, 144, 144, EPI_RESID, "hat_convw_n9_resid", CONVW_WAVES_N9_RESID, false},
                                 {144, 144, 144, EPI_RESID, "hat_convwino_resid", 8, true}};
             for (const WCase& c : wc) {
@@ -892,7 +895,7 @@ int gpu_selftest(std::string* err)
                 p.eps = 1e-5f;
                 p.wu = (const unsigned short*)dwu.p;
                 if (c.wino) launch(s, c.k, (W / 16) * (H / 8), 1, 1, 512, p);
-                else launch(s, c.k, (W / 16) * (H / 16), 1, 1, c.waves * 64, p);
+                else launch(s, c.k, (W / 16) * (H / 16), 1, 1, c.waves * 64, p);  // convw and conv_first: 16 x 16
                 std::vector<double> want((size_t)HW * CO), wxn((size_t)HW * CO);
                 for (int y = 0; y < H; ++y)
                     for (int x = 0; x < W; ++x) {
