@@ -68,6 +68,31 @@ static void split_chunks(const float* w, int N, int K, int ldw, unsigned short* 
         }
 }
 
+// The last k-step of a K = 144 split linear in the packed form (common.h
+// ws_mma_half): only k = 128 .. 143 are real, so lane group g's slots j < 4
+// hold k = 128 + 4 g + j and slots 4 + j the same k, and the three planes hold
+// the part pairs (a0 | a0), (a1 | a0), (a1 | a2): against the activation pairs
+// (b0 | b1), (b0 | b2), (b1 | b0) they give the six products of order <= 2 in
+// three MFMAs. Row n of w (ldw apart) goes to row n of the chunk at dst, whose
+// planes are N * 32 elements apart.
+static void split_half_step(const float* w, int N, int ldw, unsigned short* dst)
+{
+    for (int n = 0; n < N; ++n)
+        for (int kk = 0; kk < 16; ++kk) {
+            const float x = w[(size_t)n * ldw + 128 + kk];
+            const unsigned short h0 = bf16_rne(x);
+            const float r1 = x - bf16_float(h0);
+            const unsigned short h1 = bf16_rne(r1);
+            const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+            const int g = kk / 4, j = kk % 4;
+            unsigned short* d = dst + (size_t)n * 32 + hatk::ws_slot(n, g) * 8 + j;
+            const size_t pl = (size_t)N * 32;
+            d[0] = h0, d[4] = h0;            // (a0 | a0)
+            d[pl] = h1, d[pl + 4] = h0;      // (a1 | a0)
+            d[2 * pl] = h1, d[2 * pl + 4] = h2;  // (a1 | a2)
+        }
+}
+
 std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K)
 {
     constexpr int BN = 144;
@@ -92,6 +117,27 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
     const int real = K == 144 ? 144 : 90, rows = K == 144 ? 144 : 96, ks_n = (K + 32) / 32;
     const size_t chunk = (size_t)3 * rows * 32;
     std::vector<unsigned short> out((size_t)(N / real) * ks_n * chunk, 0);
+    if (K == 144) {
+        // four whole k-steps, then k = 128 .. 143 packed (split_half_step);
+        // the bias is the accumulators' start value (hat_gemmx_qkv reads it)
+        for (int sl = 0; sl < N / real; ++sl) {
+            for (int n = 0; n < real; ++n)
+                for (int k = 0; k < 128; ++k) {
+                    const float x = w[((size_t)sl * real + n) * K + k];
+                    const unsigned short h0 = bf16_rne(x);
+                    const float r1 = x - bf16_float(h0);
+                    const unsigned short h1 = bf16_rne(r1);
+                    const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
+                    const int s = k / 32, g = (k % 32) / 8, j = k % 8;
+                    unsigned short* d = &out[((size_t)sl * ks_n + s) * chunk + (size_t)n * 32 + hatk::ws_slot(n, g) * 8 + j];
+                    d[0] = h0;
+                    d[(size_t)rows * 32] = h1;
+                    d[(size_t)2 * rows * 32] = h2;
+                }
+            split_half_step(w + (size_t)sl * real * K, real, K, &out[((size_t)sl * ks_n + 4) * chunk]);
+        }
+        return out;
+    }
     for (int n = 0; n < N; ++n)
         for (int k = 0; k <= K; ++k) {
             if (k == K && !bias) break;

@@ -90,6 +90,28 @@ __device__ __forceinline__ f32x4 mfma16x6(const u32x4 (&a)[3], const u32x4 (&b)[
     return mfma16_bf16(a[0], b[0], c);
 }
 
+// The packed last k-step of a K = 144 linear (the host's split_half_step):
+// the lane's four activations v (k = 128 + 4 lg + j) as the operand pairs
+// (b0 | b1), (b0 | b2), (b1 | b0), the weights' planes holding (a0 | a0),
+// (a1 | a0), (a1 | a2): three MFMAs give the six products of order <= 2 that
+// six give for a whole step, and the split covers four values, not eight.
+__device__ __forceinline__ void half_operands(const f32x4& v, u32x4 (&b)[3])
+{
+    unsigned p0a, p1a, p2a, p0b, p1b, p2b;
+    split3_pk(v[0], v[1], p0a, p1a, p2a);
+    split3_pk(v[2], v[3], p0b, p1b, p2b);
+    b[0] = (u32x4){p0a, p0b, p1a, p1b};
+    b[1] = (u32x4){p0a, p0b, p2a, p2b};
+    b[2] = (u32x4){p1a, p1b, p0a, p0b};
+}
+
+__device__ __forceinline__ f32x4 mfma16x3(const u32x4 (&a)[3], const u32x4 (&b)[3], f32x4 c)
+{
+    c = mfma16_bf16(a[2], b[2], c);  // a1 b1 + a2 b0
+    c = mfma16_bf16(a[1], b[1], c);  // a1 b0 + a0 b2
+    return mfma16_bf16(a[0], b[0], c);  // a0 b0 + a0 b1
+}
+
 // The same on v_mfma_f32_32x32x16_bf16 (lane l: row / column l % 32, k 8 (l / 32)
 // .. +7; D: column l % 32, rows 8 (i / 4) + 4 (l / 32) + i % 4).
 __device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c)

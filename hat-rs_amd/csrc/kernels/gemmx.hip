@@ -59,6 +59,12 @@ struct WcRows {
 #pragma unroll
             for (int j = 0; j < 2; ++j) dst[mt][j] = load_or_zero(rows[mt] + k0 + 4 * j, alive[mt] && k0 + 4 * j < K);
     }
+    // the packed last step of K = 144: channels 128 + 4 lg .. +3 (dst[mt][1] unused)
+    __device__ __forceinline__ void load_half(int lg, f32x4 (&dst)[MT][2]) const
+    {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) dst[mt][0] = load_or_zero(rows[mt] + 128 + 4 * lg, alive[mt]);
+    }
     __device__ __forceinline__ void load_b(int ks, int lg, f32x4 (&dst)[MT][2]) const
     {
         const int k0 = ks * 32 + lg * 8;
@@ -91,10 +97,14 @@ constexpr int gx_stage_stride(int hd) { return hd == 24 ? 48 : 100; }
 // NH: heads per slice (HD * NH <= 16 NT columns are real, the rest zero); MT:
 // 16-token tiles per subtile (each weight fragment read from LDS feeds MT
 // tiles, so MT sets the LDS bytes per MFMA).
+// K = 144 (HALF): the last step packed (half_operands, mfma16x3: k = 128 ..
+// 143, no bias column), the bias the accumulators' start value (Bs, the
+// slice's 144 columns in LDS); K = 180: the bias as column k = K.
 template <int K, int NT, int NS, int HD, int NH, int MT>
-__device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short* Wsl, float* Qs)
+__device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short* Wsl, float* Qs, float* Bs)
 {
-    constexpr int KS = (K + 32) / 32;             // 32-k steps, the bias column included
+    constexpr bool HALF = K == 144;
+    constexpr int KS = (K + 32) / 32;             // 32-k steps (the bias column or the packed step included)
     constexpr int ROWS = 16 * NT;                 // slice rows in LDS
     constexpr int CHUNK = 3 * ROWS * 32;          // one k-step: three bf16 planes [ROWS][32]
     constexpr int NLOAD = KS * CHUNK / 512;       // 1 KB loads
@@ -126,6 +136,8 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
         for (int i = wave; i < NLOAD; i += GX_WAVES)
             __builtin_amdgcn_global_load_lds((const void*)((const char*)src + (size_t)i * 1024 + loff),
                                              (__attribute__((address_space(3))) void*)(Wsl + i * 512), 16, 0, 0);
+        if (HALF)
+            for (int i = tid; i < 16 * NT; i += GX_WAVES * 64) Bs[i] = p.bias[sl * 16 * NT + i];
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();  // the slice is in LDS; no barrier after this one
     }
@@ -147,13 +159,21 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            for (int nt = 0; nt < NT; ++nt)
+                acc[mt][nt] = HALF ? *(const f32x4*)(Bs + 16 * nt + 4 * lg) : (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
+            const bool half = HALF && ks == KS - 1;  // compile-time: the loop is unrolled
             u32x4 xb[MT][3];
-            split_pre(y, xb);
+            if (half) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) half_operands(y[mt][0], xb[mt]);
+            } else {
+                split_pre(y, xb);
+            }
             if (ks + 1 < KS) {
-                xr.load_b(ks + 1, lg, y);
+                if (HALF && ks + 1 == KS - 1) xr.load_half(lg, y);
+                else xr.load_b(ks + 1, lg, y);
             } else {
                 // the next subtile's first k-step, or (past the last) this
                 // one's again: the loads are issued either way, so that their
@@ -176,7 +196,8 @@ __device__ __forceinline__ void gemmx_qkv_body(const GemmArgs& p, unsigned short
                         wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * 32 + pl * ROWS * 32);
                 }
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
+                for (int mt = 0; mt < MT; ++mt)
+                    acc[mt][nt] = half ? mfma16x3(wa[nt & 1], xb[mt], acc[mt][nt]) : mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
             }
         }
 #pragma unroll
@@ -243,12 +264,13 @@ extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv(Gem
 {
     __shared__ __attribute__((aligned(16))) unsigned short Wsl[5 * WS_CHUNK];  // the slice
     __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * gx_stage_stride(24)];  // per-wave staging
-    gemmx_qkv_body<144, 9, 3, 24, 6, 2>(p, Wsl, Qs);
+    __shared__ __attribute__((aligned(16))) float Bs[144];  // the slice's bias
+    gemmx_qkv_body<144, 9, 3, 24, 6, 2>(p, Wsl, Qs, Bs);
 }
 
 extern "C" __global__ __launch_bounds__(GX_WAVES * 64, 1) void hat_gemmx_qkv180(GemmArgs p)
 {
     __shared__ __attribute__((aligned(16))) unsigned short Wsl[6 * WS_CHUNK180];  // the slice
     __shared__ __attribute__((aligned(16))) float Qs[GX_WAVES * 16 * gx_stage_stride(30)];  // per-wave staging
-    gemmx_qkv_body<180, 6, 6, 30, 3, 3>(p, Wsl, Qs);
+    gemmx_qkv_body<180, 6, 6, 30, 3, 3>(p, Wsl, Qs, nullptr);
 }
