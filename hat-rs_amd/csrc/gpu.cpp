@@ -101,10 +101,12 @@ std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int
     std::vector<unsigned short> out((size_t)(N / BN) * steps * WC_CHUNK, 0);
     for (int sl = 0; sl < N / BN; ++sl) {
         unsigned short* dst = &out[(size_t)sl * steps * WC_CHUNK];
-        split_chunks(w + (size_t)sl * BN * K, BN, K, K, dst);
-        // the bias as column k = K (= 144: step 4, j = 16), split like the rest
-        if (bias) split_chunks(bias + (size_t)sl * BN, BN, 1, 1, dst, K);
+        // four whole k-steps, then k = 128 .. 143 packed (split_half_step);
+        // the tails add the bias in fp32
+        split_chunks(w + (size_t)sl * BN * K, BN, 128, K, dst);
+        split_half_step(w + (size_t)sl * BN * K, BN, K, dst + (size_t)4 * WC_CHUNK);
     }
+    (void)bias;
     return out;
 }
 
@@ -197,20 +199,26 @@ int mlpx_fused_channel(int k)
     return g == 0 && j == 4 ? -1 : -2;
 }
 
-void pack_mlp_xf(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w)
+void pack_mlp_xf(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
+                 std::vector<float>* b1x)
 {
-    constexpr int C = 144, H = 288, KP = 160;
-    std::vector<float> f1((size_t)MX_HID * KP);
+    // per third: fc1's steps 0..3 in the fused input order, step 4 (channels
+    // 128 .. 143, whose fused positions are 128 + 4 g + j) packed
+    // (split_half_step), b1 added in fp32 before the GELU (b1x, in the
+    // third's permuted row order), then fc2's three steps
+    constexpr int C = 144, H = 288, KF = 128;
+    std::vector<float> f1((size_t)MX_HID * KF), rows((size_t)MX_HID * C);
     w->assign((size_t)24 * WC_CHUNK, 0);
+    b1x->assign(H, 0.0f);
     for (int q = 0; q < H / MX_HID; ++q) {
         for (int row = 0; row < MX_HID; ++row) {
             const int u = q * MX_HID + mlpx_unit(row);
-            for (int k = 0; k < KP; ++k) {
-                const int c = mlpx_fused_channel(k);
-                f1[(size_t)row * KP + k] = c >= 0 ? w1[(size_t)u * C + c] : c == -1 ? b1[u] : 0.0f;
-            }
+            for (int k = 0; k < KF; ++k) f1[(size_t)row * KF + k] = w1[(size_t)u * C + mlpx_fused_channel(k)];
+            memcpy(&rows[(size_t)row * C], w1 + (size_t)u * C, C * sizeof(float));
+            (*b1x)[(size_t)q * MX_HID + row] = b1[u];
         }
-        split_chunks(f1.data(), MX_HID, KP, KP, &(*w)[(size_t)(8 * q) * WC_CHUNK]);
+        split_chunks(f1.data(), MX_HID, KF, KF, &(*w)[(size_t)(8 * q) * WC_CHUNK]);
+        split_half_step(rows.data(), MX_HID, C, &(*w)[(size_t)(8 * q + 4) * WC_CHUNK]);
         split_chunks(w2 + q * MX_HID, C, MX_HID, H, &(*w)[(size_t)(8 * q + 5) * WC_CHUNK]);
     }
 }
@@ -664,6 +672,7 @@ void run_tailx(hipStream_t s, bool cab, const DevLinear& proj, const DevMlpX& ml
         f.xn = nw ? xn : nullptr;
         f.w = proj.wx;
         f.wm = mlp.wf;
+        f.b1x = mlp.b1x;
         f.bias = bias;
         f.b2 = b2;
         f.w2gx = w2gx;
@@ -1110,8 +1119,10 @@ void GpuBackend::upload_mlpx(const std::string& name)
         pack_mlp_x(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
         m.C = 144;
         std::vector<unsigned short> wf;
-        pack_mlp_xf(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &wf);
+        std::vector<float> b1x;
+        pack_mlp_xf(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &wf, &b1x);
         m.wf = (unsigned short*)upload_bytes(wf.data(), wf.size() * sizeof(unsigned short));
+        m.b1x = upload(b1x.data(), b1x.size());
     } else if (t1.shape == std::vector<size_t>{360, 180} && t2.shape == std::vector<size_t>{180, 360}) {
         pack_mlp_x180(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
         m.C = 180;
@@ -2058,7 +2069,7 @@ struct OpLinear {
 // An op's MLP pre-split for hat_mlpx (C = 144) or hat_mlpx180 (C = 180), as
 // upload_mlpx packs it; other shapes leave m.w null (the FP32 kernels).
 struct OpMlpX {
-    std::unique_ptr<DevBuf> buf, fbuf;
+    std::unique_ptr<DevBuf> buf, fbuf, bbuf;
     DevMlpX m;
     OpMlpX(const float* w1, const float* b1, const float* w2, int c, size_t hid)
     {
@@ -2066,9 +2077,12 @@ struct OpMlpX {
         if (c == 144 && hid == 288) {
             pack_mlp_x(w1, b1, w2, &w);
             std::vector<unsigned short> wf;
-            pack_mlp_xf(w1, b1, w2, &wf);
+            std::vector<float> b1x;
+            pack_mlp_xf(w1, b1, w2, &wf, &b1x);
             fbuf = dev_u16(wf);
             m.wf = (unsigned short*)fbuf->p;
+            bbuf.reset(new DevBuf(b1x.data(), b1x.size()));
+            m.b1x = bbuf->p;
         }
         else if (c == 180 && hid == 360)
             pack_mlp_x180(w1, b1, w2, &w);

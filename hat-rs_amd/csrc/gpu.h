@@ -55,6 +55,7 @@ std::vector<unsigned short> pack_cab_conv1(const float* w);
 struct DevMlpX {
     unsigned short* w = nullptr;  // C = 144: 24 weight chunks (pack_mlp_x); 180: 48 (pack_mlp_x180)
     unsigned short* wf = nullptr;  // C = 144: the same in the fused tail's input order (pack_mlp_xf)
+    float* b1x = nullptr;          // C = 144: fc1's bias in the fused tail's row order (pack_mlp_xf)
     int C = 144;
 };
 
@@ -85,8 +86,11 @@ std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, in
 void pack_mlp_x(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
 // The same for the fused tails (hat_habx*), whose fc1 reads x' in the order a
 // lane holds the projection's accumulators: input position k = 32 ks + 8 g + j
-// is channel mlpx_fused_channel(k) (b1 at the position that returns -1).
-void pack_mlp_xf(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
+// of steps 0..3 is channel mlpx_fused_channel(k), step 4 (channels 128 ..
+// 143) is packed as the K = 144 linears' last step, and b1 comes back in b1x
+// (the thirds' permuted row order), added to fc1's output in fp32.
+void pack_mlp_xf(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
+                 std::vector<float>* b1x);
 int mlpx_fused_channel(int k);
 // The C = 180 projection [180][180] for hat_projx180*: six chunks (one per
 // 32-k step, k 180..191 zero) of three bf16 planes [192][32] (rows 180..191

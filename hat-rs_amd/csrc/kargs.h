@@ -311,6 +311,9 @@ struct TailXArgs {
     // hat_habx*: the MLP's 24 weight chunks in the fused input order (w holds
     // the projection's)
     const unsigned short* wm;
+    // hat_habx*: fc1's bias in the thirds' permuted row order (added to fc1's
+    // output before the GELU)
+    const float* b1x;
 };
 
 struct LnArgs {

@@ -161,8 +161,9 @@ __device__ __forceinline__ void wc_issue(unsigned short* dst, const unsigned sho
 // three planes [ROWS][32] (plane stride ROWS * 32), row r's four 16-byte
 // k-groups g stored at slot ws_slot(r, g), so that the fragment reads down the
 // rows at one k-group are free of bank conflicts without padding (a 192-row
-// chunk fits TX_BUF).
-template <int NT, int ROWS>
+// chunk fits TX_BUF). HALF: the packed last step of a K = 144 linear (xb from
+// half_operands, three MFMAs per tile).
+template <int NT, int ROWS, bool HALF = false>
 __device__ __forceinline__ void ws_mma(const unsigned short* Ws, int lr, int lg, const u32x4 (&xb)[2][3],
                                        f32x4 (&acc)[2][NT])
 {
@@ -179,7 +180,8 @@ __device__ __forceinline__ void ws_mma(const unsigned short* Ws, int lr, int lg,
                 wa[(nt + 1) & 1][pl] = *(const u32x4*)(wr + (nt + 1) * 16 * 32 + pl * ROWS * 32);
         }
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) acc[mt][nt] = mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
+        for (int mt = 0; mt < 2; ++mt)
+            acc[mt][nt] = HALF ? mfma16x3(wa[nt & 1], xb[mt], acc[mt][nt]) : mfma16x6(wa[nt & 1], xb[mt], acc[mt][nt]);
     }
 }
 

@@ -163,7 +163,8 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
         WcRows<144> ar;
         ar.init(p.a, mbase, M, lr);
 #pragma unroll
-        for (int ks = 0; ks < 5; ++ks) ar.load(ks, lg, y[ks]);
+        for (int ks = 0; ks < 4; ++ks) ar.load(ks, lg, y[ks]);
+        ar.load_half(lg, y[4]);  // the packed step: channels 128 + 4 lg .. +3
     }
     // conv2's B operand for k-step s: the 3x3 neighbourhood of t1 at this
     // lane's tokens, k = 32 s + 8 lg + j = tap*6 + ci (pairs of channels;
@@ -192,9 +193,15 @@ __device__ __forceinline__ void projx_body(const TailXArgs& p)
         __syncthreads();                // everyone's have, and everyone is done with chunk c - 1
         if (c + 1 < NCH) wc_issue<NL, TX_WAVES>(c & 1 ? Ws0 : Ws1, chunk(c + 1), wave, lane);
         u32x4 xb[2][3];
-        split_pre(c < 5 ? y[c < 5 ? c : 0] : t1v, xb);
+        if (c == 4) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) half_operands(y[4][mt][0], xb[mt]);
+        } else {
+            split_pre(c < 5 ? y[c < 5 ? c : 0] : t1v, xb);
+        }
         if (CAB && c >= 4 && c + 1 < NCH) gather_t1(c - 4, t1v);
-        ws_mma<9, 144>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
+        if (c == 4) ws_mma<9, 144, true>(Ws0, lr, lg, xb, acc);
+        else ws_mma<9, 144>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
     }
     tx_store_rows<144>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, p.xn);
 }
@@ -506,8 +513,11 @@ __device__ __forceinline__ void mlpx180_body(const TailXArgs& p)
 // hidden units comes from the same registers: fc1's input columns are packed
 // in the order a lane holds x' (pack_mlp_xf), so k-step ks of lane group g is
 // the lane's accumulator tiles 2 ks and 2 ks + 1, i.e. channels 32 ks + 4 g +
-// j and 32 ks + 16 + 4 g + j (j < 4), and in the last step channels 128 + 4 g
-// + j with the 1 of b1's column at lane group 0, j = 4. The first third forms
+// j and 32 ks + 16 + 4 g + j (j < 4), and the last step, channels 128 + 4 g
+// + j (j < 4), is packed (half_operands, common.h: slots 4..7 carry a second
+// part of the same four channels, three MFMAs instead of six); b1 (b1x) is
+// added to fc1's output before the GELU. The projection's last step (channels
+// 128 .. 143 of ao) is packed the same way. The first third forms
 // y = norm2(x') from them and leaves y in the output rows; the other two
 // thirds read y back (each lane reads exactly the addresses it wrote, so
 // program order is what makes the values visible) and need no norm; those
@@ -574,7 +584,8 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
             WcRows<144> ar;
             ar.init(p.a, mbase, M, lr);
 #pragma unroll
-            for (int ks = 0; ks < 5; ++ks) ar.load(ks, lg, y[ks]);
+            for (int ks = 0; ks < 4; ++ks) ar.load(ks, lg, y[ks]);
+            ar.load_half(lg, y[4]);  // the packed step: channels 128 + 4 lg .. +3
         }
         auto gather_t1 = [&](int s, f32x4 (&dst)[2][2]) {
 #pragma unroll
@@ -602,9 +613,15 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
             if (c + 1 < NCH) wc_issue<NLP, TX_WAVES>(c & 1 ? Ws0 : Ws1, pchunk(c + 1), wave, lane);
             else wc_issue<NL1, TX_WAVES>(Ws1, p.wm, wave, lane);  // the MLP's first chunk
             u32x4 xb[2][3];
-            split_pre(c < 5 ? y[c < 5 ? c : 0] : t1v, xb);
+            if (c == 4) {
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) half_operands(y[4][mt][0], xb[mt]);
+            } else {
+                split_pre(c < 5 ? y[c < 5 ? c : 0] : t1v, xb);
+            }
             if (CAB && c >= 4 && c + 1 < NCH) gather_t1(c - 4, t1v);
-            ws_mma<9, 144>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
+            if (c == 4) ws_mma<9, 144, true>(Ws0, lr, lg, xb, acc);
+            else ws_mma<9, 144>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
         }
     }
     // x' = acc + bias, kept in acc; norm2's statistics from it
@@ -631,7 +648,7 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
     // y = LN2(x') in the fused order for k-step ks: third 0 forms it from the
     // registers and leaves it in the output rows (the lane's own channels, in
     // place of x', which stays in acc), thirds 1 and 2 read it back; the last
-    // step's second half is b1's 1 (lane group 0) or zeros
+    // (packed) step uses only the first half
     float* yrow[2];
     bool yalive[2];
 #pragma unroll
@@ -644,8 +661,7 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             dst[mt][0] = *(const f32x4*)(yalive[mt] ? yrow[mt] + 32 * ks : hat_zero_row);
-            dst[mt][1] = *(const f32x4*)(yalive[mt] && ks < 4 ? yrow[mt] + 32 * ks + 16
-                                                               : (ks == 4 && lg == 0 ? hat_one_row : hat_zero_row));
+            dst[mt][1] = *(const f32x4*)(yalive[mt] && ks < 4 ? yrow[mt] + 32 * ks + 16 : hat_zero_row);
         }
     };
     // fc2 over a third's units from registers: chunks 5..7 of the third
@@ -658,12 +674,16 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
             if (s < 2) wc_issue<NL2, TX_WAVES>(s & 1 ? Ws0 : Ws1, wq + (size_t)(6 + s) * WC_CHUNK, wave, lane);
             else if (q < 2) wc_issue<NL1, TX_WAVES>(Ws1, wq + (size_t)8 * WC_CHUNK, wave, lane);
             if (s == 0) {
+                // + b1 (the lane's four units of each tile, in the third's
+                // permuted row order), then GELU
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
+                for (int nt = 0; nt < 6; ++nt) {
+                    const f32x4 b = *(const f32x4*)(p.b1x + q * MX_HID + 16 * nt + 4 * lg);
 #pragma unroll
-                    for (int nt = 0; nt < 6; ++nt)
+                    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) h[mt][nt][j] = gelu(h[mt][nt][j]);
+                        for (int j = 0; j < 4; ++j) h[mt][nt][j] = gelu(h[mt][nt][j] + b[j]);
+                }
             }
             u32x4 xb[2][3];
 #pragma unroll
@@ -703,8 +723,15 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
                 *(f32x4*)yr = pre[mt][0];
                 if (ks < 4) *(f32x4*)(yr + (yalive[mt] ? 16 : 4)) = pre[mt][1];
             }
-            split_pre(pre, xb);
-            ws_mma<6, MX_HID>(ks & 1 ? Ws0 : Ws1, lr, lg, xb, h);
+            if (ks == 4) {
+                // the packed step: channels 128 + 4 g + j (pre[mt][0])
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) half_operands(pre[mt][0], xb[mt]);
+                ws_mma<6, MX_HID, true>(ks & 1 ? Ws0 : Ws1, lr, lg, xb, h);
+            } else {
+                split_pre(pre, xb);
+                ws_mma<6, MX_HID>(ks & 1 ? Ws0 : Ws1, lr, lg, xb, h);
+            }
         }
         fc2_third(0, wq, h);
     }
@@ -717,24 +744,30 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
         f32x4 h[2][6];
 #pragma unroll
         for (int nt = 0; nt < 6; ++nt) h[0][nt] = h[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        auto fc1_step = [&](int ks, auto parv) {
-            constexpr int PAR = decltype(parv)::value;  // = ks & 1
+        auto fc1_step = [&](int ks, auto parv, auto halfv) {
+            constexpr int PAR = decltype(parv)::value;     // = ks & 1
+            constexpr bool HALF = decltype(halfv)::value;  // ks = 4: the packed step
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             if (ks < 4) wc_issue<NL1, TX_WAVES>(PAR ? Ws1 : Ws0, wq + (size_t)(ks + 1) * WC_CHUNK, wave, lane);
             else wc_issue<NL2, TX_WAVES>(Ws0, wq + (size_t)5 * WC_CHUNK, wave, lane);
             u32x4 xb[2][3];
-            split_pre(pre, xb);
+            if (HALF) {
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) half_operands(pre[mt][0], xb[mt]);
+            } else {
+                split_pre(pre, xb);
+            }
             if (ks < 4) load_y(ks + 1, pre);
             else if (q < 2) load_y(0, pre);
-            ws_mma<6, MX_HID>(PAR ? Ws0 : Ws1, lr, lg, xb, h);
+            ws_mma<6, MX_HID, HALF>(PAR ? Ws0 : Ws1, lr, lg, xb, h);
         };
 #pragma unroll 1
         for (int ks = 0; ks < 4; ks += 2) {
-            fc1_step(ks, CInt<0>{});
-            fc1_step(ks + 1, CInt<1>{});
+            fc1_step(ks, CInt<0>{}, CInt<0>{});
+            fc1_step(ks + 1, CInt<1>{}, CInt<0>{});
         }
-        fc1_step(4, CInt<0>{});
+        fc1_step(4, CInt<0>{}, CInt<1>{});
         fc2_third(q, wq, h);
     }
     tx_store_rows<144>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);

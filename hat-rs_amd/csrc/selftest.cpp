@@ -741,8 +741,10 @@ int gpu_selftest(std::string* err)
                 // as the forward runs them (out over the block input, the next
                 // norm over norm2's rows); 12 row tiles of 128.
                 std::vector<unsigned short> pwx = pack_linear_x(wp.data(), nullptr, C, C), mwx, mwf;
+                std::vector<float> mb1x;
                 pack_mlp_x(f1.data(), fb1.data(), f2.data(), &mwx);
-                pack_mlp_xf(f1.data(), fb1.data(), f2.data(), &mwf);
+                pack_mlp_xf(f1.data(), fb1.data(), f2.data(), &mwf, &mb1x);
+                Dev dmb1x(mb1x);
                 Dev dpwx(std::vector<float>((pwx.size() + 1) / 2)), dmwx(std::vector<float>((mwx.size() + 1) / 2)),
                     dmwf(std::vector<float>((mwf.size() + 1) / 2)), dout_x(res), dxn_x((size_t)T * C),
                     dout_f(res), dxn_f((size_t)T * C);
@@ -794,6 +796,7 @@ int gpu_selftest(std::string* err)
                 xf.out = dout_f.p;
                 xf.xn = dxn_f.p;
                 xf.wm = (const unsigned short*)dmwf.p;
+                xf.b1x = dmb1x.p;
                 xf.b2 = dfb2.p;
                 xf.inw = dnw.p;
                 xf.inb = dnb.p;
@@ -835,6 +838,7 @@ int gpu_selftest(std::string* err)
                 xof.out = dout_of.p;
                 xof.xn = nullptr;
                 xof.wm = (const unsigned short*)dmwf.p;
+                xof.b1x = dmb1x.p;
                 xof.b2 = dfb2.p;
                 xof.inw = dnw.p;
                 xof.inb = dnb.p;
