@@ -317,12 +317,16 @@ std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int
 // [kc][xi][nt][part][lane][8]: lane r + 16 g of (kc, xi, nt) holds part `part`
 // of U[xi][16 nt + r][32 kc + 8 g .. +7]; channels past CO and CI are zero
 // (CO padded to 16s, CI to 32s). With r > 0 the output channels are permuted
-// as pack_conv permutes them.
+// as pack_conv permutes them. When the last chunk holds at most 16 real
+// channels (CI = 144), it is packed as the K = 144 linears' last step
+// (split_half_step): lane r + 16 g, slots j < 4 hold channel 32 kc + 4 g + j,
+// slots 4 + j the same channel, the parts as (0 | 0), (1 | 0), (1 | 2).
 std::vector<unsigned short> pack_wino(const float* w, int CO, int CI, int r)
 {
     if (r > 0 && CO % 16 != 0) throw Error("pack_wino: shuffled output channels must come in 16s");
     static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
     const int NTT = (CO + 15) / 16, NKC = (CI + 31) / 32, Cf = r > 0 ? CO / (r * r) : 0;
+    const bool packed = CI % 32 != 0 && CI % 32 <= 16;  // the kernels' PACK
     std::vector<unsigned short> out((size_t)NKC * 16 * NTT * 3 * 512, 0);
     for (int o2 = 0; o2 < CO; ++o2) {
         int o = o2;
@@ -343,6 +347,14 @@ std::vector<unsigned short> pack_wino(const float* w, int CO, int CI, int r)
                     const unsigned short h1 = bf16_rne(r1);
                     const unsigned short h2 = bf16_rne(r1 - bf16_float(h1));
                     const int xi = 4 * i + j, kc = ci / 32, c32 = ci % 32, nt = o2 / 16, rr = o2 % 16;
+                    if (packed && kc == NKC - 1) {
+                        const int lane = rr + 16 * (c32 / 4);
+                        const size_t at = ((((size_t)kc * 16 + xi) * NTT + nt) * 3 * 64 + lane) * 8 + c32 % 4;
+                        out[at] = h0, out[at + 4] = h0;
+                        out[at + 512] = h1, out[at + 512 + 4] = h0;
+                        out[at + 1024] = h1, out[at + 1024 + 4] = h2;
+                        continue;
+                    }
                     const int lane = rr + 16 * (c32 / 8);
                     const size_t at = ((((size_t)kc * 16 + xi) * NTT + nt) * 3 * 64 + lane) * 8 + c32 % 8;
                     out[at] = h0;

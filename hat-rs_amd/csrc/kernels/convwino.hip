@@ -65,6 +65,11 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
                   "residual, store, shuffle or column-sum epilogues");
     static_assert(NTT % NT == 0 && 16 * NTT >= CO && 16 * (NTT - 1) < CO, "the column blocks cover CO");
     static_assert(32 * NKC >= CI && 32 * (NKC - 1) < CI && CI % 4 == 0, "the 32-channel chunks cover CI");
+    // PACK: the last chunk holds at most 16 real channels (CI = 144), so it is
+    // packed as the K = 144 linears' last step (common.h half_operands, the
+    // host's pack_wino): each lane forms V for four channels (quad lg), and
+    // three MFMAs per step give the six products.
+    constexpr bool PACK = CI % 32 != 0 && CI % 32 <= 16;
     __shared__ __attribute__((aligned(16))) float Pb0[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Pb1[WG_SLOTS * 4];
     __shared__ __attribute__((aligned(16))) float Ms0[16 * 32 * WG_MS];
@@ -192,6 +197,7 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         constexpr bool LAST = decltype(lastc)::value;
         const float* B = Q ? Pb1 : Pb0;
         const int kn = LAST ? kc : kc + 1;
+        constexpr bool HALF = PACK && LAST;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             u32x4 vb[2][3];
@@ -199,8 +205,9 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
             for (int nt2 = 0; nt2 < 2; ++nt2) {
                 float f[8];
 #pragma unroll
-                for (int hq = 0; hq < 2; ++hq) {
-                    const float* P = B + pbase[nt2] + hq * WG_PPX * 4;
+                for (int hq = 0; hq < (HALF ? 1 : 2); ++hq) {
+                    // HALF: quad lg (the lane's four channels), not 2 lg + hq
+                    const float* P = B + pbase[nt2] + (HALF ? -lg : hq) * WG_PPX * 4;
                     const int c0 = e == 0 ? 0 : 2, c1 = c0 + 1;
                     const f32x4 r0 = *(const f32x4*)(P + uoff[c0][0]) + sr * *(const f32x4*)(P + uoff[c0][1]);
                     const f32x4 r1 = *(const f32x4*)(P + uoff[c1][0]) + sr * *(const f32x4*)(P + uoff[c1][1]);
@@ -208,14 +215,17 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) f[4 * hq + j] = v[j];
                 }
-                split3_x8(f, vb[nt2]);
+                if (HALF) half_operands((f32x4){f[0], f[1], f[2], f[3]}, vb[nt2]);
+                else split3_x8(f, vb[nt2]);
             }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const int t = e * NT + nt;
                 if (!LAST && t == 0) fetch(kc + 1, CInt<Q ^ 1>{});
 #pragma unroll
-                for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = mfma16x6(ur[t % 2].v, vb[nt2], acc[e][nt][nt2]);
+                for (int nt2 = 0; nt2 < 2; ++nt2)
+                    acc[e][nt][nt2] = HALF ? mfma16x3(ur[t % 2].v, vb[nt2], acc[e][nt][nt2])
+                                           : mfma16x6(ur[t % 2].v, vb[nt2], acc[e][nt][nt2]);
                 // step t + 2's load into the slot step t's MFMAs have read (the
                 // step count per chunk is even, so slot t % 2 lines up across
                 // chunks)
