@@ -93,7 +93,7 @@ static void split_half_step(const float* w, int N, int ldw, unsigned short* dst)
         }
 }
 
-std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K)
+std::vector<unsigned short> pack_linear_x(const float* w, int N, int K)
 {
     constexpr int BN = 144;
     if (K != 144 || N % BN != 0) throw Error("pack_linear_x: needs K = 144 and N a multiple of 144");
@@ -106,7 +106,6 @@ std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int
         split_chunks(w + (size_t)sl * BN * K, BN, 128, K, dst);
         split_half_step(w + (size_t)sl * BN * K, BN, K, dst + (size_t)4 * WC_CHUNK);
     }
-    (void)bias;
     return out;
 }
 
@@ -1114,7 +1113,7 @@ void GpuBackend::upload_linear(const std::string& name)
     if ((L.K == 180 && L.N == 540 && ends(".qkv")) || (L.K == 144 && ((L.N == 432 && ends(".qkv")) || (L.N == 144 && ends("proj"))))) {
         // qkv: the weight-stationary layout of hat_gemmx_qkv; proj: streamed chunks (tailx)
         std::vector<unsigned short> x = ends(".qkv") ? pack_linear_ws(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K)
-                                                     : pack_linear_x(wt_.t(name + ".weight"), wt_.t(name + ".bias"), L.N, L.K);
+                                                     : pack_linear_x(wt_.t(name + ".weight"), L.N, L.K);
         L.wx = (unsigned short*)upload_bytes(x.data(), x.size() * sizeof(unsigned short));
     }
     lin_[name] = L;
@@ -2068,7 +2067,7 @@ struct OpLinear {
         if (sp == kQkv && ((N == 432 && K == 144) || (N == 540 && K == 180)))
             xs = pack_linear_ws(wt, bias, N, K);
         else if (sp == kProj && N == 144 && K == 144)
-            xs = pack_linear_x(wt, bias, N, K);
+            xs = pack_linear_x(wt, N, K);
         else if (sp == kProj && N == 180 && K == 180)
             xs = pack_linear_x180(wt);
         if (!xs.empty()) {

@@ -71,12 +71,15 @@ std::vector<float> pack_linear(const float* w, int N, int K, int* Kp);
 // [N][144] -> per 144-row slice, five weight chunks (one per 32-k step) of
 // three bf16 planes [144][32] (k-groups swizzled as in pack_linear_ws): w =
 // p0 + p1 + p2, each part the round-to-nearest bf16 of what the earlier ones
-// leave; the bias (if given) as column k = 144, split the same way; the rest
-// of k 144..159 zero.
-std::vector<unsigned short> pack_linear_x(const float* w, const float* bias, int N, int K);
-// The same split for hat_gemmx_qkv's weight-stationary slices: per 144-row
-// slice five chunks of three planes [144][32], each row's 16-byte k-groups
-// swizzled (ws_slot), WS_CHUNK elements apart; bias at k = 144.
+// leave; the fifth step (k = 128..143) packed, two parts per MFMA operand
+// (split_half_step). The tails add the bias in fp32.
+std::vector<unsigned short> pack_linear_x(const float* w, int N, int K);
+// The same split for hat_gemmx_qkv's weight-stationary slices: per slice
+// (144 rows at K = 144, 96 at 180) five or six chunks of three planes
+// [rows][32], each row's 16-byte k-groups swizzled (ws_slot), WS_CHUNK
+// elements apart. K = 144: the fifth step packed as in pack_linear_x, the bias
+// not in the chunks (the kernel starts its accumulators from it); K = 180: the
+// bias at k = 180.
 std::vector<unsigned short> pack_linear_ws(const float* w, const float* bias, int N, int K);
 // The C = 144 MLP (fc1 [288][144] + b1, fc2 [144][288]) for hat_mlpx: per
 // third of the hidden layer eight weight chunks - five of fc1's 96 rows (b1

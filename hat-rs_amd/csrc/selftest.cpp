@@ -740,7 +740,7 @@ int gpu_selftest(std::string* err)
                 // The split-bf16 tails (tailx.hip) on the same inputs, in place
                 // as the forward runs them (out over the block input, the next
                 // norm over norm2's rows); 12 row tiles of 128.
-                std::vector<unsigned short> pwx = pack_linear_x(wp.data(), nullptr, C, C), mwx, mwf;
+                std::vector<unsigned short> pwx = pack_linear_x(wp.data(), C, C), mwx, mwf;
                 std::vector<float> mb1x;
                 pack_mlp_x(f1.data(), fb1.data(), f2.data(), &mwx);
                 pack_mlp_xf(f1.data(), fb1.data(), f2.data(), &mwf, &mb1x);
