@@ -279,6 +279,44 @@ void pack_mlp_x180(const float* w1, const float* b1, const float* w2, std::vecto
     }
 }
 
+// Fused C = 180 tail input position k = 32 ks + 8 g + j (ks < 6: 32-k step, g:
+// lane group, j < 8) -> channel of x': the lane's accumulator tiles 2 ks and
+// 2 ks + 1 (channels 32 ks + 4 g + j and 32 ks + 16 + 4 g + j - 4); -1 past
+// channel 179. The device twin is habx180_channel (tailx.hip).
+int mlpx180_fused_channel(int k)
+{
+    const int ks = k >> 5, g = (k >> 3) & 3, j = k & 7;
+    const int c = 32 * ks + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+    return c < 180 ? c : -1;
+}
+
+void pack_mlp_xf180(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
+                    std::vector<float>* b1x)
+{
+    // per part: fc1's six steps with rows permuted by mlpx_unit and input
+    // columns in the fused order, b1 in b1x (the same row order, added in
+    // fp32 before the GELU), then fc2's two steps as in pack_mlp_x180
+    constexpr int C = 180, H = 360, NP = 6;
+    w->assign((size_t)8 * NP * MX180_SLOT, 0);
+    b1x->assign((size_t)NP * MX180_HID, 0.0f);
+    for (int q = 0; q < NP; ++q) {
+        for (int r = 0; r < MX180_HID; ++r) {
+            const int u = q * MX180_HID + mlpx_unit(r);
+            if (u < H) (*b1x)[(size_t)q * MX180_HID + r] = b1[u];
+        }
+        for (int ks = 0; ks < 6; ++ks)
+            split_ws_step(MX180_HID, [&](int r, int kk) {
+                const int u = q * MX180_HID + mlpx_unit(r), c = mlpx180_fused_channel(ks * 32 + kk);
+                return u < H && c >= 0 ? w1[(size_t)u * C + c] : 0.0f;
+            }, &(*w)[(size_t)(8 * q + ks) * MX180_SLOT]);
+        for (int st = 0; st < 2; ++st)
+            split_ws_step(192, [&](int n, int kk) {
+                const int u = q * MX180_HID + st * 32 + kk;
+                return n < C && u < H ? w2[(size_t)n * H + u] : 0.0f;
+            }, &(*w)[(size_t)(8 * q + 6 + st) * MX180_SLOT]);
+    }
+}
+
 // [CO][CI][3][3] -> [CIp/16][9][COp][16]; with r > 0 the output channels are
 // permuted so that channel o = c*r*r + i*r + j lands at o' = (i*r + j)*Cf + c
 // (Cf = CO / r^2), which lets the conv store four consecutive o' as four
@@ -1137,6 +1175,12 @@ void GpuBackend::upload_mlpx(const std::string& name)
     } else if (t1.shape == std::vector<size_t>{360, 180} && t2.shape == std::vector<size_t>{180, 360}) {
         pack_mlp_x180(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &w);
         m.C = 180;
+        std::vector<unsigned short> wf;
+        std::vector<float> b1x;
+        pack_mlp_xf180(wt_.t(name + ".fc1.weight"), wt_.t(name + ".fc1.bias"), wt_.t(name + ".fc2.weight"), &wf,
+                       &b1x);
+        m.wf = (unsigned short*)upload_bytes(wf.data(), wf.size() * sizeof(unsigned short));
+        m.b1x = upload(b1x.data(), b1x.size());
     } else {
         return;
     }
@@ -1436,6 +1480,45 @@ void run_mlpx180(hipStream_t s, const DevMlpX& m, const float* b2, const float* 
     launch(s, nw ? "hat_mlpx180_ln" : "hat_mlpx180", (unsigned)wx_tiles((int)M), 1, 1, WX_THREADS, q);
 }
 
+// The C = 180 tail: with the fused weights and a form hat_habx180* has (the
+// HAB's with the unfolded CAB's gated conv2 output aux and the next norm, the
+// OCAB's with neither) one kernel with x' kept on the chip; otherwise the
+// projection writes x' (hat_projx180*) and the MLP forms norm2(x') from the
+// rows it reads (hat_mlpx180*). out may alias res.
+void run_tailx180(hipStream_t s, const DevLinear& proj, const DevMlpX& mlp, const float* b2, const float* ao,
+                  const float* res, float* out, float* xn, const float* n2w, const float* n2b, const float* aux,
+                  const float* gate, float cscale, const float* nw, const float* nb, long M)
+{
+    if (!proj.wx || proj.K != 180 || proj.N != 180 || mlp.C != 180)
+        throw Error("tailx180: needs the pre-split C = 180 projection and MLP");
+    if (M > 0x7fffffffL) throw Error("tailx180: too many rows");
+    if (mlp.wf && mlp.b1x && (aux != nullptr) == (nw != nullptr)) {
+        TailXArgs f{};
+        f.a = ao;
+        f.res = res;
+        f.out = out;
+        f.xn = nw ? xn : nullptr;
+        f.w = proj.wx;
+        f.wm = mlp.wf;
+        f.b1x = mlp.b1x;
+        f.bias = proj.b;
+        f.b2 = b2;
+        f.aux = aux;
+        f.gate = gate;
+        f.cscale = cscale;
+        f.inw = n2w;
+        f.inb = n2b;
+        f.nw = nw;
+        f.nb = nb;
+        f.M = (int)M;
+        f.eps = 1e-5f;
+        launch(s, aux ? "hat_habx180_hab_ln" : "hat_habx180", (unsigned)wx_tiles((int)M), 1, 1, WX_THREADS, f);
+        return;
+    }
+    run_projx180(s, proj, ao, res, out, nullptr, n2w, n2b, aux, gate, cscale, M);
+    run_mlpx180(s, mlp, b2, n2w, n2b, out, xn, nw, nb, M);
+}
+
 void GpuBackend::mlp(const std::string& prefix, float* x, int epi, const std::string& norm)
 {
     GemmEpilogue e;
@@ -1512,14 +1595,12 @@ void GpuBackend::hab(int stage, int block, float* x_in, float* x_out, const std:
     const DevLinear& proj = lin_.at(p + ".attn.proj");
     auto mx = mlpx_.find(p + ".mlp");
     if (proj.wx && C == 180 && mx != mlpx_.end() && mx->second.C == 180) {
-        // split-bf16: projection + gated conv branch + shortcut (x' only), then
-        // the MLP, which forms norm2(x') from the x' rows, + residual + next norm
-        run_projx180(stream_, proj, a_.ao, x_in, x_out, nullptr, raw_.at(p + ".norm2.weight"),
-                     raw_.at(p + ".norm2.bias"), a_.t2, a_.gate, wt_.conv_scale, T);
-        run_mlpx180(stream_, mx->second, lin_.at(p + ".mlp.fc2").b, raw_.at(p + ".norm2.weight"),
-                    raw_.at(p + ".norm2.bias"), x_out, a_.xn,
-                    next_norm.empty() ? nullptr : raw_.at(next_norm + ".weight"),
-                    next_norm.empty() ? nullptr : raw_.at(next_norm + ".bias"), T);
+        // split-bf16: projection + gated conv branch + shortcut, norm2, the
+        // MLP + residual + next norm
+        run_tailx180(stream_, proj, mx->second, lin_.at(p + ".mlp.fc2").b, a_.ao, x_in, x_out, a_.xn,
+                     raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"), a_.t2, a_.gate, wt_.conv_scale,
+                     next_norm.empty() ? nullptr : raw_.at(next_norm + ".weight"),
+                     next_norm.empty() ? nullptr : raw_.at(next_norm + ".bias"), T);
         return;
     }
     gemm(proj, a_.ao, C, T, x_out, C, EPI_HAB_LN, x_in, a_.t2, a_.gate, a_.xn, p + ".norm2");
@@ -1552,10 +1633,8 @@ void GpuBackend::ocab(int stage, float* x)
         return;
     }
     if (proj.wx && C == 180 && mx != mlpx_.end() && mx->second.C == 180) {
-        run_projx180(stream_, proj, a_.ao, x, x, nullptr, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"),
-                     nullptr, nullptr, 0.0f, T);
-        run_mlpx180(stream_, mx->second, fc2.b, raw_.at(p + ".norm2.weight"), raw_.at(p + ".norm2.bias"), x, nullptr,
-                    nullptr, nullptr, T);
+        run_tailx180(stream_, proj, mx->second, fc2.b, a_.ao, x, x, nullptr, raw_.at(p + ".norm2.weight"),
+                     raw_.at(p + ".norm2.bias"), nullptr, nullptr, 0.0f, nullptr, nullptr, T);
         return;
     }
     gemm(proj, a_.ao, C, T, x, C, EPI_RESID_LN, x, nullptr, nullptr, a_.xn, p + ".norm2");
@@ -2084,21 +2163,21 @@ struct OpMlpX {
     DevMlpX m;
     OpMlpX(const float* w1, const float* b1, const float* w2, int c, size_t hid)
     {
-        std::vector<unsigned short> w;
+        std::vector<unsigned short> w, wf;
+        std::vector<float> b1x;
         if (c == 144 && hid == 288) {
             pack_mlp_x(w1, b1, w2, &w);
-            std::vector<unsigned short> wf;
-            std::vector<float> b1x;
             pack_mlp_xf(w1, b1, w2, &wf, &b1x);
-            fbuf = dev_u16(wf);
-            m.wf = (unsigned short*)fbuf->p;
-            bbuf.reset(new DevBuf(b1x.data(), b1x.size()));
-            m.b1x = bbuf->p;
-        }
-        else if (c == 180 && hid == 360)
+        } else if (c == 180 && hid == 360) {
             pack_mlp_x180(w1, b1, w2, &w);
-        else
+            pack_mlp_xf180(w1, b1, w2, &wf, &b1x);
+        } else {
             return;
+        }
+        fbuf = dev_u16(wf);
+        m.wf = (unsigned short*)fbuf->p;
+        bbuf.reset(new DevBuf(b1x.data(), b1x.size()));
+        m.b1x = bbuf->p;
         m.C = c;
         buf = dev_u16(w);
         m.w = (unsigned short*)buf->p;
@@ -2218,8 +2297,8 @@ void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int m
                 run_tailx(s, false, proj.L, mx.m, fc2.L.b, dao.p, dx.p, dwork.p, dxn.p, nullptr, nullptr, proj.L.b,
                           d2w.p, d2b.p, nullptr, nullptr, hp, wp);
             } else if (proj.L.wx && mx.m.w && c == 180) {
-                run_projx180(s, proj.L, dao.p, dx.p, dwork.p, nullptr, d2w.p, d2b.p, nullptr, nullptr, 0.f, (long)T);
-                run_mlpx180(s, mx.m, fc2.L.b, d2w.p, d2b.p, dwork.p, nullptr, nullptr, nullptr, (long)T);
+                run_tailx180(s, proj.L, mx.m, fc2.L.b, dao.p, dx.p, dwork.p, nullptr, d2w.p, d2b.p, nullptr, nullptr, 0.f,
+                             nullptr, nullptr, (long)T);
             } else {
                 run_gemm(s, proj.L, dao.p, c, (long)T, dwork.p, c, EPI_RESID_LN, resid_ln, heads, D, 0.f);
                 run_mlp(s, fc1.L, fc2.L, dxn.p, (long)T, dwork.p, dwork.p, EPI_RESID, none, dh.p);

@@ -54,8 +54,8 @@ std::vector<unsigned short> pack_cab_conv1(const float* w);
 // hat_mlpx's weights: the packed slices and b1 in fc1's row order.
 struct DevMlpX {
     unsigned short* w = nullptr;  // C = 144: 24 weight chunks (pack_mlp_x); 180: 48 (pack_mlp_x180)
-    unsigned short* wf = nullptr;  // C = 144: the same in the fused tail's input order (pack_mlp_xf)
-    float* b1x = nullptr;          // C = 144: fc1's bias in the fused tail's row order (pack_mlp_xf)
+    unsigned short* wf = nullptr;  // the same in the fused tail's input order (pack_mlp_xf, pack_mlp_xf180)
+    float* b1x = nullptr;          // fc1's bias in the fused tail's row order (pack_mlp_xf, pack_mlp_xf180)
     int C = 144;
 };
 
@@ -104,6 +104,14 @@ std::vector<unsigned short> pack_linear_x180(const float* w);
 // part of MX180_HID hidden units six fc1 chunks (64 permuted rows, b1 as
 // their column k = 180) then two fc2 chunks (192 rows), 48 chunks in all.
 void pack_mlp_x180(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w);
+// The same for the fused C = 180 tails (hat_habx180*), whose fc1 reads x' in
+// the order a lane holds the projection's accumulators: input position k =
+// 32 ks + 8 g + j is channel mlpx180_fused_channel(k) (zero where that is -1),
+// and b1 comes back in b1x (the parts' permuted row order), added to fc1's
+// output in fp32.
+void pack_mlp_xf180(const float* w1, const float* b1, const float* w2, std::vector<unsigned short>* w,
+                    std::vector<float>* b1x);
+int mlpx180_fused_channel(int k);
 // Winograd U = G g G^T of a 3x3 conv [CO][CI][3][3] (formed in double), split
 // into three bf16 parts in the layout convwino.hip streams:
 // [32-channel chunk][point][16-channel tile][part][lane][8].

@@ -17,7 +17,7 @@ const std::vector<std::string>& required_kernels()
     static const std::vector<std::string> k = {
         "hat_attn_sw_d24",     "hat_attn_sw_d30",     "hat_attn_oca_d24",   "hat_attn_oca_d30",
         "hat_attnx_sw_d24",    "hat_attnx_sw_d30",    "hat_attnx_oca_d24",  "hat_attnx_oca_d30",
-        "hat_gemmx_qkv", "hat_gemmx_qkv180", "hat_mlpx180_ln", "hat_mlpx180", "hat_projx180_hab", "hat_projx180",       "hat_projx_cab",       "hat_projx",          "hat_mlpx_ln", "hat_habx_cab_ln", "hat_habx", "hat_attnx_swp_d30",
+        "hat_gemmx_qkv", "hat_gemmx_qkv180", "hat_mlpx180_ln", "hat_mlpx180", "hat_projx180_hab", "hat_projx180",       "hat_projx_cab",       "hat_projx",          "hat_mlpx_ln", "hat_habx_cab_ln", "hat_habx", "hat_habx180_hab_ln", "hat_habx180", "hat_attnx_swp_d30",
         "hat_mlpx", "hat_conv_first_ln144", "hat_conv_first_ln180",
         "hat_conv_n1_store",   "hat_conv_n3_store",   "hat_conv_n4_store",  "hat_conv_n3_resid",
         "hat_conv_n3_colsum",  "hat_conv_n4_shuffle", "hat_conv_n1_final", "hat_conv_last3",

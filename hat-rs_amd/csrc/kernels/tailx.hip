@@ -773,6 +773,233 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
     tx_store_rows<144>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
 }
 
+// The whole second half of a block in one kernel, C = 180 (HAB with the
+// unfolded CAB's gated conv2 output p.aux, or OCAB): hat_projx180(_hab)
+// followed by hat_mlpx180(_ln) with x' kept on the chip, as hat_habx* keeps it
+// at C = 144. x' is the projection's accumulators (2 x 12 tiles), which stay
+// in registers as the MLP's residual. fc1's input columns are packed in the
+// order a lane holds x' (pack_mlp_xf180): k-step ks of lane group g is the
+// lane's tiles 2 ks and 2 ks + 1, channels 32 ks + 4 g + j and 32 ks + 16 +
+// 4 g + j (j < 4); positions past channel 179 (tile 11 outside lane group 0)
+// are zero, and b1 (b1x) is added to fc1's output before the GELU. Part 0 of
+// the hidden layer forms y = norm2(x') from the registers and leaves it in the
+// output rows, each lane at its own channels; parts 1..5 read it back (each
+// lane the addresses it wrote, after a full wait) and need no norm; the result
+// overwrites those rows at the end.
+//
+// The projection's six chunks alternate buffers 0, 1, ... and end in buffer
+// 1, so the MLP's first chunk goes to buffer 0 during the last one and the MLP
+// keeps hat_mlpx180's parities (a part's even chunks in buffer 0).
+
+// fused input position k = 32 ks + 8 g + j -> channel of x' (-1: an empty
+// position, channel >= 180)
+__device__ __forceinline__ int habx180_channel(int k)
+{
+    const int ks = k >> 5, g = (k >> 3) & 3, j = k & 7;
+    const int c = 32 * ks + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+    return c < 180 ? c : -1;
+}
+
+template <bool HAB, bool LN>
+__device__ __forceinline__ void habx180_body(const TailXArgs& p)
+{
+    constexpr int C = 180, NT = 12, NP = 6, NLP = 36, NL1 = 12, NL2 = 36;
+    static_assert(NLP * 512 == MX180_SLOT && NL1 * 512 == 3 * MX180_HID * 32 && MX180_SLOT <= TX_BUF, "chunk loads");
+    __shared__ __attribute__((aligned(16))) unsigned short Ws0[TX_BUF];
+    __shared__ __attribute__((aligned(16))) unsigned short Ws1[TX_BUF];
+    __shared__ __attribute__((aligned(16))) float Cp[2 * 192];  // the projection's bias, gate * cscale (zero past 180)
+    __shared__ __attribute__((aligned(16))) float Cs[3 * 192];  // b2, next norm w, b (the epilogue's)
+    // norm2's w and b over fc1's 192 input positions in the fused order
+    // (zeros at the empty ones)
+    __shared__ __attribute__((aligned(16))) float Cn[2 * 192];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in a scalar register
+    const int lr = lane & 15, lg = lane >> 4;
+    const int M = p.M;
+    if ((int)blockIdx.x * TX_ROWS >= M) return;  // whole block, before any barrier
+    wc_issue<NLP, TX_WAVES>(Ws0, p.w, wave, lane);
+    for (int i = tid; i < 2 * 192; i += TX_WAVES * 64) {
+        const int c = i < 192 ? i : i - 192;
+        Cp[i] = c >= C ? 0.0f : i < 192 ? p.bias[c] : (HAB ? p.gate[c] * p.cscale : 0.0f);
+    }
+    for (int i = tid; i < 3 * 192; i += TX_WAVES * 64) {
+        const int part = i / 192, c = i - part * 192;
+        Cs[i] = c >= C ? 0.0f : part == 0 ? p.b2[c] : (LN ? (part == 1 ? p.nw[c] : p.nb[c]) : 0.0f);
+    }
+    for (int i = tid; i < 2 * 192; i += TX_WAVES * 64) {
+        const int k = i < 192 ? i : i - 192, c = habx180_channel(k);
+        Cn[i] = c < 0 ? 0.0f : i < 192 ? p.inw[c] : p.inb[c];
+    }
+    const int mbase = blockIdx.x * TX_ROWS + wave * 32;
+    f32x4 acc[2][NT];
+    tx_load_res<C>(p.res, mbase, M, lr, lg, acc);
+
+    // ---- the projection: acc = x + ao . Wp^T, ao's rows one k-step ahead
+    {
+        WcRows<C> ar;
+        ar.init(p.a, mbase, M, lr);
+        f32x4 pre[2][2];
+        ar.load(0, lg, pre);
+#pragma unroll
+        for (int c = 0; c < 6; ++c) {
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk c (and its rows) have landed
+            __syncthreads();                // everyone's have, and everyone is done with chunk c - 1
+            if (c + 1 < 6) wc_issue<NLP, TX_WAVES>(c & 1 ? Ws0 : Ws1, p.w + (size_t)(c + 1) * MX180_SLOT, wave, lane);
+            else wc_issue<NL1, TX_WAVES>(Ws0, p.wm, wave, lane);  // the MLP's first chunk
+            u32x4 xb[2][3];
+            split_pre(pre, xb);
+            if (c + 1 < 6) ar.load(c + 1, lg, pre);
+            ws_mma<NT, 16 * NT>(c & 1 ? Ws1 : Ws0, lr, lg, xb, acc);
+        }
+    }
+    // x' = acc (+ conv2's output times gate * cscale) + bias, kept in acc;
+    // norm2's statistics from it
+    float2 st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = mbase + mt * 16 + lr;
+        const float* arow = HAB && m < M ? p.aux + (size_t)m * C + lg * 4 : hat_zero_row;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const f32x4 b4 = *(const f32x4*)(Cp + nt * 16 + lg * 4);
+            if constexpr (HAB) {
+                const f32x4 a4 = *(const f32x4*)(m < M && tx_live<C>(nt, lg) ? arow + nt * 16 : hat_zero_row);
+                const f32x4 g4 = *(const f32x4*)(Cp + 192 + nt * 16 + lg * 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[mt][nt][j] += a4[j] * g4[j];
+            }
+            acc[mt][nt] += b4;
+        }
+        st[mt] = tx_row_stats<C>(acc[mt], lg, p.eps);
+        // an opaque copy of the mean: otherwise the compiler reuses the
+        // statistics' x' - mean in part 0's norm and keeps those 48 values
+        // live beside x' through part 0 (35 VGPRs spilled)
+        asm volatile("" : "+v"(st[mt].x));
+    }
+
+    // ---- the MLP on x' (acc), in six parts of 64 hidden units
+    auto norm_pre = [&](int ks, f32x4 (&pre)[2][2]) {
+        const float* wk = Cn + ks * 32 + lg * 8;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const f32x4 w4 = *(const f32x4*)(wk + 4 * j), b4 = *(const f32x4*)(wk + 192 + 4 * j);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pre[mt][j][i] = (pre[mt][j][i] - st[mt].x) * st[mt].y * w4[i] + b4[i];
+        }
+    };
+    // y = norm2(x') in the fused order for k-step ks, at the lane's own
+    // channels of the output rows (tile 11 only in lane group 0)
+    float* yrow[2];
+    bool yalive[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = mbase + mt * 16 + lr;
+        yalive[mt] = m < M;
+        yrow[mt] = p.out + (size_t)(yalive[mt] ? m : 0) * C + lg * 4;
+    }
+    auto load_y = [&](int ks, f32x4 (&dst)[2][2]) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            dst[mt][0] = *(const f32x4*)(yalive[mt] ? yrow[mt] + 32 * ks : hat_zero_row);
+            dst[mt][1] = *(const f32x4*)(yalive[mt] && (ks < 5 || lg == 0) ? yrow[mt] + 32 * ks + 16 : hat_zero_row);
+        }
+    };
+    // fc2 over a part's units from registers: chunks 6, 7 of the part
+    auto fc2_part = [&](int q, const unsigned short* wq, f32x4 (&h)[2][4]) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (s == 0) wc_issue<NL2, TX_WAVES>(Ws1, wq + (size_t)7 * MX180_SLOT, wave, lane);
+            else if (q < NP - 1) wc_issue<NL1, TX_WAVES>(Ws0, wq + (size_t)8 * MX180_SLOT, wave, lane);
+            if (s == 0) {
+                // + b1 (the lane's four units of each tile, in the part's
+                // permuted row order), then GELU
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) {
+                    const f32x4 b = *(const f32x4*)(p.b1x + q * MX180_HID + 16 * nt + 4 * lg);
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) h[mt][nt][j] = gelu(h[mt][nt][j] + b[j]);
+                }
+            }
+            u32x4 xb[2][3];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const float f[8] = {h[mt][2 * s][0],     h[mt][2 * s][1],     h[mt][2 * s][2],
+                                    h[mt][2 * s][3],     h[mt][2 * s + 1][0], h[mt][2 * s + 1][1],
+                                    h[mt][2 * s + 1][2], h[mt][2 * s + 1][3]};
+                split3_x8(f, xb[mt]);
+            }
+            ws_mma<NT, 16 * NT>(s == 0 ? Ws0 : Ws1, lr, lg, xb, acc);
+        }
+    };
+    // part 0: fc1's input from the registers
+    {
+        const unsigned short* wq = p.wm;
+        f32x4 h[2][4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) h[0][nt] = h[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 6; ++ks) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (ks < 5) wc_issue<NL1, TX_WAVES>(ks & 1 ? Ws0 : Ws1, wq + (size_t)(ks + 1) * MX180_SLOT, wave, lane);
+            else wc_issue<NL2, TX_WAVES>(Ws0, wq + (size_t)6 * MX180_SLOT, wave, lane);
+            f32x4 pre[2][2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                pre[mt][0] = acc[mt][2 * ks];
+                pre[mt][1] = acc[mt][2 * ks + 1];
+            }
+            norm_pre(ks, pre);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                // y for parts 1..5 (rows past M: the sink)
+                float* yr = yalive[mt] ? yrow[mt] + 32 * ks : hat_sink_row;
+                *(f32x4*)yr = pre[mt][0];
+                if (ks < 5 || lg == 0) *(f32x4*)(yr + (yalive[mt] ? 16 : 4)) = pre[mt][1];
+            }
+            u32x4 xb[2][3];
+            split_pre(pre, xb);
+            ws_mma<4, MX180_HID>(ks & 1 ? Ws1 : Ws0, lr, lg, xb, h);
+        }
+        fc2_part(0, wq, h);
+    }
+    // parts 1..5: fc1's input read back from the output rows, one k-step ahead
+    f32x4 pre[2][2];
+    load_y(0, pre);
+#pragma unroll 1
+    for (int q = 1; q < NP; ++q) {
+        const unsigned short* wq = p.wm + (size_t)(8 * q) * MX180_SLOT;
+        f32x4 h[2][4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) h[0][nt] = h[1][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        auto fc1_step = [&](int ks, auto parv) {
+            constexpr int PAR = decltype(parv)::value;  // = ks & 1
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (ks < 5) wc_issue<NL1, TX_WAVES>(PAR ? Ws0 : Ws1, wq + (size_t)(ks + 1) * MX180_SLOT, wave, lane);
+            else wc_issue<NL2, TX_WAVES>(Ws0, wq + (size_t)6 * MX180_SLOT, wave, lane);
+            u32x4 xb[2][3];
+            split_pre(pre, xb);
+            if (ks < 5) load_y(ks + 1, pre);
+            else if (q < NP - 1) load_y(0, pre);
+            ws_mma<4, MX180_HID>(PAR ? Ws1 : Ws0, lr, lg, xb, h);
+        };
+#pragma unroll 1
+        for (int ks = 0; ks < 6; ks += 2) {
+            fc1_step(ks, CInt<0>{});
+            fc1_step(ks + 1, CInt<1>{});
+        }
+        fc2_part(q, wq, h);
+    }
+    tx_store_rows<C>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
+}
+
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx_cab(TailXArgs p) { projx_body<true>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx(TailXArgs p) { projx_body<false>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_mlpx_ln(TailXArgs p) { mlpx_body<true>(p); }
@@ -783,3 +1010,5 @@ extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx180_hab(
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_projx180(TailXArgs p) { projx180_body<false>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_habx_cab_ln(TailXArgs p) { habx_body<true, true>(p); }
 extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_habx(TailXArgs p) { habx_body<false, false>(p); }
+extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_habx180_hab_ln(TailXArgs p) { habx180_body<true, true>(p); }
+extern "C" __global__ __launch_bounds__(TX_WAVES * 64, 2) void hat_habx180(TailXArgs p) { habx180_body<false, false>(p); }

@@ -483,6 +483,78 @@ int gpu_selftest(std::string* err)
             note(std::string(k) + " C 180 M 600 (split-bf16, in place)");
         }
 
+        // ---- the fused C = 180 tails (x' on the chip) against the two
+        // kernels above on the same inputs, in place over the residual, 600
+        // rows (the last tile partial): HAB form (gated conv2 output + next
+        // norm) and OCAB form (neither).
+        for (int hab : {1, 0}) {
+            const int M = 600, C = 180, H = 360;
+            const float cscale = 0.01f;
+            std::vector<float> a = rng.vec((size_t)M * C, 1.0f), wp = rng.vec((size_t)C * C, 0.08f),
+                               bp = rng.vec(C, 0.1f), res = rng.vec((size_t)M * C, 1.0f),
+                               aux = rng.vec((size_t)M * C, 1.0f), gate = rng.vec(C, 1.0f),
+                               n2w = rng.vec(C, 1.0f), n2b = rng.vec(C, 0.1f), w1 = rng.vec((size_t)H * C, 0.08f),
+                               b1 = rng.vec(H, 0.1f), w2 = rng.vec((size_t)C * H, 0.05f), b2 = rng.vec(C, 0.1f),
+                               nw = rng.vec(C, 1.0f), nb = rng.vec(C, 0.1f);
+            std::vector<unsigned short> pwx = pack_linear_x180(wp.data()), mw, mwf;
+            std::vector<float> mb1x;
+            pack_mlp_x180(w1.data(), b1.data(), w2.data(), &mw);
+            pack_mlp_xf180(w1.data(), b1.data(), w2.data(), &mwf, &mb1x);
+            Dev da(a), dbp(bp), daux(aux), dg(gate), dn2w(n2w), dn2b(n2b), db2(b2), dnw(nw), dnb(nb), dmb1x(mb1x),
+                dx2(res), dxn2((size_t)M * C), dxf(res), dxnf((size_t)M * C), dpw((pwx.size() + 1) / 2),
+                dmw((mw.size() + 1) / 2), dmwf((mwf.size() + 1) / 2);
+            Runtime::get().h2d(dpw.p, pwx.data(), pwx.size() * sizeof(unsigned short));
+            Runtime::get().h2d(dmw.p, mw.data(), mw.size() * sizeof(unsigned short));
+            Runtime::get().h2d(dmwf.p, mwf.data(), mwf.size() * sizeof(unsigned short));
+            TailXArgs q{};
+            q.a = da.p;
+            q.res = dx2.p;
+            q.out = dx2.p;
+            q.w = (const unsigned short*)dpw.p;
+            q.bias = dbp.p;
+            q.M = M;
+            q.eps = 1e-5f;
+            q.aux = hab ? daux.p : nullptr;
+            q.gate = hab ? dg.p : nullptr;
+            q.cscale = cscale;
+            launch(s, hab ? "hat_projx180_hab" : "hat_projx180", (unsigned)wx_tiles(M), 1, 1, WX_THREADS, q);
+            TailXArgs m2{};
+            m2.a = dx2.p;
+            m2.inw = dn2w.p;
+            m2.inb = dn2b.p;
+            m2.res = dx2.p;
+            m2.out = dx2.p;
+            m2.xn = hab ? dxn2.p : nullptr;
+            m2.w = (const unsigned short*)dmw.p;
+            m2.b2 = db2.p;
+            m2.nw = hab ? dnw.p : nullptr;
+            m2.nb = hab ? dnb.p : nullptr;
+            m2.M = M;
+            m2.eps = 1e-5f;
+            launch(s, hab ? "hat_mlpx180_ln" : "hat_mlpx180", (unsigned)wx_tiles(M), 1, 1, WX_THREADS, m2);
+            TailXArgs f = q;
+            f.res = dxf.p;
+            f.out = dxf.p;
+            f.xn = hab ? dxnf.p : nullptr;
+            f.wm = (const unsigned short*)dmwf.p;
+            f.b1x = dmb1x.p;
+            f.b2 = db2.p;
+            f.inw = dn2w.p;
+            f.inb = dn2b.p;
+            f.nw = hab ? dnw.p : nullptr;
+            f.nb = hab ? dnb.p : nullptr;
+            const char* k = hab ? "hat_habx180_hab_ln" : "hat_habx180";
+            launch(s, k, (unsigned)wx_tiles(M), 1, 1, WX_THREADS, f);
+            const std::vector<float> two = dx2.get();
+            check_close(k, dxf.get(), std::vector<double>(two.begin(), two.end()), 2e-5);
+            if (hab) {
+                const std::vector<float> twon = dxn2.get();
+                check_close(std::string(k) + " next norm", dxnf.get(), std::vector<double>(twon.begin(), twon.end()),
+                            2e-5);
+            }
+            note(std::string(k) + " (fused split-bf16 C 180 tail, M 600, in place) vs the two-kernel path");
+        }
+
         // ---- folded CAB (144 -> 6 -> 144) against the unfolded computation:
         // conv1 + GELU, conv2 in full, its pixel mean, squeeze-excite, gate, and
         // shortcut + proj + gated conv2 * cscale + LayerNorm - in double. A 32 x 48
