@@ -1,5 +1,5 @@
 // The second half of a HAB (and of an OCAB), C = 144 and 180, on split-bf16
-// MFMA, as two kernels (hat_arch.py HAB.forward / OCAB.forward; cpu.rs hab
+// MFMA, as two kernels or one (hat_arch.py HAB.forward / OCAB.forward; cpu.rs hab
 // 1090-1166, ocab 983-1055; the reference GPU graph's proj, CAB conv2 and
 // channel scale, adds, norm2, fc1 + GELU + fc2 and the next norm1,
 // src/gpu.rs:469-588):
@@ -10,6 +10,8 @@
 //                               formed from the x' rows (xn = LN_next(out))
 //   hat_projx180(_hab), hat_mlpx180(_ln): the same at C = 180 (the HAB form
 //                               adds the unfolded CAB's gated conv2 output)
+//   hat_habx_cab_ln / hat_habx, hat_habx180_hab_ln / hat_habx180: each pair
+//                               above in one kernel
 //
 // ao is the attention output, nb(t1) the 3x3 neighbourhood of the CAB's conv1
 // output (k = tap*6 + ci, 54 values) and W2g / bias the gate-scaled conv2
@@ -39,8 +41,10 @@
 // the third; fc2's 32-k step s then finds units 32s + 8g .. +7 in tiles 2s
 // and 2s+1 of lane group g, its weights in natural order.
 //
-// Split in two at x' (written, then read back by the MLP): one kernel would
-// hold x', LN2(x') and the MLP's registers at once.
+// The forward runs the fused forms below (hat_habx*, hat_habx180*: both
+// halves in one kernel, x' kept in registers); the two-kernel forms split at x'
+// (written, then read back by the MLP) are the selftest's comparison and the
+// fallback for the combinations the fused kernels do not take.
 //
 // Included after gemmx.hip (WcRows, split_pre).
 
