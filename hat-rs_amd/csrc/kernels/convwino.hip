@@ -36,7 +36,9 @@
 // each lane forms V for its (tile, eight channels) from the patch, splits it
 // and feeds it to the MFMAs as the B operand. U (pre-transformed and split on
 // the host, 2.2 MB at 144 -> 144 with the channels padded to 160, L2-resident)
-// streams from global memory as the A operand, two steps ahead of its MFMAs.
+// streams from global memory as the A operand, two or three steps ahead of its
+// MFMAs (a ring of three or four registers sets, whichever divides the 2 NT
+// steps of a chunk; three ahead measured up to 2% faster than two at NT = 4).
 //
 // Epilogue, per 16-channel slice: the waves write their M slices to LDS, then
 // each thread forms the 2x2 outputs of one (tile, channel) from the 16 points.
@@ -182,10 +184,14 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 #pragma unroll
             for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    U3 ur[2];
+    // U loads RING - 1 steps ahead (2 NT steps a chunk, a multiple of RING, so
+    // slot t % RING lines up across chunks)
+    constexpr int RING = (2 * NT) % 3 == 0 ? 3 : 4;
+    static_assert((2 * NT) % RING == 0 && 2 * NT >= RING, "the ring lines up across chunks");
+    U3 ur[RING];
     fetch(0, CInt<0>{});
-    ur[0] = ldu(0, 0);
-    ur[1] = ldu(0, 1);
+#pragma unroll
+    for (int t = 0; t < RING - 1; ++t) ur[t] = ldu(0, t);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -225,12 +231,14 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
                 if (!LAST && t == 0) fetch(kc + 1, CInt<Q ^ 1>{});
 #pragma unroll
                 for (int nt2 = 0; nt2 < 2; ++nt2)
-                    acc[e][nt][nt2] = HALF ? mfma16x3(ur[t % 2].v, vb[nt2], acc[e][nt][nt2])
-                                           : mfma16x6(ur[t % 2].v, vb[nt2], acc[e][nt][nt2]);
-                // step t + 2's load into the slot step t's MFMAs have read (the
-                // step count per chunk is even, so slot t % 2 lines up across
-                // chunks)
-                ur[t % 2] = t + 2 < 2 * NT ? ldu(kc, t + 2) : ldu(kn, t + 2 - 2 * NT);
+                    acc[e][nt][nt2] = HALF ? mfma16x3(ur[t % RING].v, vb[nt2], acc[e][nt][nt2])
+                                           : mfma16x6(ur[t % RING].v, vb[nt2], acc[e][nt][nt2]);
+                // step t + RING - 1's load into the slot step t - 1's MFMAs
+                // have read
+                {
+                    constexpr int A = RING - 1;  // steps ahead
+                    ur[(t + A) % RING] = t + A < 2 * NT ? ldu(kc, t + A) : ldu(kn, t + A - 2 * NT);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
