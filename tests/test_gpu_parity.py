@@ -303,7 +303,7 @@ def test_host_forward_staging_equals_the_device_pass(hl, weights_dir, variant, s
     be.close()
 
 
-@pytest.mark.parametrize("variant,scale", [("hat-s", 4), ("hat", 3), ("hat-s", 2)])
+@pytest.mark.parametrize("variant,scale", [("hat-s", 4), ("hat", 3), ("hat-s", 2), ("hat", 2)])
 def test_tiny_and_ragged_inputs_match_oracle(hl, weights_dir, variant, scale):
     """Inputs far below and just past one window (1x1, 3x5, 17x33: edge-replicated
     to 16x16, 16x16 and 32x48, Pre::adjust backend.rs:71-89, and cropped back), on
