@@ -914,12 +914,13 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
     // conv_before_upsample and the x2 upsample convs by Winograd F(2x2, 3x3):
     // 8 x 16 output tiles, 32-bit element offsets into both planes
     p.wu = C.wu;
+    auto wino = [&](const char* name, unsigned tiles, unsigned ncb) { launch_wino(s, name, tiles, ncb, p); };
     const size_t rr = C.r > 0 ? (size_t)C.r * C.r : 1;
     if (C.wu && H % 16 == 0 && W % 16 == 0 && cin_stride % 4 == 0 && cin_stride >= C.CI &&
         (size_t)H * W * cin_stride < ((size_t)1 << 31) && (size_t)H * W * rr * co_stride < ((size_t)1 << 31)) {
         const unsigned tiles = (unsigned)((W / 16) * (H / 8));
         if (epi == CEPI_STORE && act == 2 && C.CO == 64 && C.CI == 144 && co_stride >= 64) {
-            launch(s, "hat_convwino_n4_store", tiles, 1, 1, 512, p);
+            wino("hat_convwino_n4_store", tiles, 1);
             return;
         }
         if (epi == CEPI_SHUFFLE && C.r == 2 && C.CO == 256 && C.CI == 64 && co_stride >= 64) {
@@ -929,26 +930,26 @@ void run_conv(hipStream_t s, const DevConv& C, const float* in, int cin_stride, 
                 p.tile0 = band_r0 * (W / 16);
                 nt = (unsigned)((band_r1 - band_r0) * (W / 16));
             }
-            launch(s, "hat_convwino_n8_shuffle", 2 * nt, 1, 1, 512, p);
+            wino("hat_convwino_n8_shuffle", nt, 2);
             return;
         }
         if (band) throw Error("conv: only the Winograd upsample conv and conv_last run in bands");
         // the C = 180 family (the residual epilogue's planes are 180 wide)
         if (epi == CEPI_STORE && act == 2 && C.CO == 64 && C.CI == 180 && co_stride >= 64) {
-            launch(s, "hat_convwino_n4_store180", tiles, 1, 1, 512, p);
+            wino("hat_convwino_n4_store180", tiles, 1);
             return;
         }
         if (epi == CEPI_STORE && act == 1 && C.CO == 60 && C.CI == 180 && co_stride >= 60) {
-            launch(s, "hat_convwino_cab1_180", tiles, 1, 1, 512, p);
+            wino("hat_convwino_cab1_180", tiles, 1);
             return;
         }
         if (epi == CEPI_COLSUM && C.CO == 180 && C.CI == 60 && co_stride >= 180) {
-            launch(s, "hat_convwino_cab2_180", 2 * tiles, 1, 1, 512, p);
+            wino("hat_convwino_cab2_180", tiles, 2);
             return;
         }
         if (epi == CEPI_RESID && C.CO == 180 && C.CI == 180 && co_stride == 180) {
             if (in == out) throw Error("conv: the output must not overlap the input");
-            launch(s, "hat_convwino_resid180", 2 * tiles, 1, 1, 512, p);
+            wino("hat_convwino_resid180", tiles, 2);
             return;
         }
     }
@@ -1023,7 +1024,7 @@ void run_convw(hipStream_t s, const DevConv& C, const float* in, int cin_stride,
     if (C.wu && C.CI == 144 && (epi == EPI_RESID_LN || epi == EPI_RESID) && H % 8 == 0 &&
         (size_t)H * W * cin_stride < ((size_t)1 << 31)) {
         if (in == out) throw Error("convw: the output must not overlap the input");
-        launch(s, "hat_convwino_resid", (unsigned)((W / 16) * (H / 8)), 1, 1, 512, p);
+        launch_wino(s, "hat_convwino_resid", (unsigned)((W / 16) * (H / 8)), 1, p);
         if (epi == EPI_RESID_LN) run_ln(s, out, xn, nw, nb, (long)H * W, C.CO);
         return;
     }
@@ -1092,6 +1093,25 @@ void run_ln(hipStream_t s, const float* x, float* y, const float* w, const float
 }
 
 }  // namespace
+
+bool convwino_persistent(const std::string& name)
+{
+    // convwino.hip: the column-sum kernel (the CAB's conv2 at C = 180)
+    return name == "hat_convwino_cab2_180";
+}
+
+void launch_wino(hipStream_t s, const char* name, unsigned tiles, unsigned ncb, ConvArgs& p, unsigned max_blocks)
+{
+    static const unsigned cus = (unsigned)std::max(1, Runtime::get().cu_count());
+    const unsigned nvb = tiles * ncb;
+    if (nvb == 0 || nvb > 0x7fffffffu || ncb == 0) throw Error("convwino: bad tile count");
+    const bool persist = convwino_persistent(name);
+    const unsigned cap = max_blocks ? max_blocks : cus;
+    const unsigned g = persist ? std::max(ncb, std::min(nvb, cap) / ncb * ncb) : nvb;
+    p.nblk = persist ? (int)nvb : 0;
+    launch(s, name, g, 1, 1, 512, p);
+}
+
 
 // ---------------------------------------------------------------------------
 // GpuBackend

@@ -118,6 +118,16 @@ int mlpx180_fused_channel(int k);
 std::vector<unsigned short> pack_wino(const float* w, int CO, int CI, int r);
 std::vector<float> pack_conv(const float* w, const float* b, int CO, int CI, int r,
                              std::vector<float>* bias_out, int* CIp, int* COp);
+// A Winograd conv kernel (convwino.hip) over `tiles` 8 x 16 tiles in `ncb`
+// column blocks (p.nblk set here). The persistent ones (convwino_persistent:
+// the column-sum kernel) take a grid of at most one block a CU (or
+// max_blocks), a multiple of ncb so that each block keeps its column block,
+// each walking the virtual blocks blockIdx.x + i gridDim.x and fetching its
+// next tile's first patch chunk under the current tile's epilogue; the others
+// take one block a tile.
+bool convwino_persistent(const std::string& name);
+void launch_wino(hipStream_t s, const char* name, unsigned tiles, unsigned ncb, hatk::ConvArgs& p,
+                 unsigned max_blocks = 0);
 
 class GpuBackend : public Backend {
 public:

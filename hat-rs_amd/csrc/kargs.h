@@ -149,6 +149,9 @@ struct ConvArgs {
     // hat_convwino_* and hat_conv_last3 launched over a band of tile rows (the
     // host-memory forward's head): the band's first tile; 0 for a whole plane
     int tile0;
+    // hat_convwino_*: the launch's virtual blocks (tiles x column blocks),
+    // walked by a grid of at most one block per CU; 0: one per block
+    int nblk;
 };
 
 // Squeeze-excite gate: gate[c] = sigmoid(b2 + W2 relu(b1 + W1 mean)).

@@ -25,7 +25,9 @@
 // MACs per tile against 4 * 9 * 144 * 144 for the direct form (2.25x fewer).
 //
 // A block owns an 8 x 16 output tile (32 Winograd tiles, two 16-wide MFMA
-// column tiles) and 16 NT output channels. Wave w computes the two transform
+// column tiles) and 16 NT output channels (the column-sum kernel walks several
+// such tiles, one block a CU, fetching the next tile's first patch chunk under
+// the current tile's epilogue). Wave w computes the two transform
 // points xi = 2w, 2w + 1 (B^T row i = w / 2, columns j = 2 (w % 2) + {0, 1}),
 // accumulating M[xi] (co 16 NT x tile 32) in 16 NT registers per lane (144
 // for the trunk convs), on split-bf16 MFMA (v_mfma_f32_16x16x32_bf16, each
@@ -64,6 +66,14 @@
 template <int NT, int NTT, int NKC, int CI, int CO, int HEAD>
 __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 {
+    // Persistent over tiles only for the column-sum epilogue (CAB conv2 60 ->
+    // 180: two input chunks, a six-slice epilogue and the sums), where fetching
+    // the next tile under the epilogue measured 257 -> 243 us. For the others
+    // the wait at the top of a tile (for this tile's stores as well as the
+    // next patch) and the barrier cost more than the overlap gains (same box:
+    // 4-9% slower), and the NT = 8 and 9 kernels spill 120-300 bytes more in
+    // the loop.
+    constexpr bool PERSIST = HEAD == CEPI_COLSUM;
     static_assert(HEAD == -1 || HEAD == CEPI_STORE || HEAD == CEPI_SHUFFLE || HEAD == CEPI_COLSUM,
                   "residual, store, shuffle or column-sum epilogues");
     static_assert(NTT % NT == 0 && 16 * NTT >= CO && 16 * (NTT - 1) < CO, "the column blocks cover CO");
@@ -86,13 +96,23 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     const int lg = lane >> 4;
     const int H = p.H, W = p.W;
     const int tiles_x = W / WG_TW;
-    // a tile's column blocks are consecutive blocks, so they read its patch
-    // from L2 at about the same time
+    // Persistent over the launch's virtual blocks vb = blockIdx.x + i
+    // gridDim.x, p.nblk of them (0: the grid's own, one a block): tile vb / NCB
+    // (after a band's first tile tile0, 0 for the whole plane), column block
+    // vb % NCB, the same for all of a block's tiles (the host makes gridDim.x
+    // a multiple of NCB). A tile's column blocks are consecutive virtual
+    // blocks, so they read its patch from L2 at about the same time.
     constexpr int NCB = NTT / NT;
-    const int bt = (int)blockIdx.x / NCB, cb = (int)blockIdx.x - bt * NCB;
-    const int tile = p.tile0 + bt;  // tile0: a band's first tile (0 for the whole plane)
-    const int y0 = (tile / tiles_x) * WG_TH;
-    const int x0 = (tile % tiles_x) * WG_TW;
+    const int nvb = PERSIST && p.nblk > 0 ? p.nblk : (int)gridDim.x;
+    int vb = (int)blockIdx.x;
+    const int cb = vb % NCB;
+    int tile, y0, x0;
+    auto set_tile = [&](int v) {
+        tile = p.tile0 + v / NCB;
+        y0 = (tile / tiles_x) * WG_TH;
+        x0 = (tile % tiles_x) * WG_TW;
+    };
+    set_tile(vb);
 
     for (int i = tid; i < 16 * NT; i += 512) Cs[i] = 16 * NT * cb + i < CO ? p.bias[16 * NT * cb + i] : 0.0f;
 
@@ -110,16 +130,19 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     // -1 for slots outside the plane or past the 1440 used.
     constexpr bool PSPLIT = NT != 9;
     int soff[3], squad[3];
+    auto set_offsets = [&](int ty0, int tx0) {  // for the tile at (ty0, tx0)
 #pragma unroll
-    for (int r = 0; r < 3; ++r) {
-        const int s = r * 512 + tid;
-        const int q = s / WG_PPX, pix = s - q * WG_PPX;
-        const int hy = pix / WG_PW, c = pix - hy * WG_PW, hx = !PSPLIT ? c : c < 9 ? 2 * c : 2 * c - 17;
-        const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
-        const bool ok = s < WG_PPX * 8 && gy >= 0 && gy < H && gx >= 0 && gx < W;
-        soff[r] = ok ? (gy * W + gx) * p.cin_stride + q * 4 : -1;
-        squad[r] = 4 * q;
-    }
+        for (int r = 0; r < 3; ++r) {
+            const int s = r * 512 + tid;
+            const int q = s / WG_PPX, pix = s - q * WG_PPX;
+            const int hy = pix / WG_PW, c = pix - hy * WG_PW, hx = !PSPLIT ? c : c < 9 ? 2 * c : 2 * c - 17;
+            const int gy = ty0 - 1 + hy, gx = tx0 - 1 + hx;
+            const bool ok = s < WG_PPX * 8 && gy >= 0 && gy < H && gx >= 0 && gx < W;
+            soff[r] = ok ? (gy * W + gx) * p.cin_stride + q * 4 : -1;
+            squad[r] = 4 * q;
+        }
+    };
+    set_offsets(y0, x0);
     auto fetch = [&](int kc, auto bufc) {
         float* B = decltype(bufc)::value ? Pb1 : Pb0;
 #pragma unroll
@@ -177,12 +200,6 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
     }
 
     f32x4 acc[2][NT][2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-            for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     // U loads RING - 1 steps ahead (2 NT steps a chunk, a multiple of RING, so
     // slot t % RING lines up across chunks)
@@ -203,7 +220,9 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         constexpr int Q = decltype(bufc)::value;
         constexpr bool LAST = decltype(lastc)::value;
         const float* B = Q ? Pb1 : Pb0;
-        const int kn = LAST ? kc : kc + 1;
+        // the chunk after this one; after the last, chunk 0 of the block's next
+        // tile (U is the same for every tile of the column block)
+        const int kn = LAST ? 0 : kc + 1;
         constexpr bool HALF = PACK && LAST;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -246,132 +265,160 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
         __syncthreads();
     };
 #pragma unroll 1
-    for (int kc = 0; kc + 2 < NKC; kc += 2) {
-        chunk(kc, CInt<0>{}, CInt<0>{});
-        chunk(kc + 1, CInt<1>{}, CInt<0>{});
-    }
-    if constexpr (NKC % 2 == 1) {
-        chunk(NKC - 1, CInt<0>{}, CInt<1>{});
-    } else {
-        chunk(NKC - 2, CInt<0>{}, CInt<0>{});
-        chunk(NKC - 1, CInt<1>{}, CInt<1>{});
-    }
-
-    // ---- epilogue. Thread (tile = tid / 16, c = tid % 16): outputs of tile
-    // (ty, tx) for channels 16 nt + c.
-    const int et = tid >> 4, ec = tid & 15;
-    // An M slice entry (a row of 16 floats) keeps its four float4s at slots
-    // ws_slot(row, g), so that the waves' writes (8 lanes: rows r0 .. r0 + 7)
-    // and the reads here (16 lanes a row, two rows at a time) meet no bank
-    // conflicts; row x * 32 + et has (row >> 1) & 3 == (et >> 1) & 3.
-    // (The NT = 9 trunk conv keeps plain rows of WG_MS floats, 2-way conflicted
-    // reads: the swizzle's offset register makes the compiler spill more.)
-    constexpr int MS = PSPLIT ? 16 : WG_MS;
-    const int moff = PSPLIT ? 4 * ws_slot(et, ec >> 2) + (ec & 3) : ec;
-    const int ety = et >> 3, etx = et & 7;
-    const int py = y0 + 2 * ety, px = x0 + 2 * etx;
-    // element offsets of the thread's four pixels in the residual epilogue's
-    // planes (below 2^31 elements: checked at launch)
-    const int pix0 = ((py * W) + px) * CO, prow = W * CO;
-    const int ocb = 16 * NT * cb + ec;  // the thread's channel in slice 0
-    constexpr bool PADCO = 16 * NTT != CO;  // channels past CO in the last column block
-    float y[NT][4];
-    auto out_slice = [&](int nt, auto bufc) {
-        float* Ms = decltype(bufc)::value ? Ms1 : Ms0;
-        // the slice's residual, loaded under the barrier and the transforms
-        const bool live = PADCO ? ocb + 16 * nt < CO : true;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            y[nt][q] = HEAD < 0 ? p.res[live ? pix0 + (q >> 1) * prow + (q & 1) * CO + ocb + nt * 16 : 0] : 0.0f;
+    for (;;) {  // the block's tiles
+        // an opaque copy of the U base each tile: otherwise the compiler keeps
+        // every step's U address live across the tiles and spills
+        if constexpr (PERSIST) asm volatile("" : "+v"(ubase));
 #pragma unroll
         for (int e = 0; e < 2; ++e)
 #pragma unroll
-            for (int nt2 = 0; nt2 < 2; ++nt2)
-                *(f32x4*)(Ms + ((2 * wave + e) * 32 + nt2 * 16 + lr) * MS + 4 * (PSPLIT ? ws_slot(lr, lg) : lg)) =
-                    acc[e][nt][nt2];
-        __syncthreads();
-        float m[16];
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int x = 0; x < 16; ++x) m[x] = Ms[(x * 32 + et) * MS + moff];
-        float t0[4], t1[4];  // T[i][0], T[i][1] = M[i] A
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            t0[i] = m[4 * i] + m[4 * i + 1] + m[4 * i + 2];
-            t1[i] = m[4 * i + 1] - m[4 * i + 2] - m[4 * i + 3];
+                for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int kc = 0; kc + 2 < NKC; kc += 2) {
+            chunk(kc, CInt<0>{}, CInt<0>{});
+            chunk(kc + 1, CInt<1>{}, CInt<0>{});
         }
-        const float bias = Cs[nt * 16 + ec];
-        y[nt][0] += (t0[0] + t0[1] + t0[2]) + bias;
-        y[nt][1] += (t1[0] + t1[1] + t1[2]) + bias;
-        y[nt][2] += (t0[1] - t0[2] - t0[3]) + bias;
-        y[nt][3] += (t1[1] - t1[2] - t1[3]) + bias;
-    };
-#pragma unroll
-    for (int nt = 0; nt + 1 < NT; nt += 2) {
-        out_slice(nt, CInt<0>{});
-        out_slice(nt + 1, CInt<1>{});
-    }
-    if constexpr (NT % 2 == 1) out_slice(NT - 1, CInt<0>{});
+        if constexpr (NKC % 2 == 1) {
+            chunk(NKC - 1, CInt<0>{}, CInt<1>{});
+        } else {
+            chunk(NKC - 2, CInt<0>{}, CInt<0>{});
+            chunk(NKC - 1, CInt<1>{}, CInt<1>{});
+        }
+        // The next tile's first patch chunk, in flight under this tile's epilogue:
+        // the last chunk ended at a barrier, so no wave still reads the patch
+        // buffers, and the epilogue uses Ms0 / Ms1 only.
+        const int vn = vb + (int)gridDim.x;
+        const bool more = PERSIST && vn < nvb;  // block-uniform
+        if (more) {
+            const int nt_tile = p.tile0 + vn / NCB;
+            set_offsets((nt_tile / tiles_x) * WG_TH, (nt_tile % tiles_x) * WG_TW);
+            fetch(0, CInt<0>{});
+        }
 
-    if constexpr (HEAD >= 0) {
-        // Channel o = 16 NT cb + 16 nt + c of pixel (y, x): CEPI_STORE and
-        // CEPI_COLSUM write it there (CEPI_STORE after p.act); CEPI_SHUFFLE
-        // writes o = (i r + jj) Cf + c' to pixel (y r + i, x r + jj), channel c'
-        // of the r-times larger plane.
+        // ---- epilogue. Thread (tile = tid / 16, c = tid % 16): outputs of tile
+        // (ty, tx) for channels 16 nt + c.
+        const int et = tid >> 4, ec = tid & 15;
+        // An M slice entry (a row of 16 floats) keeps its four float4s at slots
+        // ws_slot(row, g), so that the waves' writes (8 lanes: rows r0 .. r0 + 7)
+        // and the reads here (16 lanes a row, two rows at a time) meet no bank
+        // conflicts; row x * 32 + et has (row >> 1) & 3 == (et >> 1) & 3.
+        // (The NT = 9 trunk conv keeps plain rows of WG_MS floats, 2-way conflicted
+        // reads: the swizzle's offset register makes the compiler spill more.)
+        constexpr int MS = PSPLIT ? 16 : WG_MS;
+        const int moff = PSPLIT ? 4 * ws_slot(et, ec >> 2) + (ec & 3) : ec;
+        const int ety = et >> 3, etx = et & 7;
+        const int py = y0 + 2 * ety, px = x0 + 2 * etx;
+        // element offsets of the thread's four pixels in the residual epilogue's
+        // planes (below 2^31 elements: checked at launch)
+        const int pix0 = ((py * W) + px) * CO, prow = W * CO;
+        const int ocb = 16 * NT * cb + ec;  // the thread's channel in slice 0
+        constexpr bool PADCO = 16 * NTT != CO;  // channels past CO in the last column block
+        float y[NT][4];
+        auto out_slice = [&](int nt, auto bufc) {
+            float* Ms = decltype(bufc)::value ? Ms1 : Ms0;
+            // the slice's residual, loaded under the barrier and the transforms
+            const bool live = PADCO ? ocb + 16 * nt < CO : true;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const int o = ocb + 16 * nt;
-            if (PADCO && o >= CO) continue;
+            for (int q = 0; q < 4; ++q)
+                y[nt][q] = HEAD < 0 ? p.res[live ? pix0 + (q >> 1) * prow + (q & 1) * CO + ocb + nt * 16 : 0] : 0.0f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int yy = py + (q >> 1), xx = px + (q & 1);
-                float v = y[nt][q];
-                if (HEAD == CEPI_STORE || HEAD == CEPI_COLSUM) {
-                    if (HEAD == CEPI_STORE && p.act == 2) v = v < 0.0f ? v * 0.01f : v;
-                    if (HEAD == CEPI_STORE && p.act == 1) v = gelu(v);
-                    p.out[(yy * W + xx) * p.co_stride + o] = v;
-                } else {
-                    const int r = p.r, Cf = p.CO / (r * r);
-                    const int sub = o / Cf, c = o - sub * Cf, i = sub / r, jj = sub - i * r;
-                    p.out[((yy * r + i) * (W * r) + xx * r + jj) * p.co_stride + c] = v;
-                }
+            for (int e = 0; e < 2; ++e)
+#pragma unroll
+                for (int nt2 = 0; nt2 < 2; ++nt2)
+                    *(f32x4*)(Ms + ((2 * wave + e) * 32 + nt2 * 16 + lr) * MS + 4 * (PSPLIT ? ws_slot(lr, lg) : lg)) =
+                        acc[e][nt][nt2];
+            __syncthreads();
+            float m[16];
+#pragma unroll
+            for (int x = 0; x < 16; ++x) m[x] = Ms[(x * 32 + et) * MS + moff];
+            float t0[4], t1[4];  // T[i][0], T[i][1] = M[i] A
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                t0[i] = m[4 * i] + m[4 * i + 1] + m[4 * i + 2];
+                t1[i] = m[4 * i + 1] - m[4 * i + 2] - m[4 * i + 3];
             }
+            const float bias = Cs[nt * 16 + ec];
+            y[nt][0] += (t0[0] + t0[1] + t0[2]) + bias;
+            y[nt][1] += (t1[0] + t1[1] + t1[2]) + bias;
+            y[nt][2] += (t0[1] - t0[2] - t0[3]) + bias;
+            y[nt][3] += (t1[1] - t1[2] - t1[3]) + bias;
+        };
+#pragma unroll
+        for (int nt = 0; nt + 1 < NT; nt += 2) {
+            out_slice(nt, CInt<0>{});
+            out_slice(nt + 1, CInt<1>{});
         }
-        if constexpr (HEAD == CEPI_COLSUM) {
-            // Column sums of the tile's 128 pixels: the thread's four, the four
-            // tiles of the wave with this channel (lanes ec + 16 k), then the
-            // eight waves in order through LDS (Ms0, free after this barrier);
-            // one partial row per 8 x 16 tile, [tile][co_stride].
-            float cs[NT];
+        if constexpr (NT % 2 == 1) out_slice(NT - 1, CInt<0>{});
+
+        if constexpr (HEAD >= 0) {
+            // Channel o = 16 NT cb + 16 nt + c of pixel (y, x): CEPI_STORE and
+            // CEPI_COLSUM write it there (CEPI_STORE after p.act); CEPI_SHUFFLE
+            // writes o = (i r + jj) Cf + c' to pixel (y r + i, x r + jj), channel c'
+            // of the r-times larger plane.
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                float v = (y[nt][0] + y[nt][1]) + (y[nt][2] + y[nt][3]);
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
-                cs[nt] = v;
-            }
-            __syncthreads();
-            if (lane < 16) {
+                const int o = ocb + 16 * nt;
+                if (PADCO && o >= CO) continue;
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) Ms0[wave * 16 * NT + nt * 16 + ec] = cs[nt];
+                for (int q = 0; q < 4; ++q) {
+                    const int yy = py + (q >> 1), xx = px + (q & 1);
+                    float v = y[nt][q];
+                    if (HEAD == CEPI_STORE || HEAD == CEPI_COLSUM) {
+                        if (HEAD == CEPI_STORE && p.act == 2) v = v < 0.0f ? v * 0.01f : v;
+                        if (HEAD == CEPI_STORE && p.act == 1) v = gelu(v);
+                        p.out[(yy * W + xx) * p.co_stride + o] = v;
+                    } else {
+                        const int r = p.r, Cf = p.CO / (r * r);
+                        const int sub = o / Cf, c = o - sub * Cf, i = sub / r, jj = sub - i * r;
+                        p.out[((yy * r + i) * (W * r) + xx * r + jj) * p.co_stride + c] = v;
+                    }
+                }
             }
-            __syncthreads();
-            if (tid < 16 * NT) {
-                const int o = 16 * NT * cb + tid;
-                float v = 0.0f;
+            if constexpr (HEAD == CEPI_COLSUM) {
+                // Column sums of the tile's 128 pixels: the thread's four, the four
+                // tiles of the wave with this channel (lanes ec + 16 k), then the
+                // eight waves in order through LDS (Ms0, free after this barrier);
+                // one partial row per 8 x 16 tile, [tile][co_stride].
+                float cs[NT];
 #pragma unroll
-                for (int w = 0; w < 8; ++w) v += Ms0[w * 16 * NT + tid];
-                if (o < CO) p.partial[(size_t)tile * p.co_stride + o] = v;
+                for (int nt = 0; nt < NT; ++nt) {
+                    float v = (y[nt][0] + y[nt][1]) + (y[nt][2] + y[nt][3]);
+                    v += __shfl_xor(v, 16, 64);
+                    v += __shfl_xor(v, 32, 64);
+                    cs[nt] = v;
+                }
+                __syncthreads();
+                if (lane < 16) {
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) Ms0[wave * 16 * NT + nt * 16 + ec] = cs[nt];
+                }
+                __syncthreads();
+                if (tid < 16 * NT) {
+                    const int o = 16 * NT * cb + tid;
+                    float v = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < 8; ++w) v += Ms0[w * 16 * NT + tid];
+                    if (o < CO) p.partial[(size_t)tile * p.co_stride + o] = v;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                if (PADCO && ocb + 16 * nt >= CO) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) p.out[pix0 + (q >> 1) * prow + (q & 1) * CO + ocb + nt * 16] = y[nt][q];
             }
         }
-        return;
-    }
-
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        if (PADCO && ocb + 16 * nt >= CO) continue;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) p.out[pix0 + (q >> 1) * prow + (q & 1) * CO + ocb + nt * 16] = y[nt][q];
-    }
+        if (!more) break;
+        vb = vn;
+        set_tile(vb);
+        // this wave's copies of the next patch have landed; everyone's have, and
+        // everyone is done with this tile's Ms
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }  // the block's tiles
 }
 
 extern "C" __global__ __launch_bounds__(512) void hat_convwino_resid(ConvArgs p)

@@ -970,7 +970,7 @@ int gpu_selftest(std::string* err)
                 p.nb = dnb.p;
                 p.eps = 1e-5f;
                 p.wu = (const unsigned short*)dwu.p;
-                if (c.wino) launch(s, c.k, (W / 16) * (H / 8), 1, 1, 512, p);
+                if (c.wino) launch_wino(s, c.k, (W / 16) * (H / 8), 1, p, 5);  // persistent ones over 5 blocks
                 else launch(s, c.k, (W / 16) * (H / 16), 1, 1, c.waves * 64, p);  // convw and conv_first: 16 x 16
                 std::vector<double> want((size_t)HW * CO), wxn((size_t)HW * CO);
                 for (int y = 0; y < H; ++y)
@@ -1177,7 +1177,10 @@ int gpu_selftest(std::string* err)
                 p.out = dout4.p;
                 p.partial = dpart4.p;
                 p.wu = (const unsigned short*)dwu.p;
-                launch(s, wino, (W / 16) * (H / 8) * ncb, 1, 1, 512, p);
+                // the persistent kernels over 5 ncb blocks (2 or 3 of the 12 tiles
+                // each, the next tile's patch fetched under an epilogue)
+                launch_wino(s, wino, (W / 16) * (H / 8), ncb, p, 5 * ncb);
+                p.nblk = 0;
                 check_close(std::string(wino) + " " + cc.what, dout4.get(), want, 5e-5);
                 if (cc.epi == CEPI_COLSUM) {
                     // one partial row per 8x16 tile
