@@ -261,7 +261,18 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        __builtin_amdgcn_s_waitcnt(0);
+        if constexpr (LAST) {
+            __builtin_amdgcn_s_waitcnt(0);
+        } else {
+            // The next chunk's patch copies landed: they were issued at step 0,
+            // before this chunk's 6 NT U loads, and the memory counter
+            // completes in order, so vmcnt(6 NT) covers them while the U loads
+            // for the next chunk's first steps stay in flight under its V
+            // transform.
+            constexpr int VM = 6 * NT;
+            static_assert(VM <= 63, "the 6-bit vmcnt field");
+            __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+        }
         __syncthreads();
     };
 #pragma unroll 1
@@ -275,7 +286,10 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
             for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                 for (int nt2 = 0; nt2 < 2; ++nt2) acc[e][nt][nt2] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
+        // unrolled (at most six chunks): at a loop's back edge the compiler's
+        // memory-counter waits merge to vmcnt(0), which would wait for the U
+        // loads in flight as well
+#pragma unroll
         for (int kc = 0; kc + 2 < NKC; kc += 2) {
             chunk(kc, CInt<0>{}, CInt<0>{});
             chunk(kc + 1, CInt<1>{}, CInt<0>{});
