@@ -668,8 +668,11 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
             dst[mt][1] = *(const f32x4*)(yalive[mt] && ks < 4 ? yrow[mt] + 32 * ks + 16 : hat_zero_row);
         }
     };
-    // fc2 over a third's units from registers: chunks 5..7 of the third
-    auto fc2_third = [&](int q, const unsigned short* wq, f32x4 (&h)[2][6]) {
+    // fc2 over a third's units from registers: chunks 5..7 of the third;
+    // at_last runs in the last step, after its copies are issued (the next
+    // third's first rows: read there, not in fc1's last step, so that fc2's
+    // first two waits are not for them)
+    auto fc2_third = [&](int q, const unsigned short* wq, f32x4 (&h)[2][6], auto&& at_last) {
 #pragma unroll
         for (int s = 0; s < 3; ++s) {
             __builtin_amdgcn_s_waitcnt(0);
@@ -677,6 +680,7 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
             // buffers swapped: the third's chunk 5 + s is in buffer (s & 1 ? 1 : 0)
             if (s < 2) wc_issue<NL2, TX_WAVES>(s & 1 ? Ws0 : Ws1, wq + (size_t)(6 + s) * WC_CHUNK, wave, lane);
             else if (q < 2) wc_issue<NL1, TX_WAVES>(Ws1, wq + (size_t)8 * WC_CHUNK, wave, lane);
+            if (s == 2) at_last();
             if (s == 0) {
                 // + b1 (the lane's four units of each tile, in the third's
                 // permuted row order), then GELU
@@ -737,7 +741,7 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
                 ws_mma<6, MX_HID>(ks & 1 ? Ws0 : Ws1, lr, lg, xb, h);
             }
         }
-        fc2_third(0, wq, h);
+        fc2_third(0, wq, h, [] {});
     }
     // thirds 1, 2: fc1's input read back from the output rows, one k-step ahead
     f32x4 pre[2][2];
@@ -763,7 +767,6 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
                 split_pre(pre, xb);
             }
             if (ks < 4) load_y(ks + 1, pre);
-            else if (q < 2) load_y(0, pre);
             ws_mma<6, MX_HID, HALF>(PAR ? Ws0 : Ws1, lr, lg, xb, h);
         };
 #pragma unroll 1
@@ -772,7 +775,9 @@ __device__ __forceinline__ void habx_body(const TailXArgs& p)
             fc1_step(ks + 1, CInt<1>{}, CInt<0>{});
         }
         fc1_step(4, CInt<0>{}, CInt<1>{});
-        fc2_third(q, wq, h);
+        fc2_third(q, wq, h, [&] {
+            if (q < 2) load_y(0, pre);
+        });
     }
     tx_store_rows<144>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
 }
@@ -910,14 +915,18 @@ __device__ __forceinline__ void habx180_body(const TailXArgs& p)
             dst[mt][1] = *(const f32x4*)(yalive[mt] && (ks < 5 || lg == 0) ? yrow[mt] + 32 * ks + 16 : hat_zero_row);
         }
     };
-    // fc2 over a part's units from registers: chunks 6, 7 of the part
-    auto fc2_part = [&](int q, const unsigned short* wq, f32x4 (&h)[2][4]) {
+    // fc2 over a part's units from registers: chunks 6, 7 of the part;
+    // at_last runs in the last step, after its copies are issued (the next
+    // part's first rows: read there, not in fc1's last step, so that fc2's
+    // first wait is not for them)
+    auto fc2_part = [&](int q, const unsigned short* wq, f32x4 (&h)[2][4], auto&& at_last) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             if (s == 0) wc_issue<NL2, TX_WAVES>(Ws1, wq + (size_t)7 * MX180_SLOT, wave, lane);
             else if (q < NP - 1) wc_issue<NL1, TX_WAVES>(Ws0, wq + (size_t)8 * MX180_SLOT, wave, lane);
+            if (s == 1) at_last();
             if (s == 0) {
                 // + b1 (the lane's four units of each tile, in the part's
                 // permuted row order), then GELU
@@ -971,7 +980,7 @@ __device__ __forceinline__ void habx180_body(const TailXArgs& p)
             split_pre(pre, xb);
             ws_mma<4, MX180_HID>(ks & 1 ? Ws1 : Ws0, lr, lg, xb, h);
         }
-        fc2_part(0, wq, h);
+        fc2_part(0, wq, h, [] {});
     }
     // parts 1..5: fc1's input read back from the output rows, one k-step ahead
     f32x4 pre[2][2];
@@ -991,7 +1000,6 @@ __device__ __forceinline__ void habx180_body(const TailXArgs& p)
             u32x4 xb[2][3];
             split_pre(pre, xb);
             if (ks < 5) load_y(ks + 1, pre);
-            else if (q < NP - 1) load_y(0, pre);
             ws_mma<4, MX180_HID>(PAR ? Ws1 : Ws0, lr, lg, xb, h);
         };
 #pragma unroll 1
@@ -999,7 +1007,9 @@ __device__ __forceinline__ void habx180_body(const TailXArgs& p)
             fc1_step(ks, CInt<0>{});
             fc1_step(ks + 1, CInt<1>{});
         }
-        fc2_part(q, wq, h);
+        fc2_part(q, wq, h, [&] {
+            if (q < NP - 1) load_y(0, pre);
+        });
     }
     tx_store_rows<C>(acc, Cs, mbase, M, lr, lg, p.eps, p.out, LN ? p.xn : nullptr);
 }
