@@ -68,11 +68,11 @@ __device__ __forceinline__ void convwino_body(const ConvArgs& p)
 {
     // Persistent over tiles only for the column-sum epilogue (CAB conv2 60 ->
     // 180: two input chunks, a six-slice epilogue and the sums), where fetching
-    // the next tile under the epilogue measured 257 -> 243 us. For the others
-    // the wait at the top of a tile (for this tile's stores as well as the
-    // next patch) and the barrier cost more than the overlap gains (same box:
-    // 4-9% slower), and the NT = 8 and 9 kernels spill 120-300 bytes more in
-    // the loop.
+    // the next tile under the epilogue measured 254.5 -> 244.8 us. For the
+    // others the wait at the top of a tile (one memory counter, completing in
+    // order: for the previous tile's stores as well as the next patch) and the
+    // barrier cost more than the overlap gains (same box: 4-9% slower), and the
+    // NT = 8 and 9 kernels spill 120-300 bytes more in the loop.
     constexpr bool PERSIST = HEAD == CEPI_COLSUM;
     static_assert(HEAD == -1 || HEAD == CEPI_STORE || HEAD == CEPI_SHUFFLE || HEAD == CEPI_COLSUM,
                   "residual, store, shuffle or column-sum epilogues");
