@@ -218,8 +218,13 @@ CONV_INST(hat_conv_n1_final, 1, CEPI_FINAL)
 // 64-deep product with 27 (of 32) outputs on MFMA, and the conv output at p is
 // sum over the 9 taps of P[p + d(tap)][tap*3 + co], read from LDS. Against a
 // GEMM with the 3 output channels padded to 16 columns this executes 2.4x less
-// MFMA work. The weights (32 x 64) stay in registers; each wave streams its halo
-// row tiles with the next row tile's 4 channel chunks loaded ahead.
+// MFMA work. The products run on split-bf16 MFMA (v_mfma_f32_16x16x32_bf16,
+// every fp32 operand as three bf16 parts and every product as the six terms of
+// order <= 2, as accurate as FP32 MFMA; common.h split3_x8 / mfma16x6): per
+// 16-pixel row tile two 32-channel steps of 2 x 6 MFMAs, against 32 FP32
+// 16x16x4 MFMAs of twice the issue time each. The weights (32 x 64) are split
+// once per block and stay in registers; each wave streams its halo row tiles,
+// reading each one's channels two row tiles ahead.
 // Requires CI = CIp = 64, CO = 3 (the repacked [4][9][COp][16] weights).
 #define CL_TH 16
 #define CL_TW 32
@@ -247,16 +252,23 @@ extern "C" __global__ __launch_bounds__(CL_WAVES * 64) void hat_conv_last3(ConvA
     const int ty = bt / ntx, tx = bt - ty * ntx;
     const int y0 = ty * CL_TH, x0 = tx * CL_TW;
 
-    // A operand: row n = tap*3 + co of the per-tap products (rows 27.. zero).
-    f32x4 wreg[2][4];
+    // A operand: row n = tap*3 + co of the per-tap products (rows 27.. zero),
+    // k-step ks: channels 32 ks + 8 lg .. +7 (in the repacked layout, 16-channel
+    // chunk 2 ks + lg / 2 at 8 (lg & 1)), split.
+    u32x4 wb[2][2][3];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int n = nt * 16 + lr, tap = n / 3, co = n - tap * 3;
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-            if (n < 27) v = *(const f32x4*)(p.w + ((size_t)(kc * 9 + tap) * p.COp + co) * 16 + lg * 4);
-            wreg[nt][kc] = v;
+        for (int ks = 0; ks < 2; ++ks) {
+            f32x4 v0 = (f32x4){0.f, 0.f, 0.f, 0.f}, v1 = v0;
+            if (n < 27) {
+                const float* w = p.w + ((size_t)((2 * ks + (lg >> 1)) * 9 + tap) * p.COp + co) * 16 + 8 * (lg & 1);
+                v0 = *(const f32x4*)w;
+                v1 = *(const f32x4*)(w + 4);
+            }
+            const float f[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            split3_x8(f, wb[nt][ks]);
         }
     }
     // Every wave walks NPW row tiles (the last one past the 39 for wave 7:
@@ -270,28 +282,35 @@ extern "C" __global__ __launch_bounds__(CL_WAVES * 64) void hat_conv_last3(ConvA
         const int hy = hi / CL_HW, hx = hi - hy * CL_HW;
         const int gy = y0 - 1 + hy, gx = x0 - 1 + hx;
         const bool valid = i < NPW && hi < CL_HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
-        return valid ? p.in + ((size_t)gy * W + gx) * p.cin_stride + lg * 4 : hat_zero_row;
+        return valid ? p.in + ((size_t)gy * W + gx) * p.cin_stride + lg * 8 : hat_zero_row;
     };
-    f32x4 xa[4];
-    auto load = [&](int kc, const float* src) { xa[kc] = *(const f32x4*)(src + kc * 16); };
-    {
-        const float* first = src_of(0);
+    // the lane's channels 32 ks + 8 lg .. +7 of its pixel, as two float4s, for
+    // two row tiles: row tile i in slot i % 2, read two row tiles ahead
+    f32x4 xa[2][2][2];
+    auto load = [&](int slot, int ks, const float* src) {
+        xa[slot][ks][0] = *(const f32x4*)(src + ks * 32);
+        xa[slot][ks][1] = *(const f32x4*)(src + ks * 32 + 4);
+    };
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) load(kc, first);
+    for (int i = 0; i < 2; ++i) {
+        const float* first = src_of(i);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) load(i, ks, first);
     }
 #pragma unroll
     for (int i = 0; i < NPW; ++i) {
-        const float* nxt = src_of(i + 1);
+        const float* nxt = src_of(i + 2);
         f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-            const f32x4 a = xa[kc];
-            load(kc, nxt);  // chunk kc of the next row tile
+        for (int ks = 0; ks < 2; ++ks) {
+            const f32x4(&x)[2] = xa[i % 2][ks];
+            const float f[8] = {x[0][0], x[0][1], x[0][2], x[0][3], x[1][0], x[1][1], x[1][2], x[1][3]};
+            u32x4 xb[3];
+            split3_x8(f, xb);
+            load(i % 2, ks, nxt);  // step ks of row tile i + 2
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) acc[nt] = mfma16(wreg[nt][kc][s], a[s], acc[nt]);
-            __builtin_amdgcn_sched_barrier(0);  // the loads stay in their chunk
+            for (int nt = 0; nt < 2; ++nt) acc[nt] = mfma16x6(wb[nt][ks], xb, acc[nt]);
+            __builtin_amdgcn_sched_barrier(0);  // the loads stay in their step
         }
         // lane (lr, lg) holds P[hi][16nt + 4lg .. +3]; columns 28.. are not stored
         const int hi = (wave + CL_WAVES * i) * 16 + lr;
