@@ -349,13 +349,20 @@ int hat_verify(const hat_weights* w, const char* device, const char* fixture_pat
             throw hat::Error(std::string(fixture_path) + ": a " + std::to_string(c) +
                              "-channel fixture; the model takes 3-channel RGB input");
         if (h == 0 || wd == 0 || scale == 0) throw hat::Error(std::string(fixture_path) + ": empty fixture");
+        if ((int)scale != w->w->scale)
+            throw hat::Error(std::string(fixture_path) + " is a x" + std::to_string(scale) +
+                             " fixture but the model is x" + std::to_string(w->w->scale));
+        // Sides are 32-bit fields: bounded here, so that the sizes below cannot
+        // wrap (a header whose products wrap to the file's length would size
+        // the buffers for a few values and run the forward at its real sides)
+        // and the sides fit the forward's int arguments.
+        if (h > (1u << 20) || wd > (1u << 20))
+            throw hat::Error(std::string(fixture_path) + ": a " + std::to_string(h) + "x" + std::to_string(wd) +
+                             " fixture; sides above 2^20 are refused");
         const size_t need = 36 + 4 * ((size_t)h * wd * c + (size_t)h * scale * wd * scale * c);
         if (b.size() != need)
             throw hat::Error(std::string(fixture_path) + ": " + std::to_string(need) + " bytes expected, " +
                              std::to_string(b.size()) + " present");
-        if ((int)scale != w->w->scale)
-            throw hat::Error(std::string(fixture_path) + " is a x" + std::to_string(scale) +
-                             " fixture but the model is x" + std::to_string(w->w->scale));
         std::vector<float> in((size_t)h * wd * c), exp((size_t)h * scale * wd * scale * c);
         memcpy(in.data(), &b[36], in.size() * 4);
         memcpy(exp.data(), &b[36 + in.size() * 4], exp.size() * 4);

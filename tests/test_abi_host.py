@@ -175,6 +175,24 @@ def test_verify_rejects_a_fixture_that_is_not_rgb(weights_dir):
     assert "3-channel" in str(e.value)
 
 
+def test_verify_refuses_sides_whose_sizes_would_wrap(weights_dir):
+    """A HATF header's sides are 32-bit: 2154230017 x 2854344542 at x4 makes
+    3 h w wrap to 26 values and the output to 416 in 64-bit arithmetic, so a
+    1804-byte file would match its own size check while the forward ran at the
+    real sides. Sides above 2^20 are refused before anything is sized."""
+    W = hat_amd.Weights(make_weights(weights_dir, "hat-s", 4, 2, [1]))
+    h, w, scale, c = 2154230017, 2854344542, 4, 3
+    assert (3 * h * w) % 2**64 == 26 and (3 * h * scale * w * scale) % 2**64 == 416
+    wrap = str(weights_dir / "wrap.hatf")
+    with open(wrap, "wb") as f:
+        f.write(struct.pack("<4sIIIIIIII", b"HATF", 1, h, w, c, scale, 0, 0, 0))
+        f.write(np.zeros(26 + 416, dtype="<f4").tobytes())
+    assert os.path.getsize(wrap) == 1804
+    with pytest.raises(hat_amd.HatError) as e:
+        hat_amd.verify(W, wrap)
+    assert "above 2^20" in str(e.value)
+
+
 @pytest.mark.parametrize("shift", [-8, 1, 4, 7, 9, 16, 32])
 def test_swmsa_refuses_a_shift_the_kernels_do_not_build(shift):
     """The attention kernels roll by the plan's half window or not at all; any
