@@ -254,12 +254,25 @@ Weights* Weights::load(const std::string& path)
             throw Error(path + ": tensor `" + kv.first + "` has an incomplete header entry");
         TensorInfo ti;
         ti.dtype = dt->str;
-        for (auto& d : sh->arr) ti.shape.push_back((size_t)d.num);
-        ti.begin = (size_t)off->arr[0].num;
-        ti.end = (size_t)off->arr[1].num;
-        size_t esz = ti.dtype == "F32" ? 4 : ti.dtype == "I64" ? 8 : 0;
-        if (esz == 0) throw Error(path + ": tensor `" + kv.first + "` has unsupported dtype " + ti.dtype);
-        if (ti.end < ti.begin || ti.end > data_len || ti.end - ti.begin != ti.numel() * esz)
+        // Dimensions and offsets are JSON numbers: only exact integers in
+        // [0, 2^53) are taken (a cast of anything else to size_t is undefined),
+        // and the element and byte counts are formed without wrapping, so that
+        // no shape passes the length check below by overflowing to it.
+        auto count = [&](const JVal& v, const char* what) -> size_t {
+            if (v.kind != JVal::Num || !(v.num >= 0.0) || v.num >= 9007199254740992.0 || v.num != std::floor(v.num))
+                throw Error(path + ": tensor `" + kv.first + "` has a " + what + " that is not a count");
+            return (size_t)v.num;
+        };
+        size_t nbytes = ti.dtype == "F32" ? 4 : ti.dtype == "I64" ? 8 : 0;
+        if (nbytes == 0) throw Error(path + ": tensor `" + kv.first + "` has unsupported dtype " + ti.dtype);
+        for (auto& d : sh->arr) {
+            ti.shape.push_back(count(d, "dimension"));
+            if (__builtin_mul_overflow(nbytes, ti.shape.back(), &nbytes))
+                throw Error(path + ": tensor `" + kv.first + "` is larger than any file");
+        }
+        ti.begin = count(off->arr[0], "data offset");
+        ti.end = count(off->arr[1], "data offset");
+        if (ti.end < ti.begin || ti.end > data_len || ti.end - ti.begin != nbytes)
             throw Error(path + ": tensor `" + kv.first + "` has inconsistent offsets");
         if (ti.dtype == "F32" && (ti.begin % 4) != 0)
             throw Error(path + ": tensor `" + kv.first + "` is not 4-byte aligned");
@@ -292,9 +305,11 @@ Weights* Weights::load(const std::string& path)
         std::string t = trim(d);
         char* end = nullptr;
         long v = strtol(t.c_str(), &end, 10);
-        if (t.empty() || *end != '\0' || v <= 0) throw Error(path + ": depths: bad entry `" + t + "`");
+        if (t.empty() || *end != '\0' || v <= 0 || v > 1024) throw Error(path + ": depths: bad entry `" + t + "`");
         w->depths.push_back((int)v);
     }
+    if (w->depths.empty() || w->depths.size() > 64)
+        throw Error(path + ": depths: " + std::to_string(w->depths.size()) + " stages");
     std::vector<std::string> ms = split(meta["rgb_mean"], ',');
     if (ms.size() != 3) throw Error("rgb_mean has " + std::to_string(ms.size()) + " entries, expected 3");
     for (int i = 0; i < 3; ++i) w->mean[i] = strtof(trim(ms[i]).c_str(), nullptr);
@@ -307,11 +322,18 @@ Weights* Weights::load(const std::string& path)
                     std::to_string(w->heads));
     w->window = num("window_size");
     const float overlap = fnum("overlap_ratio");
+    if (!(overlap >= 0.0f && overlap <= 1.0f) || w->window <= 0 || w->window > 256)
+        throw Error(path + ": window_size " + std::to_string(w->window) + " or overlap_ratio " + meta["overlap_ratio"] +
+                    " out of range");
     // int(window_size * overlap_ratio) + window_size, a truncation (weights.rs:93-97)
     w->owin = w->window + (int)((float)w->window * overlap);
     w->scale = num("scale");
     w->head_dim = w->embed / w->heads;
     w->mlp_ratio = num("mlp_ratio");
+    // far past every HAT configuration; what validate() sizes its shape table by
+    if (w->embed <= 0 || w->embed > 4096 || w->heads > 64 || w->window <= 0 || w->window > 256 || w->owin > 512 ||
+        w->mlp_ratio <= 0 || w->mlp_ratio > 16)
+        throw Error(path + ": embed_dim, num_heads, window_size, overlap_ratio or mlp_ratio out of range");
     const int cr = num("compress_ratio"), sf = num("squeeze_factor");
     if (cr <= 0 || sf <= 0) throw Error(path + ": compress_ratio and squeeze_factor must be positive");
     w->compressed = w->embed / cr;
@@ -320,7 +342,10 @@ Weights* Weights::load(const std::string& path)
     w->img_range = fnum("img_range");
     if (!w->has("conv_before_upsample.0.weight"))
         throw Error(path + ": the checkpoint has no `conv_before_upsample.0.weight`");
-    w->head_feat = (int)w->info("conv_before_upsample.0.weight").shape[0];
+    const std::vector<size_t>& hs = w->info("conv_before_upsample.0.weight").shape;
+    if (hs.empty() || hs[0] == 0 || hs[0] > 4096)
+        throw Error(path + ": `conv_before_upsample.0.weight` is " + join_dims(hs));
+    w->head_feat = (int)hs[0];
     w->validate(path);
     return w.release();
 }

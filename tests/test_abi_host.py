@@ -136,6 +136,43 @@ def test_validation_rejects_bad_checkpoints(weights_dir):
         hat_amd.Weights(str(weights_dir / "does_not_exist.safetensors"))
 
 
+def _entry(name, shape, nbytes=None):
+    """An edit that gives tensor `name` this shape, its data starting where it
+    did and spanning nbytes (default: unchanged)."""
+    def edit(h):
+        t = h[name]
+        b = t["data_offsets"][0]
+        t["shape"] = shape
+        if nbytes is not None:
+            t["data_offsets"] = [b, b + nbytes]
+    return edit
+
+
+@pytest.mark.parametrize("case,edit,needle", [
+    # [2^32, 2^32] F32 is 2^66 bytes: with a 64-bit product it wraps to 0 and
+    # an empty byte range would match it
+    ("wrap", _entry("layers.0.conv.weight", [2**32, 2**32], 0), "larger than any file"),
+    ("negative", _entry("layers.0.conv.weight", [-1, 144, 3, 3]), "not a count"),
+    ("fraction", lambda h: h["layers.0.conv.bias"].__setitem__("data_offsets", [0.5, 576.5]), "not a count"),
+    ("huge_depth", lambda h: h["__metadata__"].__setitem__("depths", "2000000000"), "bad entry"),
+    ("many_stages", lambda h: h["__metadata__"].__setitem__("depths", ",".join(["1"] * 65)), "stages"),
+    ("nan_overlap", lambda h: h["__metadata__"].__setitem__("overlap_ratio", "nan"), "out of range"),
+    ("huge_embed", lambda h: h["__metadata__"].__setitem__("embed_dim", "1000000002"), "out of range"),
+    ("rank0_head", _entry("conv_before_upsample.0.weight", [], 4), "conv_before_upsample.0.weight"),
+])
+def test_checkpoint_counts_and_ranges_are_checked_before_use(weights_dir, case, edit, needle):
+    """Shapes and offsets are JSON numbers and the architecture comes from
+    string metadata: values that would wrap a size, are not integers, would
+    make the shape table unbounded, or leave a dimension to read that is not
+    there are refused with an error, not used."""
+    good = make_weights(weights_dir, "hat-s", 4, 2, [1])
+    p = str(weights_dir / f"range_{case}.safetensors")
+    _rewrite_header(good, p, edit)
+    with pytest.raises(hat_amd.HatError) as e:
+        hat_amd.Weights(p)
+    assert needle in str(e.value), (case, str(e.value))
+
+
 def test_backend_refuses_a_cpu_device(weights_dir):
     W = hat_amd.Weights(make_weights(weights_dir, "hat-s", 4, 2, [1]))
     with pytest.raises(hat_amd.HatError) as e:
