@@ -42,6 +42,14 @@ int guard(F&& f)
     }
     return -1;
 }
+
+// A side or count of the C ABI as the int the backend takes: refused past
+// INT_MAX, not truncated to a smaller one the caller's buffers do not match.
+int as_int(size_t v, const char* what)
+{
+    if (v > (size_t)INT32_MAX) throw hat::Error(std::string(what) + " " + std::to_string(v) + " is out of range");
+    return (int)v;
+}
 }  // namespace
 
 extern "C" {
@@ -168,7 +176,7 @@ int hat_backend_forward(hat_backend* b, size_t h, size_t w, const float* in, flo
 {
     return guard([&] {
         if (!b || !in || !out) throw hat::Error("null argument");
-        b->b->forward((int)h, (int)w, in, out);
+        b->b->forward(as_int(h, "height"), as_int(w, "width"), in, out);
         return 0;
     });
 }
@@ -177,7 +185,7 @@ int hat_backend_forward_device(hat_backend* b, size_t h, size_t w, const float* 
 {
     return guard([&] {
         if (!b || !d_in || !d_out) throw hat::Error("null argument");
-        b->b->forward_device((int)h, (int)w, d_in, d_out);
+        b->b->forward_device(as_int(h, "height"), as_int(w, "width"), d_in, d_out);
         return 0;
     });
 }
@@ -187,7 +195,7 @@ int hat_backend_forward_noalloc(hat_backend* b, size_t h, size_t w, const float*
     return guard([&] {
         if (!b || !d_in || !d_out) throw hat::Error("null argument");
         if (h > 65536 || w > 65536) throw hat::Error("forward_noalloc: image too large");
-        b->b->forward_noalloc((int)h, (int)w, d_in, d_out);
+        b->b->forward_noalloc(as_int(h, "height"), as_int(w, "width"), d_in, d_out);
         return 0;
     });
 }
@@ -208,7 +216,7 @@ int hat_backend_hab(hat_backend* b, int stage, int block, size_t hp, size_t wp, 
     return guard([&] {
         if (!b || !x || !out) throw hat::Error("null argument");
         if (hp > 65536 || wp > 65536) throw hat::Error("hab: plane too large");
-        b->b->op_hab(stage, block, (int)hp, (int)wp, x, out, iters, ms);
+        b->b->op_hab(stage, block, as_int(hp, "height"), as_int(wp, "width"), x, out, iters, ms);
         return 0;
     });
 }
@@ -222,7 +230,7 @@ int hat_backend_forward_batch(hat_backend* b, size_t n, size_t h, size_t w, cons
     return guard([&] {
         if (!b || !in || !out) throw hat::Error("null argument");
         if (n > (1u << 20) || h > 65536 || w > 65536) throw hat::Error("forward_batch: too large");
-        b->b->forward_batch((int)n, (int)h, (int)w, in, out);
+        b->b->forward_batch(as_int(n, "image count"), as_int(h, "height"), as_int(w, "width"), in, out);
         return 0;
     });
 }

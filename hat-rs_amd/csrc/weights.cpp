@@ -308,7 +308,7 @@ Weights* Weights::load(const std::string& path)
         if (t.empty() || *end != '\0' || v <= 0 || v > 1024) throw Error(path + ": depths: bad entry `" + t + "`");
         w->depths.push_back((int)v);
     }
-    if (w->depths.empty() || w->depths.size() > 64)
+    if (w->depths.empty() || w->depths.size() > 32)  // hat_model_info holds 32
         throw Error(path + ": depths: " + std::to_string(w->depths.size()) + " stages");
     std::vector<std::string> ms = split(meta["rgb_mean"], ',');
     if (ms.size() != 3) throw Error("rgb_mean has " + std::to_string(ms.size()) + " entries, expected 3");

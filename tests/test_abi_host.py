@@ -155,7 +155,7 @@ def _entry(name, shape, nbytes=None):
     ("negative", _entry("layers.0.conv.weight", [-1, 144, 3, 3]), "not a count"),
     ("fraction", lambda h: h["layers.0.conv.bias"].__setitem__("data_offsets", [0.5, 576.5]), "not a count"),
     ("huge_depth", lambda h: h["__metadata__"].__setitem__("depths", "2000000000"), "bad entry"),
-    ("many_stages", lambda h: h["__metadata__"].__setitem__("depths", ",".join(["1"] * 65)), "stages"),
+    ("many_stages", lambda h: h["__metadata__"].__setitem__("depths", ",".join(["1"] * 33)), "33 stages"),
     ("nan_overlap", lambda h: h["__metadata__"].__setitem__("overlap_ratio", "nan"), "out of range"),
     ("huge_embed", lambda h: h["__metadata__"].__setitem__("embed_dim", "1000000002"), "out of range"),
     ("rank0_head", _entry("conv_before_upsample.0.weight", [], 4), "conv_before_upsample.0.weight"),

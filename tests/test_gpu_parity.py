@@ -246,6 +246,23 @@ def test_verify_contract(hl, weights_dir):
         hl.verify(W, os.path.join(GOLDEN, other["file"]))
 
 
+def test_sides_past_int_max_are_refused(hl, weights_dir):
+    """The C ABI's size_t sides are refused past INT_MAX before any device
+    work (no launch, no allocation), not truncated to a side the caller's
+    buffers do not match: 2^32 + 16 would otherwise run a 16-pixel forward."""
+    W = hl.Weights(make_weights(weights_dir, "hat-s", 4, 31, [2]))
+    be = hl.Backend(W)
+    d_in = hl.DeviceBuffer(3 * 16 * 16 * 4)
+    d_out = hl.DeviceBuffer(3 * 64 * 64 * 4)
+    d_in.upload(np.zeros(3 * 16 * 16, dtype=np.float32))
+    for h, w in [(2**32 + 16, 16), (16, 2**31)]:
+        with pytest.raises(hl.HatError) as e:
+            be.forward_device(h, w, d_in.ptr, d_out.ptr)
+        assert "out of range" in str(e.value)
+    be.forward_device(16, 16, d_in.ptr, d_out.ptr)  # the backend is still usable
+    be.synchronize()
+
+
 def test_plan_cache_and_determinism(hl, weights_dir):
     """Two sizes in turn on one backend (the per-plan buffers are rebuilt), and
     a repeated forward is bit-identical."""
