@@ -198,7 +198,13 @@ void run(const Args& a)
         if (hat_gpu_plan(wt, h, w, &mp) != 0) throw CliError{last_error()};
         const size_t hp = (h + win - 1) / win * win, wp = (w + win - 1) / win * win;
         const unsigned long long per_pixel = mp.activations / 4 / std::max<size_t>(1, hp * wp);
-        const unsigned long long budget = (unsigned long long)(a.mem * 1024.0 * 1024.0);
+        // (mib * 1024 * 1024) as u64 (main.rs:270), Rust's saturating cast:
+        // NaN and negatives give 0, values past the range u64::MAX (a plain C++
+        // cast of those is undefined)
+        const double bytes = a.mem * 1024.0 * 1024.0;
+        const unsigned long long budget = !(bytes > 0.0)                ? 0ull
+                                          : bytes >= 18446744073709551616.0 ? ~0ull
+                                                                            : (unsigned long long)bytes;
         const size_t t = hat_auto_tile(h, w, win, budget, per_pixel, 0, margin);
         if (t == 0) {
             char m[160];

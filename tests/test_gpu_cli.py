@@ -145,6 +145,14 @@ def test_cli_upscales_a_png(hl, small, tmp_path):
     assert "  --mem 100 MiB -> tile 32px (margin 32)" in r.stdout.splitlines()
     assert "  tiled 45x37 into 4 tiles (32px cores, 32px margin, largest 37x45)" in r.stdout.splitlines()
     assert hl.png_load(dst).shape == (3, 148, 180)
+    # the budget in bytes is main.rs:270's `as u64`, a saturating cast: NaN and
+    # negative budgets hold no window, a huge one holds the whole image
+    for m in ("nan", "-5"):
+        r = _cli(hl, "-m", wp, "-i", src, "-o", dst, "--mem", m)
+        assert r.returncode != 0 and "too small even for one window" in r.stderr, (m, r.stderr)
+    r = _cli(hl, "-m", wp, "-i", src, "-o", dst, "--mem", "1e300")
+    assert r.returncode == 0, r.stderr
+    assert "  --mem 1e+300 MiB -> tile 45px (margin 32)" in r.stdout.splitlines()
 
 
 def test_cli_verify_and_selftest(hl, tmp_path):
