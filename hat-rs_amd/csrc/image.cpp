@@ -26,6 +26,23 @@ const unsigned char kSig[8] = {0x89, 'P', 'N', 'G', '\r', '\n', 0x1a, '\n'};
 
 uint32_t be32(const unsigned char* p) { return (uint32_t)p[0] << 24 | (uint32_t)p[1] << 16 | (uint32_t)p[2] << 8 | p[3]; }
 
+// A chunk type for a message: its bytes come from the file, so anything
+// outside printable ASCII is written as \xNN (messages stay valid text)
+std::string chunk_name(const unsigned char* type)
+{
+    std::string s;
+    for (int i = 0; i < 4; ++i) {
+        if (type[i] >= 0x20 && type[i] < 0x7f) {
+            s += (char)type[i];
+        } else {
+            char e[8];
+            snprintf(e, sizeof e, "\\x%02x", type[i]);
+            s += e;
+        }
+    }
+    return s;
+}
+
 void put32(std::vector<unsigned char>& o, uint32_t v)
 {
     o.push_back((unsigned char)(v >> 24));
@@ -100,7 +117,7 @@ Image load_png(const std::string& path)
             const unsigned char* data = &b[off + 8];
             const uint32_t crc = be32(&b[off + 8 + len]);
             if ((uint32_t)crc32(crc32(0L, Z_NULL, 0), type, len + 4) != crc)
-                throw Error(std::string("CRC error in chunk ") + std::string((const char*)type, 4));
+                throw Error(std::string("CRC error in chunk ") + chunk_name(type));
             if (!memcmp(type, "IHDR", 4)) {
                 if (len != 13) throw Error("IHDR has the wrong length");
                 w = be32(data);
@@ -120,7 +137,7 @@ Image load_png(const std::string& path)
                 // an unknown critical chunk (PLTE is critical but only meaningful
                 // for the indexed type, which is refused below)
                 if (memcmp(type, "PLTE", 4) != 0)
-                    throw Error(std::string("unknown critical chunk ") + std::string((const char*)type, 4));
+                    throw Error(std::string("unknown critical chunk ") + chunk_name(type));
             }
             off += 12 + len;
         }

@@ -38,6 +38,34 @@ struct JVal {
     }
 };
 
+// Whether s is well-formed UTF-8 (no overlong forms, no surrogates, at most
+// U+10FFFF): a safetensors header is UTF-8 JSON, and its strings name tensors
+// and end up in messages.
+bool utf8_ok(const std::string& s)
+{
+    const unsigned char* q = (const unsigned char*)s.data();
+    const unsigned char* end = q + s.size();
+    while (q < end) {
+        const unsigned c = *q++;
+        if (c < 0x80) continue;
+        int n;
+        unsigned cp;
+        if (c >= 0xC2 && c <= 0xDF) n = 1, cp = c & 0x1F;
+        else if (c >= 0xE0 && c <= 0xEF) n = 2, cp = c & 0x0F;
+        else if (c >= 0xF0 && c <= 0xF4) n = 3, cp = c & 0x07;
+        else return false;
+        if (end - q < n) return false;
+        for (int i = 0; i < n; ++i) {
+            if ((q[i] & 0xC0) != 0x80) return false;
+            cp = cp << 6 | (q[i] & 0x3F);
+        }
+        q += n;
+        if ((n == 2 && (cp < 0x800 || (cp >= 0xD800 && cp <= 0xDFFF))) || (n == 3 && (cp < 0x10000 || cp > 0x10FFFF)))
+            return false;
+    }
+    return true;
+}
+
 struct JParser {
     const char* p;
     const char* e;
@@ -79,6 +107,7 @@ struct JParser {
         }
         if (p >= e) fail("unterminated string");
         ++p;
+        if (!utf8_ok(s)) fail("a string that is not UTF-8");
         return s;
     }
     JVal value()

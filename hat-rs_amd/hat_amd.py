@@ -120,7 +120,8 @@ def lib():
 
 
 def _err():
-    return lib().hat_last_error().decode()
+    # messages can quote names read from a file: never fail on their bytes
+    return lib().hat_last_error().decode(errors="replace")
 
 
 def _check(rc, what):
