@@ -2229,6 +2229,7 @@ void op_swmsa(const float* x, float* out, int hp, int wp, int c, int heads, int 
     // Arguments are checked before the runtime is touched.
     if (!x || !out || !qkv_w || !qkv_b || !proj_w || !proj_b || !table) throw Error("swmsa: null argument");
     if (hp <= 0 || wp <= 0 || c <= 0 || heads <= 0) throw Error("swmsa: empty plane or no channels");
+    if ((size_t)hp * wp > (1u << 26) || c > 4096) throw Error("swmsa: plane or channels too large");  // int token counts
     if (c % heads) throw Error("swmsa: c must be divisible by heads");
     const int D = c / heads;
     if (D != 24 && D != 30) throw Error("swmsa: head_dim " + std::to_string(D) + " has no kernel (24, 30)");
@@ -2285,6 +2286,7 @@ void op_ocab(const float* x, float* out, int hp, int wp, int c, int heads, int m
         !fc1_w || !fc1_b || !fc2_w || !fc2_b)
         throw Error("ocab: null argument");
     if (hp <= 0 || wp <= 0 || c <= 0 || heads <= 0 || mlp_ratio <= 0) throw Error("ocab: empty plane or no channels");
+    if ((size_t)hp * wp > (1u << 26) || c > 4096) throw Error("ocab: plane or channels too large");  // int token counts
     if (c % heads) throw Error("ocab: c must be divisible by heads");
     const int D = c / heads;
     if (D != 24 && D != 30) throw Error("ocab: head_dim " + std::to_string(D) + " has no kernel (24, 30)");

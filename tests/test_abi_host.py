@@ -242,6 +242,18 @@ def test_swmsa_refuses_a_shift_the_kernels_do_not_build(shift):
     assert "shift" in str(e.value)
 
 
+def test_ops_refuse_planes_past_their_int_token_counts():
+    """The isolated ops count tokens in ints: a 16384 x 16384 plane (2^28
+    tokens) is refused before any buffer is read, not overflowed."""
+    L = hat_amd.lib()
+    x = np.zeros(16, dtype=np.float32)
+    p = hat_amd._fp(x)
+    rc = L.hat_op_swmsa(p, p, 16384, 16384, 144, 6, 0, p, p, p, p, p, 1, None, None)
+    assert rc == -1 and "too large" in hat_amd._err()
+    rc = L.hat_op_ocab(p, p, 16384, 16384, 144, 6, 2, *([p] * 13), 1, None, None)
+    assert rc == -1 and "too large" in hat_amd._err()
+
+
 def _tamper_i64(src, dst, name, index, value):
     b = bytearray(open(src, "rb").read())
     (n,) = struct.unpack("<Q", b[:8])
