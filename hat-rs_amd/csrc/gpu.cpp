@@ -2088,8 +2088,10 @@ void GpuBackend::forward(int h, int w, const float* in, float* out)
         copy_out(t);
     };
     std::vector<std::thread> pool;
-    for (unsigned t = 1; t < T; ++t) pool.emplace_back(worker, t);
     try {
+        // inside the try: if a thread cannot be started, the ones that were are
+        // released (queued = -1) and joined below, not destroyed while joinable
+        for (unsigned t = 1; t < T; ++t) pool.emplace_back(worker, t);
         copy_in(0);
         while (in_done.load(std::memory_order_acquire) < T) std::this_thread::yield();
         rt.check(api.MemcpyAsync(a_.din, stage_in_, in_bytes, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync H2D");
